@@ -1,0 +1,204 @@
+"""Calibration tables for a bit allocation: the setup that produces BlockGTQParameters.
+
+Follows the published Block-GTQ setup (upstream commit 3fe14e7, as vendored by
+the reference): greedy bit allocation (src/reference/allocator.py:4-17),
+grouping of RoPE pairs by width (src/reference/mixed_layout.py:5-18), one
+Lloyd-Max codebook per width for N(0, 1/d_group) and one Haar rotation per
+width >= rotation_threshold (vendor/blockgtq/block_gtq_pipeline.py:24-92,
+151-246), and the 256-bin code LUT (vendor/blockgtq/quant_kernels.py:276-364).
+Tables are inputs of the hot path; this module only builds them.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from .layout import BlockGTQParameters
+
+
+def allocate_bits(scores, budget: int, min_bits: int = 1, max_bits: int = 8) -> np.ndarray:
+    """Greedy: one more bit to argmax s*4^-b (FP32 scores, FP64 powers, first index on ties)."""
+    s = np.asarray(scores, dtype=np.float32)
+    w = np.full(len(s), min_bits, dtype=np.int64)
+    remaining = int(budget) - int(w.sum())
+    while remaining > 0:
+        pri = s * np.power(4.0, -w.astype(np.float64))
+        pri[w >= max_bits] = -1.0
+        best = int(np.argmax(pri))
+        if pri[best] <= 0:
+            break
+        w[best] += 1
+        remaining -= 1
+    return w
+
+
+def grouping(widths) -> dict:
+    """Pairs sorted by width, (p, p + L) interleaved.
+
+    Upstream sorts with torch's default argsort; the tables the reference
+    committed (10 mixed layouts, 90 SmolLM2 heads, written with torch 2.12)
+    all have ties in ascending pair order, i.e. a stable sort. A stable sort
+    reproduces them on any torch version.
+    """
+    order = np.argsort(np.asarray(widths, dtype=np.int64), kind="stable")
+    L = len(order)
+    head_perm = np.empty(2 * L, np.int64)
+    head_perm[0::2], head_perm[1::2] = order, order + L
+    sorted_w = np.asarray(widths)[order]
+    bits, counts = np.unique(sorted_w, return_counts=True)
+    offsets = np.concatenate([[0], np.cumsum(counts * 2)])
+    group_of = np.repeat(np.arange(len(bits)), counts * 2)
+    ns = int((np.asarray(widths) <= 4).sum()) * 2
+    return dict(pair_order=order, head_perm=head_perm, group_bits=bits, group_offsets=offsets, group_of=group_of,
+                nopack_start=ns, row_bytes=ns // 2 + 2 * L - ns)
+
+
+def _cond_mean(sigma, a, b):
+    """E[X | a < X < b] for X ~ N(0, sigma^2)."""
+    from scipy.special import ndtr
+    za = a / sigma if np.isfinite(a) else a
+    zb = b / sigma if np.isfinite(b) else b
+    if not np.isfinite(za):
+        mass = ndtr(zb)
+    elif not np.isfinite(zb):
+        mass = ndtr(-za)
+    else:
+        mass = ndtr(zb) - ndtr(za)
+    if mass < 1e-15:
+        if np.isfinite(a) and not np.isfinite(b):
+            return a + sigma
+        if np.isfinite(b) and not np.isfinite(a):
+            return b - sigma
+        if np.isfinite(a) and np.isfinite(b):
+            return (a + b) / 2.0
+        return 0.0
+    phi = lambda z: 0.0 if not np.isfinite(z) else math.exp(-0.5 * z * z) / math.sqrt(2 * math.pi)
+    return sigma * (phi(za) - phi(zb)) / mass
+
+
+def gaussian_codebook(bits: int, dim: int) -> np.ndarray:
+    """MSE-optimal scalar codebook for one coordinate of a random unit vector in R^dim."""
+    n = 1 << bits
+    if bits == 1:
+        c = math.sqrt(2.0 / (math.pi * dim))
+        return np.array([-c, c], np.float32)
+    if bits == 2:
+        return (np.array([-1.51, -0.453, 0.453, 1.51]) / math.sqrt(dim)).astype(np.float32)
+    from scipy.special import ndtri
+    sigma = 1.0 / math.sqrt(dim)
+    bounds = ndtri(np.linspace(0, 1, n + 1)[1:-1]) * sigma
+    cents = np.zeros(n)
+
+    def update(bd):
+        cents[0] = _cond_mean(sigma, -np.inf, bd[0])
+        for i in range(1, n - 1):
+            cents[i] = _cond_mean(sigma, bd[i - 1], bd[i])
+        cents[-1] = _cond_mean(sigma, bd[-1], np.inf)
+
+    update(bounds)
+    for _ in range(100):
+        bounds = (cents[:-1] + cents[1:]) / 2.0
+        update(bounds)
+    return np.sort(cents).astype(np.float32)
+
+
+def haar_rotation(dim: int, seed: int) -> np.ndarray:
+    """Haar-distributed rotation: QR of a Gaussian matrix, sign-fixed, det +1."""
+    g = np.random.default_rng(seed).standard_normal((dim, dim))
+    q, r = np.linalg.qr(g)
+    s = np.sign(np.diag(r))
+    s[s == 0] = 1.0
+    q = q * s[None, :]
+    if np.linalg.slogdet(q)[0] < 0:
+        q[:, 0] = -q[:, 0]
+    return q.astype(np.float32)
+
+
+def code_lut(pos_centroids, pos_boundaries, n_bins: int = 256):
+    """Bin -> centroid index per distinct codebook, plus per-position bin offset and 1/width."""
+    import torch
+    cents = np.asarray(pos_centroids, np.float32)
+    bounds = np.asarray(pos_boundaries, np.float32)
+    d = cents.shape[0]
+    offsets = np.zeros(d, np.float32)
+    inv = np.zeros(d, np.float32)
+    nvalid = []
+    for j in range(d):
+        nc = max(int((bounds[j] < 1e30).sum()) + 1, 2)
+        nvalid.append(nc)
+        lo, hi = float(cents[j, :nc].min()), float(cents[j, :nc].max())
+        margin = (hi - lo) / max(nc - 1, 1) * 0.5
+        offsets[j] = lo - margin
+        inv[j] = 1.0 / (((hi + margin) - (lo - margin)) / n_bins)
+    books, pos_cb = {}, np.zeros(d, np.int64)
+    reps = []
+    for j in range(d):
+        key = (nvalid[j], tuple(cents[j, :nvalid[j]].tolist()))
+        if key not in books:
+            books[key] = len(reps)
+            reps.append(j)
+        pos_cb[j] = books[key]
+    lut = np.zeros((len(reps), n_bins), np.uint8)
+    for b, j in enumerate(reps):
+        nc = nvalid[j]
+        c = torch.from_numpy(cents[j, :nc].copy())
+        lo, hi = c.min().item(), c.max().item()
+        margin = (hi - lo) / max(nc - 1, 1) * 0.5
+        width = ((hi + margin) - (lo - margin)) / n_bins
+        centers = torch.linspace(lo - margin + width / 2, hi + margin - width / 2, n_bins, dtype=torch.float32)
+        nb = int((bounds[j] < 1e30).sum())
+        if nb > 0:
+            idx = torch.searchsorted(torch.from_numpy(bounds[j, :nb].copy()), centers).clamp(max=nc - 1)
+        else:
+            idx = (centers > (c[0] + c[1]) / 2.0).long()
+        lut[b] = idx.numpy().astype(np.uint8)
+    return lut, pos_cb, offsets, inv
+
+
+def make_parameters(widths, rotation_threshold: int = 2, row_bytes: int | None = None,
+                    norm_stride: int | None = None) -> BlockGTQParameters:
+    """Full table set for a per-pair width allocation (2*len(widths) dims)."""
+    import torch
+    widths = np.asarray(widths, np.int64)
+    grp = grouping(widths)
+    d = 2 * len(widths)
+    bits = [int(b) for b in grp["group_bits"]]
+    offs = grp["group_offsets"]
+    rot = np.zeros((d, d), np.float32)
+    maxc = max(1 << b for b in bits)
+    cents = np.zeros((d, maxc), np.float32)
+    bnds = np.full((d, maxc - 1), np.inf, np.float32)
+    for g, bw in enumerate(bits):
+        s, e = int(offs[g]), int(offs[g + 1])
+        rot[s:e, s:e] = np.eye(e - s, dtype=np.float32) if bw < rotation_threshold else haar_rotation(e - s, 42 + bw)
+        c = gaussian_codebook(bw, e - s)
+        tc = torch.from_numpy(c)
+        b = ((tc[:-1] + tc[1:]) / 2.0).numpy()  # FP32 midpoints
+        cents[s:e, :len(c)] = c
+        bnds[s:e, :len(b)] = b
+    lut, pos_cb, off, inv = code_lut(cents, bnds)
+    ng = len(bits)
+    return BlockGTQParameters(
+        dim=d, groups=ng, rowBytes=int(row_bytes or grp["row_bytes"]), normStride=int(norm_stride or ng),
+        nibbleDims=grp["nopack_start"], maxCentroids=maxc, permutation=grp["head_perm"].astype(np.uint32),
+        groupOf=grp["group_of"].astype(np.uint32), positionToCodebook=pos_cb.astype(np.uint32),
+        codeLut=lut.reshape(-1), rotation=rot.reshape(-1), centroids=cents.reshape(-1), offsets=off,
+        inverseScales=inv)
+
+
+def geometric_scores(n_pairs: int, ratio: float = 0.9) -> np.ndarray:
+    """Per-pair energy decaying geometrically (ratio**i)."""
+    return (ratio ** np.arange(n_pairs)).astype(np.float32)
+
+
+def layout_b(dim: int) -> BlockGTQParameters:
+    """Widths in {4, 8}, half each (6.0 bits average): 4 x allocate_bits(0.9**i, 1.5*pairs, 1, 2)."""
+    n = dim // 2
+    return make_parameters(4 * allocate_bits(geometric_scores(n), (3 * n) // 2, 1, 2))
+
+
+def layout_a(dim: int) -> BlockGTQParameters:
+    """allocate_bits(0.9**i, 6*pairs, 4, 8): widths 4..8 at a 6.0 average."""
+    n = dim // 2
+    return make_parameters(allocate_bits(geometric_scores(n), 6 * n, 4, 8))

@@ -1,0 +1,101 @@
+"""Build libbgtq.so (HIP kernels for gfx950 + the C ABI) in place.
+
+    python block-gqt-webgpu_amd/build.py            # library
+    python block-gqt-webgpu_amd/build.py --napi     # library + Node N-API addon
+
+hipcc cross-compiles for gfx950 without a GPU present. All device code is
+built with -ffp-contract=off (the encoder reproduces a CPU rounding sequence
+bit for bit, so nothing may be fused behind its back), correctly rounded fp32
+division/square root, FP32 denormals kept, and packed-FP32 instruction
+selection disabled.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB_DIR = PKG / "lib"
+OBJ_DIR = PKG / "_build"
+INCLUDE = PKG.parent / "include"
+ARCH = os.environ.get("BGTQ_OFFLOAD_ARCH", "gfx950")
+
+DEVICE_SOURCES = ["encode.hip", "decode.hip", "reconstruct.hip"]
+HOST_SOURCES = ["bgtq_api.cpp"]
+
+COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}"]
+DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+                "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang",
+                "-packed-fp32-ops"]
+
+
+def hipcc():
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns about the packed-fp32 target feature; drop that noise.
+    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build_library(verbose=False) -> Path:
+    OBJ_DIR.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    cc = hipcc()
+    jobs = []
+    for src in DEVICE_SOURCES:
+        jobs.append([cc, *COMMON, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(OBJ_DIR / (src + ".o"))])
+    for src in HOST_SOURCES:
+        jobs.append([cc, *COMMON, f"--offload-arch={ARCH}", "-c", str(CSRC / src), "-o", str(OBJ_DIR / (src + ".o"))])
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        for out in ex.map(_run, jobs):
+            if verbose and out:
+                print(out, file=sys.stderr)
+    target = LIB_DIR / "libbgtq.so"
+    tmp = LIB_DIR / "libbgtq.so.tmp"
+    objs = [str(OBJ_DIR / (s + ".o")) for s in DEVICE_SOURCES + HOST_SOURCES]
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
+    os.replace(tmp, target)
+    return target
+
+
+def build_napi() -> Path:
+    """Node N-API addon over libbgtq.so (headers from the image's Node)."""
+    node_inc = None
+    for cand in ("/usr/include/node", "/usr/local/include/node"):
+        if (Path(cand) / "node_api.h").exists():
+            node_inc = cand
+    if node_inc is None:
+        raise RuntimeError("node_api.h not found")
+    src = PKG / "node" / "bgtq_napi.cc"
+    out = PKG / "node" / "bgtq_napi.node"
+    _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", f"-I{node_inc}", f"-I{INCLUDE}", str(src),
+          "-o", str(out), f"-L{LIB_DIR}", "-lbgtq", "-Wl,-rpath,$ORIGIN/../lib"])
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--napi", action="store_true")
+    ap.add_argument("-v", "--verbose", action="store_true")
+    a = ap.parse_args()
+    print(build_library(a.verbose))
+    if a.napi:
+        print(build_napi())
+
+
+if __name__ == "__main__":
+    main()

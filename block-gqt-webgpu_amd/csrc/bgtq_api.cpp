@@ -1,0 +1,906 @@
+// Host side of the C ABI declared in include/bgtq.h.
+//
+// Each object validates its inputs with the reference's checks and messages
+// before any device work, and mutates its state only after the device work
+// it depends on has completed.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/bgtq.h"
+#include "bgtq_internal.h"
+
+using namespace bgtq;
+
+namespace {
+
+thread_local std::string g_error;
+
+bgtq_status fail(bgtq_status code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+bgtq_status hip_fail(hipError_t e, const char *what) {
+  return fail(BGTQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                   \
+  do {                                        \
+    hipError_t e_ = (expr);                   \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+// RNE FP32 -> FP16 bits with subnormals and overflow to infinity
+// (src/webgpu/half.wgsl:2-12 states the same rule).
+uint16_t f32_to_f16(float x) {
+  uint32_t b;
+  std::memcpy(&b, &x, 4);
+  const uint32_t sign = (b >> 16) & 0x8000u, e = (b >> 23) & 0xffu, m = b & 0x7fffffu;
+  if (e == 0xffu) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u : 0u));
+  const int32_t he = (int32_t)e - 112;
+  if (he >= 31) return (uint16_t)(sign | 0x7c00u);
+  uint32_t mant = m, shift = 13;
+  if (he <= 0) {
+    if (he < -10) return (uint16_t)sign;
+    mant = m | 0x800000u;
+    shift = (uint32_t)(14 - he);
+  }
+  const uint32_t base = mant >> shift, rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+  const uint32_t inc = (rem > half || (rem == half && (base & 1u))) ? 1u : 0u;
+  return (uint16_t)(sign | ((he > 0 ? (uint32_t)he << 10 : 0u) + base + inc));
+}
+
+struct DeviceBuffer {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  ~DeviceBuffer() {
+    if (ptr) (void)hipFree(ptr);
+  }
+  bgtq_status alloc(size_t n, const char *what) {
+    // Round up to 256 bytes: kernels may read the dword holding a row's last byte.
+    const size_t padded = ((n + 16 + 255) / 256) * 256;
+    hipError_t e = hipMalloc(&ptr, padded);
+    if (e != hipSuccess) {
+      ptr = nullptr;
+      return fail(BGTQ_ERR_NOMEM, "%s: hipMalloc(%zu) failed: %s", what, padded, hipGetErrorString(e));
+    }
+    bytes = n;
+    e = hipMemset(ptr, 0, padded);  // new buffers start zeroed (src/runtime/compressed-keys.ts:25)
+    if (e != hipSuccess) return hip_fail(e, what);
+    return BGTQ_OK;
+  }
+};
+
+struct Ledger {
+  std::vector<bgtq_allocation> items;
+  void add(const char *name, int32_t role, uint64_t bytes) {
+    bgtq_allocation a{};
+    std::snprintf(a.name, sizeof(a.name), "%s", name);
+    a.role = role;
+    a.bytes = bytes;
+    items.push_back(a);
+  }
+  bgtq_status copy(bgtq_allocation *out, size_t cap, size_t *n) const {
+    if (n) *n = items.size();
+    if (out) std::memcpy(out, items.data(), sizeof(bgtq_allocation) * std::min(cap, items.size()));
+    return BGTQ_OK;
+  }
+};
+
+}  // namespace
+
+struct bgtq_context {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  DeviceBuffer staging;  // per-call upload area, never part of an object's ledger
+  bgtq_status use() {
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    return BGTQ_OK;
+  }
+  bgtq_status ensure_staging(size_t bytes) {
+    if (staging.ptr && staging.bytes >= bytes) return BGTQ_OK;
+    HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (staging.ptr) {
+      (void)hipFree(staging.ptr);
+      staging.ptr = nullptr;
+      staging.bytes = 0;
+    }
+    return staging.alloc(std::max<size_t>(bytes, 1 << 20), "upload staging");
+  }
+};
+
+struct bgtq_tables {
+  bgtq_context *ctx = nullptr;
+  bgtq_tables_info info{};
+  DeviceBuffer blob;
+  std::vector<uint8_t> host;  // the DevTables image uploaded to blob
+  const DevTables *dev() const { return static_cast<const DevTables *>(blob.ptr); }
+  const DevTables *h() const { return reinterpret_cast<const DevTables *>(host.data()); }
+};
+
+struct bgtq_keys {
+  int32_t kind = 0;
+  bgtq_context *ctx = nullptr;
+  bgtq_tables *tables = nullptr;
+  uint32_t dim = 0, capacity = 0, length = 0;
+  bool pending = false;
+  DeviceBuffer packed, norms, fp16, decoded;
+  Ledger ledger;
+};
+
+struct bgtq_values {
+  bgtq_context *ctx = nullptr;
+  uint32_t dim = 0, capacity = 0, length = 0;
+  int32_t dtype = BGTQ_DTYPE_F32;
+  DeviceBuffer buf;
+  Ledger ledger;
+};
+
+struct bgtq_attention {
+  bgtq_keys *keys = nullptr;
+  bgtq_values *values = nullptr;
+  uint32_t max_queries = 0, queries = 0, max_splits = 1;
+  int32_t causal = 0, materialize = 0;
+  std::vector<uint32_t> positions;
+  DeviceBuffer q, qr, out, logits, probs, part, stats, small;  // small: lengths[1] + ends[maxQ]
+  uint32_t *pinned = nullptr;                                  // host staging of small
+  Ledger ledger;
+  ~bgtq_attention() {
+    if (pinned) (void)hipHostFree(pinned);
+  }
+};
+
+extern "C" {
+
+const char *bgtq_last_error(void) { return g_error.c_str(); }
+int32_t bgtq_abi_version(void) { return 1; }
+
+// ---------------------------------------------------------------- context
+bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
+  if (!out) return fail(BGTQ_ERR_RANGE, "null output pointer");
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0) return fail(BGTQ_ERR_DEVICE, "no HIP device available");
+  if (device < 0 || device >= count) return fail(BGTQ_ERR_RANGE, "device %d out of range", device);
+  auto *c = new bgtq_context();
+  c->device = device;
+  if ((e = hipSetDevice(device)) != hipSuccess || (e = hipStreamCreate(&c->own)) != hipSuccess) {
+    delete c;
+    return hip_fail(e, "context");
+  }
+  c->stream = c->own;
+  *out = c;
+  return BGTQ_OK;
+}
+
+void bgtq_context_destroy(bgtq_context *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->staging.ptr) {
+    (void)hipFree(ctx->staging.ptr);
+    ctx->staging.ptr = nullptr;
+  }
+  (void)hipStreamDestroy(ctx->own);
+  delete ctx;
+}
+
+bgtq_status bgtq_context_synchronize(bgtq_context *ctx) {
+  if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
+  if (bgtq_status s = ctx->use()) return s;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return BGTQ_OK;
+}
+
+void *bgtq_context_stream(bgtq_context *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+bgtq_status bgtq_context_set_stream(bgtq_context *ctx, void *hip_stream) {
+  if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
+  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+  return BGTQ_OK;
+}
+
+// ---------------------------------------------------------------- tables
+bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_t n_integer,
+                               const float *floating, size_t n_floating, bgtq_tables **out) {
+  if (!ctx || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (!integer || n_integer < 10) return fail(BGTQ_ERR_RANGE, "Invalid Block-GTQ layout");
+  // validateLayout (src/webgpu/layout.ts:8-23)
+  const int64_t d = integer[0], ng = integer[1], rb = integer[2], nstride = integer[3], nib = integer[4],
+                mc = integer[5];
+  if (d < 2 || d > 128 || d % 2 || ng < 1 || ng > 8 || nstride < ng || nib < 0 || nib > d || nib % 2 ||
+      rb < nib / 2 + d - nib || mc < 2 || mc > 256)
+    return fail(BGTQ_ERR_RANGE, "Invalid Block-GTQ layout");
+  const uint64_t o_perm = integer[6], o_group = integer[7], o_cb = integer[8], o_lut = integer[9];
+  const auto in_range = [&](uint64_t o, uint64_t n) { return o <= n_integer && n <= n_integer - o; };
+  if (!in_range(o_perm, d) || !in_range(o_group, d) || !in_range(o_cb, d) || o_lut > n_integer)
+    return fail(BGTQ_ERR_RANGE, "Invalid calibration table shape");
+  const uint64_t lut_len = n_integer - o_lut;
+  const uint32_t *perm = integer + o_perm, *group_of = integer + o_group, *pos_cb = integer + o_cb;
+  const uint32_t *lut = integer + o_lut;
+  std::vector<int> seen(d, 0);
+  bool bad = lut_len % 256 != 0 || lut_len == 0;
+  for (int64_t i = 0; i < d && !bad; ++i) {
+    if (perm[i] >= d || seen[perm[i]]++) bad = true;
+    if (group_of[i] >= ng) bad = true;
+    if ((uint64_t)pos_cb[i] * 256 >= lut_len) bad = true;
+  }
+  if (!floating || n_floating != (size_t)(d * d + d * mc + 2 * d)) bad = true;
+  if (bad) return fail(BGTQ_ERR_RANGE, "Invalid calibration table shape");
+  for (size_t i = 0; i < n_floating; ++i)
+    if (!std::isfinite(floating[i])) return fail(BGTQ_ERR_RANGE, "Nonfinite calibration table");
+  for (int64_t i = 0; i < d; ++i)
+    for (int bin = 0; bin < 256; ++bin) {
+      const uint32_t code = lut[(uint64_t)pos_cb[i] * 256 + bin];
+      if (code >= mc || (i < nib && code > 15)) return fail(BGTQ_ERR_RANGE, "Code LUT incompatible with packing");
+    }
+  const float *rot = floating, *cent = floating + d * d, *off = cent + d * mc, *inv = off + d;
+  // PackedKeys constructor checks (src/runtime/packed-keys.ts:16-23).
+  int32_t gstart[8], gend[8], gsize[8];
+  for (int g = 0; g < 8; ++g) gstart[g] = gend[g] = gsize[g] = 0;
+  for (int64_t j = 0; j < d; ++j) {
+    int64_t first = -1, last = -1, members = 0;
+    for (int64_t i = 0; i < d; ++i)
+      if (group_of[i] == group_of[j]) {
+        if (first < 0) first = i;
+        last = i;
+        ++members;
+      }
+    if (last + 1 - first != members) return fail(BGTQ_ERR_STATE, "Non-contiguous transform group");
+    for (int64_t i = 0; i < d; ++i)
+      if ((i < first || i > last) && rot[i * d + j] != 0.0f)
+        return fail(BGTQ_ERR_STATE, "Off-group transform is nonzero");
+    gstart[group_of[j]] = (int32_t)first;
+    gend[group_of[j]] = (int32_t)(last + 1);
+    gsize[group_of[j]] = (int32_t)members;
+  }
+  for (int g = 0; g < ng; ++g)
+    if (gsize[g] == 0) return fail(BGTQ_ERR_UNSUPPORTED, "group %d has no positions", g);
+  // Distinct centroid rows ("books"), as build_code_lut groups positions by signature.
+  std::vector<int> pos_book(d);
+  std::vector<int64_t> book_rows;
+  for (int64_t j = 0; j < d; ++j) {
+    int found = -1;
+    for (size_t b = 0; b < book_rows.size() && found < 0; ++b)
+      if (std::memcmp(cent + book_rows[b] * mc, cent + j * mc, sizeof(float) * mc) == 0) found = (int)b;
+    if (found < 0) {
+      found = (int)book_rows.size();
+      book_rows.push_back(j);
+    }
+    pos_book[j] = found;
+  }
+  const int nb = (int)book_rows.size(), ncb = (int)(lut_len / 256);
+  if (nb > 255 || ncb > 255) return fail(BGTQ_ERR_UNSUPPORTED, "more than 255 distinct codebooks");
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const size_t off_lut = align(sizeof(DevTables));
+  const size_t off_books = align(off_lut + lut_len);
+  const size_t off_rot = align(off_books + sizeof(float) * nb * mc);
+  const size_t total = off_rot + sizeof(float) * d * d;
+  auto *t = new bgtq_tables();
+  t->ctx = ctx;
+  t->host.assign(total, 0);
+  auto *T = reinterpret_cast<DevTables *>(t->host.data());
+  T->dim = (int32_t)d;
+  T->groups = (int32_t)ng;
+  T->row_bytes = (int32_t)rb;
+  T->norm_stride = (int32_t)nstride;
+  T->nibble_dims = (int32_t)nib;
+  T->max_centroids = (int32_t)mc;
+  T->n_books = nb;
+  T->n_codebooks = ncb;
+  for (int g = 0; g < 8; ++g) {
+    T->gstart[g] = gstart[g];
+    T->gend[g] = gend[g];
+    T->gsize[g] = gsize[g];
+  }
+  T->off_lut = (uint32_t)off_lut;
+  T->off_books = (uint32_t)off_books;
+  T->off_rot = (uint32_t)off_rot;
+  T->total_bytes = (uint32_t)total;
+  for (int64_t j = 0; j < d; ++j) {
+    T->perm[j] = (uint8_t)perm[j];
+    T->group_of[j] = (uint8_t)group_of[j];
+    T->pos_cb[j] = (uint8_t)pos_cb[j];
+    T->pos_book[j] = (uint8_t)pos_book[j];
+    T->lut_off[j] = off[j];
+    T->lut_inv[j] = inv[j];
+  }
+  uint8_t *h = t->host.data();
+  for (uint64_t i = 0; i < lut_len; ++i) h[off_lut + i] = (uint8_t)lut[i];
+  for (int b = 0; b < nb; ++b)
+    std::memcpy(h + off_books + sizeof(float) * b * mc, cent + book_rows[b] * mc, sizeof(float) * mc);
+  std::memcpy(h + off_rot, rot, sizeof(float) * d * d);
+  t->info = bgtq_tables_info{(int32_t)d, (int32_t)ng, (int32_t)rb, (int32_t)nstride, (int32_t)nib, (int32_t)mc, ncb, nb};
+  bgtq_status s = ctx->use();
+  if (!s) s = t->blob.alloc(total, "K tables");
+  if (!s) {
+    hipError_t e = hipMemcpy(t->blob.ptr, h, total, hipMemcpyHostToDevice);
+    if (e != hipSuccess) s = hip_fail(e, "upload tables");
+  }
+  if (s) {
+    delete t;
+    return s;
+  }
+  *out = t;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_tables_info_get(const bgtq_tables *t, bgtq_tables_info *out) {
+  if (!t || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  *out = t->info;
+  return BGTQ_OK;
+}
+
+void bgtq_tables_destroy(bgtq_tables *t) {
+  if (!t) return;
+  (void)t->ctx->use();
+  (void)hipStreamSynchronize(t->ctx->stream);
+  delete t;
+}
+
+// ---------------------------------------------------------------- keys
+static bool encode_dim_supported(int d) { return d == 16 || d == 32 || d == 64 || d == 128; }
+
+bgtq_status bgtq_fp16_keys_create(bgtq_context *ctx, uint32_t dim, uint32_t capacity, bgtq_keys **out) {
+  if (!ctx || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (dim < 2 || dim % 2 || dim > 128 || capacity < 1) return fail(BGTQ_ERR_RANGE, "Invalid K dimensions");
+  auto *k = new bgtq_keys();
+  k->kind = BGTQ_KEYS_FP16;
+  k->ctx = ctx;
+  k->dim = dim;
+  k->capacity = capacity;
+  bgtq_status s = ctx->use();
+  if (!s) s = k->fp16.alloc((size_t)capacity * dim * 2, "FP16 K");
+  if (s) {
+    delete k;
+    return s;
+  }
+  k->ledger.add("FP16 K", BGTQ_ROLE_PERSISTENT_K, (size_t)capacity * dim * 2);
+  *out = k;
+  return BGTQ_OK;
+}
+
+static bgtq_status make_packed(bgtq_tables *t, uint32_t capacity, int32_t kind, bgtq_keys **out) {
+  if (!t || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  // The reference bounds capacity by maxComputeWorkgroupsPerDimension (65535,
+  // src/runtime/packed-keys.ts:13); HBM is the only bound here.
+  if (capacity < 1 || capacity > 0x7fffffffu) return fail(BGTQ_ERR_RANGE, "Invalid capacity");
+  if (!encode_dim_supported(t->info.dim))
+    return fail(BGTQ_ERR_UNSUPPORTED, "K encode is built for dim 16, 32, 64 and 128 (got %d)", t->info.dim);
+  auto *k = new bgtq_keys();
+  k->kind = kind;
+  k->ctx = t->ctx;
+  k->tables = t;
+  k->dim = (uint32_t)t->info.dim;
+  k->capacity = capacity;
+  const size_t pb = (size_t)capacity * t->info.row_bytes, nb = (size_t)capacity * t->info.norm_stride * 2;
+  bgtq_status s = t->ctx->use();
+  if (!s) s = k->packed.alloc(pb, "K nibble/byte capacity");
+  if (!s) s = k->norms.alloc(nb, "K FP16 scale capacity");
+  if (!s && kind == BGTQ_KEYS_COMPRESSED) s = k->decoded.alloc((size_t)capacity * k->dim * 4, "materialized FP32 K");
+  if (s) {
+    delete k;
+    return s;
+  }
+  k->ledger.add("K tables", BGTQ_ROLE_SHARED, t->blob.bytes);
+  k->ledger.add("K nibble/byte capacity", BGTQ_ROLE_PERSISTENT_K, pb);
+  k->ledger.add("K FP16 scale capacity", BGTQ_ROLE_PERSISTENT_K, nb);
+  if (kind == BGTQ_KEYS_COMPRESSED)
+    k->ledger.add("materialized FP32 K", BGTQ_ROLE_SCRATCH, (size_t)capacity * k->dim * 4);
+  *out = k;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_packed_keys_create(bgtq_tables *t, uint32_t capacity, bgtq_keys **out) {
+  return make_packed(t, capacity, BGTQ_KEYS_PACKED, out);
+}
+bgtq_status bgtq_compressed_keys_create(bgtq_tables *t, uint32_t capacity, bgtq_keys **out) {
+  return make_packed(t, capacity, BGTQ_KEYS_COMPRESSED, out);
+}
+
+// appendCount (src/runtime/keys.ts:11-15)
+static bgtq_status append_count(const uint16_t *v, size_t n, uint32_t dim, uint32_t length, uint32_t capacity,
+                                uint32_t *count) {
+  if (!n || n % dim || !v) return fail(BGTQ_ERR_RANGE, "K append must contain whole nonempty rows");
+  for (size_t i = 0; i < n; ++i)
+    if ((v[i] & 0x7c00u) == 0x7c00u) return fail(BGTQ_ERR_RANGE, "Finite FP16 K required");
+  const uint64_t c = n / dim;
+  if ((uint64_t)length + c > capacity) return fail(BGTQ_ERR_RANGE, "K capacity exceeded");
+  *count = (uint32_t)c;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_keys_append(bgtq_keys *k, const uint16_t *v, size_t n) {
+  if (!k) return fail(BGTQ_ERR_RANGE, "null keys");
+  if (k->pending) return fail(BGTQ_ERR_STATE, "Concurrent K appends unsupported");
+  uint32_t count = 0;
+  if (bgtq_status s = append_count(v, n, k->dim, k->length, k->capacity, &count)) return s;
+  bgtq_context *ctx = k->ctx;
+  if (bgtq_status s = ctx->use()) return s;
+  if (k->kind == BGTQ_KEYS_FP16) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    HIP_TRY(hipMemcpy(static_cast<uint16_t *>(k->fp16.ptr) + (size_t)k->length * k->dim, v, n * 2,
+                      hipMemcpyHostToDevice),
+            "FP16 K upload");
+    k->length += count;
+    return BGTQ_OK;
+  }
+  k->pending = true;
+  bgtq_status s = ctx->ensure_staging(n * 2);
+  if (!s) {
+    hipError_t e = hipMemcpy(ctx->staging.ptr, v, n * 2, hipMemcpyHostToDevice);
+    if (e != hipSuccess) s = hip_fail(e, "K append upload");
+  }
+  if (!s) {
+    bgtq_encode_job job{k->tables, ctx->staging.ptr, (int64_t)k->dim, (int64_t)count,
+                        static_cast<uint8_t *>(k->packed.ptr), static_cast<uint16_t *>(k->norms.ptr),
+                        (int64_t)k->length};
+    s = bgtq_encode_batched(ctx, BGTQ_DTYPE_F16, &job, 1);
+  }
+  if (!s) {
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) s = hip_fail(e, "K encode");
+  }
+  k->pending = false;
+  if (!s) k->length += count;  // only after the encode has completed
+  return s;
+}
+
+bgtq_status bgtq_keys_ready(const bgtq_keys *k) {
+  if (!k) return fail(BGTQ_ERR_RANGE, "null keys");
+  if (k->pending || !k->length) return fail(BGTQ_ERR_STATE, "K storage not ready");
+  return BGTQ_OK;
+}
+int32_t bgtq_keys_kind(const bgtq_keys *k) { return k ? k->kind : -1; }
+uint32_t bgtq_keys_length(const bgtq_keys *k) { return k ? k->length : 0; }
+uint32_t bgtq_keys_capacity(const bgtq_keys *k) { return k ? k->capacity : 0; }
+uint32_t bgtq_keys_dim(const bgtq_keys *k) { return k ? k->dim : 0; }
+
+bgtq_status bgtq_keys_read_packed(const bgtq_keys *k, uint8_t *packed, size_t packed_bytes, uint16_t *norms,
+                                  size_t norm_count) {
+  if (!k || k->kind == BGTQ_KEYS_FP16) return fail(BGTQ_ERR_RANGE, "packed read needs packed keys");
+  if (packed_bytes > k->packed.bytes || norm_count * 2 > k->norms.bytes)
+    return fail(BGTQ_ERR_RANGE, "Invalid readback length");
+  if (bgtq_status s = k->ctx->use()) return s;
+  HIP_TRY(hipStreamSynchronize(k->ctx->stream), "hipStreamSynchronize");
+  if (packed && packed_bytes) HIP_TRY(hipMemcpy(packed, k->packed.ptr, packed_bytes, hipMemcpyDeviceToHost), "read packed");
+  if (norms && norm_count) HIP_TRY(hipMemcpy(norms, k->norms.ptr, norm_count * 2, hipMemcpyDeviceToHost), "read norms");
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_keys_read_fp16(const bgtq_keys *k, uint16_t *out, size_t count) {
+  if (!k || k->kind != BGTQ_KEYS_FP16 || !out) return fail(BGTQ_ERR_RANGE, "FP16 read needs FP16 keys");
+  if (count * 2 > k->fp16.bytes) return fail(BGTQ_ERR_RANGE, "Invalid readback length");
+  if (bgtq_status s = k->ctx->use()) return s;
+  HIP_TRY(hipStreamSynchronize(k->ctx->stream), "hipStreamSynchronize");
+  HIP_TRY(hipMemcpy(out, k->fp16.ptr, count * 2, hipMemcpyDeviceToHost), "read FP16 K");
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_keys_prepare(bgtq_keys *k, float *out, size_t count) {
+  if (!k || k->kind != BGTQ_KEYS_COMPRESSED) return fail(BGTQ_ERR_RANGE, "prepare needs compressed keys");
+  if (k->pending) return fail(BGTQ_ERR_STATE, "K append is still pending");
+  if (count > (size_t)k->length * k->dim) return fail(BGTQ_ERR_RANGE, "Invalid readback length");
+  if (bgtq_status s = k->ctx->use()) return s;
+  if (k->length) {
+    HIP_TRY(launch_reconstruct(k->tables->dev(), static_cast<const uint8_t *>(k->packed.ptr),
+                               static_cast<const uint16_t *>(k->norms.ptr), k->length,
+                               static_cast<float *>(k->decoded.ptr), k->ctx->stream),
+            "reconstruct");
+  }
+  if (out && count) {
+    HIP_TRY(hipStreamSynchronize(k->ctx->stream), "hipStreamSynchronize");
+    HIP_TRY(hipMemcpy(out, k->decoded.ptr, count * 4, hipMemcpyDeviceToHost), "read decoded K");
+  }
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_keys_allocations(const bgtq_keys *k, bgtq_allocation *out, size_t cap, size_t *n) {
+  if (!k) return fail(BGTQ_ERR_RANGE, "null keys");
+  return k->ledger.copy(out, cap, n);
+}
+
+void bgtq_keys_destroy(bgtq_keys *k) {
+  if (!k) return;
+  (void)k->ctx->use();
+  (void)hipStreamSynchronize(k->ctx->stream);
+  delete k;
+}
+
+// ---------------------------------------------------------------- values
+bgtq_status bgtq_values_create(bgtq_context *ctx, uint32_t dim, uint32_t capacity, int32_t dtype,
+                               bgtq_values **out) {
+  if (!ctx || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (dim < 1 || dim > 128 || capacity < 1 || (dtype != BGTQ_DTYPE_F32 && dtype != BGTQ_DTYPE_F16))
+    return fail(BGTQ_ERR_RANGE, "Invalid V dimensions");
+  auto *v = new bgtq_values();
+  v->ctx = ctx;
+  v->dim = dim;
+  v->capacity = capacity;
+  v->dtype = dtype;
+  const size_t bytes = (size_t)capacity * dim * (dtype == BGTQ_DTYPE_F32 ? 4 : 2);
+  bgtq_status s = ctx->use();
+  if (!s) s = v->buf.alloc(bytes, "V");
+  if (s) {
+    delete v;
+    return s;
+  }
+  v->ledger.add(dtype == BGTQ_DTYPE_F32 ? "FP32 V" : "FP16 V", BGTQ_ROLE_PERSISTENT_V, bytes);
+  *out = v;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_values_append(bgtq_values *v, const float *values, size_t n) {
+  if (!v) return fail(BGTQ_ERR_RANGE, "null values");
+  if (!n || n % v->dim || !values) return fail(BGTQ_ERR_RANGE, "V append must contain whole rows");
+  for (size_t i = 0; i < n; ++i)
+    if (!std::isfinite(values[i])) return fail(BGTQ_ERR_RANGE, "V: finite inputs required");
+  const uint64_t count = n / v->dim;
+  if (v->length + count > v->capacity) return fail(BGTQ_ERR_RANGE, "V capacity exceeded");
+  if (bgtq_status s = v->ctx->use()) return s;
+  HIP_TRY(hipStreamSynchronize(v->ctx->stream), "hipStreamSynchronize");
+  if (v->dtype == BGTQ_DTYPE_F32) {
+    HIP_TRY(hipMemcpy(static_cast<float *>(v->buf.ptr) + (size_t)v->length * v->dim, values, n * 4,
+                      hipMemcpyHostToDevice),
+            "V upload");
+  } else {
+    std::vector<uint16_t> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = f32_to_f16(values[i]);
+    HIP_TRY(hipMemcpy(static_cast<uint16_t *>(v->buf.ptr) + (size_t)v->length * v->dim, h.data(), n * 2,
+                      hipMemcpyHostToDevice),
+            "V upload");
+  }
+  v->length += (uint32_t)count;
+  return BGTQ_OK;
+}
+
+uint32_t bgtq_values_length(const bgtq_values *v) { return v ? v->length : 0; }
+bgtq_status bgtq_values_allocations(const bgtq_values *v, bgtq_allocation *out, size_t cap, size_t *n) {
+  if (!v) return fail(BGTQ_ERR_RANGE, "null values");
+  return v->ledger.copy(out, cap, n);
+}
+void bgtq_values_destroy(bgtq_values *v) {
+  if (!v) return;
+  (void)v->ctx->use();
+  (void)hipStreamSynchronize(v->ctx->stream);
+  delete v;
+}
+
+// ---------------------------------------------------------------- batched entry points
+bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq_encode_job *jobs, size_t n_jobs) {
+  if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
+  if (src_dtype != BGTQ_DTYPE_F16 && src_dtype != BGTQ_DTYPE_F32) return fail(BGTQ_ERR_RANGE, "invalid source dtype");
+  if (n_jobs && !jobs) return fail(BGTQ_ERR_RANGE, "null jobs");
+  for (size_t i = 0; i < n_jobs; ++i) {
+    const bgtq_encode_job &j = jobs[i];
+    if (!j.tables) return fail(BGTQ_ERR_RANGE, "encode job %zu: null tables", i);
+    if (!encode_dim_supported(j.tables->info.dim))
+      return fail(BGTQ_ERR_UNSUPPORTED, "K encode is built for dim 16, 32, 64 and 128 (got %d)", j.tables->info.dim);
+    if (j.rows < 0 || j.dst_row0 < 0) return fail(BGTQ_ERR_RANGE, "encode job %zu: negative rows", i);
+    if (j.rows && (!j.src || !j.packed || !j.norms)) return fail(BGTQ_ERR_RANGE, "encode job %zu: null buffer", i);
+    if (j.src_row_stride < j.tables->info.dim) return fail(BGTQ_ERR_RANGE, "encode job %zu: row stride below dim", i);
+  }
+  if (bgtq_status s = ctx->use()) return s;
+  // Group jobs by dimension into launches of at most kEncodeJobsPerLaunch.
+  std::map<int, std::vector<size_t>> by_dim;
+  for (size_t i = 0; i < n_jobs; ++i)
+    if (jobs[i].rows > 0) by_dim[jobs[i].tables->info.dim].push_back(i);
+  for (auto &kv : by_dim) {
+    const std::vector<size_t> &idx = kv.second;
+    for (size_t b = 0; b < idx.size(); b += kEncodeJobsPerLaunch) {
+      EncodeLaunch L{};
+      int64_t max_rows = 0;
+      for (size_t k = b; k < std::min(idx.size(), b + kEncodeJobsPerLaunch); ++k) {
+        const bgtq_encode_job &j = jobs[idx[k]];
+        EncodeJobDev &J = L.jobs[L.n_jobs++];
+        J.t = j.tables->dev();
+        J.src = j.src;
+        J.src_stride = j.src_row_stride;
+        J.rows = j.rows;
+        J.packed = j.packed;
+        J.norms = j.norms;
+        J.dst_row0 = j.dst_row0;
+        J.dst_step = 1;
+        max_rows = std::max(max_rows, j.rows);
+      }
+      HIP_TRY(launch_encode(L, kv.first, src_dtype == BGTQ_DTYPE_F32, max_rows, ctx->stream), "encode launch");
+    }
+  }
+  return BGTQ_OK;
+}
+
+static int choose_splits(int64_t units, uint32_t max_length, int32_t requested) {
+  const int64_t max_splits = std::max<int64_t>(1, (max_length + 255) / 256);
+  if (requested > 0) return (int)std::min<int64_t>(requested, max_splits);
+  const int64_t want = std::max<int64_t>(1, (2048 + units - 1) / units);
+  return (int)std::min<int64_t>(want, max_splits);
+}
+
+struct DecodeWorkspace {
+  size_t qr, part, stats, total;
+};
+
+static DecodeWorkspace decode_ws(int64_t heads, int dim, int splits) {
+  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
+  DecodeWorkspace w;
+  w.qr = 0;
+  w.part = al(sizeof(float) * heads * dim);
+  w.stats = w.part + al(sizeof(float) * heads * splits * (dim + 2));
+  w.total = w.stats + al(sizeof(float) * heads * 2);
+  return w;
+}
+
+static bgtq_status validate_decode(const bgtq_decode_desc *d, int *splits) {
+  if (!d) return fail(BGTQ_ERR_RANGE, "null descriptor");
+  if (d->batch < 1 || d->kv_heads < 1 || d->kv_heads > kMaxKvHeads || d->q_heads < d->kv_heads ||
+      d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 16)
+    return fail(BGTQ_ERR_RANGE, "invalid head geometry");
+  if (d->dim < 2 || d->dim > 128 || d->dim % 2) return fail(BGTQ_ERR_RANGE, "invalid head dim");
+  if (d->max_length < 1) return fail(BGTQ_ERR_RANGE, "max_length must be >= 1");
+  if (d->key_format == BGTQ_KEYS_PACKED) {
+    for (int h = 0; h < d->kv_heads; ++h) {
+      if (!d->tables[h]) return fail(BGTQ_ERR_RANGE, "null tables for KV head %d", h);
+      if (d->tables[h]->info.dim != d->dim) return fail(BGTQ_ERR_RANGE, "tables dim mismatch");
+    }
+    if (!d->packed || !d->norms) return fail(BGTQ_ERR_RANGE, "null packed K");
+  } else if (d->key_format == BGTQ_KEYS_FP16) {
+    if (!d->k_f16) return fail(BGTQ_ERR_RANGE, "null FP16 K");
+  } else {
+    return fail(BGTQ_ERR_RANGE, "invalid key format");
+  }
+  if (!d->v || (d->v_dtype != BGTQ_DTYPE_F16 && d->v_dtype != BGTQ_DTYPE_F32)) return fail(BGTQ_ERR_RANGE, "invalid V");
+  if (!d->q || !d->out || !d->lengths) return fail(BGTQ_ERR_RANGE, "null q/out/lengths");
+  *splits = choose_splits((int64_t)d->batch * d->kv_heads, d->max_length, d->splits);
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes) {
+  int splits = 1;
+  if (bgtq_status s = validate_decode(d, &splits)) return s;
+  if (!bytes) return fail(BGTQ_ERR_RANGE, "null output");
+  *bytes = decode_ws((int64_t)d->batch * d->q_heads, d->dim, splits).total;
+  return BGTQ_OK;
+}
+
+static bgtq_status launch_decode_common(bgtq_context *ctx, DecodeParams &p, const float *q,
+                                        const bgtq_tables *const *tables) {
+  int lds = 0;
+  for (int h = 0; h < (p.key_format == 1 ? p.kv_heads : 1); ++h) {
+    const bgtq_tables_info *ti = p.key_format == 1 ? &tables[h]->info : nullptr;
+    const int books = ti ? ti->n_books * ti->max_centroids * 4 : 0;
+    lds = std::max(lds, decode_lds_bytes(p.G, p.dim, p.key_format, books, ti ? ti->row_bytes : 0,
+                                         ti ? ti->norm_stride : 0));
+  }
+  if (lds > 65536) return fail(BGTQ_ERR_UNSUPPORTED, "decode needs %d bytes of LDS (limit 65536)", lds);
+  HIP_TRY(launch_rotate_q(p, q, const_cast<float *>(p.qr), ctx->stream), "rotate_q launch");
+  HIP_TRY(launch_decode(p, lds, ctx->stream), "decode launch");
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) {
+  if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
+  int splits = 1;
+  if (bgtq_status s = validate_decode(d, &splits)) return s;
+  const int64_t heads = (int64_t)d->batch * d->q_heads;
+  const DecodeWorkspace w = decode_ws(heads, d->dim, splits);
+  if (!d->workspace || d->workspace_bytes < w.total)
+    return fail(BGTQ_ERR_RANGE, "workspace of %zu bytes required", w.total);
+  if (bgtq_status s = ctx->use()) return s;
+  DecodeParams p{};
+  for (int h = 0; h < d->kv_heads; ++h) p.tables[h] = d->key_format == BGTQ_KEYS_PACKED ? d->tables[h]->dev() : nullptr;
+  p.batch = d->batch;
+  p.q_heads = d->q_heads;
+  p.kv_heads = d->kv_heads;
+  p.dim = d->dim;
+  p.G = d->q_heads / d->kv_heads;
+  p.key_format = d->key_format == BGTQ_KEYS_PACKED ? 1 : 0;
+  p.packed = d->packed;
+  p.packed_seq_stride = d->packed_seq_stride;
+  p.packed_head_stride = d->packed_head_stride;
+  p.norms = d->norms;
+  p.norms_seq_stride = d->norms_seq_stride;
+  p.norms_head_stride = d->norms_head_stride;
+  p.k = d->k_f16;
+  p.k_seq_stride = d->k_seq_stride;
+  p.k_head_stride = d->k_head_stride;
+  p.v = d->v;
+  p.v_dtype = d->v_dtype;
+  p.v_seq_stride = d->v_seq_stride;
+  p.v_head_stride = d->v_head_stride;
+  uint8_t *ws = static_cast<uint8_t *>(d->workspace);
+  p.qr = reinterpret_cast<float *>(ws + w.qr);
+  p.part = reinterpret_cast<float *>(ws + w.part);
+  p.stats = reinterpret_cast<float *>(ws + w.stats);
+  p.lengths = d->lengths;
+  p.ends = nullptr;
+  p.splits = splits;
+  p.split_tokens = (int)((d->max_length + splits - 1) / splits);
+  p.split_tokens = ((p.split_tokens + 255) / 256) * 256;
+  p.out = d->out;
+  p.logits = nullptr;
+  p.probs = nullptr;
+  p.logit_stride = 0;
+  return launch_decode_common(ctx, p, d->q, d->tables);
+}
+
+// ---------------------------------------------------------------- attention sessions
+bgtq_status bgtq_attention_create(bgtq_keys *k, bgtq_values *v, uint32_t max_queries, int32_t materialize,
+                                  bgtq_attention **out) {
+  if (!k || !v || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (k->ctx != v->ctx || k->dim != v->dim || k->capacity != v->capacity || max_queries < 1 || max_queries > 16)
+    return fail(BGTQ_ERR_RANGE, "Incompatible attention storage");
+  auto *a = new bgtq_attention();
+  a->keys = k;
+  a->values = v;
+  a->max_queries = max_queries;
+  a->materialize = materialize ? 1 : 0;
+  a->max_splits = (uint32_t)std::max<int64_t>(1, ((int64_t)k->capacity + 255) / 256);
+  const size_t d = k->dim, Q = max_queries;
+  bgtq_status s = k->ctx->use();
+  struct Item {
+    DeviceBuffer *b;
+    const char *name;
+    size_t bytes;
+  } items[] = {
+      {&a->q, "Q", Q * d * 4},
+      {&a->small, "query positions", (Q + 1) * 4},
+      {&a->logits, "logits", a->materialize ? Q * k->capacity * 4 : 0},
+      {&a->probs, "probabilities", a->materialize ? Q * k->capacity * 4 : 0},
+      {&a->out, "output", Q * d * 4},
+      {&a->qr, "rotated Q", Q * d * 4},
+      {&a->part, "split partials", Q * a->max_splits * (d + 2) * 4},
+      {&a->stats, "softmax statistics", Q * 2 * 4},
+  };
+  for (auto &it : items) {
+    if (s || !it.bytes) continue;
+    s = it.b->alloc(it.bytes, it.name);
+    if (!s) a->ledger.add(it.name, BGTQ_ROLE_SCRATCH, it.bytes);
+  }
+  if (!s) {
+    hipError_t e = hipHostMalloc((void **)&a->pinned, (Q + 1) * 4, hipHostMallocDefault);
+    if (e != hipSuccess) s = hip_fail(e, "pinned staging");
+  }
+  if (s) {
+    delete a;
+    return s;
+  }
+  *out = a;
+  return BGTQ_OK;
+}
+
+static bool optimized(const bgtq_attention *a) { return a->keys->kind == BGTQ_KEYS_PACKED; }
+
+bgtq_status bgtq_attention_set_queries(bgtq_attention *a, const float *q, size_t n_q, const uint32_t *positions,
+                                       size_t n_pos, int32_t causal) {
+  if (!a) return fail(BGTQ_ERR_RANGE, "null attention");
+  bgtq_keys *k = a->keys;
+  const size_t d = k->dim;
+  if (optimized(a)) {
+    // OptimizedAttention.setQueries (src/attention/optimized.ts:28-32)
+    if (bgtq_status s = bgtq_keys_ready(k)) return s;
+    const bool whole = n_q % d == 0;
+    const size_t n = n_q / d;
+    bool bad = k->length != a->values->length || !whole || n < 1 || n > a->max_queries || n_pos != n || !positions;
+    for (size_t i = 0; !bad && i < n; ++i) bad = positions[i] >= k->length;
+    if (bad) return fail(BGTQ_ERR_RANGE, "Invalid Q/K/V shape or positions");
+  } else {
+    // AttentionSession.setQueries (src/attention/attention.ts:35-41)
+    if (k->length != a->values->length || !k->length) return fail(BGTQ_ERR_RANGE, "K/V lengths must match and be nonzero");
+    const bool whole = n_q % d == 0;
+    const size_t n = n_q / d;
+    bool bad = !whole || n < 1 || n > a->max_queries || n_pos != n || !positions;
+    for (size_t i = 0; !bad && i < n; ++i) bad = positions[i] >= k->length;
+    if (bad) return fail(BGTQ_ERR_RANGE, "Invalid query shape or causal positions");
+  }
+  for (size_t i = 0; i < n_q; ++i)
+    if (!std::isfinite(q[i])) return fail(BGTQ_ERR_RANGE, "Q: finite inputs required");
+  if (bgtq_status s = k->ctx->use()) return s;
+  HIP_TRY(hipStreamSynchronize(k->ctx->stream), "hipStreamSynchronize");
+  HIP_TRY(hipMemcpy(a->q.ptr, q, n_q * 4, hipMemcpyHostToDevice), "Q upload");
+  a->positions.assign(positions, positions + n_pos);
+  a->queries = (uint32_t)(n_q / d);
+  a->causal = causal ? 1 : 0;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_attention_record(bgtq_attention *a) {
+  if (!a) return fail(BGTQ_ERR_RANGE, "null attention");
+  bgtq_keys *k = a->keys;
+  bgtq_values *v = a->values;
+  if (optimized(a))
+    if (bgtq_status s = bgtq_keys_ready(k)) return s;
+  if (!a->queries || k->length != v->length) return fail(BGTQ_ERR_STATE, "Attention not ready");
+  if (k->kind == BGTQ_KEYS_COMPRESSED)
+    if (bgtq_status s = bgtq_keys_prepare(k, nullptr, 0)) return s;
+  bgtq_context *ctx = k->ctx;
+  if (bgtq_status s = ctx->use()) return s;
+  const uint32_t T = k->length, nq = a->queries;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  a->pinned[0] = T;
+  for (uint32_t i = 0; i < nq; ++i) a->pinned[1 + i] = a->causal ? a->positions[i] + 1 : T;
+  HIP_TRY(hipMemcpyAsync(a->small.ptr, a->pinned, (nq + 1) * 4, hipMemcpyHostToDevice, ctx->stream), "query upload");
+  DecodeParams p{};
+  p.batch = 1;
+  p.q_heads = (int32_t)nq;
+  p.kv_heads = 1;
+  p.dim = (int32_t)k->dim;
+  p.G = (int32_t)nq;
+  if (k->kind == BGTQ_KEYS_PACKED) {
+    p.key_format = 1;
+    p.tables[0] = k->tables->dev();
+    p.packed = static_cast<const uint8_t *>(k->packed.ptr);
+    p.norms = static_cast<const uint16_t *>(k->norms.ptr);
+  } else if (k->kind == BGTQ_KEYS_FP16) {
+    p.key_format = 0;
+    p.k = k->fp16.ptr;
+  } else {
+    p.key_format = 2;
+    p.k = k->decoded.ptr;
+  }
+  p.v = v->buf.ptr;
+  p.v_dtype = v->dtype;
+  p.qr = static_cast<float *>(a->qr.ptr);
+  p.lengths = static_cast<const uint32_t *>(a->small.ptr);
+  p.ends = reinterpret_cast<const int32_t *>(static_cast<const uint32_t *>(a->small.ptr) + 1);
+  p.splits = choose_splits(1, T, 0);
+  p.splits = (int)std::min<uint32_t>((uint32_t)p.splits, a->max_splits);
+  p.split_tokens = (int)(((T + p.splits - 1) / p.splits + 255) / 256 * 256);
+  p.part = static_cast<float *>(a->part.ptr);
+  p.stats = static_cast<float *>(a->stats.ptr);
+  p.out = static_cast<float *>(a->out.ptr);
+  if (a->materialize) {
+    p.logits = static_cast<float *>(a->logits.ptr);
+    p.probs = static_cast<float *>(a->probs.ptr);
+    p.logit_stride = T;  // inspect() buffers are [queries x tokens]
+  }
+  const bgtq_tables *tabs[1] = {k->tables};
+  return launch_decode_common(ctx, p, static_cast<const float *>(a->q.ptr), tabs);
+}
+
+bgtq_status bgtq_attention_attend(bgtq_attention *a, const float *q, size_t n_q, const uint32_t *positions,
+                                  size_t n_pos, int32_t causal) {
+  if (bgtq_status s = bgtq_attention_set_queries(a, q, n_q, positions, n_pos, causal)) return s;
+  if (bgtq_status s = bgtq_attention_record(a)) return s;
+  HIP_TRY(hipStreamSynchronize(a->keys->ctx->stream), "attention");
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_attention_read(const bgtq_attention *a, int32_t which, float *out, size_t count) {
+  if (!a || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  const DeviceBuffer *b = which == 0 ? &a->logits : which == 1 ? &a->probs : which == 2 ? &a->out : nullptr;
+  if (!b) return fail(BGTQ_ERR_RANGE, "invalid buffer selector");
+  if (!b->ptr) return fail(BGTQ_ERR_STATE, "intermediates are not materialised by this session");
+  if (count * 4 > b->bytes) return fail(BGTQ_ERR_RANGE, "Invalid readback length");
+  if (bgtq_status s = a->keys->ctx->use()) return s;
+  HIP_TRY(hipStreamSynchronize(a->keys->ctx->stream), "hipStreamSynchronize");
+  HIP_TRY(hipMemcpy(out, b->ptr, count * 4, hipMemcpyDeviceToHost), "readback");
+  return BGTQ_OK;
+}
+
+uint32_t bgtq_attention_queries(const bgtq_attention *a) { return a ? a->queries : 0; }
+bgtq_status bgtq_attention_allocations(const bgtq_attention *a, bgtq_allocation *out, size_t cap, size_t *n) {
+  if (!a) return fail(BGTQ_ERR_RANGE, "null attention");
+  return a->ledger.copy(out, cap, n);
+}
+void bgtq_attention_destroy(bgtq_attention *a) {
+  if (!a) return;
+  (void)a->keys->ctx->use();
+  (void)hipStreamSynchronize(a->keys->ctx->stream);
+  delete a;
+}
+
+}  // extern "C"

@@ -1,0 +1,95 @@
+// Internal structures shared by the host library and the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bgtq {
+
+constexpr int kMaxDim = 128;
+constexpr int kMaxGroups = 8;
+constexpr int kMaxKvHeads = 16;
+constexpr int kEncodeJobsPerLaunch = 24;
+
+// Device-resident calibration tables, built once on the host from the
+// reference's serialized tables (src/webgpu/layout.ts:24-31). Fixed header,
+// then variable sections at byte offsets from the start of the struct.
+struct DevTables {
+  int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids, n_books, n_codebooks;
+  int32_t gstart[kMaxGroups], gend[kMaxGroups], gsize[kMaxGroups];  // group ranges (head-perm order)
+  uint32_t off_lut, off_books, off_rot, total_bytes;
+  uint8_t perm[kMaxDim];      // head_perm
+  uint8_t group_of[kMaxDim];
+  uint8_t pos_cb[kMaxDim];    // position -> code LUT row
+  uint8_t pos_book[kMaxDim];  // position -> distinct centroid row
+  float lut_off[kMaxDim];
+  float lut_inv[kMaxDim];
+  // [off_lut]   uint8 code_lut[n_codebooks*256]
+  // [off_books] float books[n_books*max_centroids]
+  // [off_rot]   float rotation[dim*dim], y_j = sum_i x_i R[j*dim+i]
+};
+
+__host__ __device__ inline const uint8_t *tables_lut(const DevTables *t) {
+  return reinterpret_cast<const uint8_t *>(t) + t->off_lut;
+}
+__host__ __device__ inline const float *tables_books(const DevTables *t) {
+  return reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(t) + t->off_books);
+}
+__host__ __device__ inline const float *tables_rot(const DevTables *t) {
+  return reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(t) + t->off_rot);
+}
+
+struct EncodeJobDev {
+  const DevTables *t;
+  const void *src;
+  int64_t src_stride;  // elements
+  int64_t rows;
+  uint8_t *packed;
+  uint16_t *norms;
+  int64_t dst_row0;
+  int64_t dst_step;  // destination row step per source row (>= 1)
+};
+
+struct EncodeLaunch {
+  EncodeJobDev jobs[kEncodeJobsPerLaunch];
+  int32_t n_jobs;
+};
+
+// Decode attention of one layer. Units are (sequence, KV head); each unit
+// serves G query heads (GQA). Work per unit is split over token ranges.
+struct DecodeParams {
+  const DevTables *tables[kMaxKvHeads];
+  int32_t batch, q_heads, kv_heads, dim, G;
+  int32_t key_format;  // 0 = FP16 K rows, 1 = packed, 2 = FP32 K rows
+  const uint8_t *packed;
+  int64_t packed_seq_stride, packed_head_stride;  // bytes
+  const uint16_t *norms;
+  int64_t norms_seq_stride, norms_head_stride;  // elements
+  const void *k;
+  int64_t k_seq_stride, k_head_stride;  // elements
+  const void *v;
+  int32_t v_dtype;  // 0 = FP32, 1 = FP16
+  int64_t v_seq_stride, v_head_stride;  // elements
+  const float *qr;        // [B*Hq*dim] rotated, permuted, scaled by 1/sqrt(dim)
+  const uint32_t *lengths;  // [B]
+  const int32_t *ends;      // optional [B*Hq] exclusive causal ends
+  int32_t splits, split_tokens;
+  float *part;    // [B*Hq*splits*(dim+2)] (m, l, o[dim])
+  float *stats;   // [B*Hq*2] final (m, l)
+  float *out;     // [B*Hq*dim]
+  float *logits;  // optional [B*Hq*logit_stride]
+  float *probs;   // optional [B*Hq*logit_stride]
+  int64_t logit_stride;
+};
+
+// Launchers (kernels live in encode.hip / decode.hip).
+hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
+                         hipStream_t stream);
+hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
+int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_bytes, int norm_stride);
+hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream);
+hipError_t launch_reconstruct(const DevTables *t, const uint8_t *packed, const uint16_t *norms,
+                              int64_t rows, float *out, hipStream_t stream);
+hipError_t launch_half_convert(const float *src, uint16_t *dst, int64_t n, hipStream_t stream);
+
+}  // namespace bgtq

@@ -1,0 +1,207 @@
+/* bgtq.h — C ABI of the MI355X (gfx950) Block-GTQ hot path.
+ *
+ * Replaces the WebGPU substrate under the reference's TypeScript runtime
+ * (src/webgpu) with HIP kernels. Every entry point takes plain pointers and
+ * sizes, returns a bgtq_status (0 = success) and leaves a thread-local
+ * message in bgtq_last_error(). On failure no object state changes: lengths
+ * advance only after the device work of an append has completed
+ * (src/runtime/packed-keys.ts:47), and validation happens before any launch.
+ *
+ * Two layers:
+ *  1. Objects that mirror the reference's classes one to one (context =
+ *     GPUDevice + queue, tables = tables(p), keys/values stores, attention
+ *     sessions). Host buffers in, device-resident state, reads for tests.
+ *  2. Stream-ordered batched entry points over caller-owned device memory for
+ *     model geometry (the src/model dispatch names encode_k / compressed_dot /
+ *     softmax / weighted / append), used for layers x sequences x heads.
+ */
+#ifndef BGTQ_H
+#define BGTQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t bgtq_status;
+#define BGTQ_OK 0
+#define BGTQ_ERR_RANGE 1       /* invalid argument; the reference throws RangeError */
+#define BGTQ_ERR_STATE 2       /* invalid object state; the reference throws Error */
+#define BGTQ_ERR_DEVICE 3      /* HIP runtime failure */
+#define BGTQ_ERR_UNSUPPORTED 4 /* valid input this build does not handle */
+#define BGTQ_ERR_NOMEM 5
+
+#define BGTQ_DTYPE_F32 0
+#define BGTQ_DTYPE_F16 1
+
+/* Roles of src/webgpu/buffers.ts:1 (Allocation.role). */
+#define BGTQ_ROLE_PERSISTENT_K 0
+#define BGTQ_ROLE_PERSISTENT_V 1
+#define BGTQ_ROLE_SHARED 2
+#define BGTQ_ROLE_SCRATCH 3
+
+typedef struct {
+  char name[48];
+  int32_t role;
+  uint64_t bytes;
+} bgtq_allocation;
+
+/* Thread-local message of the last failing call on this thread. */
+const char *bgtq_last_error(void);
+int32_t bgtq_abi_version(void);
+
+/* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
+typedef struct bgtq_context bgtq_context;
+bgtq_status bgtq_context_create(int32_t device, bgtq_context **out);
+void bgtq_context_destroy(bgtq_context *ctx);
+/* Queue-ordered completion, replaces device.queue.onSubmittedWorkDone(). */
+bgtq_status bgtq_context_synchronize(bgtq_context *ctx);
+/* The hipStream_t all work of this context is ordered on. A caller may set a
+ * stream it owns (for example PyTorch's current stream); NULL restores the
+ * context's own stream. */
+void *bgtq_context_stream(bgtq_context *ctx);
+bgtq_status bgtq_context_set_stream(bgtq_context *ctx, void *hip_stream);
+
+/* ---- calibration tables: replaces tables(p)/validateLayout --------------- *
+ * src/webgpu/layout.ts:8-31. integer = [dim, groups, rowBytes, normStride,
+ * nibbleDims, maxCentroids, o_perm, o_groupOf, o_posToCb, o_lut] ++ perm ++
+ * groupOf ++ positionToCodebook ++ codeLut (one u32 per LUT byte); floating =
+ * rotation[d*d] (y_j = sum_i x_i R[j*d+i]) ++ centroids[d*maxC] ++
+ * offsets[d] ++ inverseScales[d]. The per-head model calibration blob
+ * (src/model/calibration.ts:15-20) has the same format. Validation also
+ * applies the PackedKeys constructor checks (src/runtime/packed-keys.ts:16-23):
+ * contiguous groups, zero off-group rotation. */
+typedef struct bgtq_tables bgtq_tables;
+typedef struct {
+  int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids;
+  int32_t n_codebooks, n_books; /* LUT rows; distinct centroid rows */
+} bgtq_tables_info;
+bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_t n_integer,
+                               const float *floating, size_t n_floating, bgtq_tables **out);
+bgtq_status bgtq_tables_info_get(const bgtq_tables *t, bgtq_tables_info *out);
+void bgtq_tables_destroy(bgtq_tables *t);
+
+/* ---- key stores: replace KeyStore implementations ------------------------ *
+ * FP16Keys (src/runtime/keys.ts:16-27), PackedKeys (src/runtime/packed-keys.ts:7-52),
+ * CompressedKeys (src/runtime/compressed-keys.ts:5-59; packed storage plus a
+ * materialised FP32 K for phase-3 attention). append() takes FP16 bit patterns
+ * of whole rows and validates like appendCount (src/runtime/keys.ts:11-15). */
+typedef struct bgtq_keys bgtq_keys;
+#define BGTQ_KEYS_FP16 0
+#define BGTQ_KEYS_PACKED 1
+#define BGTQ_KEYS_COMPRESSED 2
+bgtq_status bgtq_fp16_keys_create(bgtq_context *ctx, uint32_t dim, uint32_t capacity, bgtq_keys **out);
+bgtq_status bgtq_packed_keys_create(bgtq_tables *t, uint32_t capacity, bgtq_keys **out);
+bgtq_status bgtq_compressed_keys_create(bgtq_tables *t, uint32_t capacity, bgtq_keys **out);
+bgtq_status bgtq_keys_append(bgtq_keys *k, const uint16_t *fp16_bits, size_t n_values);
+/* PackedKeys.ready(): Error "K storage not ready" while empty. */
+bgtq_status bgtq_keys_ready(const bgtq_keys *k);
+int32_t bgtq_keys_kind(const bgtq_keys *k);
+uint32_t bgtq_keys_length(const bgtq_keys *k);
+uint32_t bgtq_keys_capacity(const bgtq_keys *k);
+uint32_t bgtq_keys_dim(const bgtq_keys *k);
+/* readBuffer(packed) / readBuffer(norms): capacity*rowBytes bytes and
+ * capacity*normStride FP16 bit patterns, row major (packed/compressed kinds). */
+bgtq_status bgtq_keys_read_packed(const bgtq_keys *k, uint8_t *packed, size_t packed_bytes,
+                                  uint16_t *norms, size_t norm_count);
+/* FP16 kind: the raw FP16 K rows [capacity*dim]. */
+bgtq_status bgtq_keys_read_fp16(const bgtq_keys *k, uint16_t *out, size_t count);
+/* CompressedKeys.prepare(): materialise FP32 K [length*dim] (head order) on
+ * the device; with out != NULL also copy it to the host. */
+bgtq_status bgtq_keys_prepare(bgtq_keys *k, float *out, size_t count);
+bgtq_status bgtq_keys_allocations(const bgtq_keys *k, bgtq_allocation *out, size_t cap, size_t *n);
+void bgtq_keys_destroy(bgtq_keys *k);
+
+/* ---- Values (src/runtime/values.ts:3-16) --------------------------------- *
+ * dtype BGTQ_DTYPE_F32 stores FP32 V exactly (the synthetic path); F16 stores
+ * RNE-rounded FP16 V (src/model/append.wgsl:6-10). append() is synchronous. */
+typedef struct bgtq_values bgtq_values;
+bgtq_status bgtq_values_create(bgtq_context *ctx, uint32_t dim, uint32_t capacity, int32_t dtype,
+                               bgtq_values **out);
+bgtq_status bgtq_values_append(bgtq_values *v, const float *values, size_t n_values);
+uint32_t bgtq_values_length(const bgtq_values *v);
+bgtq_status bgtq_values_allocations(const bgtq_values *v, bgtq_allocation *out, size_t cap, size_t *n);
+void bgtq_values_destroy(bgtq_values *v);
+
+/* ---- attention sessions -------------------------------------------------- *
+ * OptimizedAttention (src/attention/optimized.ts:5-45) over PACKED keys, and
+ * AttentionSession (src/attention/attention.ts:19-70) over FP16 or
+ * COMPRESSED keys. set_queries validates like setQueries; record enqueues the
+ * work; attend = set_queries + record + wait. read() returns the inspect()
+ * buffers: which = 0 logits [n*T], 1 probabilities [n*T], 2 output [n*dim].
+ * Logits and probabilities are materialised only when the session was made
+ * with materialize != 0 (the fused path otherwise never writes them). */
+typedef struct bgtq_attention bgtq_attention;
+bgtq_status bgtq_attention_create(bgtq_keys *k, bgtq_values *v, uint32_t max_queries,
+                                  int32_t materialize, bgtq_attention **out);
+bgtq_status bgtq_attention_set_queries(bgtq_attention *a, const float *q, size_t n_q_values,
+                                       const uint32_t *positions, size_t n_positions, int32_t causal);
+bgtq_status bgtq_attention_record(bgtq_attention *a);
+bgtq_status bgtq_attention_attend(bgtq_attention *a, const float *q, size_t n_q_values,
+                                  const uint32_t *positions, size_t n_positions, int32_t causal);
+bgtq_status bgtq_attention_read(const bgtq_attention *a, int32_t which, float *out, size_t count);
+uint32_t bgtq_attention_queries(const bgtq_attention *a);
+bgtq_status bgtq_attention_allocations(const bgtq_attention *a, bgtq_allocation *out, size_t cap, size_t *n);
+void bgtq_attention_destroy(bgtq_attention *a);
+
+/* ---- batched, caller-owned device memory --------------------------------- */
+
+/* K encode of strided rows into packed rows (src/model/codec.wgsl:11-33 and
+ * src/webgpu/mixed.wgsl:14-41, arithmetic of src/reference/production_math.py:4-24).
+ * src holds FP16 bits (BGTQ_DTYPE_F16) or FP32 values that are first rounded
+ * to FP16 (BGTQ_DTYPE_F32, src/model/codec.wgsl:14). Row r of a job reads
+ * src + r*src_row_stride elements and writes packed row dst_row0 + r
+ * (tables->row_bytes bytes, every byte written) and norms row dst_row0 + r. */
+typedef struct {
+  const bgtq_tables *tables;
+  const void *src;
+  int64_t src_row_stride; /* elements */
+  int64_t rows;
+  uint8_t *packed;
+  uint16_t *norms;
+  int64_t dst_row0;
+} bgtq_encode_job;
+bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq_encode_job *jobs,
+                                size_t n_jobs);
+
+/* Decode attention for one layer: B sequences x Hkv KV heads, G = Hq/Hkv
+ * query heads per KV head (src/model/compressed-dot.wgsl:14-31 +
+ * src/model/attention.wgsl:24-39 fused). Query head h uses KV head h / G.
+ * key_format: BGTQ_KEYS_PACKED (packed rows + FP16 scales, tables[kv]) or
+ * BGTQ_KEYS_FP16 (k_f16 rows). Layouts (element strides for norms/V/K):
+ *   packed[b*packed_seq_stride + kv*packed_head_stride + t*row_bytes]
+ *   norms [b*norms_seq_stride  + kv*norms_head_stride  + t*norm_stride]
+ *   v/k   [b*seq_stride        + kv*head_stride        + t*dim]
+ *   q, out: [B, Hq, dim] FP32 contiguous; lengths: device uint32 [B] (tokens
+ *   attended per sequence, 1..max_length). workspace: device memory of at
+ *   least bgtq_decode_workspace_size() bytes. */
+typedef struct {
+  int32_t batch, q_heads, kv_heads, dim;
+  int32_t key_format;
+  const bgtq_tables *tables[16];
+  const uint8_t *packed;
+  int64_t packed_seq_stride, packed_head_stride; /* bytes */
+  const uint16_t *norms;
+  int64_t norms_seq_stride, norms_head_stride;   /* elements */
+  const uint16_t *k_f16;
+  int64_t k_seq_stride, k_head_stride;           /* elements */
+  const void *v;
+  int32_t v_dtype;
+  int64_t v_seq_stride, v_head_stride;           /* elements */
+  const float *q;
+  float *out;
+  const uint32_t *lengths;
+  uint32_t max_length;
+  int32_t splits; /* token splits per (sequence, KV head); 0 = choose */
+  void *workspace;
+  size_t workspace_bytes;
+} bgtq_decode_desc;
+bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes);
+bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,170 @@
+"""K encode on the GPU: bit-exact against the reference goldens and the oracle.
+
+Mirrors the checks of the reference's tests/test_mixed.py:38-64 (exact
+packed bytes and scale bits) and tests/webgpu/optimized-test.ts:23-27 (an odd
+append boundary, packed/norm buffers read back raw), through the C ABI.
+"""
+import json
+
+import numpy as np
+import pytest
+
+from conftest import REF
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(m, a):
+    import bgtq
+    return bgtq.BlockGTQParameters.from_mixed_fixture(m, a)
+
+
+def _olayout(oracle, p):
+    return oracle.Layout(dim=p.dim, groups=p.groups, row_bytes=p.rowBytes, norm_stride=p.normStride,
+                         nibble_dims=p.nibbleDims, max_centroids=p.maxCentroids, perm=p.permutation,
+                         group_of=p.groupOf, pos_to_cb=p.positionToCodebook, code_lut=p.codeLut,
+                         rotation=p.rotation, centroids=p.centroids, offsets=p.offsets, inv_scales=p.inverseScales)
+
+
+def test_mixed_fixture_rows_exact(device, mixed_cases):
+    import bgtq
+    for name, m, a in mixed_cases:
+        print("case", name, flush=True)
+        keys = bgtq.PackedKeys.create(device, _params(m, a), m["capacity"])
+        try:
+            x = a["original"].astype(np.float16).view(np.uint16)
+            assert np.array_equal(x.view(np.float16).astype(np.float32), a["original"])
+            keys.append(x[:2])
+            keys.append(x[2:])
+            packed, norms = keys.read()
+            np.testing.assert_array_equal(packed, a["cache_packed"].reshape(-1), err_msg=name)
+            np.testing.assert_array_equal(norms, a["cache_norms"].view(np.uint16).reshape(-1), err_msg=name)
+            assert keys.length == m["rows"]
+        finally:
+            keys.destroy()
+
+
+def test_attention_fixture_rows_exact(device, attention_cases):
+    import bgtq
+    for name, m, a, lm, la in attention_cases:
+        print("case", name, flush=True)
+        keys = bgtq.PackedKeys.create(device, _params(lm, la), m["context_length"])
+        try:
+            k = a["k"].view(np.uint16)
+            keys.append(k[:3])  # odd row boundary shares packed words with the next append
+            keys.append(k[3:])
+            packed, norms = keys.read()
+            np.testing.assert_array_equal(packed.reshape(a["packed_k"].shape), a["packed_k"], err_msg=name)
+            np.testing.assert_array_equal(norms.reshape(a["norms"].shape), a["norms"].view(np.uint16), err_msg=name)
+        finally:
+            keys.destroy()
+
+
+def _random_half_rows(rng, rows, dim):
+    """FP16 K rows with mixed magnitudes: normal, tiny, subnormal, large, zeros, duplicates."""
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    scale = np.exp(rng.uniform(-12, 8, size=(rows, 1))).astype(np.float32)
+    x = (x * scale).clip(-60000, 60000)
+    x[rng.random(rows) < 0.02] = 0.0
+    x[rng.random((rows, dim)) < 0.01] = 0.0
+    sub = rng.random(rows) < 0.01
+    x[sub] = rng.integers(-1023, 1024, size=(int(sub.sum()), dim)).astype(np.float32) * 2.0 ** -24
+    h = x.astype(np.float16)
+    return h.view(np.uint16)
+
+
+def _layouts(oracle):
+    from bgtq import BlockGTQParameters
+    out = []
+    for name in ("low_d16", "mixed_d32", "mixed_d64", "low_d128", "mixed_d128", "awkward_all_widths", "only_high"):
+        m, a = oracle.read_fixture(REF / "mixed" / f"{name}.json")
+        out.append((name, BlockGTQParameters.from_mixed_fixture(m, a)))
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    for i in (0, 1, 17, 89):
+        out.append((f"smollm2_h{i}", BlockGTQParameters.from_serialized(a[f"h{i}_config"], a[f"h{i}_table"])))
+    return out
+
+
+def test_random_rows_bit_exact_vs_oracle(device, oracle):
+    import bgtq
+    rng = np.random.default_rng(2024)
+    for name, p in _layouts(oracle):
+        print("layout", name, flush=True)
+        rows = 6000
+        k = _random_half_rows(rng, rows, p.dim)
+        ol = _olayout(oracle, p)
+        ref_packed, ref_norms = oracle.encode_pack(ol, k)
+        keys = bgtq.PackedKeys.create(device, p, rows + 5)
+        try:
+            cuts = [0, 1, 130, 257, 3000, rows]  # ragged appends
+            for a, b in zip(cuts[:-1], cuts[1:]):
+                keys.append(k[a:b])
+            packed, norms = keys.read()
+            packed = packed[: rows * p.rowBytes].reshape(rows, p.rowBytes)
+            norms = norms[: rows * p.normStride].reshape(rows, p.normStride)
+            bad = np.nonzero(np.any(packed != ref_packed, axis=1) | np.any(norms != ref_norms, axis=1))[0]
+            assert bad.size == 0, f"{name}: {bad.size} rows differ, first {bad[:5]}"
+        finally:
+            keys.destroy()
+
+
+def test_batched_encode_fp32_source_rounds_to_half(device, oracle):
+    """Model path: FP32 post-RoPE rows [rows, kv_heads, dim], rounded to FP16 first (src/model/codec.wgsl:14)."""
+    import torch
+    import bgtq
+    from bgtq import batched
+    p = _layouts(oracle)[9][1]  # a real SmolLM2 head, d = 64
+    tables = bgtq.Tables(device, p)
+    rng = np.random.default_rng(7)
+    rows, kvh = 1000, 3
+    kr = (rng.standard_normal((rows, kvh, 64)) * 1.7).astype(np.float32)
+    src = torch.from_numpy(kr).cuda()
+    packed = torch.zeros((kvh, rows + 4, p.rowBytes), dtype=torch.uint8, device="cuda")
+    norms = torch.zeros((kvh, rows + 4, p.normStride), dtype=torch.int16, device="cuda")
+    jobs = [dict(tables=tables, src=src[:, h], src_row_stride=kvh * 64, rows=rows, packed=packed[h],
+                 norms=norms[h], dst_row0=2) for h in range(kvh)]
+    batched.encode(device, jobs, "f32")
+    device.synchronize()
+    ol = _olayout(oracle, p)
+    for h in range(kvh):
+        ref_p, ref_n = oracle.encode_pack(ol, kr[:, h].astype(np.float16).view(np.uint16))
+        got_p = packed[h].cpu().numpy()
+        got_n = norms[h].cpu().numpy().view(np.uint16)
+        np.testing.assert_array_equal(got_p[2:2 + rows], ref_p)
+        np.testing.assert_array_equal(got_n[2:2 + rows], ref_n)
+        assert not got_p[:2].any() and not got_p[2 + rows:].any()
+    tables.destroy()
+
+
+def test_append_contracts(device, attention_cases):
+    """appendCount and PackedKeys constructor rejections; failed calls leave state unchanged."""
+    import bgtq
+    name, m, a, lm, la = attention_cases[0]
+    p = _params(lm, la)
+    keys = bgtq.PackedKeys.create(device, p, 3)
+    try:
+        k = a["k"].view(np.uint16)
+        with pytest.raises(bgtq.RangeError, match="whole nonempty rows"):
+            keys.append(k[0, :5])
+        with pytest.raises(bgtq.RangeError, match="whole nonempty rows"):
+            keys.append(np.zeros(0, np.uint16))
+        bad = k[:1].copy()
+        bad[0, 3] = 0x7C00
+        with pytest.raises(bgtq.RangeError, match="Finite FP16 K required"):
+            keys.append(bad)
+        with pytest.raises(bgtq.StateError, match="not ready"):
+            keys.ready()
+        keys.append(k[:3])
+        with pytest.raises(bgtq.RangeError, match="K capacity exceeded"):
+            keys.append(k[3:4])
+        assert keys.length == 3
+        keys.ready()
+    finally:
+        keys.destroy()
+    changed = _params(lm, la)
+    changed.rotation = changed.rotation.copy()
+    grp = np.asarray(changed.groupOf)
+    other = int(np.nonzero(grp != grp[0])[0][0])
+    changed.rotation.reshape(p.dim, p.dim)[other, 0] = 0.01
+    with pytest.raises(bgtq.StateError, match="Off-group transform is nonzero"):
+        bgtq.PackedKeys.create(device, changed, 3)
