@@ -311,6 +311,9 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   T->off_books = (uint32_t)off_books;
   T->off_rot = (uint32_t)off_rot;
   T->total_bytes = (uint32_t)total;
+  float cmax = 0.0f;
+  for (int64_t i = 0; i < d * mc; ++i) cmax = std::max(cmax, std::fabs(cent[i]));
+  T->cent_exp = cmax > 0.0f ? 14 - (int32_t)std::ceil(std::log2(cmax)) : 0;
   for (int64_t j = 0; j < d; ++j) {
     T->perm[j] = (uint8_t)perm[j];
     T->group_of[j] = (uint8_t)group_of[j];
@@ -676,8 +679,54 @@ bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes)
   return BGTQ_OK;
 }
 
+// Whether the MFMA kernel handles this launch (see FastLayout in bgtq_internal.h).
+static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables, FastLayout *fl) {
+  auto a16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  if (p.v_dtype != BGTQ_DTYPE_F16 || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
+  if (!a16(p.v) || (p.v_seq_stride * 2) % 16 || (p.v_head_stride * 2) % 16) return false;
+  if (p.key_format == 0) return a16(p.k) && (p.k_seq_stride * 2) % 16 == 0 && (p.k_head_stride * 2) % 16 == 0;
+  if (p.key_format != 1) return false;
+  if ((reinterpret_cast<uintptr_t>(p.packed) & 7) || p.packed_seq_stride % 8 || p.packed_head_stride % 8) return false;
+  if (!a16(p.norms) || (p.norms_seq_stride * 2) % 16 || (p.norms_head_stride * 2) % 16) return false;
+  const int ks = p.dim / 32;
+  for (int h = 0; h < p.kv_heads; ++h) {
+    const DevTables *T = tables[h]->h();
+    if (T->row_bytes % 8 || T->norm_stride != 2 || T->groups > 2 || T->nibble_dims % 32) return false;
+    for (int s = 0; s < ks; ++s) {
+      const int g = T->group_of[32 * s], bk = T->pos_book[32 * s];
+      for (int j = 32 * s; j < 32 * s + 32; ++j)
+        if (T->group_of[j] != g || T->pos_book[j] != bk) return false;
+      const int nib = 32 * s + 32 <= T->nibble_dims;
+      const int off = nib ? 16 * s : T->nibble_dims / 2 + 32 * s - T->nibble_dims;
+      if (h == 0) {
+        fl->nib[s] = nib;
+        fl->byte_off[s] = off;
+        fl->group[s] = g;
+        fl->book[s] = bk;
+      } else if (fl->nib[s] != nib || fl->byte_off[s] != off || fl->group[s] != g || fl->book[s] != bk) {
+        return false;
+      }
+    }
+  }
+  return true;
+}
+
 static bgtq_status launch_decode_common(bgtq_context *ctx, DecodeParams &p, const float *q,
                                         const bgtq_tables *const *tables) {
+  FastLayout fl{};
+  if (fast_layout(p, tables, &fl)) {
+    int books = 0;
+    if (p.key_format == 1)
+      for (int h = 0; h < p.kv_heads; ++h)
+        books = std::max(books, tables[h]->info.n_books * tables[h]->info.max_centroids * 4);
+    p.lds_bytes = decode_mfma_lds_bytes(p.dim, p.key_format, books);
+    if (p.lds_bytes <= 65536) {
+      HIP_TRY(launch_rotate_q(p, q, const_cast<float *>(p.qr), ctx->stream), "rotate_q launch");
+      HIP_TRY(launch_decode_mfma(p, fl, ctx->stream), "decode launch");
+      HIP_TRY(launch_decode_tail(p, ctx->stream), "decode combine launch");
+      return BGTQ_OK;
+    }
+  }
   int lds = 0;
   for (int h = 0; h < (p.key_format == 1 ? p.kv_heads : 1); ++h) {
     const bgtq_tables_info *ti = p.key_format == 1 ? &tables[h]->info : nullptr;

@@ -18,6 +18,7 @@ struct DevTables {
   int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids, n_books, n_codebooks;
   int32_t gstart[kMaxGroups], gend[kMaxGroups], gsize[kMaxGroups];  // group ranges (head-perm order)
   uint32_t off_lut, off_books, off_rot, total_bytes;
+  int32_t cent_exp;  // 2^cent_exp * max|centroid| <= 2^14: fp16 hi/lo split range for MFMA operands
   uint8_t perm[kMaxDim];      // head_perm
   uint8_t group_of[kMaxDim];
   uint8_t pos_cb[kMaxDim];    // position -> code LUT row
@@ -80,14 +81,26 @@ struct DecodeParams {
   float *logits;  // optional [B*Hq*logit_stride]
   float *probs;   // optional [B*Hq*logit_stride]
   int64_t logit_stride;
+  int32_t lds_bytes;  // dynamic LDS of the split kernel
 };
 
-// Launchers (kernels live in encode.hip / decode.hip).
+// Structure of a layout the MFMA decode path handles: every 32-dim K-step of
+// the head-perm order lies in one group and one centroid book and is either
+// all nibble codes or all byte codes; rows are 8-byte aligned; norm_stride 2.
+struct FastLayout {
+  int32_t nib[4], byte_off[4], group[4], book[4];
+};
+
+// Launchers (kernels live in encode.hip / decode.hip / decode_mfma.hip).
 hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
                          hipStream_t stream);
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
 int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_bytes, int norm_stride);
 hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream);
+// LSE merge of split partials and the optional probabilities pass.
+hipError_t launch_decode_tail(const DecodeParams &p, hipStream_t stream);
+hipError_t launch_decode_mfma(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
+int decode_mfma_lds_bytes(int dim, int key_format, int books_bytes);
 hipError_t launch_reconstruct(const DevTables *t, const uint8_t *packed, const uint16_t *norms,
                               int64_t rows, float *out, hipStream_t stream);
 hipError_t launch_half_convert(const float *src, uint16_t *dst, int64_t n, hipStream_t stream);

@@ -333,15 +333,8 @@ hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hip
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream) {
-  hipError_t e;
-  const int G = p.G;
-  if (G <= 1) e = launch_gp<1>(p, lds_bytes, stream);
-  else if (G <= 2) e = launch_gp<2>(p, lds_bytes, stream);
-  else if (G <= 4) e = launch_gp<4>(p, lds_bytes, stream);
-  else if (G <= 8) e = launch_gp<8>(p, lds_bytes, stream);
-  else e = launch_gp<16>(p, lds_bytes, stream);
-  if (e != hipSuccess) return e;
+hipError_t launch_decode_tail(const DecodeParams &p, hipStream_t stream) {
+  hipError_t e = hipSuccess;
   if (p.splits > 1) {
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)(p.batch * p.q_heads)), dim3(128), 0, stream, p);
     e = hipGetLastError();
@@ -352,6 +345,18 @@ hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t strea
     e = hipGetLastError();
   }
   return e;
+}
+
+hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream) {
+  hipError_t e;
+  const int G = p.G;
+  if (G <= 1) e = launch_gp<1>(p, lds_bytes, stream);
+  else if (G <= 2) e = launch_gp<2>(p, lds_bytes, stream);
+  else if (G <= 4) e = launch_gp<4>(p, lds_bytes, stream);
+  else if (G <= 8) e = launch_gp<8>(p, lds_bytes, stream);
+  else e = launch_gp<16>(p, lds_bytes, stream);
+  if (e != hipSuccess) return e;
+  return launch_decode_tail(p, stream);
 }
 
 }  // namespace bgtq

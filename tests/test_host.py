@@ -1,0 +1,142 @@
+"""Host-side checks that need no GPU: the C ABI library, the Python mirror of the
+reference's table/validation logic, and the calibration-table generator."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from conftest import REF, ROOT
+
+
+def test_library_exports_every_declared_symbol():
+    import bgtq
+    header = (ROOT / "include" / "bgtq.h").read_text()
+    decl = r"^(?:const\s+)?(?:bgtq_status|void|char|int32_t|uint32_t)\s*\*?\s*(bgtq_[a-z0-9_]+)\s*\("
+    declared = set(re.findall(decl, header, re.MULTILINE))
+    assert len(declared) > 30
+    lib = ctypes.CDLL(str(bgtq.LIB_PATH))
+    missing = [name for name in sorted(declared) if not hasattr(lib, name)]
+    assert not missing, missing
+    assert lib.bgtq_abi_version() == 1
+
+
+def test_no_device_is_reported_cleanly():
+    import bgtq
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(bgtq.DeviceError):
+        bgtq.Device(0)
+
+
+def _mixed(oracle, name):
+    import bgtq
+    m, a = oracle.read_fixture(REF / "mixed" / f"{name}.json")
+    return m, a, bgtq.BlockGTQParameters.from_mixed_fixture(m, a)
+
+
+def test_tables_serialization_matches_model_blob(oracle):
+    """tables(p) (src/webgpu/layout.ts:24-31) reproduces the committed per-head model blobs."""
+    import bgtq
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    for i in range(len(m["heads"])):
+        p = bgtq.BlockGTQParameters.from_serialized(a[f"h{i}_config"], a[f"h{i}_table"])
+        ints, fl = bgtq.tables(p)
+        np.testing.assert_array_equal(ints, a[f"h{i}_config"])
+        np.testing.assert_array_equal(fl.view(np.uint32), a[f"h{i}_table"].view(np.uint32))
+
+
+def test_validate_layout_messages(oracle):
+    import bgtq
+    m, a, p = _mixed(oracle, "mixed_d64")
+    bgtq.validate_layout(p)
+    for field, value, msg in (("dim", 130, "Invalid Block-GTQ layout"), ("groups", 9, "Invalid Block-GTQ layout"),
+                              ("normStride", 1, "Invalid Block-GTQ layout"), ("rowBytes", 10, "Invalid Block-GTQ layout"),
+                              ("maxCentroids", 1, "Invalid Block-GTQ layout")):
+        bad = bgtq.BlockGTQParameters(**{**p.__dict__, field: value})
+        with pytest.raises(bgtq.RangeError, match=msg):
+            bgtq.validate_layout(bad)
+    perm = np.array(p.permutation).copy()
+    perm[1] = perm[0]
+    with pytest.raises(bgtq.RangeError, match="Invalid calibration table shape"):
+        bgtq.validate_layout(bgtq.BlockGTQParameters(**{**p.__dict__, "permutation": perm}))
+    rot = np.array(p.rotation, np.float32).copy()
+    rot[5] = np.inf
+    with pytest.raises(bgtq.RangeError, match="Nonfinite calibration table"):
+        bgtq.validate_layout(bgtq.BlockGTQParameters(**{**p.__dict__, "rotation": rot}))
+    lut = np.array(p.codeLut).copy()
+    lut[0] = 200  # position 0 is a nibble position
+    with pytest.raises(bgtq.RangeError, match="Code LUT incompatible with packing"):
+        bgtq.validate_layout(bgtq.BlockGTQParameters(**{**p.__dict__, "codeLut": lut}))
+
+
+def test_append_count_messages():
+    import bgtq
+    with pytest.raises(bgtq.RangeError, match="whole nonempty rows"):
+        bgtq.append_count(np.zeros(0, np.uint16), 4, 0, 8)
+    with pytest.raises(bgtq.RangeError, match="whole nonempty rows"):
+        bgtq.append_count(np.zeros(6, np.uint16), 4, 0, 8)
+    with pytest.raises(bgtq.RangeError, match="Finite FP16 K required"):
+        bgtq.append_count(np.array([0, 0x7C00, 0, 0], np.uint16), 4, 0, 8)
+    with pytest.raises(bgtq.RangeError, match="Finite FP16 K required"):
+        bgtq.append_count(np.array([0, 0xFE00, 0, 0], np.uint16), 4, 0, 8)
+    with pytest.raises(bgtq.RangeError, match="K capacity exceeded"):
+        bgtq.append_count(np.zeros(8, np.uint16), 4, 7, 8)
+    assert bgtq.append_count(np.zeros(8, np.uint16), 4, 6, 8) == 2
+
+
+def test_calibration_tables_reproduce_reference(oracle):
+    """The table generator rebuilds every committed reference table set bit for bit: the 90 real
+    SmolLM2 heads and the mixed layouts up to 32 pairs (d <= 64). For 64 pairs the reference's
+    tie order among equal widths came from torch 2.12's unstable sort and is not reproduced;
+    every other table (rotations, codebooks, LUTs, offsets) still matches."""
+    import json
+    import bgtq
+    from bgtq import calibrate
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    for i in range(len(m["heads"])):
+        p = calibrate.make_parameters(a[f"h{i}_widths"].astype(np.int64))
+        ints, fl = bgtq.tables(p)
+        np.testing.assert_array_equal(ints, a[f"h{i}_config"], err_msg=f"head {i}")
+        np.testing.assert_array_equal(fl.view(np.uint32), a[f"h{i}_table"].view(np.uint32), err_msg=f"head {i}")
+    for c in json.loads((REF / "mixed" / "index.json").read_text())["cases"]:
+        mm, aa = oracle.read_fixture(REF / "mixed" / f"{c['name']}.json")
+        p = calibrate.make_parameters(aa["allocation"].astype(np.int64), row_bytes=mm["row_bytes"],
+                                      norm_stride=mm["norm_stride"])
+        for key, mine in (("group_of", p.groupOf), ("pos_to_cb", p.positionToCodebook), ("code_lut", p.codeLut),
+                          ("rotation", p.rotation), ("centroids", p.centroids), ("lut_offsets", p.offsets),
+                          ("lut_inv_scales", p.inverseScales)):
+            np.testing.assert_array_equal(np.asarray(mine).reshape(-1), aa[key].reshape(-1), err_msg=f"{c['name']} {key}")
+        if mm["dim"] <= 64:
+            np.testing.assert_array_equal(p.permutation, aa["head_perm"], err_msg=c["name"])
+        g = calibrate.grouping(aa["allocation"].astype(np.int64))
+        for key in ("group_bits", "group_offsets", "group_of"):
+            np.testing.assert_array_equal(g[key], aa[key], err_msg=f"{c['name']} {key}")
+        assert g["nopack_start"] == mm["nopack_start"]
+
+
+def test_layout_b_and_a_shapes():
+    from bgtq import calibrate
+    for d, rb, groups in ((64, 48, 2), (128, 96, 2)):
+        p = calibrate.layout_b(d)
+        widths = np.asarray(p.permutation)  # grouping sorted: first half 4-bit, second half 8-bit
+        assert p.rowBytes == rb and p.groups == groups and p.nibbleDims == d // 2 and p.normStride == 2
+        assert np.array_equal(np.asarray(p.groupOf), np.repeat([0, 1], d // 2))
+        assert sorted(widths.tolist()) == list(range(d))
+    pa = calibrate.layout_a(64)
+    assert pa.groups == 3 and pa.rowBytes == 64 and pa.nibbleDims == 0
+    pa = calibrate.layout_a(128)
+    assert pa.groups == 5 and pa.rowBytes == 116
+
+
+def test_allocator_mirror_matches_oracle(oracle):
+    from bgtq import calibrate
+    rng = np.random.default_rng(1)
+    for _ in range(200):
+        n = int(rng.integers(1, 40))
+        s = rng.exponential(size=n).astype(np.float32) * (rng.random(n) > 0.2)
+        budget = int(rng.integers(0, 8 * n + 4))
+        lo = int(rng.integers(0, 3))
+        hi = int(rng.integers(lo, 9))
+        np.testing.assert_array_equal(calibrate.allocate_bits(s, budget, lo, hi), oracle.allocate_bits(s, budget, lo, hi))
