@@ -1,21 +1,30 @@
 """Benchmark: compressed-K decode attention at Qwen2.5-0.5B geometry on one MI355X.
 
-Workload (one step): decode attention for all 24 layers of 64 independent
-sequences x 32768 context tokens, 14 query heads over 2 KV heads (GQA 7:1),
-head_dim 64. K is Block-GTQ packed with layout B (widths 4/8 half each, 6.0
-bits average: 48 code bytes + 2 FP16 scales per token-head), V is FP16. Inputs
-are synthetic N(0,1), encoded by the library's own encoder, resident in HBM
-before timing. Per layer and (sequence, KV head): T*(48 + 4 + 128) bytes.
+Headline workload (one step): decode attention for all 24 layers of 64
+independent sequences x 32768 context tokens, 14 query heads over 2 KV heads
+(GQA 7:1), head_dim 64. K is Block-GTQ packed with layout B (widths 4/8 half
+each, 6.0 bits average: 48 code bytes + 2 FP16 scales per token-head), V is
+FP16. Inputs are synthetic N(0,1), encoded by the library's own encoder and
+resident in HBM before timing. Algorithmic bytes per layer and (sequence, KV
+head): T * (48 + 4 + 128). One step = 24 per-layer launches, issued as one
+HIP graph (the way a serving loop replays a decode step).
 
-    python bench.py [--steps K] [--warmup W] [--layout B|A] [--no-cpu]
+Side measurements in the same JSON line: SmolLM2 K-encode throughput (4096 x 3
+x 30 rows), a SmolLM2-geometry decode step at batch 1 (30 layers x encode one
+token + attend over 4096), the single-head T=4096 d=128 attention, and an
+FP16-K kernel at the headline shape.
+
+    python bench.py [--steps K] [--warmup W] [--layout B|A] [--no-cpu] [--no-extra]
 
 Prints one JSON line (value = algorithmic HBM GB/s of the decode step).
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -39,10 +48,10 @@ def layout_params(name, dim):
 
 
 class DecodeWorkload:
-    """All layers' caches for the C5 shape, plus per-layer descriptors."""
+    """All layers' caches for one decode shape, plus per-layer descriptors."""
 
     def __init__(self, dev, layout="B", layers=LAYERS, batch=BATCH, ctx=CTX, hq=HQ, hkv=HKV, dim=DIM, seed=0,
-                 key_format="packed"):
+                 key_format="packed", splits=0):
         import torch
         import bgtq
         from bgtq import batched
@@ -77,15 +86,13 @@ class DecodeWorkload:
             else:
                 kw = dict(k_f16=k, k_seq_stride=k.stride(0), k_head_stride=k.stride(1))
                 self.keep += [k, v, q]
-            desc = batched.decode_desc(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=q, out=self.out,
-                                       lengths=self.lengths, max_length=ctx, v=v, v_dtype="f16",
-                                       v_seq_stride=v.stride(0), v_head_stride=v.stride(1), **kw)
+            args = dict(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=q, out=self.out, lengths=self.lengths,
+                        max_length=ctx, v=v, v_dtype="f16", v_seq_stride=v.stride(0), v_head_stride=v.stride(1),
+                        splits=splits, **kw)
             if ws is None:
-                ws = torch.empty(batched.workspace_bytes(desc), dtype=torch.uint8, device="cuda")
-            desc = batched.decode_desc(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=q, out=self.out,
-                                       lengths=self.lengths, max_length=ctx, v=v, v_dtype="f16",
-                                       v_seq_stride=v.stride(0), v_head_stride=v.stride(1), workspace=ws, **kw)
-            self.descs.append(desc)
+                ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8,
+                                 device="cuda")
+            self.descs.append(batched.decode_desc(workspace=ws, **args))
         self.ws = ws
         torch.cuda.synchronize()
 
@@ -93,38 +100,67 @@ class DecodeWorkload:
         per_token = self.row_bytes + 2 * self.norm_stride + 2 * self.dim
         return self.batch * self.hkv * self.ctx * per_token
 
-    def step(self, events=None):
+    def set_splits(self, splits):
         from bgtq import batched
-        for i, d in enumerate(self.descs):
-            if events is not None:
-                events[i][0].record()
+        for d in self.descs:
+            d.splits = splits
+        self.ws = self.torch.zeros(batched.workspace_bytes(self.descs[0]), dtype=self.torch.uint8, device="cuda")
+        for d in self.descs:
+            d.workspace, d.workspace_bytes = ctypes.c_void_p(self.ws.data_ptr()), self.ws.numel()
+
+    def step(self):
+        from bgtq import batched
+        for d in self.descs:
             batched.decode(self.dev, d)
-            if events is not None:
-                events[i][1].record()
 
 
-def time_decode(w, steps, warmup):
-    torch = w.torch
+def graph_of(torch, dev, fn, warmup=2):
+    """Capture fn() (stream-ordered library calls) as a HIP graph on a side stream."""
+    from bgtq import batched
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        batched.bind_torch_stream(dev)
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        batched.bind_torch_stream(dev)
+        fn()
+    batched.bind_torch_stream(dev)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, steps, warmup):
     for _ in range(warmup):
-        w.step()
+        g.replay()
     torch.cuda.synchronize()
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in w.descs]
-          for _ in range(steps)]
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        g.replay()
+    b.record()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for s in range(steps):
-        w.step(ev[s])
-    stop.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    total_ms = start.elapsed_time(stop)
-    per_launch = [a.elapsed_time(b) for row in ev for a, b in row]
-    return total_ms / steps, sum(per_launch) / len(per_launch), wall
+    return a.elapsed_time(b) / steps
 
 
-def encode_throughput(dev, layout="B", reps=5):
+def time_eager(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def encode_throughput(dev, layout="B", reps=10):
     """Prefill K encode at SmolLM2 geometry: 4096 tokens x 3 KV heads x 30 layers, d=64."""
     import torch
     import bgtq
@@ -136,23 +172,76 @@ def encode_throughput(dev, layout="B", reps=5):
     norms = torch.empty((90, 4096 * p.normStride + 32), dtype=torch.int16, device="cuda")
     jobs = [dict(tables=tabs[l * 3 + h], src=k[l, :, h], src_row_stride=3 * 64, rows=4096, packed=packed[l * 3 + h],
                  norms=norms[l * 3 + h], dst_row0=0) for l in range(30) for h in range(3)]
-    batched.encode(dev, jobs, "f16")
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(reps):
-        batched.encode(dev, jobs, "f16")
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
+    ms = time_eager(torch, lambda: batched.encode(dev, jobs, "f16"), reps, 2)
     rows = 30 * 3 * 4096
     for t in tabs:
         t.destroy()
-    return {"rows_per_s": rows / (ms / 1e3), "tokens_per_s": 4096 / (ms / 1e3), "ms": ms,
-            "gbs_algorithmic": rows * (128 + p.rowBytes + 2 * p.normStride) / (ms / 1e3) / 1e9}
+    return {"rows_per_s": round(rows / (ms / 1e3)), "tokens_per_s": round(4096 / (ms / 1e3)), "ms": round(ms, 4),
+            "gbs_algorithmic": round(rows * (128 + p.rowBytes + 2 * p.normStride) / (ms / 1e3) / 1e9, 1)}
 
 
-def cpu_baseline(layout="B", budget_s=12.0):
+def smollm2_decode_step(dev, steps, layout="B"):
+    """SmolLM2-135M geometry at batch 1: per layer, encode the new token's K for
+    3 KV heads, then attend 9 query heads over the 4096 + 1 cached tokens."""
+    import torch
+    import bgtq
+    from bgtq import batched
+    L, HKV2, HQ2, T = 30, 3, 9, 4096
+    p = layout_params(layout, 64)
+    tabs = [bgtq.Tables(dev, p) for _ in range(L * HKV2)]
+    packed = torch.empty((L, 1, HKV2, (T + 1) * p.rowBytes + 64), dtype=torch.uint8, device="cuda")
+    # per-head scale rows padded to 16 bytes (the fused kernel reads four tokens' scales at once)
+    norms = torch.empty((L, 1, HKV2, ((T + 1) * p.normStride + 32 + 7) // 8 * 8), dtype=torch.int16, device="cuda")
+    hist = torch.randn((L, HKV2, T, 64), device="cuda").half()
+    for l in range(L):
+        batched.encode(dev, [dict(tables=tabs[l * HKV2 + h], src=hist[l, h], src_row_stride=64, rows=T,
+                                  packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=0) for h in range(HKV2)], "f16")
+    del hist
+    knew = torch.randn((L, HKV2, 64), device="cuda")  # post-RoPE FP32 K of the new token
+    v = torch.randn((L, 1, HKV2, T + 1, 64), device="cuda").half()
+    q = torch.randn((L, 1, HQ2, 64), device="cuda")
+    out = torch.empty((L, 1, HQ2, 64), device="cuda")
+    lengths = torch.full((1,), T + 1, dtype=torch.int32, device="cuda")
+    jobs, descs, ws = [], [], None
+    for l in range(L):
+        jobs.append([dict(tables=tabs[l * HKV2 + h], src=knew[l, h], src_row_stride=64, rows=1,
+                          packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=T) for h in range(HKV2)])
+        args = dict(batch=1, q_heads=HQ2, kv_heads=HKV2, dim=64, q=q[l], out=out[l], lengths=lengths,
+                    max_length=T + 1, v=v[l], v_seq_stride=v.stride(1), v_head_stride=v.stride(2),
+                    tables=tabs[l * HKV2:(l + 1) * HKV2], packed=packed[l], packed_seq_stride=packed.stride(1),
+                    packed_head_stride=packed.stride(2), norms=norms[l], norms_seq_stride=norms.stride(1),
+                    norms_head_stride=norms.stride(2))
+        if ws is None:
+            ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8, device="cuda")
+        descs.append(batched.decode_desc(workspace=ws, **args))
+
+    def step():
+        for l in range(L):
+            batched.encode(dev, jobs[l], "f32")
+            batched.decode(dev, descs[l])
+
+    g = graph_of(torch, dev, step)
+    ms = time_graph(torch, g, steps, 3)
+    per_token = p.rowBytes + 2 * p.normStride + 128
+    bytes_step = L * HKV2 * (T + 1) * per_token
+    for t in tabs:
+        t.destroy()
+    return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(bytes_step / (ms / 1e3) / 1e9, 1),
+            "workload": "30 layers x (encode 1 token x 3 KV heads + attend 9 q heads over 4097 tokens), d=64, "
+                        "batch 1, layout B, FP16 V"}
+
+
+def single_head(dev, steps, layout="B"):
+    """One query over T=4096, d=128, one head (the reference's CPU-runnable shape)."""
+    import torch
+    w = DecodeWorkload(dev, layout, layers=1, batch=1, ctx=4096, hq=1, hkv=1, dim=128)
+    g = graph_of(torch, dev, w.step)
+    ms = time_graph(torch, g, steps * 10, 5)
+    return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(w.bytes_per_layer() / (ms / 1e3) / 1e9, 1),
+            "workload": "1 query, T=4096, d=128, one head, layout B, FP16 V"}
+
+
+def cpu_baseline(layout="B", budget_s=10.0):
     """The oracle (scalar C, 1 thread) on whole (sequence, KV head) units of the same workload."""
     import numpy as np
     from oracle import oracle as O
@@ -175,16 +264,18 @@ def cpu_baseline(layout="B", budget_s=12.0):
         units += 1
     dt = time.perf_counter() - t0
     unit_bytes = CTX * (p.rowBytes + 2 * p.normStride + 2 * DIM)
-    return {"value": units * unit_bytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(units * unit_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{units} (sequence, KV head) units of {CTX} tokens x {HQ // HKV} query heads, d={DIM}, "
                       f"oracle unpack+reconstruct+attention, {dt:.1f} s"}
 
 
 def read_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if present."""
-    f = ROOT / "profiles" / "decode_c5_layoutB_pmc.json"
+    f = ROOT / "profiles" / "decode_fast_qwen_b64_t32k_layoutB_pmc.txt"
     if f.exists():
-        return json.loads(f.read_text()).get("traffic_bytes_per_launch")
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read_text())
+        if m:
+            return int(m.group(1))
     return None
 
 
@@ -195,48 +286,81 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layout", default="B", choices=["A", "B"])
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the encode and FP16-K side measurements")
+    ap.add_argument("--no-extra", action="store_true", help="skip the side measurements")
+    ap.add_argument("--eager", action="store_true", help="issue the per-layer launches directly, no HIP graph")
+    ap.add_argument("--splits", type=int, default=0, help="token splits per (sequence, KV head); 0 = library choice")
+    ap.add_argument("--sweep-splits", default="", help="comma list: time the decode at each split count and exit")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB three times (HBM counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path shards by (sequence, KV head) with no exchange, "
               "and this build runs on a single MI355X; use --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
+    if a.copy_probe:
+        src = torch.ones(a.copy_probe << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4}))
+        return
     import bgtq
     from bgtq import batched
     dev = bgtq.Device(0)
     batched.bind_torch_stream(dev)
     log("building workload ...")
-    w = DecodeWorkload(dev, a.layout)
+    w = DecodeWorkload(dev, a.layout, splits=a.splits)
+    if a.sweep_splits:
+        for sp in [int(x) for x in a.sweep_splits.split(",")]:
+            w.set_splits(sp)
+            ms = time_eager(torch, w.step, a.steps, a.warmup) if a.eager else \
+                time_graph(torch, graph_of(torch, dev, w.step), a.steps, a.warmup)
+            print(json.dumps({"splits": sp, "ms_per_step": ms, "us_per_launch": ms * 1e3 / LAYERS,
+                              "gbs": w.bytes_per_layer() * LAYERS / (ms / 1e3) / 1e9}), flush=True)
+        return
     log("timing ...")
-    ms_step, ms_launch, wall = time_decode(w, a.steps, a.warmup)
+    if a.eager:
+        ms_step = time_eager(torch, w.step, a.steps, a.warmup)
+    else:
+        ms_step = time_graph(torch, graph_of(torch, dev, w.step), a.steps, a.warmup)
+    ms_eager = time_eager(torch, w.step, max(2, a.steps // 2), 1)
     bytes_layer = w.bytes_per_layer()
     gbs = LAYERS * bytes_layer / (ms_step / 1e3) / 1e9
+    ms_launch = ms_step / LAYERS  # one decode launch per layer, back to back in the graph
     achieved = bytes_layer / (ms_launch / 1e3) / 1e9
-    extra = {}
+    extra = {"eager_ms_per_step": round(ms_eager, 4)}
     if not a.no_extra:
         del w
         torch.cuda.empty_cache()
+        log("FP16-K kernel at the same shape ...")
+        wf = DecodeWorkload(dev, key_format="fp16")
+        ms_f = time_graph(torch, graph_of(torch, dev, wf.step), max(2, a.steps // 2), 1)
+        extra["fp16_k_same_shape"] = {"ms_per_step": round(ms_f, 4), "bytes_per_step": LAYERS * wf.bytes_per_layer(),
+                                      "gbs_algorithmic": round(LAYERS * wf.bytes_per_layer() / (ms_f / 1e3) / 1e9, 1)}
+        del wf
+        torch.cuda.empty_cache()
         log("encode throughput ...")
         extra["encode_smollm2_prefill"] = encode_throughput(dev, a.layout)
-        log("FP16-K baseline kernel ...")
-        wf = DecodeWorkload(dev, key_format="fp16")
-        ms_f, _, _ = time_decode(wf, max(2, a.steps // 2), 1)
-        extra["fp16_k_baseline"] = {"ms_per_step": ms_f,
-                                    "gbs_algorithmic": LAYERS * wf.bytes_per_layer() / (ms_f / 1e3) / 1e9}
-        del wf
+        log("SmolLM2 decode step ...")
+        extra["smollm2_decode_step_b1"] = smollm2_decode_step(dev, a.steps, a.layout)
+        log("single head ...")
+        extra["single_head_t4096_d128"] = single_head(dev, a.steps, a.layout)
     cpu = None if a.no_cpu else cpu_baseline(a.layout)
     rec = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms_step, 4), "us_per_layer": round(ms_step * 1e3 / LAYERS, 2),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8 codes + f16 scales/V, f32 accumulate",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
         "data": "synthetic N(0,1) K/V/Q, K encoded by the library",
         "config": {"workload": f"Qwen2.5-0.5B-geometry decode attention: batch {BATCH} x {CTX} ctx, {LAYERS} layers, "
-                               f"{HQ} q / {HKV} kv heads, d={DIM}, layout {a.layout}, FP16 V",
-                   "global_batch": BATCH, "seq_len": CTX, "parallelism": "single GPU"},
+                               f"{HQ} q / {HKV} kv heads, d={DIM}, layout {a.layout} (u8 codes, f16 scales), "
+                               f"FP16 V, f32 accumulate",
+                   "global_batch": BATCH, "seq_len": CTX, "parallelism": "single GPU",
+                   "launch": "eager" if a.eager else "hip graph of 24 per-layer launches"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "kernel": "bgtq decode (per-layer launch)", "bytes_per_launch": bytes_layer},
+                     "kernel": "decode_fast_kernel<64,1,1,1> (one launch per layer)", "bytes_per_launch": bytes_layer},
         "cpu_baseline": cpu,
         **extra,
     }

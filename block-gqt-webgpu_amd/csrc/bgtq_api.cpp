@@ -63,6 +63,33 @@ uint16_t f32_to_f16(float x) {
   return (uint16_t)(sign | ((he > 0 ? (uint32_t)he << 10 : 0u) + base + inc));
 }
 
+// FP32 -> FP16 bits rounded toward zero (subnormals kept, overflow to the
+// largest finite value), and FP16 bits -> FP32.
+uint16_t f32_to_f16_rtz(float x) {
+  uint32_t b;
+  std::memcpy(&b, &x, 4);
+  const uint32_t sign = (b >> 16) & 0x8000u, e = (b >> 23) & 0xffu, m = b & 0x7fffffu;
+  const int32_t he = (int32_t)e - 112;
+  if (e == 0xffu) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u : 0u));
+  if (he >= 31) return (uint16_t)(sign | 0x7bffu);
+  if (he <= 0) {
+    if (he < -10) return (uint16_t)sign;
+    return (uint16_t)(sign | ((m | 0x800000u) >> (14 - he)));
+  }
+  return (uint16_t)(sign | ((uint32_t)he << 10) | (m >> 13));
+}
+float f16_to_f32(uint16_t h) {
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+  float v;
+  if (e == 0) {
+    v = std::ldexp((float)m, -24);
+    return sign ? -v : v;
+  }
+  const uint32_t bits = e == 31 ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+  std::memcpy(&v, &bits, 4);
+  return v;
+}
+
 struct DeviceBuffer {
   void *ptr = nullptr;
   size_t bytes = 0;
@@ -157,6 +184,7 @@ struct bgtq_attention {
   int32_t causal = 0, materialize = 0;
   std::vector<uint32_t> positions;
   DeviceBuffer q, qr, out, logits, probs, part, stats, small;  // small: lengths[1] + ends[maxQ]
+  DeviceBuffer counters;                                       // split arrival counter (zero between launches)
   uint32_t *pinned = nullptr;                                  // host staging of small
   Ledger ledger;
   ~bgtq_attention() {
@@ -289,7 +317,9 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   const size_t off_lut = align(sizeof(DevTables));
   const size_t off_books = align(off_lut + lut_len);
   const size_t off_rot = align(off_books + sizeof(float) * nb * mc);
-  const size_t total = off_rot + sizeof(float) * d * d;
+  const size_t off_rot_t = align(off_rot + sizeof(float) * d * d);
+  const size_t off_mfma = align(off_rot_t + sizeof(float) * d * d);
+  const size_t total = off_mfma + (size_t)kMfmaTableBytes * nb;
   auto *t = new bgtq_tables();
   t->ctx = ctx;
   t->host.assign(total, 0);
@@ -310,6 +340,8 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   T->off_lut = (uint32_t)off_lut;
   T->off_books = (uint32_t)off_books;
   T->off_rot = (uint32_t)off_rot;
+  T->off_rot_t = (uint32_t)off_rot_t;
+  T->off_mfma = (uint32_t)off_mfma;
   T->total_bytes = (uint32_t)total;
   float cmax = 0.0f;
   for (int64_t i = 0; i < d * mc; ++i) cmax = std::max(cmax, std::fabs(cent[i]));
@@ -327,6 +359,30 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   for (int b = 0; b < nb; ++b)
     std::memcpy(h + off_books + sizeof(float) * b * mc, cent + book_rows[b] * mc, sizeof(float) * mc);
   std::memcpy(h + off_rot, rot, sizeof(float) * d * d);
+  float *rot_t = reinterpret_cast<float *>(h + off_rot_t);
+  for (int64_t j = 0; j < d; ++j)
+    for (int64_t i = 0; i < d; ++i) rot_t[i * d + j] = rot[j * d + i];
+  // MFMA lookup tables: c * 2^cent_exp = hi + lo, hi and lo fp16 rounded toward zero.
+  const float csc = std::ldexp(1.0f, T->cent_exp);
+  for (int b = 0; b < nb; ++b) {
+    const float *c = cent + book_rows[b] * mc;
+    uint8_t *tb = h + off_mfma + (size_t)kMfmaTableBytes * b;
+    uint32_t *pair_hi = reinterpret_cast<uint32_t *>(tb), *pair_lo = pair_hi + 256;
+    uint16_t *code_hi = reinterpret_cast<uint16_t *>(tb + 2048), *code_lo = code_hi + 256;
+    auto split = [&](int e, uint16_t *hi, uint16_t *lo) {
+      const float x = e < mc ? c[e] * csc : 0.0f;
+      *hi = f32_to_f16_rtz(x);
+      *lo = f32_to_f16_rtz(x - f16_to_f32(*hi));
+    };
+    for (int e = 0; e < 256; ++e) {
+      uint16_t h0, l0, h1, l1;
+      split(e & 15, &h0, &l0);
+      split(e >> 4, &h1, &l1);
+      pair_hi[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+      pair_lo[e] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+      split(e, &code_hi[e], &code_lo[e]);
+    }
+  }
   t->info = bgtq_tables_info{(int32_t)d, (int32_t)ng, (int32_t)rb, (int32_t)nstride, (int32_t)nib, (int32_t)mc, ncb, nb};
   bgtq_status s = ctx->use();
   if (!s) s = t->blob.alloc(total, "K tables");
@@ -626,22 +682,41 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
   return BGTQ_OK;
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Token splits per (sequence, KV head): at least 256 tokens each, at most 256
+// splits (the fused kernel merges them through LDS). By default enough splits
+// for two resident workgroups per compute unit: more, shorter-lived
+// workgroups only add per-workgroup set-up and merge round trips.
 static int choose_splits(int64_t units, uint32_t max_length, int32_t requested) {
-  const int64_t max_splits = std::max<int64_t>(1, (max_length + 255) / 256);
+  const int64_t max_splits = std::min<int64_t>(256, std::max<int64_t>(1, (max_length + 255) / 256));
   if (requested > 0) return (int)std::min<int64_t>(requested, max_splits);
-  const int64_t want = std::max<int64_t>(1, (2048 + units - 1) / units);
+  const int64_t target = 2 * (int64_t)device_cus();
+  const int64_t want = std::max<int64_t>(1, (target + units - 1) / units);
   return (int)std::min<int64_t>(want, max_splits);
 }
 
 struct DecodeWorkspace {
-  size_t qr, part, stats, total;
+  size_t counters, qr, part, stats, total;
 };
 
-static DecodeWorkspace decode_ws(int64_t heads, int dim, int splits) {
+static DecodeWorkspace decode_ws(int64_t units, int64_t heads, int dim, int splits) {
   auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
   DecodeWorkspace w;
-  w.qr = 0;
-  w.part = al(sizeof(float) * heads * dim);
+  w.counters = 0;
+  w.qr = al(sizeof(uint32_t) * units);
+  w.part = w.qr + al(sizeof(float) * heads * dim);
   w.stats = w.part + al(sizeof(float) * heads * splits * (dim + 2));
   w.total = w.stats + al(sizeof(float) * heads * 2);
   return w;
@@ -653,7 +728,7 @@ static bgtq_status validate_decode(const bgtq_decode_desc *d, int *splits) {
       d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 16)
     return fail(BGTQ_ERR_RANGE, "invalid head geometry");
   if (d->dim < 2 || d->dim > 128 || d->dim % 2) return fail(BGTQ_ERR_RANGE, "invalid head dim");
-  if (d->max_length < 1) return fail(BGTQ_ERR_RANGE, "max_length must be >= 1");
+  if (d->max_length < 1 || d->max_length > (1u << 24)) return fail(BGTQ_ERR_RANGE, "max_length must be in 1..2^24");
   if (d->key_format == BGTQ_KEYS_PACKED) {
     for (int h = 0; h < d->kv_heads; ++h) {
       if (!d->tables[h]) return fail(BGTQ_ERR_RANGE, "null tables for KV head %d", h);
@@ -675,57 +750,62 @@ bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes)
   int splits = 1;
   if (bgtq_status s = validate_decode(d, &splits)) return s;
   if (!bytes) return fail(BGTQ_ERR_RANGE, "null output");
-  *bytes = decode_ws((int64_t)d->batch * d->q_heads, d->dim, splits).total;
+  *bytes = decode_ws((int64_t)d->batch * d->kv_heads, (int64_t)d->batch * d->q_heads, d->dim, splits).total;
   return BGTQ_OK;
 }
 
-// Whether the MFMA kernel handles this launch (see FastLayout in bgtq_internal.h).
-static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables, FastLayout *fl) {
+// Whether the fused matrix-core kernel handles this launch (FastLayout in
+// bgtq_internal.h); on success fills the K-step books, nn and sg.
+static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables, FastLayout *fl, int *nn, int *sg) {
   auto a16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   if (p.v_dtype != BGTQ_DTYPE_F16 || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
   if (!a16(p.v) || (p.v_seq_stride * 2) % 16 || (p.v_head_stride * 2) % 16) return false;
-  if (p.key_format == 0) return a16(p.k) && (p.k_seq_stride * 2) % 16 == 0 && (p.k_head_stride * 2) % 16 == 0;
+  const int ks = p.dim / 32;
+  if (p.key_format == 0) {
+    *nn = 0;
+    *sg = ks;
+    return a16(p.k) && (p.k_seq_stride * 2) % 16 == 0 && (p.k_head_stride * 2) % 16 == 0;
+  }
   if (p.key_format != 1) return false;
   if ((reinterpret_cast<uintptr_t>(p.packed) & 7) || p.packed_seq_stride % 8 || p.packed_head_stride % 8) return false;
   if (!a16(p.norms) || (p.norms_seq_stride * 2) % 16 || (p.norms_head_stride * 2) % 16) return false;
-  const int ks = p.dim / 32;
   for (int h = 0; h < p.kv_heads; ++h) {
     const DevTables *T = tables[h]->h();
     if (T->row_bytes % 8 || T->norm_stride != 2 || T->groups > 2 || T->nibble_dims % 32) return false;
+    const int n = T->nibble_dims / 32;
+    if (T->row_bytes != decode_fast_row_bytes(p.dim, n)) return false;
+    int g0 = 0;
     for (int s = 0; s < ks; ++s) {
       const int g = T->group_of[32 * s], bk = T->pos_book[32 * s];
       for (int j = 32 * s; j < 32 * s + 32; ++j)
         if (T->group_of[j] != g || T->pos_book[j] != bk) return false;
-      const int nib = 32 * s + 32 <= T->nibble_dims;
-      const int off = nib ? 16 * s : T->nibble_dims / 2 + 32 * s - T->nibble_dims;
-      if (h == 0) {
-        fl->nib[s] = nib;
-        fl->byte_off[s] = off;
-        fl->group[s] = g;
-        fl->book[s] = bk;
-      } else if (fl->nib[s] != nib || fl->byte_off[s] != off || fl->group[s] != g || fl->book[s] != bk) {
-        return false;
+      if (g == 0) {
+        if (g0 != s) return false;  // group 0 steps first
+        ++g0;
       }
+      if (h == 0) fl->book[s] = bk;
+      else if (fl->book[s] != bk) return false;
+    }
+    const int sgv = T->groups == 1 ? ks : g0;
+    if (h == 0) {
+      *nn = n;
+      *sg = sgv;
+    } else if (*nn != n || *sg != sgv) {
+      return false;
     }
   }
-  return true;
+  return decode_fast_supported(p.dim, 1, *nn, *sg);
 }
 
 static bgtq_status launch_decode_common(bgtq_context *ctx, DecodeParams &p, const float *q,
                                         const bgtq_tables *const *tables) {
+  p.q = q;
   FastLayout fl{};
-  if (fast_layout(p, tables, &fl)) {
-    int books = 0;
-    if (p.key_format == 1)
-      for (int h = 0; h < p.kv_heads; ++h)
-        books = std::max(books, tables[h]->info.n_books * tables[h]->info.max_centroids * 4);
-    p.lds_bytes = decode_mfma_lds_bytes(p.dim, p.key_format, books);
-    if (p.lds_bytes <= 65536) {
-      HIP_TRY(launch_rotate_q(p, q, const_cast<float *>(p.qr), ctx->stream), "rotate_q launch");
-      HIP_TRY(launch_decode_mfma(p, fl, ctx->stream), "decode launch");
-      HIP_TRY(launch_decode_tail(p, ctx->stream), "decode combine launch");
-      return BGTQ_OK;
-    }
+  int nn = 0, sg = 0;
+  if (p.counters && fast_layout(p, tables, &fl, &nn, &sg)) {
+    HIP_TRY(launch_decode_fast(p, fl, nn, sg, ctx->stream), "decode launch");
+    if (p.probs) HIP_TRY(launch_decode_probs(p, ctx->stream), "probabilities launch");
+    return BGTQ_OK;
   }
   int lds = 0;
   for (int h = 0; h < (p.key_format == 1 ? p.kv_heads : 1); ++h) {
@@ -745,7 +825,7 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) {
   int splits = 1;
   if (bgtq_status s = validate_decode(d, &splits)) return s;
   const int64_t heads = (int64_t)d->batch * d->q_heads;
-  const DecodeWorkspace w = decode_ws(heads, d->dim, splits);
+  const DecodeWorkspace w = decode_ws((int64_t)d->batch * d->kv_heads, heads, d->dim, splits);
   if (!d->workspace || d->workspace_bytes < w.total)
     return fail(BGTQ_ERR_RANGE, "workspace of %zu bytes required", w.total);
   if (bgtq_status s = ctx->use()) return s;
@@ -771,14 +851,17 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) {
   p.v_seq_stride = d->v_seq_stride;
   p.v_head_stride = d->v_head_stride;
   uint8_t *ws = static_cast<uint8_t *>(d->workspace);
+  p.counters = reinterpret_cast<uint32_t *>(ws + w.counters);
   p.qr = reinterpret_cast<float *>(ws + w.qr);
   p.part = reinterpret_cast<float *>(ws + w.part);
   p.stats = reinterpret_cast<float *>(ws + w.stats);
   p.lengths = d->lengths;
+  p.max_length = (int32_t)d->max_length;
   p.ends = nullptr;
   p.splits = splits;
   p.split_tokens = (int)((d->max_length + splits - 1) / splits);
   p.split_tokens = ((p.split_tokens + 255) / 256) * 256;
+  p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
   p.out = d->out;
   p.logits = nullptr;
   p.probs = nullptr;
@@ -797,7 +880,7 @@ bgtq_status bgtq_attention_create(bgtq_keys *k, bgtq_values *v, uint32_t max_que
   a->values = v;
   a->max_queries = max_queries;
   a->materialize = materialize ? 1 : 0;
-  a->max_splits = (uint32_t)std::max<int64_t>(1, ((int64_t)k->capacity + 255) / 256);
+  a->max_splits = (uint32_t)std::min<int64_t>(256, std::max<int64_t>(1, ((int64_t)k->capacity + 255) / 256));
   const size_t d = k->dim, Q = max_queries;
   bgtq_status s = k->ctx->use();
   struct Item {
@@ -813,6 +896,7 @@ bgtq_status bgtq_attention_create(bgtq_keys *k, bgtq_values *v, uint32_t max_que
       {&a->qr, "rotated Q", Q * d * 4},
       {&a->part, "split partials", Q * a->max_splits * (d + 2) * 4},
       {&a->stats, "softmax statistics", Q * 2 * 4},
+      {&a->counters, "split counter", 4},
   };
   for (auto &it : items) {
     if (s || !it.bytes) continue;
@@ -904,12 +988,15 @@ bgtq_status bgtq_attention_record(bgtq_attention *a) {
   p.v_dtype = v->dtype;
   p.qr = static_cast<float *>(a->qr.ptr);
   p.lengths = static_cast<const uint32_t *>(a->small.ptr);
+  p.max_length = (int32_t)T;
   p.ends = reinterpret_cast<const int32_t *>(static_cast<const uint32_t *>(a->small.ptr) + 1);
   p.splits = choose_splits(1, T, 0);
   p.splits = (int)std::min<uint32_t>((uint32_t)p.splits, a->max_splits);
   p.split_tokens = (int)(((T + p.splits - 1) / p.splits + 255) / 256 * 256);
   p.part = static_cast<float *>(a->part.ptr);
   p.stats = static_cast<float *>(a->stats.ptr);
+  p.counters = static_cast<uint32_t *>(a->counters.ptr);
+  p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)k->dim));
   p.out = static_cast<float *>(a->out.ptr);
   if (a->materialize) {
     p.logits = static_cast<float *>(a->logits.ptr);

@@ -17,7 +17,7 @@ constexpr int kEncodeJobsPerLaunch = 24;
 struct DevTables {
   int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids, n_books, n_codebooks;
   int32_t gstart[kMaxGroups], gend[kMaxGroups], gsize[kMaxGroups];  // group ranges (head-perm order)
-  uint32_t off_lut, off_books, off_rot, total_bytes;
+  uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, total_bytes;
   int32_t cent_exp;  // 2^cent_exp * max|centroid| <= 2^14: fp16 hi/lo split range for MFMA operands
   uint8_t perm[kMaxDim];      // head_perm
   uint8_t group_of[kMaxDim];
@@ -28,7 +28,14 @@ struct DevTables {
   // [off_lut]   uint8 code_lut[n_codebooks*256]
   // [off_books] float books[n_books*max_centroids]
   // [off_rot]   float rotation[dim*dim], y_j = sum_i x_i R[j*dim+i]
+  // [off_rot_t] float rotation transposed, Rt[i*dim+j] = R[j*dim+i]
+  // [off_mfma]  per book, kMfmaTableBytes: the fp16 (hi, lo) split of
+  //             centroid * 2^cent_exp as MFMA lookup tables,
+  //             uint32 pair_hi[256], pair_lo[256]  (entry = packed nibble byte:
+  //                                                 low nibble in the low half)
+  //             uint16 code_hi[256], code_lo[256]  (entry = byte code)
 };
+constexpr int kMfmaTableBytes = 3072;
 
 __host__ __device__ inline const uint8_t *tables_lut(const DevTables *t) {
   return reinterpret_cast<const uint8_t *>(t) + t->off_lut;
@@ -38,6 +45,12 @@ __host__ __device__ inline const float *tables_books(const DevTables *t) {
 }
 __host__ __device__ inline const float *tables_rot(const DevTables *t) {
   return reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(t) + t->off_rot);
+}
+__host__ __device__ inline const float *tables_rot_t(const DevTables *t) {
+  return reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(t) + t->off_rot_t);
+}
+__host__ __device__ inline const uint8_t *tables_mfma(const DevTables *t) {
+  return reinterpret_cast<const uint8_t *>(t) + t->off_mfma;
 }
 
 struct EncodeJobDev {
@@ -71,10 +84,14 @@ struct DecodeParams {
   const void *v;
   int32_t v_dtype;  // 0 = FP32, 1 = FP16
   int64_t v_seq_stride, v_head_stride;  // elements
+  const float *q;         // [B*Hq*dim] queries
   const float *qr;        // [B*Hq*dim] rotated, permuted, scaled by 1/sqrt(dim)
-  const uint32_t *lengths;  // [B]
+  const uint32_t *lengths;  // [B]; kernels clamp them to max_length
+  int32_t max_length;       // tokens every K/V buffer holds per (sequence, KV head)
   const int32_t *ends;      // optional [B*Hq] exclusive causal ends
   int32_t splits, split_tokens;
+  float inv_sqrt_d;
+  uint32_t *counters;  // [B*Hkv] split arrival counters: zero between launches
   float *part;    // [B*Hq*splits*(dim+2)] (m, l, o[dim])
   float *stats;   // [B*Hq*2] final (m, l)
   float *out;     // [B*Hq*dim]
@@ -84,14 +101,15 @@ struct DecodeParams {
   int32_t lds_bytes;  // dynamic LDS of the split kernel
 };
 
-// Structure of a layout the MFMA decode path handles: every 32-dim K-step of
-// the head-perm order lies in one group and one centroid book and is either
-// all nibble codes or all byte codes; rows are 8-byte aligned; norm_stride 2.
+// Structure of a layout the fused matrix-core decode handles: every 32-dim
+// K-step of the head-perm order lies in one group and one centroid book and is
+// either all nibble codes or all byte codes (nibble steps first); at most two
+// groups (norm_stride 2), group 0 first; rows 8-byte aligned.
 struct FastLayout {
-  int32_t nib[4], byte_off[4], group[4], book[4];
+  int32_t book[4];  // centroid book of each K-step
 };
 
-// Launchers (kernels live in encode.hip / decode.hip / decode_mfma.hip).
+// Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).
 hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
                          hipStream_t stream);
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
@@ -99,8 +117,13 @@ int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_by
 hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream);
 // LSE merge of split partials and the optional probabilities pass.
 hipError_t launch_decode_tail(const DecodeParams &p, hipStream_t stream);
-hipError_t launch_decode_mfma(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
-int decode_mfma_lds_bytes(int dim, int key_format, int books_bytes);
+// Materialised probabilities exp(logit - m)/l from the final statistics.
+hipError_t launch_decode_probs(const DecodeParams &p, hipStream_t stream);
+// Fused decode (decode_fast.hip): nn leading nibble K-steps, sg K-steps in group 0.
+bool decode_fast_supported(int dim, int key_format, int nn, int sg);
+// Row bytes of the packed layout with nn leading nibble K-steps (no padding).
+int decode_fast_row_bytes(int dim, int nn);
+hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
 hipError_t launch_reconstruct(const DevTables *t, const uint8_t *packed, const uint16_t *norms,
                               int64_t rows, float *out, hipStream_t stream);
 hipError_t launch_half_convert(const float *src, uint16_t *dst, int64_t n, hipStream_t stream);

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) 
   const int d = p.dim, G = p.G, Hq = p.q_heads;
   const int hq0 = kv * G;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int T_b = (int)p.lengths[b];
+  const int T_b = (int)min(p.lengths[b], (uint32_t)p.max_length);
   const int t_begin = split * p.split_tokens;
   const int t_end = min(T_b, t_begin + p.split_tokens);
 
@@ -299,7 +299,7 @@ __global__ void combine_kernel(DecodeParams p) {
 __global__ void probs_kernel(DecodeParams p) {
   const int64_t head = blockIdx.y;
   const int b = (int)(head / p.q_heads);
-  const int T_b = (int)p.lengths[b];
+  const int T_b = (int)min(p.lengths[b], (uint32_t)p.max_length);
   const float M = p.stats[head * 2], Lsum = p.stats[head * 2 + 1];
   for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < T_b; t += gridDim.x * blockDim.x) {
     const float lg = p.logits[head * p.logit_stride + t];
@@ -330,6 +330,11 @@ int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_by
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream) {
   const float inv = (float)(1.0 / __builtin_sqrt((double)p.dim));
   hipLaunchKernelGGL(rotate_q_kernel, dim3((unsigned)(p.batch * p.q_heads)), dim3(128), 0, stream, p, q, qr, inv);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_probs(const DecodeParams &p, hipStream_t stream) {
+  hipLaunchKernelGGL(probs_kernel, dim3(16, (unsigned)(p.batch * p.q_heads)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -1,0 +1,639 @@
+// Fused single-launch decode attention for gfx950 on the matrix cores.
+//
+// One workgroup (4 waves) per (sequence, KV head, token split). Everything a
+// decode step of one layer needs happens in this one launch:
+//   prologue  the KV head's G query rows are rotated into the code domain
+//             (qr = R q[perm] / sqrt(d), a dense d x d product whose
+//             off-group entries are exact zeros) and split into fp16 hi/lo
+//             MFMA operands; the centroid books are expanded into LDS lookup
+//             tables of fp16 (hi, lo) pairs: for nibble K-steps one entry per
+//             packed byte (two dims), for byte K-steps one entry per code.
+//   main loop each wave streams 32-token chunks of packed codes, FP16 scales
+//             and FP16 V straight from HBM into a three-deep ring of LDS
+//             buffers with buffer_load ... lds (no VGPR staging), two chunks
+//             ahead of the one it computes on. Reads past the sequence's
+//             length return zeros, so the tail needs no clamping. From LDS it
+//             rebuilds the K operand through the tables, runs QK as 16x16x32
+//             f16 MFMAs (hi*hi + lo*hi + hi*lo, FP32-level logits), an online
+//             softmax in the log2 domain, and PV as MFMAs with the V operand
+//             read transposed by ds_read_b64_tr_b16. V rows (and FP16 K rows)
+//             land in LDS with their 16-byte pieces XOR-swizzled by row, so
+//             the transposed and row reads are free of bank conflicts.
+//   epilogue  the four waves merge in LDS; with several splits each
+//             workgroup stores an (m, l, o) partial and the last workgroup of
+//             its (sequence, KV head) to arrive (a device-scope counter)
+//             merges them by log-sum-exp and resets the counter to zero.
+//
+// The arithmetic is that of src/reference/attention.py:5-22 on the
+// reconstructed K of src/reference/production_math.py:27-31: with
+// k = ((c*s) @ R)[inv_perm], q.k = sum_g s_g sum_{j in g} c_j[code_j] (R q[perm])_j.
+// The reference computes the same product as an on-chip group rebuild
+// (src/model/compressed-dot.wgsl:14-31) followed by separate softmax and
+// weighted passes (src/model/attention.wgsl:24-39).
+#include <hip/hip_fp16.h>
+
+#include "bgtq_internal.h"
+
+namespace bgtq {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef fp16x4 __attribute__((address_space(3))) lds_fp16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kChunk = 32;  // tokens per wave iteration: two 16-token MFMA tiles
+constexpr int kRing = 3;    // LDS chunk buffers per wave: compute one, the others in flight
+constexpr int kLdsLimit = 160 * 1024;  // LDS of one gfx950 CU
+constexpr bool kInterleaved = true;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kPScale = 32768.0f;  // P is carried as p * 2^15 so its fp16 lo part stays normal
+// Buffer resource word 3 on gfx9: 32-bit dword data format, raw (unswizzled) addressing.
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+// HBM -> LDS without VGPRs: lane i writes 16 (4) bytes at lds + 16 i (4 i).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, (int)voff, (int)soff, 0, 0);
+}
+
+// Reductions over the four 16-lane rows that share a column (lane % 16).
+__device__ __forceinline__ float col_max(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_sum(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// x = hi + lo with both halves fp16 (hi rounded toward zero, so lo is exact
+// before its own rounding): ~2^-22 relative.
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t &hi, uint32_t &lo) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+  const float r0 = x0 - (float)h[0], r1 = x1 - (float)h[1];
+  const auto l = __builtin_amdgcn_cvt_pkrtz(r0, r1);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// Relaxed atomics at device scope: on gfx950 they go to the device-coherent
+// level (system-coherent bit) instead of this XCD's L2.
+__device__ __forceinline__ void coherent_store(float *ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(float *ptr) {
+  return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits for all but the newest N vector-memory operations of this wave. The
+// LDS writes of buffer_load ... lds are not tracked by the compiler, so the
+// ring's waits are explicit; the memory clobber keeps LDS reads below them.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <int D>
+struct Geo {
+  static constexpr int KS = D / 32;  // K-steps of QK
+  static constexpr int DT = D / 16;  // 16-dim tiles of PV
+  static constexpr int PR = D / 8;   // 16-byte pieces per FP16 row
+  static constexpr int VBYTES = kChunk * D * 2;
+  static constexpr int VI = VBYTES / 1024;  // 16-byte DMA instructions per V chunk
+};
+// 16-byte piece swizzle of an FP16 row in LDS (conflict-free column and row reads).
+template <int D>
+__host__ __device__ constexpr int swz(int row) {
+  return D == 64 ? (row >> 1) & 7 : row & 15;
+}
+
+// One ring buffer: V chunk, K chunk, FP16 scales (32 x 4 bytes), packed tight
+// so two workgroups of the layout-B d=64 kernel fit one CU's 160 KB.
+template <int D, int KF, int NN>
+struct Slot {
+  static constexpr int KS = D / 32;
+  static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : 2 * D;  // K row bytes
+  static constexpr int KBYTES = kChunk * RB;
+  static constexpr int KI = (KBYTES + 1023) / 1024;              // 16-byte DMA instructions per K chunk
+  static constexpr int KLAST = (KBYTES - (KI - 1) * 1024) / 16;  // lanes of the last one
+  static constexpr int NBYTES = KF == 1 ? kChunk * 4 : 0;
+  static constexpr int BYTES = Geo<D>::VBYTES + KBYTES + NBYTES;
+  static constexpr int L = Geo<D>::VI + KI + (KF == 1 ? 1 : 0);  // DMA instructions per chunk
+  static constexpr int TABLES = KF == 1 ? KS * 2048 : 0;
+  // Three buffers per wave where they fit the CU, else two (FP16 K at d=128).
+  static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
+  static constexpr int AHEAD = RING - 1;
+  static constexpr int LDS = RING * kWaves * BYTES + TABLES;
+  static_assert(LDS <= kLdsLimit, "LDS of one workgroup");
+  static_assert(AHEAD >= 1 && AHEAD <= 3, "ring waits cover up to three chunks in flight");
+};
+
+// KF: 1 = packed codes, 0 = FP16 K rows. NN: leading nibble K-steps.
+// SG: K-steps in group 0 (== KS: one scale per token).
+template <int D, int KF, int NN, int SG>
+__global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
+  using Gm = Geo<D>;
+  using Sl = Slot<D, KF, NN>;
+  constexpr int KS = Gm::KS, DT = Gm::DT, PR = Gm::PR, VI = Gm::VI;
+  constexpr int RB = Sl::RB, KI = Sl::KI, L = Sl::L, AHEAD = Sl::AHEAD;
+  static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
+  static_assert(kWaves * Sl::BYTES >= 5 * 16 * D * 4, "q staging fits one ring slot of all waves");
+  static_assert(Sl::RING * kWaves * Sl::BYTES >= kWaves * 16 * (D + 2) * 4, "wave merge fits the ring");
+  static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int unit = blockIdx.y, split = blockIdx.x;
+  const int b = unit / p.kv_heads, kv = unit - b * p.kv_heads;
+  const int G = p.G, Hq = p.q_heads, hq0 = kv * G;
+  const int tid = threadIdx.x, lane = tid & 63, gq = lane >> 4, col = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
+  const int T_b = (int)min(p.lengths[b], (uint32_t)p.max_length);
+  // Splits of one (sequence, KV head) interleave at chunk granularity: wave w
+  // of split s takes chunks (s * 4 + w) + 4 S i, so the waves working on a
+  // sequence at any moment sweep adjacent memory.
+  const int t_end = kInterleaved ? T_b : min(T_b, split * p.split_tokens + p.split_tokens);
+  const int stride = kInterleaved ? p.splits * kWaves * kChunk : kWaves * kChunk;
+  const DevTables *T = KF == 1 ? p.tables[kv] : nullptr;
+  uint8_t *tabs = smem + Sl::RING * kWaves * Sl::BYTES;
+  auto slot_base = [&](int s) { return smem + (s * kWaves + wave) * Sl::BYTES; };
+
+  // ---------------- streams of this (sequence, KV head) ----------------
+  // Each chunk's loads use buffer descriptors based at the chunk's first token
+  // and sized to the rest of the sequence: the hardware range check (which
+  // covers the per-lane offset) returns zeros for tokens past the length.
+  const _Float16 *v_base = static_cast<const _Float16 *>(p.v) + b * p.v_seq_stride + kv * p.v_head_stride;
+  const uint8_t *k_base = KF == 1 ? p.packed + b * p.packed_seq_stride + kv * p.packed_head_stride
+                                  : reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(p.k) +
+                                                                      b * p.k_seq_stride + kv * p.k_head_stride);
+  const uint16_t *n_base = KF == 1 ? p.norms + b * p.norms_seq_stride + kv * p.norms_head_stride : nullptr;
+  // Per-lane source offsets of the swizzled FP16 row pieces: DMA instruction k,
+  // lane i fills LDS piece 64k + i = (row r, slot c) with global piece c ^ swz(r).
+  uint32_t voff_rows[VI];
+#pragma unroll
+  for (int k = 0; k < VI; ++k) {
+    const int P = 64 * k + lane, r = P / PR, c = P % PR;
+    voff_rows[k] = r * (2 * D) + ((c ^ swz<D>(r)) * 16);
+  }
+  // This wave's chunks start at first + 128 i.
+  const int first = kInterleaved ? (split * kWaves + wave) * kChunk : split * p.split_tokens + wave * kChunk;
+  const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
+  auto issue = [&](int i) {
+    const int c0 = first + i * stride;
+    const uint32_t rest = (uint32_t)(T_b - c0);  // > 0: c0 < t_end <= T_b
+    uint8_t *sb = slot_base(i % Sl::RING);
+    const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
+#pragma unroll
+    for (int k = 0; k < VI; ++k) dma16(rV, sb + k * 1024, voff_rows[k], 0);
+    uint8_t *kb = sb + Gm::VBYTES;
+    if (KF == 1) {
+      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * RB, rest * RB);
+      const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * 2, rest * 4);
+#pragma unroll
+      for (int k = 0; k < KI; ++k) {
+        if (k + 1 < KI || Sl::KLAST == 64 || lane < Sl::KLAST) dma16(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+      }
+      if (lane < kChunk) dma4(rN, kb + Sl::KBYTES, lane * 4, 0);
+    } else {
+      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
+#pragma unroll
+      for (int k = 0; k < KI; ++k) dma16(rK, kb + k * 1024, voff_rows[k], 0);
+    }
+  };
+  // The first AHEAD chunks stream in while the prologue runs; the last ring
+  // slot holds the prologue's q staging.
+#pragma unroll
+  for (int i = 0; i < AHEAD; ++i)
+    if (i < n_chunks) issue(i);
+
+  // ---------------- prologue ----------------
+  // One round trip: the MFMA lookup tables of the K-steps' books and the G
+  // query rows go HBM -> LDS by DMA (query rows past G read as zeros), the
+  // wave's quarter of the transposed rotation goes to registers.
+  float *q_raw = reinterpret_cast<float *>(smem + (Sl::RING - 1) * kWaves * Sl::BYTES);  // [16][D]
+  float *q_part = q_raw + 16 * D;                                                     // [4][16][D]
+  if (KF == 1 && wave == 0) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint8_t *src = tables_mfma(T) + fl.book[s] * kMfmaTableBytes + (s < NN ? 0 : 2048);
+      const __amdgpu_buffer_rsrc_t rt = rsrc(src, s < NN ? 2048 : 1024);
+      dma16(rt, tabs + s * 2048, lane * 16, 0);
+      if (s < NN) dma16(rt, tabs + s * 2048 + 1024, 1024 + lane * 16, 0);
+    }
+  }
+  if (wave == kWaves - 1) {
+    const __amdgpu_buffer_rsrc_t rq = rsrc(p.q + ((int64_t)b * Hq + hq0) * D, (uint32_t)(G * D * 4));
+#pragma unroll
+    for (int k = 0; k < 16 * D * 4 / 1024; ++k) dma16(rq, reinterpret_cast<uint8_t *>(q_raw) + k * 1024, k * 1024 + lane * 16, 0);
+  }
+  constexpr int IQ = D / kWaves;  // rotation rows i of this wave: wave * IQ + ii
+  constexpr int JL = D / 64;      // output dims j of this lane: lane + 64 jl
+  float rt[KF == 1 ? IQ * JL : 1];
+  int src_i[KF == 1 ? IQ : 1];
+  if (KF == 1) {
+    const float *Rt = tables_rot_t(T);  // Rt[i*D + j] = R[j][i]
+#pragma unroll
+    for (int ii = 0; ii < IQ; ++ii) {
+      src_i[ii] = T->perm[wave * IQ + ii];
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl) rt[ii * JL + jl] = Rt[(wave * IQ + ii) * D + lane + 64 * jl];
+    }
+  }
+  const int ec = KF == 1 ? T->cent_exp : 0;
+  wait_vm<0>();
+  __syncthreads();
+  // qr[h][j] = sum_i R[j][i] q[h][perm[i]]: wave w sums i in its quarter
+  // (off-group entries of R are exact zeros).
+#pragma unroll
+  for (int jl = 0; jl < JL; ++jl) {
+    const int jj = lane + 64 * jl;
+    float acc[16];
+#pragma unroll
+    for (int h = 0; h < 16; ++h) acc[h] = 0.0f;
+    if (KF == 1) {
+#pragma unroll
+      for (int ii = 0; ii < IQ; ++ii)
+#pragma unroll
+        for (int h = 0; h < 16; ++h) acc[h] = __builtin_fmaf(rt[ii * JL + jl], q_raw[h * D + src_i[ii]], acc[h]);
+    } else if (wave == 0) {
+#pragma unroll
+      for (int h = 0; h < 16; ++h) acc[h] = q_raw[h * D + jj];
+    }
+#pragma unroll
+    for (int h = 0; h < 16; ++h) q_part[(wave * 16 + h) * D + jj] = acc[h];
+  }
+  __syncthreads();
+  // B operand of QK: lane holds qr[head = col][32 s + 8 gq + 0..7], split hi/lo
+  // after scaling the head's row so its largest entry is near 2^14.
+  const bool head_ok = col < G;
+  half8 qhi[KS], qlo[KS];
+  float kq;  // log2-domain logit = (sum_g s_g acc_g) * kq
+  {
+    float qv[KS][8];
+    float qmax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int jv = 0; jv < 8; ++jv) {
+        const int jj = 32 * s + 8 * gq + jv;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) v += q_part[(w * 16 + col) * D + jj];
+        v = head_ok ? v * p.inv_sqrt_d : 0.0f;
+        qv[s][jv] = v;
+        qmax = fmaxf(qmax, fabsf(v));
+      }
+    qmax = col_max(qmax);
+    const int eq = qmax > 0.0f ? 14 - (int)ceilf(__builtin_log2f(qmax)) : 0;
+    const float qsc = __builtin_ldexpf(1.0f, eq);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int jv = 0; jv < 8; ++jv) {
+        const float x = qv[s][jv] * qsc;
+        qhi[s][jv] = (_Float16)x;
+        qlo[s][jv] = (_Float16)(x - (float)qhi[s][jv]);
+      }
+    kq = __builtin_ldexpf(kLog2e, -(eq + ec));
+  }
+  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)b * Hq + hq0 + col], T_b) : T_b) : 0;
+  const int lim = min(end_h, t_end);
+  // Wave-uniform: chunks reaching past lim_min need the per-head mask.
+  int lim_min = head_ok ? lim : t_end;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o, 64));
+  __syncthreads();  // q staging (last ring slot) is dead
+
+  const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
+  const _Float16 *tb = reinterpret_cast<const _Float16 *>(tabs);
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4 O[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) O[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // Lane-constant parts of the transposed V reads.
+  const int trow = 4 * gq + (col >> 2);
+  const int tpiece = (col & 3) >> 1, thalf = (col & 1) * 8;
+
+  for (int i = 0; i < n_chunks; ++i) {
+    const int c0 = first + i * stride;
+    // Refill the buffer computed on last iteration with chunk i + AHEAD, then
+    // wait for chunk i: its DMA is older than the (up to AHEAD) chunks issued
+    // after it. With materialised logits the loop also stores, so wait for all.
+    if (i + AHEAD < n_chunks) {
+      wait_lds();
+      issue(i + AHEAD);
+    }
+    const int newer = p.logits ? 0 : min(n_chunks - 1 - i, AHEAD);
+    if (newer == AHEAD) wait_vm<AHEAD * L>();
+    else if (AHEAD > 2 && newer == 2) wait_vm<2 * L>();
+    else if (newer >= 1) wait_vm<L>();
+    else wait_vm<0>();
+    const uint8_t *sb = slot_base(i % Sl::RING);
+    const uint8_t *kbuf = sb + Gm::VBYTES;
+
+    // QK: acc[u][g] = sum over the K-steps of group g.
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      acc[u][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const int t = 16 * u + col;  // A-operand row (token) of this lane
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int g = s < SG ? 0 : 1;
+        if (KF == 1) {
+          u32x4 hi, lo;
+          if (s < NN) {
+            const uint32_t w = *reinterpret_cast<const uint32_t *>(kbuf + t * RB + 16 * s + 4 * gq);
+            const uint32_t *t32 = tn + s * 512;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const uint32_t e = (w >> (8 * k)) & 255u;
+              hi[k] = t32[e];
+              lo[k] = t32[256 + e];
+            }
+          } else {
+            const u32x2 w = *reinterpret_cast<const u32x2 *>(kbuf + t * RB + 16 * NN + 32 * (s - NN) + 8 * gq);
+            const _Float16 *t16 = tb + s * 1024;
+            half8 h8, l8;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const uint32_t e = (w[k >> 2] >> (8 * (k & 3))) & 255u;
+              h8[k] = t16[e];
+              l8[k] = t16[256 + e];
+            }
+            hi = __builtin_bit_cast(u32x4, h8);
+            lo = __builtin_bit_cast(u32x4, l8);
+          }
+          const half8 ah = __builtin_bit_cast(half8, hi), al = __builtin_bit_cast(half8, lo);
+          acc[u][g] = mfma(ah, qhi[s], acc[u][g]);
+          acc[u][g] = mfma(al, qhi[s], acc[u][g]);
+          acc[u][g] = mfma(ah, qlo[s], acc[u][g]);
+        } else {
+          const int piece = 4 * s + gq;
+          const half8 a = *reinterpret_cast<const half8 *>(kbuf + t * (2 * D) + ((piece ^ swz<D>(t)) * 16));
+          acc[u][0] = mfma(a, qhi[s], acc[u][0]);
+          acc[u][0] = mfma(a, qlo[s], acc[u][0]);
+        }
+      }
+    }
+    // logits of this lane: head col, tokens c0 + 16u + 4gq + r
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u32x4 nr{0u, 0u, 0u, 0u};
+      if (KF == 1) nr = *reinterpret_cast<const u32x4 *>(kbuf + Sl::KBYTES + (16 * u + 4 * gq) * 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v;
+        if (KF == 1) {
+          const uint32_t w = nr[r];
+          const float s0 = __half2float(__ushort_as_half((uint16_t)(w & 0xffffu)));
+          if (SG < KS) {
+            const float s1 = __half2float(__ushort_as_half((uint16_t)(w >> 16)));
+            v = __builtin_fmaf(s1, acc[u][1][r], s0 * acc[u][0][r]);
+          } else {
+            v = s0 * acc[u][0][r];
+          }
+        } else {
+          v = acc[u][0][r];
+        }
+        x[4 * u + r] = v * kq;
+      }
+    }
+    if (c0 + kChunk > lim_min) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
+        x[j] = tok < lim ? x[j] : -INFINITY;
+      }
+    }
+    if (p.logits) {  // materialised logits for inspect() (natural units)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
+        if (head_ok && tok < t_end) p.logits[((int64_t)b * Hq + hq0 + col) * p.logit_stride + tok] = x[j] * kLn2;
+      }
+    }
+    // online softmax (log2 domain) for head col
+    float mloc = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    const float m_new = fmaxf(m_run, col_max(mloc));
+    const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    const float mb = (m_new == -INFINITY ? 0.0f : m_new) - 15.0f;
+    float pr[8], psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] = __builtin_amdgcn_exp2f(x[j] - mb);
+      psum += pr[j];
+    }
+    l_run = __builtin_fmaf(l_run, alpha, psum);
+    m_run = m_new;
+    u32x4 ph, pl;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t h, l;
+      split2(pr[2 * k], pr[2 * k + 1], h, l);
+      ph[k] = h;
+      pl[k] = l;
+    }
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * gq + r, 64);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) O[dt][r] *= ar;
+      }
+    }
+    // PV: B operand = V[tokens of this lane's P slots][16 dt + col], read transposed.
+    const half8 pha = __builtin_bit_cast(half8, ph), pla = __builtin_bit_cast(half8, pl);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int piece = 2 * dt + tpiece;
+      const fp16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+          (lds_fp16x4 *)(sb + trow * (2 * D) + ((piece ^ swz<D>(trow)) * 16) + thalf));
+      const fp16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+          (lds_fp16x4 *)(sb + (16 + trow) * (2 * D) + ((piece ^ swz<D>(16 + trow)) * 16) + thalf));
+      const u32x2 a0 = __builtin_bit_cast(u32x2, v0), a1 = __builtin_bit_cast(u32x2, v1);
+      const half8 vb = __builtin_bit_cast(half8, u32x4{a0[0], a0[1], a1[0], a1[1]});
+      O[dt] = mfma(pha, vb, O[dt]);
+      O[dt] = mfma(pla, vb, O[dt]);
+    }
+  }
+
+  // ---------------- epilogue ----------------
+  const float l_tot = col_sum(l_run) * (1.0f / kPScale);
+  __syncthreads();  // every wave is done with the ring
+  float *comb = reinterpret_cast<float *>(smem);  // [wave][16 heads][2 + D]
+  if (gq == 0) {
+    comb[(wave * 16 + col) * (D + 2)] = m_run;
+    comb[(wave * 16 + col) * (D + 2) + 1] = l_tot;
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      comb[(wave * 16 + 4 * gq + r) * (D + 2) + 2 + 16 * dt + col] = O[dt][r] * (1.0f / kPScale);
+  __syncthreads();
+  const int S = p.splits;
+  for (int e = tid; e < G * D; e += kThreads) {
+    const int g = e / D, dm = e - g * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[(w * 16 + g) * (D + 2)]);
+    float Lsum = 0.0f, Ov = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float *c = comb + (w * 16 + g) * (D + 2);
+        if (c[0] == -INFINITY) continue;
+        const float wt = exp2f(c[0] - M);
+        Lsum = __builtin_fmaf(c[1], wt, Lsum);
+        Ov = __builtin_fmaf(c[2 + dm], wt, Ov);
+      }
+    }
+    const int64_t head = (int64_t)b * Hq + hq0 + g;
+    if (S == 1) {
+      p.out[head * D + dm] = Ov / Lsum;
+      if (dm == 0 && p.stats) {
+        p.stats[head * 2] = M * kLn2;
+        p.stats[head * 2 + 1] = Lsum;
+      }
+    } else {
+      // Device-coherent (write-through) stores: the merging workgroup may run
+      // on another XCD, whose L2 does not see this one's.
+      float *pp = p.part + (head * S + split) * (D + 2);
+      coherent_store(pp + 2 + dm, Ov);
+      if (dm == 0) {
+        coherent_store(pp, M);
+        coherent_store(pp + 1, Lsum);
+      }
+    }
+  }
+  if (S == 1) return;
+  // Last workgroup of this (sequence, KV head) to finish merges the splits.
+  // Every thread waits for its partial stores to complete before the arrival
+  // is counted, so no cache write-back is needed.
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (unsigned)(S - 1);
+  __syncthreads();
+  if (!last) return;
+  // Merge with every load of a stage in flight at once: (m, l) of all heads
+  // and splits, then per-head normalised weights, then the o rows in groups
+  // of eight splits.
+  float *wgt = reinterpret_cast<float *>(smem);  // [16 heads][S] (reuses the ring)
+  float *mrow = wgt + 16 * S;                     // [16 heads][S] split maxima
+  for (int e = tid; e < G * S; e += kThreads) {
+    const int g = e / S, s = e - g * S;
+    float *pp = p.part + (((int64_t)b * Hq + hq0 + g) * S + s) * (D + 2);
+    mrow[g * S + s] = coherent_load(pp);
+    wgt[g * S + s] = coherent_load(pp + 1);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, mrow[tid * S + s]);
+    float Lsum = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float m = mrow[tid * S + s];
+      const float w = m == -INFINITY ? 0.0f : exp2f(m - M);
+      Lsum = __builtin_fmaf(wgt[tid * S + s], w, Lsum);
+      mrow[tid * S + s] = w;
+    }
+    for (int s = 0; s < S; ++s) wgt[tid * S + s] = mrow[tid * S + s] / Lsum;
+    if (p.stats) {
+      const int64_t head = (int64_t)b * Hq + hq0 + tid;
+      p.stats[head * 2] = M * kLn2;
+      p.stats[head * 2 + 1] = Lsum;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < G * D; e += kThreads) {
+    const int g = e / D, dm = e - g * D;
+    const int64_t head = (int64_t)b * Hq + hq0 + g;
+    float *pp = p.part + head * S * (D + 2) + 2 + dm;
+    float Ov = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += 8) {
+      float o[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] = s0 + k < S ? coherent_load(pp + (s0 + k) * (D + 2)) : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (s0 + k < S) Ov = __builtin_fmaf(o[k], wgt[g * S + s0 + k], Ov);
+    }
+    p.out[head * D + dm] = Ov;
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int KF, int NN, int SG>
+hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
+  // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
+  static const hipError_t allowed = hipFuncSetAttribute(
+      (const void *)decode_fast_kernel<D, KF, NN, SG>, hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN>::LDS);
+  if (allowed != hipSuccess) {
+    (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
+    return allowed;
+  }
+  constexpr int lds = Slot<D, KF, NN>::LDS;
+  dim3 grid((unsigned)p.splits, (unsigned)(p.batch * p.kv_heads));
+  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG>), grid, dim3(kThreads), lds, stream, p, fl);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int decode_fast_row_bytes(int dim, int nn) { return nn * 16 + (dim / 32 - nn) * 32; }
+
+bool decode_fast_supported(int dim, int key_format, int nn, int sg) {
+  if (dim != 64 && dim != 128) return false;
+  if (key_format == 0) return true;
+  const int ks = dim / 32, h = ks / 2;
+  return (nn == h && sg == h) || (nn == ks && sg == ks) || (nn == 0 && sg == ks) || (nn == ks && sg == h) ||
+         (nn == 0 && sg == h);
+}
+
+hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
+  const int D = p.dim;
+  if (p.key_format == 0) return D == 64 ? launch_one<64, 0, 0, 2>(p, fl, stream) : launch_one<128, 0, 0, 4>(p, fl, stream);
+#define BGTQ_FAST(DD, N, S) \
+  if (D == DD && nn == N && sg == S) return launch_one<DD, 1, N, S>(p, fl, stream);
+  BGTQ_FAST(64, 1, 1)
+  BGTQ_FAST(64, 2, 2)
+  BGTQ_FAST(64, 0, 2)
+  BGTQ_FAST(64, 2, 1)
+  BGTQ_FAST(64, 0, 1)
+  BGTQ_FAST(128, 2, 2)
+  BGTQ_FAST(128, 4, 4)
+  BGTQ_FAST(128, 0, 4)
+  BGTQ_FAST(128, 4, 2)
+  BGTQ_FAST(128, 0, 2)
+#undef BGTQ_FAST
+  return hipErrorInvalidValue;
+}
+
+}  // namespace bgtq

@@ -176,7 +176,10 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
  *   v/k   [b*seq_stride        + kv*head_stride        + t*dim]
  *   q, out: [B, Hq, dim] FP32 contiguous; lengths: device uint32 [B] (tokens
  *   attended per sequence, 1..max_length). workspace: device memory of at
- *   least bgtq_decode_workspace_size() bytes. */
+ *   least bgtq_decode_workspace_size() bytes, zero-filled by the caller
+ *   before its first use (it holds per-(sequence, KV head) split counters
+ *   that every call leaves at zero again); calls sharing a workspace must be
+ *   ordered on one stream. */
 typedef struct {
   int32_t batch, q_heads, kv_heads, dim;
   int32_t key_format;

@@ -62,7 +62,7 @@ def _run(device, oracle, *, params, batch, hq, hkv, dim, lengths, cap, key_forma
     desc = batched.decode_desc(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=qd, out=out, lengths=ld,
                                max_length=max(lengths), v=vd, v_seq_stride=vd.stride(0), v_head_stride=vd.stride(1),
                                splits=splits, **kw)
-    ws = torch.empty(batched.workspace_bytes(desc), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(batched.workspace_bytes(desc), dtype=torch.uint8, device="cuda")
     desc = batched.decode_desc(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=qd, out=out, lengths=ld,
                                max_length=max(lengths), v=vd, v_seq_stride=vd.stride(0), v_head_stride=vd.stride(1),
                                splits=splits, workspace=ws, **kw)
@@ -185,3 +185,57 @@ def test_optimized_attention_fp16_values_mfma(device, oracle):
         att.destroy()
         values.destroy()
         keys.destroy()
+
+
+def test_graph_replays_match_eager(device, oracle):
+    """The decode captured in a HIP graph: every replay, with eager work between
+    replays, equals the eager result (the split counters reset in-kernel, no
+    memset nodes)."""
+    import torch
+    import bgtq
+    from bgtq import batched, calibrate
+    p = calibrate.layout_b(64)
+    batch, hq, hkv, dim, T = 2, 14, 2, 64, 3000
+    g = torch.Generator().manual_seed(21)
+    k = torch.randn((batch, hkv, T, dim), generator=g).half().cuda()
+    v = torch.randn((batch, hkv, T, dim), generator=g).half().cuda()
+    q = torch.randn((batch, hq, dim), generator=g).cuda()
+    tabs = [bgtq.Tables(device, p) for _ in range(hkv)]
+    packed = torch.zeros((batch, hkv, T * p.rowBytes + 64), dtype=torch.uint8, device="cuda")
+    norms = torch.zeros((batch, hkv, T * p.normStride + 32), dtype=torch.int16, device="cuda")
+    batched.bind_torch_stream(device)
+    batched.encode(device, [dict(tables=tabs[h], src=k[b, h], src_row_stride=dim, rows=T, packed=packed[b, h],
+                                 norms=norms[b, h]) for b in range(batch) for h in range(hkv)], "f16")
+    out = torch.empty((batch, hq, dim), device="cuda")
+    lengths = torch.tensor([T, T - 123], dtype=torch.int32, device="cuda")
+    args = dict(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=q, out=out, lengths=lengths, max_length=T, v=v,
+                v_seq_stride=v.stride(0), v_head_stride=v.stride(1), tables=tabs, packed=packed,
+                packed_seq_stride=packed.stride(0), packed_head_stride=packed.stride(1), norms=norms,
+                norms_seq_stride=norms.stride(0), norms_head_stride=norms.stride(1), splits=5)
+    ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8, device="cuda")
+    desc = batched.decode_desc(workspace=ws, **args)
+    batched.decode(device, desc)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        batched.bind_torch_stream(device)
+        batched.decode(device, desc)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        batched.bind_torch_stream(device)
+        batched.decode(device, desc)
+    batched.bind_torch_stream(device)
+    for rep in range(4):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from the eager result"
+        batched.decode(device, desc)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    for t in tabs:
+        t.destroy()
