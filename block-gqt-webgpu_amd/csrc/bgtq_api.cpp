@@ -639,6 +639,24 @@ void bgtq_values_destroy(bgtq_values *v) {
   delete v;
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Up to this many rows per launch the wave-per-row encoder (short latency per
+// row) runs; larger launches use the thread-per-row encoder (more rows per
+// instruction).
+constexpr int64_t kEncodeWaveMaxRows = 16384;
+
 // ---------------------------------------------------------------- batched entry points
 bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq_encode_job *jobs, size_t n_jobs) {
   if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
@@ -662,7 +680,8 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
     const std::vector<size_t> &idx = kv.second;
     for (size_t b = 0; b < idx.size(); b += kEncodeJobsPerLaunch) {
       EncodeLaunch L{};
-      int64_t max_rows = 0;
+      int64_t max_rows = 0, total_rows = 0;
+      int lds = 0;
       for (size_t k = b; k < std::min(idx.size(), b + kEncodeJobsPerLaunch); ++k) {
         const bgtq_encode_job &j = jobs[idx[k]];
         EncodeJobDev &J = L.jobs[L.n_jobs++];
@@ -675,24 +694,26 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
         J.dst_row0 = j.dst_row0;
         J.dst_step = 1;
         max_rows = std::max(max_rows, j.rows);
+        total_rows += j.rows;
+        const bgtq_tables_info &ti = j.tables->info;
+        lds = std::max(lds, encode_wave_lds_bytes(kv.first, ti.n_codebooks * 256, ti.n_books * ti.max_centroids));
       }
-      HIP_TRY(launch_encode(L, kv.first, src_dtype == BGTQ_DTYPE_F32, max_rows, ctx->stream), "encode launch");
+      if (lds <= 160 * 1024 && total_rows < kEncodeWaveMaxRows) {
+        // Few rows (a decode step's appended tokens): one wave per row, each
+        // wave striding over enough rows to keep about sixteen waves per
+        // compute unit busy. Bulk encodes keep one thread per row.
+        const int64_t target_waves = 16 * (int64_t)device_cus();
+        const int64_t rows_per_wave = std::max<int64_t>(1, (total_rows + target_waves - 1) / target_waves);
+        const int64_t wgs = std::max<int64_t>(1, (max_rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave));
+        HIP_TRY(launch_encode_wave(L, kv.first, src_dtype == BGTQ_DTYPE_F32, (int)std::min<int64_t>(wgs, 65535), lds,
+                                   ctx->stream),
+                "encode launch");
+      } else {
+        HIP_TRY(launch_encode(L, kv.first, src_dtype == BGTQ_DTYPE_F32, max_rows, ctx->stream), "encode launch");
+      }
     }
   }
   return BGTQ_OK;
-}
-
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
 }
 
 // Token splits per (sequence, KV head): at least 256 tokens each, at most 256

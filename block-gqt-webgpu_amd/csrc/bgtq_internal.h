@@ -112,6 +112,12 @@ struct FastLayout {
 // Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).
 hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
                          hipStream_t stream);
+// Wave-per-row encode (encode_wave.hip): dynamic LDS for a job with the given
+// LUT bytes and centroid floats, and its launcher (wgs_per_job workgroups of
+// four waves per job, each wave striding over the job's rows).
+int encode_wave_lds_bytes(int dim, int lut_bytes, int book_floats);
+hipError_t launch_encode_wave(const EncodeLaunch &launch, int dim, int src_f32, int wgs_per_job, int lds_bytes,
+                              hipStream_t stream);
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
 int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_bytes, int norm_stride);
 hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream);

@@ -168,3 +168,29 @@ def test_append_contracts(device, attention_cases):
     changed.rotation.reshape(p.dim, p.dim)[other, 0] = 0.01
     with pytest.raises(bgtq.StateError, match="Off-group transform is nonzero"):
         bgtq.PackedKeys.create(device, changed, 3)
+
+
+def test_bulk_encode_bit_exact(device, oracle):
+    """A launch of at least 16384 rows takes the thread-per-row encoder (smaller
+    launches the wave-per-row one); both must give the oracle's bytes."""
+    import torch
+    import bgtq
+    from bgtq import batched
+    rng = np.random.default_rng(99)
+    layouts = _layouts(oracle)
+    for name, p in [layouts[i] for i in (0, 3, 9)]:
+        print("bulk layout", name, flush=True)
+        rows = 20000
+        k = _random_half_rows(rng, rows, p.dim)
+        ref_p, ref_n = oracle.encode_pack(_olayout(oracle, p), k)
+        tables = bgtq.Tables(device, p)
+        src = torch.from_numpy(k.view(np.int16)).cuda()
+        packed = torch.zeros((rows, p.rowBytes), dtype=torch.uint8, device="cuda")
+        norms = torch.zeros((rows, p.normStride), dtype=torch.int16, device="cuda")
+        batched.encode(device, [dict(tables=tables, src=src, src_row_stride=p.dim, rows=rows, packed=packed,
+                                     norms=norms)], "f16")
+        device.synchronize()
+        got_p, got_n = packed.cpu().numpy(), norms.cpu().numpy().view(np.uint16)
+        bad = np.nonzero(np.any(got_p != ref_p, axis=1) | np.any(got_n != ref_n, axis=1))[0]
+        assert bad.size == 0, f"{name}: {bad.size} rows differ, first {bad[:5]}"
+        tables.destroy()
