@@ -82,8 +82,8 @@ def build_napi() -> Path:
         raise RuntimeError("node_api.h not found")
     src = PKG / "node" / "bgtq_napi.cc"
     out = PKG / "node" / "bgtq_napi.node"
-    _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", f"-I{node_inc}", f"-I{INCLUDE}", str(src),
-          "-o", str(out), f"-L{LIB_DIR}", "-lbgtq", "-Wl,-rpath,$ORIGIN/../lib"])
+    _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-DNAPI_VERSION=6", f"-I{node_inc}", f"-I{INCLUDE}",
+          str(src), "-o", str(out), f"-L{LIB_DIR}", "-lbgtq", "-Wl,-rpath,$ORIGIN/../lib"])
     return out
 
 

@@ -1,0 +1,218 @@
+'use strict';
+// The reference's TypeScript runtime classes over the N-API addon.
+//
+// Same names, constructor and method arguments, validation order and error
+// messages as src/webgpu/layout.ts, src/runtime/*.ts and src/attention/*.ts;
+// every computation runs in the HIP kernels of libbgtq.so. Plain CommonJS so
+// that any Node with N-API 6 loads it. Where the reference hands back a
+// GPUBuffer (attend(), inspect(), PackedKeys.packed/norms) this module hands
+// back a DeviceView whose read() copies the device data to a typed array;
+// readBuffer(device, view) is that read, as in src/webgpu/buffers.ts.
+const path = require('path');
+const native = require(path.join(__dirname, 'bgtq_napi.node'));
+
+const DTYPE_F32 = 0;
+const DTYPE_F16 = 1;
+
+// ---- GPUDevice facade ----------------------------------------------------
+class Device {
+  constructor(index) {
+    this.index = index === undefined ? 0 : index;
+    this.handle = native.contextCreate(this.index);
+    // HBM bounds capacity here, not the WebGPU dispatch limit.
+    this.limits = { maxComputeWorkgroupsPerDimension: 0x7fffffff };
+    const self = this;
+    this.queue = { onSubmittedWorkDone: async function () { native.contextSynchronize(self.handle); } };
+  }
+  destroy() {
+    if (this.handle) native.contextDestroy(this.handle);
+    this.handle = null;
+  }
+}
+async function requestDevice(index) { return new Device(index); }
+
+class DeviceView {
+  constructor(read) { this.read = read; }
+}
+async function readBuffer(device, view) { return view.read(); }
+
+// ---- calibration tables (src/webgpu/layout.ts:8-31) ------------------------
+function isInt(x) { return Number.isInteger(x); }
+function validateLayout(p) {
+  const d = p.dim;
+  if (![d, p.groups, p.rowBytes, p.normStride, p.nibbleDims, p.maxCentroids].every(isInt) ||
+      d < 2 || d > 128 || d % 2 || p.groups < 1 || p.groups > 8 || p.normStride < p.groups || p.nibbleDims < 0 ||
+      p.nibbleDims > d || p.nibbleDims % 2 || p.rowBytes < p.nibbleDims / 2 + d - p.nibbleDims ||
+      p.maxCentroids < 2 || p.maxCentroids > 256) {
+    throw new RangeError('Invalid Block-GTQ layout');
+  }
+  const some = (a, f) => Array.prototype.some.call(a, f);
+  if (p.permutation.length !== d || new Set(p.permutation).size !== d || some(p.permutation, (i) => i >= d) ||
+      p.groupOf.length !== d || some(p.groupOf, (g) => g >= p.groups) || p.positionToCodebook.length !== d ||
+      p.rotation.length !== d * d || p.centroids.length !== d * p.maxCentroids || p.offsets.length !== d ||
+      p.inverseScales.length !== d || p.codeLut.length % 256 ||
+      some(p.positionToCodebook, (c) => c * 256 >= p.codeLut.length)) {
+    throw new RangeError('Invalid calibration table shape');
+  }
+  for (const values of [p.rotation, p.centroids, p.offsets, p.inverseScales]) {
+    if (some(values, (x) => !Number.isFinite(x))) throw new RangeError('Nonfinite calibration table');
+  }
+  for (let i = 0; i < d; i++) {
+    for (let bin = 0; bin < 256; bin++) {
+      const code = p.codeLut[p.positionToCodebook[i] * 256 + bin];
+      if (code >= p.maxCentroids || (i < p.nibbleDims && code > 15)) {
+        throw new RangeError('Code LUT incompatible with packing');
+      }
+    }
+  }
+}
+function tables(p) {
+  validateLayout(p);
+  const head = [p.dim, p.groups, p.rowBytes, p.normStride, p.nibbleDims, p.maxCentroids];
+  const sections = [p.permutation, p.groupOf, p.positionToCodebook, p.codeLut];
+  const integer = new Uint32Array(10 + sections.reduce((n, s) => n + s.length, 0));
+  integer.set(head, 0);
+  let at = 10;
+  sections.forEach((s, k) => { integer[6 + k] = at; integer.set(s, at); at += s.length; });
+  const floating = new Float32Array(p.rotation.length + p.centroids.length + p.offsets.length + p.inverseScales.length);
+  let f = 0;
+  for (const s of [p.rotation, p.centroids, p.offsets, p.inverseScales]) { floating.set(s, f); f += s.length; }
+  return { integer, floating };
+}
+
+// ---- key stores (src/runtime/keys.ts, packed-keys.ts, compressed-keys.ts) ---
+function appendCount(values, dim, length, capacity) {
+  if (!values.length || values.length % dim) throw new RangeError('K append must contain whole nonempty rows');
+  if (values.some((x) => (x & 0x7c00) === 0x7c00)) throw new RangeError('Finite FP16 K required');
+  const count = values.length / dim;
+  if (length + count > capacity) throw new RangeError('K capacity exceeded');
+  return count;
+}
+
+class FP16Keys {
+  constructor(device, dim, capacity) {
+    if (!isInt(dim) || dim < 2 || dim % 2 || !isInt(capacity) || capacity < 1) throw new RangeError('Invalid K dimensions');
+    this.kind = 'fp16';
+    this.device = device; this.dim = dim; this.capacity = capacity;
+    this.handle = native.fp16KeysCreate(device.handle, dim, capacity);
+    this.allocations = native.keysAllocations(this.handle);
+    const self = this;
+    this.buffer = new DeviceView(() => native.keysReadFp16(self.handle, self.capacity * self.dim));
+  }
+  get length() { return native.keysLength(this.handle); }
+  async append(values) {
+    appendCount(values, this.dim, this.length, this.capacity);
+    native.keysAppend(this.handle, values);
+  }
+  prepare() { return { buffer: this.buffer, format: 'f16' }; }
+  destroy() { if (this.handle) native.keysDestroy(this.handle); this.handle = null; }
+}
+
+class PackedKeys {
+  constructor(device, parameters, capacity, compressed) {
+    if (!isInt(capacity) || capacity < 1 || capacity > device.limits.maxComputeWorkgroupsPerDimension) {
+      throw new RangeError('Invalid capacity');
+    }
+    const t = tables(parameters);
+    this.kind = 'block-gtq';
+    this.device = device; this.parameters = parameters; this.capacity = capacity; this.dim = parameters.dim;
+    this.tablesHandle = native.tablesCreate(device.handle, t.integer, t.floating);
+    try {
+      this.handle = native.packedKeysCreate(this.tablesHandle, capacity, !!compressed);
+    } catch (e) {
+      native.tablesDestroy(this.tablesHandle);
+      throw e;
+    }
+    this.allocations = native.keysAllocations(this.handle);
+    const self = this;
+    const both = () => native.keysRead(self.handle, self.capacity * parameters.rowBytes, self.capacity * parameters.normStride);
+    this.packed = new DeviceView(() => both()[0]);
+    this.norms = new DeviceView(() => both()[1]);
+  }
+  static async create(device, p, capacity) { return new PackedKeys(device, p, capacity, false); }
+  get length() { return native.keysLength(this.handle); }
+  async append(values) {
+    appendCount(values, this.dim, this.length, this.capacity);
+    native.keysAppend(this.handle, values);  // resolves after the encode has completed
+  }
+  ready() { native.keysReady(this.handle); }
+  destroy() {
+    if (this.handle) native.keysDestroy(this.handle);
+    if (this.tablesHandle) native.tablesDestroy(this.tablesHandle);
+    this.handle = this.tablesHandle = null;
+  }
+}
+
+class CompressedKeys extends PackedKeys {
+  static async create(device, p, capacity) { return new CompressedKeys(device, p, capacity, true); }
+  prepare() {
+    const self = this;
+    return { buffer: new DeviceView(() => native.keysPrepare(self.handle, self.length * self.dim)), format: 'f32' };
+  }
+}
+
+// ---- values (src/runtime/values.ts; the model path's FP16 cache) -----------
+class Values {
+  constructor(device, dim, capacity, dtype) {
+    if (!isInt(dim) || dim < 1 || !isInt(capacity) || capacity < 1) throw new RangeError('Invalid V dimensions');
+    this.device = device; this.dim = dim; this.capacity = capacity;
+    this.dtype = dtype === 'f16' ? 'f16' : 'f32';
+    this.handle = native.valuesCreate(device.handle, dim, capacity, this.dtype === 'f16' ? DTYPE_F16 : DTYPE_F32);
+    this.allocations = native.valuesAllocations(this.handle);
+  }
+  get length() { return native.valuesLength(this.handle); }
+  append(values) { native.valuesAppend(this.handle, values); }
+  destroy() { if (this.handle) native.valuesDestroy(this.handle); this.handle = null; }
+}
+
+// ---- attention (src/attention/attention.ts, optimized.ts) -----------------
+class Session {
+  constructor(device, keys, values, maxQueries, materialize) {
+    if (keys.device !== device || values.device !== device || keys.dim !== values.dim ||
+        keys.capacity !== values.capacity || !isInt(maxQueries) || maxQueries < 1) {
+      throw new RangeError('Incompatible attention storage');
+    }
+    this.device = device; this.keys = keys; this.values = values; this.maxQueries = maxQueries;
+    this.handle = native.attentionCreate(keys.handle, values.handle, maxQueries, materialize !== false);
+    this.allocations = native.attentionAllocations(this.handle);
+    const self = this;
+    const q = () => native.attentionQueries(self.handle);
+    this.output = new DeviceView(() => native.attentionRead(self.handle, 2, q() * self.keys.dim));
+    this._logits = new DeviceView(() => native.attentionRead(self.handle, 0, q() * self.keys.length));
+    this._probabilities = new DeviceView(() => native.attentionRead(self.handle, 1, q() * self.keys.length));
+  }
+  setQueries(q, positions, causal) { native.attentionSetQueries(this.handle, q, positions, !!causal); }
+  record() { native.attentionRecord(this.handle); }
+  async attend(q, positions, causal) {
+    this.setQueries(q, positions, causal);
+    this.record();
+    await this.device.queue.onSubmittedWorkDone();
+    return this.output;
+  }
+  inspect() {
+    return { logits: this._logits, probabilities: this._probabilities, output: this.output,
+             queries: native.attentionQueries(this.handle), tokens: this.keys.length };
+  }
+  destroy() { if (this.handle) native.attentionDestroy(this.handle); this.handle = null; }
+}
+
+class OptimizedAttention extends Session {
+  static async create(device, keys, values, maxQueries, tailMode) {
+    const s = new OptimizedAttention(device, keys, values, maxQueries === undefined ? 3 : maxQueries, true);
+    s.tailMode = tailMode === undefined ? 'parallel' : tailMode;
+    return s;
+  }
+}
+class AttentionSession extends Session {}
+class AttentionEngine {
+  constructor(device) { this.device = device; }
+  static async create(device) { return new AttentionEngine(device); }
+  session(keys, values, maxQueries) {
+    return new AttentionSession(this.device, keys, values, maxQueries === undefined ? 3 : maxQueries, true);
+  }
+}
+
+module.exports = {
+  native, Device, requestDevice, DeviceView, readBuffer, validateLayout, tables, appendCount,
+  FP16Keys, PackedKeys, CompressedKeys, Values, OptimizedAttention, AttentionEngine, AttentionSession,
+};

@@ -140,3 +140,25 @@ def test_allocator_mirror_matches_oracle(oracle):
         lo = int(rng.integers(0, 3))
         hi = int(rng.integers(lo, 9))
         np.testing.assert_array_equal(calibrate.allocate_bits(s, budget, lo, hi), oracle.allocate_bits(s, budget, lo, hi))
+
+
+def test_node_addon_loads_without_a_device():
+    """The N-API addon and the JS classes load (no device work) and export every entry point."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    addon = ROOT / "block-gqt-webgpu_amd" / "node" / "bgtq_napi.node"
+    if node is None or not addon.exists():
+        pytest.skip("node or the built addon is absent")
+    script = ("const b=require(process.argv[1]);"
+              "const want=['contextCreate','tablesCreate','packedKeysCreate','keysAppend','keysRead','valuesCreate',"
+              "'valuesAppend','attentionCreate','attentionSetQueries','attentionRecord','attentionRead'];"
+              "const miss=want.filter(k=>typeof b.native[k]!=='function');"
+              "const cls=['PackedKeys','CompressedKeys','FP16Keys','Values','OptimizedAttention','AttentionEngine','tables'];"
+              "const missc=cls.filter(k=>!b[k]);"
+              "console.log(JSON.stringify({abi:b.native.abiVersion,miss,missc}));")
+    r = subprocess.run([node, "-e", script, str(addon.parent / "bgtq.js")], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    import json
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out == {"abi": 1, "miss": [], "missc": []}, out
