@@ -1,0 +1,99 @@
+// Type declarations for bgtq.js: the reference's public runtime types
+// (src/webgpu/layout.ts:2-5, src/webgpu/buffers.ts:1, src/runtime/keys.ts:3-10,
+// src/attention/attention.ts, src/attention/optimized.ts) with GPUDevice and
+// GPUBuffer replaced by the HIP-backed Device and DeviceView.
+
+export type BlockGTQParameters = {
+  dim: number; groups: number; rowBytes: number; normStride: number; nibbleDims: number; maxCentroids: number;
+  permutation: Uint32Array; groupOf: Uint32Array; positionToCodebook: Uint32Array; codeLut: Uint8Array;
+  rotation: Float32Array; centroids: Float32Array; offsets: Float32Array; inverseScales: Float32Array;
+};
+export type Allocation = { name: string; role: "persistent-k" | "persistent-v" | "shared" | "scratch"; bytes: number };
+
+export class Device {
+  readonly index: number;
+  readonly limits: { maxComputeWorkgroupsPerDimension: number };
+  readonly queue: { onSubmittedWorkDone(): Promise<void> };
+  destroy(): void;
+}
+export function requestDevice(index?: number): Promise<Device>;
+
+/** Device-resident data; read() copies it to host memory. */
+export class DeviceView<T extends ArrayBufferView = ArrayBufferView> {
+  read(): T;
+}
+export function readBuffer<T extends ArrayBufferView>(device: Device, view: DeviceView<T>): Promise<T>;
+
+export function validateLayout(p: BlockGTQParameters): void;
+export function tables(p: BlockGTQParameters): { integer: Uint32Array; floating: Float32Array };
+export function appendCount(values: Uint16Array, dim: number, length: number, capacity: number): number;
+
+export type KeyView = { buffer: DeviceView<Uint16Array | Float32Array>; format: "f16" | "f32" };
+export interface KeyStore {
+  readonly device: Device; readonly dim: number; readonly capacity: number; readonly length: number;
+  readonly allocations: Allocation[]; readonly kind: "fp16" | "block-gtq";
+  append(values: Uint16Array): Promise<void>;
+  prepare(): KeyView;
+  destroy(): void;
+}
+
+export class FP16Keys implements KeyStore {
+  constructor(device: Device, dim: number, capacity: number);
+  readonly device: Device; readonly dim: number; readonly capacity: number; readonly length: number;
+  readonly allocations: Allocation[]; readonly kind: "fp16";
+  readonly buffer: DeviceView<Uint16Array>;
+  append(values: Uint16Array): Promise<void>;
+  prepare(): KeyView;
+  destroy(): void;
+}
+
+export class PackedKeys {
+  static create(device: Device, p: BlockGTQParameters, capacity: number): Promise<PackedKeys>;
+  readonly device: Device; readonly parameters: BlockGTQParameters; readonly dim: number;
+  readonly capacity: number; readonly length: number; readonly allocations: Allocation[];
+  readonly kind: "block-gtq";
+  readonly packed: DeviceView<Uint8Array>;
+  readonly norms: DeviceView<Uint16Array>;
+  append(values: Uint16Array): Promise<void>;
+  ready(): void;
+  destroy(): void;
+}
+export class CompressedKeys extends PackedKeys implements KeyStore {
+  static create(device: Device, p: BlockGTQParameters, capacity: number): Promise<CompressedKeys>;
+  prepare(): KeyView;
+}
+
+export class Values {
+  constructor(device: Device, dim: number, capacity: number, dtype?: "f32" | "f16");
+  readonly device: Device; readonly dim: number; readonly capacity: number; readonly length: number;
+  readonly dtype: "f32" | "f16"; readonly allocations: Allocation[];
+  append(values: Float32Array): void;
+  destroy(): void;
+}
+
+export type Inspection = {
+  logits: DeviceView<Float32Array>; probabilities: DeviceView<Float32Array>; output: DeviceView<Float32Array>;
+  queries: number; tokens: number;
+};
+declare class Session {
+  readonly device: Device; readonly maxQueries: number; readonly allocations: Allocation[];
+  readonly output: DeviceView<Float32Array>;
+  setQueries(q: Float32Array, positions: Uint32Array, causal?: boolean): void;
+  record(): void;
+  attend(q: Float32Array, positions: Uint32Array, causal?: boolean): Promise<DeviceView<Float32Array>>;
+  inspect(): Inspection;
+  destroy(): void;
+}
+export class OptimizedAttention extends Session {
+  static create(device: Device, keys: PackedKeys, values: Values, maxQueries?: number,
+                tailMode?: "serial" | "parallel"): Promise<OptimizedAttention>;
+  readonly keys: PackedKeys; readonly values: Values; tailMode: "serial" | "parallel";
+}
+export class AttentionSession extends Session {
+  readonly keys: KeyStore; readonly values: Values;
+}
+export class AttentionEngine {
+  static create(device: Device): Promise<AttentionEngine>;
+  readonly device: Device;
+  session(keys: KeyStore, values: Values, maxQueries?: number): AttentionSession;
+}
