@@ -61,6 +61,19 @@ class DecodeDesc(ctypes.Structure):
                 ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
 
 
+
+class PrefillDesc(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int32), ("rows", ctypes.c_int32), ("q_heads", ctypes.c_int32),
+                ("kv_heads", ctypes.c_int32), ("dim", ctypes.c_int32), ("key_format", ctypes.c_int32),
+                ("tables", ctypes.c_void_p * 16), ("packed", ctypes.c_void_p), ("packed_seq_stride", ctypes.c_int64),
+                ("packed_head_stride", ctypes.c_int64), ("norms", ctypes.c_void_p),
+                ("norms_seq_stride", ctypes.c_int64), ("norms_head_stride", ctypes.c_int64),
+                ("k_f16", ctypes.c_void_p), ("k_seq_stride", ctypes.c_int64), ("k_head_stride", ctypes.c_int64),
+                ("v", ctypes.c_void_p), ("v_seq_stride", ctypes.c_int64), ("v_head_stride", ctypes.c_int64),
+                ("q", ctypes.c_void_p), ("out", ctypes.c_void_p), ("starts", ctypes.c_void_p),
+                ("max_length", ctypes.c_uint32), ("split_tokens", ctypes.c_int32),
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+
 _VP, _SZ, _I32, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32
 _PP = ctypes.POINTER(ctypes.c_void_p)
 
@@ -105,6 +118,8 @@ SIGNATURES = {
     "bgtq_encode_batched": (_I32, [_VP, _I32, ctypes.POINTER(EncodeJob), _SZ]),
     "bgtq_decode_workspace_size": (_I32, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_decode": (_I32, [_VP, ctypes.POINTER(DecodeDesc)]),
+    "bgtq_prefill_workspace_size": (_I32, [ctypes.POINTER(PrefillDesc), ctypes.POINTER(ctypes.c_size_t)]),
+    "bgtq_prefill": (_I32, [_VP, ctypes.POINTER(PrefillDesc)]),
 }
 
 _lib = None

@@ -64,3 +64,34 @@ def workspace_bytes(desc) -> int:
 
 def decode(device, desc) -> None:
     check(lib().bgtq_decode(device.handle, ctypes.byref(desc)))
+
+
+def prefill_desc(*, batch, rows, q_heads, kv_heads, dim, q, out, starts, max_length, v, v_seq_stride,
+                 v_head_stride, tables=None, packed=None, packed_seq_stride=0, packed_head_stride=0, norms=None,
+                 norms_seq_stride=0, norms_head_stride=0, k_f16=None, k_seq_stride=0, k_head_stride=0,
+                 split_tokens=0, workspace=None):
+    """bgtq_prefill_desc over device tensors: q/out [B, rows, Hq, dim] FP32, v FP16, starts uint32 [B]."""
+    d = _lib.PrefillDesc()
+    d.batch, d.rows, d.q_heads, d.kv_heads, d.dim = batch, rows, q_heads, kv_heads, dim
+    d.key_format = _lib.KEYS_PACKED if packed is not None else _lib.KEYS_FP16
+    for i, t in enumerate(tables or []):
+        d.tables[i] = t.handle.value if hasattr(t.handle, "value") else t.handle
+    d.packed, d.packed_seq_stride, d.packed_head_stride = _addr(packed), packed_seq_stride, packed_head_stride
+    d.norms, d.norms_seq_stride, d.norms_head_stride = _addr(norms), norms_seq_stride, norms_head_stride
+    d.k_f16, d.k_seq_stride, d.k_head_stride = _addr(k_f16), k_seq_stride, k_head_stride
+    d.v, d.v_seq_stride, d.v_head_stride = _addr(v), v_seq_stride, v_head_stride
+    d.q, d.out, d.starts = _addr(q), _addr(out), _addr(starts)
+    d.max_length, d.split_tokens = int(max_length), int(split_tokens)
+    if workspace is not None:
+        d.workspace, d.workspace_bytes = _addr(workspace), workspace.numel() * workspace.element_size()
+    return d
+
+
+def prefill_workspace_bytes(desc) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().bgtq_prefill_workspace_size(ctypes.byref(desc), ctypes.byref(n)))
+    return n.value
+
+
+def prefill(device, desc) -> None:
+    check(lib().bgtq_prefill(device.handle, ctypes.byref(desc)))

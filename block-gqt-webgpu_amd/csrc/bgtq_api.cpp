@@ -890,6 +890,147 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) {
   return launch_decode_common(ctx, p, d->q, d->tables);
 }
 
+// ---------------------------------------------------------------- chunked prefill
+struct PrefillWorkspace {
+  size_t counters, qr, part, total;
+};
+
+static PrefillWorkspace prefill_ws(int64_t counters, int64_t queries, int dim, int splits) {
+  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
+  PrefillWorkspace w;
+  w.counters = 0;
+  w.qr = al(sizeof(uint32_t) * counters);
+  w.part = w.qr + al(sizeof(float) * queries * dim);
+  w.total = w.part + (splits > 1 ? al(sizeof(float) * queries * splits * (dim + 2)) : 0);
+  return w;
+}
+
+struct PrefillPlan {
+  int tiles, split_tokens, splits;
+};
+
+// Token splits: enough (tile, split) workgroups for about four per compute
+// unit over the causal half of the history, at least 128 tokens each and at
+// most kPrefillMaxSplits splits (the merge holds one split per lane).
+static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
+  if (!d) return fail(BGTQ_ERR_RANGE, "null descriptor");
+  if (d->batch < 1 || d->rows < 1 || d->kv_heads < 1 || d->kv_heads > kMaxKvHeads || d->q_heads < d->kv_heads ||
+      d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 16)
+    return fail(BGTQ_ERR_RANGE, "invalid head geometry");
+  if (d->dim != 64 && d->dim != 128) return fail(BGTQ_ERR_UNSUPPORTED, "prefill handles head dim 64 or 128");
+  if (d->max_length < 1 || d->max_length > (1u << 24)) return fail(BGTQ_ERR_RANGE, "max_length must be in 1..2^24");
+  if ((uint32_t)d->rows > d->max_length) return fail(BGTQ_ERR_RANGE, "rows exceed max_length");
+  if (d->key_format == BGTQ_KEYS_PACKED) {
+    for (int h = 0; h < d->kv_heads; ++h) {
+      if (!d->tables[h]) return fail(BGTQ_ERR_RANGE, "null tables for KV head %d", h);
+      if (d->tables[h]->info.dim != d->dim) return fail(BGTQ_ERR_RANGE, "tables dim mismatch");
+    }
+    if (!d->packed || !d->norms) return fail(BGTQ_ERR_RANGE, "null packed K");
+  } else if (d->key_format == BGTQ_KEYS_FP16) {
+    if (!d->k_f16) return fail(BGTQ_ERR_RANGE, "null FP16 K");
+  } else {
+    return fail(BGTQ_ERR_RANGE, "invalid key format");
+  }
+  if (!d->v || !d->q || !d->out || !d->starts) return fail(BGTQ_ERR_RANGE, "null v/q/out/starts");
+  if (d->split_tokens < 0) return fail(BGTQ_ERR_RANGE, "negative split_tokens");
+  const int64_t G = d->q_heads / d->kv_heads;
+  plan->tiles = (int)((d->rows * G + prefill_tile_queries(d->dim) - 1) / prefill_tile_queries(d->dim));
+  const int64_t L = d->max_length;
+  int64_t sp = d->split_tokens;
+  if (sp == 0) {
+    const int64_t units = (int64_t)d->batch * d->kv_heads * plan->tiles;
+    sp = std::max<int64_t>(128, units * (L / 2 + 1) / (4 * (int64_t)device_cus()));
+  }
+  sp = std::max<int64_t>(sp, (L + kPrefillMaxSplits - 1) / kPrefillMaxSplits);
+  sp = std::min<int64_t>((sp + 31) / 32 * 32, (L + 31) / 32 * 32);
+  plan->split_tokens = (int)sp;
+  plan->splits = (int)((L + sp - 1) / sp);
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *bytes) {
+  PrefillPlan plan{};
+  if (bgtq_status s = plan_prefill(d, &plan)) return s;
+  if (!bytes) return fail(BGTQ_ERR_RANGE, "null output");
+  const int64_t queries = (int64_t)d->batch * d->rows * d->q_heads;
+  *bytes = prefill_ws((int64_t)d->batch * d->kv_heads * plan.tiles, queries, d->dim, plan.splits).total;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
+  if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
+  PrefillPlan plan{};
+  if (bgtq_status s = plan_prefill(d, &plan)) return s;
+  const int64_t queries = (int64_t)d->batch * d->rows * d->q_heads;
+  const PrefillWorkspace w = prefill_ws((int64_t)d->batch * d->kv_heads * plan.tiles, queries, d->dim, plan.splits);
+  if (!d->workspace || d->workspace_bytes < w.total)
+    return fail(BGTQ_ERR_RANGE, "workspace of %zu bytes required", w.total);
+  // The layout check and the query rotation use the decode parameter block:
+  // the chunk's rows act as batch * rows query sets of Hq heads.
+  DecodeParams dp{};
+  for (int h = 0; h < d->kv_heads; ++h) dp.tables[h] = d->key_format == BGTQ_KEYS_PACKED ? d->tables[h]->dev() : nullptr;
+  dp.batch = d->batch * d->rows;
+  dp.q_heads = d->q_heads;
+  dp.kv_heads = d->kv_heads;
+  dp.dim = d->dim;
+  dp.G = d->q_heads / d->kv_heads;
+  dp.key_format = d->key_format == BGTQ_KEYS_PACKED ? 1 : 0;
+  dp.packed = d->packed;
+  dp.packed_seq_stride = d->packed_seq_stride;
+  dp.packed_head_stride = d->packed_head_stride;
+  dp.norms = d->norms;
+  dp.norms_seq_stride = d->norms_seq_stride;
+  dp.norms_head_stride = d->norms_head_stride;
+  dp.k = d->k_f16;
+  dp.k_seq_stride = d->k_seq_stride;
+  dp.k_head_stride = d->k_head_stride;
+  dp.v = d->v;
+  dp.v_dtype = BGTQ_DTYPE_F16;
+  dp.v_seq_stride = d->v_seq_stride;
+  dp.v_head_stride = d->v_head_stride;
+  FastLayout fl{};
+  int nn = 0, sg = 0;
+  if (!fast_layout(dp, d->tables, &fl, &nn, &sg))
+    return fail(BGTQ_ERR_UNSUPPORTED, "prefill needs 16-byte aligned FP16 V/K/scales and a layout whose 32-dim "
+                                      "K-steps each lie in one group and book (at most two groups)");
+  if (bgtq_status s = ctx->use()) return s;
+  uint8_t *ws = static_cast<uint8_t *>(d->workspace);
+  float *qr = reinterpret_cast<float *>(ws + w.qr);
+  HIP_TRY(launch_rotate_q(dp, d->q, qr, ctx->stream), "rotate_q launch");
+  PrefillParams p{};
+  for (int h = 0; h < d->kv_heads; ++h) p.tables[h] = dp.tables[h];
+  p.batch = d->batch;
+  p.rows = d->rows;
+  p.q_heads = d->q_heads;
+  p.kv_heads = d->kv_heads;
+  p.dim = d->dim;
+  p.G = dp.G;
+  p.key_format = dp.key_format;
+  p.packed = d->packed;
+  p.packed_seq_stride = d->packed_seq_stride;
+  p.packed_head_stride = d->packed_head_stride;
+  p.norms = d->norms;
+  p.norms_seq_stride = d->norms_seq_stride;
+  p.norms_head_stride = d->norms_head_stride;
+  p.k = d->k_f16;
+  p.k_seq_stride = d->k_seq_stride;
+  p.k_head_stride = d->k_head_stride;
+  p.v = d->v;
+  p.v_seq_stride = d->v_seq_stride;
+  p.v_head_stride = d->v_head_stride;
+  p.qr = qr;
+  p.starts = d->starts;
+  p.max_length = (int32_t)d->max_length;
+  p.split_tokens = plan.split_tokens;
+  p.splits = plan.splits;
+  p.tiles = plan.tiles;
+  p.counters = reinterpret_cast<uint32_t *>(ws + w.counters);
+  p.part = reinterpret_cast<float *>(ws + w.part);
+  p.out = d->out;
+  HIP_TRY(launch_prefill(p, fl, nn, sg, ctx->stream), "prefill launch");
+  return BGTQ_OK;
+}
+
 // ---------------------------------------------------------------- attention sessions
 bgtq_status bgtq_attention_create(bgtq_keys *k, bgtq_values *v, uint32_t max_queries, int32_t materialize,
                                   bgtq_attention **out) {

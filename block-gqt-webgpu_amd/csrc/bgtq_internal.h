@@ -101,6 +101,36 @@ struct DecodeParams {
   int32_t lds_bytes;  // dynamic LDS of the split kernel
 };
 
+// Chunked-prefill attention of one layer (prefill.hip). Units are (sequence,
+// KV head); a unit's queries are its chunk's rows x G heads (qi = row*G + h),
+// tiled by prefill_tile_queries(dim) and split over token ranges.
+struct PrefillParams {
+  const DevTables *tables[kMaxKvHeads];
+  int32_t batch, rows, q_heads, kv_heads, dim, G;
+  int32_t key_format;  // 0 = FP16 K rows, 1 = packed
+  const uint8_t *packed;
+  int64_t packed_seq_stride, packed_head_stride;  // bytes
+  const uint16_t *norms;
+  int64_t norms_seq_stride, norms_head_stride;  // elements
+  const void *k;
+  int64_t k_seq_stride, k_head_stride;  // elements
+  const void *v;                        // FP16
+  int64_t v_seq_stride, v_head_stride;  // elements
+  const float *qr;          // [B*rows*Hq*dim] rotated, permuted, scaled by 1/sqrt(dim)
+  const uint32_t *starts;   // [B] position of each chunk's first row
+  int32_t max_length;       // tokens every K/V buffer holds; kernels clamp starts to max_length - rows
+  int32_t split_tokens;     // multiple of 32
+  int32_t splits;           // ceil(max_length / split_tokens) <= 64
+  int32_t tiles;            // query tiles per unit
+  uint32_t *counters;       // [B*Hkv*tiles] split arrival counters: zero between launches
+  float *part;              // [B*rows*Hq*splits*(dim+2)] (m, l, o[dim])
+  float *out;               // [B*rows*Hq*dim]
+};
+// 16-query MFMA column blocks per wave of the prefill kernel, and queries per tile (four waves).
+__host__ __device__ constexpr int prefill_column_blocks(int dim) { return dim == 64 ? 4 : 2; }
+__host__ __device__ constexpr int prefill_tile_queries(int dim) { return 4 * 16 * prefill_column_blocks(dim); }
+constexpr int kPrefillMaxSplits = 64;
+
 // Structure of a layout the fused matrix-core decode handles: every 32-dim
 // K-step of the head-perm order lies in one group and one centroid book and is
 // either all nibble codes or all byte codes (nibble steps first); at most two
@@ -130,6 +160,8 @@ bool decode_fast_supported(int dim, int key_format, int nn, int sg);
 // Row bytes of the packed layout with nn leading nibble K-steps (no padding).
 int decode_fast_row_bytes(int dim, int nn);
 hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
+// Chunked prefill (prefill.hip), same layout requirements as the fused decode.
+hipError_t launch_prefill(const PrefillParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
 hipError_t launch_reconstruct(const DevTables *t, const uint8_t *packed, const uint16_t *norms,
                               int64_t rows, float *out, hipStream_t stream);
 hipError_t launch_half_convert(const float *src, uint16_t *dst, int64_t n, hipStream_t stream);

@@ -33,87 +33,18 @@
 #include <hip/hip_fp16.h>
 
 #include "bgtq_internal.h"
+#include "gfx950_common.h"
 
 namespace bgtq {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef fp16x4 __attribute__((address_space(3))) lds_fp16x4;
-typedef __attribute__((address_space(3))) void lds_void;
+using namespace gfx;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kChunk = 32;  // tokens per wave iteration: two 16-token MFMA tiles
 constexpr int kRing = 3;    // LDS chunk buffers per wave: compute one, the others in flight
-constexpr int kLdsLimit = 160 * 1024;  // LDS of one gfx950 CU
 constexpr bool kInterleaved = true;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kPScale = 32768.0f;  // P is carried as p * 2^15 so its fp16 lo part stays normal
-// Buffer resource word 3 on gfx9: 32-bit dword data format, raw (unswizzled) addressing.
-constexpr int kRsrcWord3 = 0x00020000;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kRsrcWord3);
-}
-// HBM -> LDS without VGPRs: lane i writes 16 (4) bytes at lds + 16 i (4 i).
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, (int)voff, (int)soff, 0, 0);
-}
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, (int)voff, (int)soff, 0, 0);
-}
-
-// Reductions over the four 16-lane rows that share a column (lane % 16).
-__device__ __forceinline__ float col_max(float v) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float col_sum(float v) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-__device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// x = hi + lo with both halves fp16 (hi rounded toward zero, so lo is exact
-// before its own rounding): ~2^-22 relative.
-__device__ __forceinline__ void split2(float x0, float x1, uint32_t &hi, uint32_t &lo) {
-  const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
-  const float r0 = x0 - (float)h[0], r1 = x1 - (float)h[1];
-  const auto l = __builtin_amdgcn_cvt_pkrtz(r0, r1);
-  hi = __builtin_bit_cast(uint32_t, h);
-  lo = __builtin_bit_cast(uint32_t, l);
-}
-
-// Relaxed atomics at device scope: on gfx950 they go to the device-coherent
-// level (system-coherent bit) instead of this XCD's L2.
-__device__ __forceinline__ void coherent_store(float *ptr, float v) {
-  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float coherent_load(float *ptr) {
-  return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Waits for all but the newest N vector-memory operations of this wave. The
-// LDS writes of buffer_load ... lds are not tracked by the compiler, so the
-// ring's waits are explicit; the memory clobber keeps LDS reads below them.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 template <int D>
 struct Geo {
@@ -123,11 +54,6 @@ struct Geo {
   static constexpr int VBYTES = kChunk * D * 2;
   static constexpr int VI = VBYTES / 1024;  // 16-byte DMA instructions per V chunk
 };
-// 16-byte piece swizzle of an FP16 row in LDS (conflict-free column and row reads).
-template <int D>
-__host__ __device__ constexpr int swz(int row) {
-  return D == 64 ? (row >> 1) & 7 : row & 15;
-}
 
 // One ring buffer: V chunk, K chunk, FP16 scales (32 x 4 bytes), packed tight
 // so two workgroups of the layout-B d=64 kernel fit one CU's 160 KB.
@@ -181,8 +107,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 
   // ---------------- streams of this (sequence, KV head) ----------------
   // Each chunk's loads use buffer descriptors based at the chunk's first token
-  // and sized to the rest of the sequence: the hardware range check (which
-  // covers the per-lane offset) returns zeros for tokens past the length.
+  // and sized to the chunk's tokens inside the sequence: the hardware range
+  // check (which covers the per-lane offset) returns zeros past the length.
   const _Float16 *v_base = static_cast<const _Float16 *>(p.v) + b * p.v_seq_stride + kv * p.v_head_stride;
   const uint8_t *k_base = KF == 1 ? p.packed + b * p.packed_seq_stride + kv * p.packed_head_stride
                                   : reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(p.k) +
@@ -201,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
   auto issue = [&](int i) {
     const int c0 = first + i * stride;
-    const uint32_t rest = (uint32_t)(T_b - c0);  // > 0: c0 < t_end <= T_b
+    const uint32_t rest = (uint32_t)min(T_b - c0, kChunk);  // tokens of the chunk inside the sequence (> 0)
     uint8_t *sb = slot_base(i % Sl::RING);
     const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
 #pragma unroll

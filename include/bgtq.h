@@ -204,6 +204,45 @@ typedef struct {
 bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes);
 bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d);
 
+/* Chunked-prefill attention for one layer: the model forward over a chunk of
+ * prompt rows (src/model/decoder.ts:46-56 with rows > 1, called per chunk by
+ * src/model/decoder.ts:82; the reference caps chunks at 32 rows,
+ * src/model/decoder.ts:15, this entry point takes any number). Sequence b's
+ * chunk holds `rows` query rows at positions starts[b] .. starts[b]+rows-1;
+ * row r's queries attend to tokens 0 .. starts[b]+r
+ * (src/model/compressed-dot.wgsl:28, src/model/attention.wgsl:19). The K/V
+ * buffers already hold the chunk's own tokens (encode them first).
+ *   q, out: [B, rows, Hq, dim] FP32 contiguous; query head h uses KV head h / G.
+ *   starts: device uint32 [B], starts[b] + rows <= max_length (kernels clamp).
+ *   v: FP16. Key formats, strides and the workspace contract (zero-filled
+ *   before first use, left zeroed by every call, one stream per workspace)
+ *   are those of bgtq_decode.
+ * Layouts: d 64 or 128, every 32-dim K-step of the head-perm order in one
+ * group and one centroid book, at most two groups (layout B and FP16 K);
+ * others return BGTQ_ERR_UNSUPPORTED. */
+typedef struct {
+  int32_t batch, rows, q_heads, kv_heads, dim;
+  int32_t key_format;
+  const bgtq_tables *tables[16];
+  const uint8_t *packed;
+  int64_t packed_seq_stride, packed_head_stride; /* bytes */
+  const uint16_t *norms;
+  int64_t norms_seq_stride, norms_head_stride;   /* elements */
+  const uint16_t *k_f16;
+  int64_t k_seq_stride, k_head_stride;           /* elements */
+  const uint16_t *v;
+  int64_t v_seq_stride, v_head_stride;           /* elements */
+  const float *q;
+  float *out;
+  const uint32_t *starts;
+  uint32_t max_length;
+  int32_t split_tokens; /* tokens per split, rounded up to a multiple of 32; 0 = choose */
+  void *workspace;
+  size_t workspace_bytes;
+} bgtq_prefill_desc;
+bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *bytes);
+bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d);
+
 #ifdef __cplusplus
 }
 #endif
