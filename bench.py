@@ -11,10 +11,12 @@ HIP graph (the way a serving loop replays a decode step).
 
 Side measurements in the same JSON line: SmolLM2 K-encode throughput (4096 x 3
 x 30 rows), a SmolLM2-geometry decode step at batch 1 (30 layers x encode one
-token + attend over 4096), the single-head T=4096 d=128 attention, and an
-FP16-K kernel at the headline shape.
+token + attend over 4096), the single-head T=4096 d=128 attention, an
+FP16-K kernel at the headline shape, and the Qwen2.5-0.5B 4096-token prompt
+prefill (24 layers x encode + causal attention on the matrix cores, as one
+chunk and in chunks of 32 rows).
 
-    python bench.py [--steps K] [--warmup W] [--layout B|A] [--no-cpu] [--no-extra]
+    python bench.py [--steps K] [--warmup W] [--layout B|A] [--no-cpu] [--no-extra] [--prefill-only]
 
 Prints one JSON line (value = algorithmic HBM GB/s of the decode step).
 """
@@ -231,6 +233,72 @@ def smollm2_decode_step(dev, steps, layout="B"):
                         "batch 1, layout B, FP16 V"}
 
 
+def prefill_flops(prompt, hq, dim, layers):
+    """Algorithmic causal attention FLOPs of a prompt: QK and PV, 2 * dim each per (query, visible token)."""
+    return layers * hq * (prompt * (prompt + 1) // 2) * dim * 4
+
+
+def qwen_prefill(dev, steps, layout="B", chunk=0, prompt=4096, layers=LAYERS):
+    """Qwen2.5-0.5B-geometry prompt prefill: per layer, encode the chunk's post-RoPE K for 2 KV heads,
+    then causal attention of its rows x 14 query heads over the history so far (d=64, FP16 V).
+    chunk=0: the whole prompt as one chunk; else chunks of that many rows, chunk by chunk through all layers."""
+    import torch
+    import bgtq
+    from bgtq import batched
+    p = layout_params(layout, DIM)
+    chunk = chunk or prompt
+    starts = list(range(0, prompt, chunk))
+    tabs = [bgtq.Tables(dev, p) for _ in range(layers * HKV)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    k = torch.randn((layers, HKV, prompt, DIM), generator=g, device="cuda").half()
+    v = torch.randn((layers, 1, HKV, prompt, DIM), generator=g, device="cuda").half()
+    q = torch.randn((layers, prompt, HQ, DIM), generator=g, device="cuda")
+    out = torch.empty((layers, prompt, HQ, DIM), device="cuda")
+    packed = torch.empty((layers, 1, HKV, prompt * p.rowBytes), dtype=torch.uint8, device="cuda")
+    norms = torch.empty((layers, 1, HKV, prompt * p.normStride), dtype=torch.int16, device="cuda")
+    start_t = [torch.tensor([s], dtype=torch.int32, device="cuda") for s in starts]
+    enc, args_list = [], []
+    for c, s in enumerate(starts):
+        rows = min(chunk, prompt - s)
+        for l in range(layers):
+            enc.append([dict(tables=tabs[l * HKV + h], src=k[l, h, s:s + rows], src_row_stride=DIM, rows=rows,
+                             packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=s) for h in range(HKV)])
+            args_list.append(dict(batch=1, rows=rows, q_heads=HQ, kv_heads=HKV, dim=DIM, q=q[l, s:s + rows],
+                                  out=out[l, s:s + rows], starts=start_t[c], max_length=prompt, v=v[l],
+                                  v_seq_stride=v.stride(1), v_head_stride=v.stride(2),
+                                  tables=tabs[l * HKV:(l + 1) * HKV], packed=packed[l],
+                                  packed_seq_stride=packed.stride(1), packed_head_stride=packed.stride(2),
+                                  norms=norms[l], norms_seq_stride=norms.stride(1), norms_head_stride=norms.stride(2)))
+    # one workspace for every call: they are ordered on one stream
+    need = max(batched.prefill_workspace_bytes(batched.prefill_desc(**a)) for a in args_list)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    descs = [batched.prefill_desc(workspace=ws, **a) for a in args_list]
+
+    def attend_only():
+        for d in descs:
+            batched.prefill(dev, d)
+
+    def step():
+        for e, d in zip(enc, descs):
+            batched.encode(dev, e, "f16")
+            batched.prefill(dev, d)
+
+    flops = prefill_flops(prompt, HQ, DIM, layers)
+    ms = time_graph(torch, graph_of(torch, dev, step), steps, 2)
+    ms_att = time_graph(torch, graph_of(torch, dev, attend_only), steps, 2)
+    for t in tabs:
+        t.destroy()
+    return {"ms_per_prompt": round(ms, 4), "tokens_per_s": round(prompt / (ms / 1e3)),
+            "attention_only_ms": round(ms_att, 4),
+            "attention_tflops_algorithmic": round(flops / (ms_att / 1e3) / 1e12, 1),
+            "mfma_frac_of_fp16_dense_peak": round(flops / (ms_att / 1e3) / 2.5e15, 4),
+            "algorithmic_gflop": round(flops / 1e9, 1),
+            "workload": f"{prompt}-token prompt, {layers} layers x (encode K of {HKV} KV heads + causal attention of "
+                        f"{HQ} q heads), d={DIM}, layout {layout}, FP16 V, "
+                        + ("one chunk" if chunk == prompt else f"chunks of {chunk} rows")}
+
+
 def single_head(dev, steps, layout="B"):
     """One query over T=4096, d=128, one head (the reference's CPU-runnable shape)."""
     import torch
@@ -290,6 +358,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="issue the per-layer launches directly, no HIP graph")
     ap.add_argument("--splits", type=int, default=0, help="token splits per (sequence, KV head); 0 = library choice")
     ap.add_argument("--sweep-splits", default="", help="comma list: time the decode at each split count and exit")
+    ap.add_argument("--prefill-only", action="store_true", help="only the Qwen prompt-prefill measurements")
+    ap.add_argument("--encode-only", action="store_true", help="only the SmolLM2 bulk K-encode measurement")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (HBM counter calibration)")
     a = ap.parse_args()
@@ -310,6 +380,13 @@ def main():
     from bgtq import batched
     dev = bgtq.Device(0)
     batched.bind_torch_stream(dev)
+    if a.encode_only:
+        print(json.dumps({"encode_smollm2_prefill": encode_throughput(dev, a.layout, max(a.steps, 5))}))
+        return
+    if a.prefill_only:
+        print(json.dumps({"qwen_prefill_4096": qwen_prefill(dev, a.steps, a.layout),
+                          "qwen_prefill_4096_chunk32": qwen_prefill(dev, 2, a.layout, chunk=32)}))
+        return
     log("building workload ...")
     w = DecodeWorkload(dev, a.layout, splits=a.splits)
     if a.sweep_splits:
@@ -347,6 +424,10 @@ def main():
         extra["smollm2_decode_step_b1"] = smollm2_decode_step(dev, a.steps, a.layout)
         log("single head ...")
         extra["single_head_t4096_d128"] = single_head(dev, a.steps, a.layout)
+        log("Qwen prefill, one chunk ...")
+        extra["qwen_prefill_4096"] = qwen_prefill(dev, max(2, a.steps // 2), a.layout)
+        log("Qwen prefill, chunks of 32 ...")
+        extra["qwen_prefill_4096_chunk32"] = qwen_prefill(dev, 2, a.layout, chunk=32)
     cpu = None if a.no_cpu else cpu_baseline(a.layout)
     rec = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,

@@ -319,7 +319,8 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   const size_t off_rot = align(off_books + sizeof(float) * nb * mc);
   const size_t off_rot_t = align(off_rot + sizeof(float) * d * d);
   const size_t off_mfma = align(off_rot_t + sizeof(float) * d * d);
-  const size_t total = off_mfma + (size_t)kMfmaTableBytes * nb;
+  const size_t off_rot_q = align(off_mfma + (size_t)kMfmaTableBytes * nb);
+  const size_t total = off_rot_q + (d % 32 == 0 ? (size_t)rot_q_bytes((int)d) : 0);
   auto *t = new bgtq_tables();
   t->ctx = ctx;
   t->host.assign(total, 0);
@@ -342,6 +343,7 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   T->off_rot = (uint32_t)off_rot;
   T->off_rot_t = (uint32_t)off_rot_t;
   T->off_mfma = (uint32_t)off_mfma;
+  T->off_rot_q = (uint32_t)off_rot_q;
   T->total_bytes = (uint32_t)total;
   float cmax = 0.0f;
   for (int64_t i = 0; i < d * mc; ++i) cmax = std::max(cmax, std::fabs(cent[i]));
@@ -382,6 +384,24 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
       pair_lo[e] = (uint32_t)l0 | ((uint32_t)l1 << 16);
       split(e, &code_hi[e], &code_lo[e]);
     }
+  }
+  // Query rotation operands (prefill): Rq[j][perm[i]] = R[j][i], split like
+  // the centroids (entries of an orthogonal rotation lie in [-1, 1]).
+  if (d % 32 == 0) {
+    std::vector<float> rq((size_t)(d * d));
+    for (int64_t j = 0; j < d; ++j)
+      for (int64_t i = 0; i < d; ++i) rq[j * d + perm[i]] = rot[j * d + i];
+    uint16_t *op = reinterpret_cast<uint16_t *>(h + off_rot_q);
+    for (int64_t n = 0; n < d / 16; ++n)
+      for (int64_t s = 0; s < d / 32; ++s)
+        for (int l = 0; l < 64; ++l) {
+          uint16_t *dst = op + ((n * (d / 32) + s) * 64 + l) * 16;
+          for (int jv = 0; jv < 8; ++jv) {
+            const float x = rq[(16 * n + l % 16) * d + 32 * s + 8 * (l / 16) + jv];
+            dst[jv] = f32_to_f16_rtz(x);
+            dst[8 + jv] = f32_to_f16_rtz(x - f16_to_f32(dst[jv]));
+          }
+        }
   }
   t->info = bgtq_tables_info{(int32_t)d, (int32_t)ng, (int32_t)rb, (int32_t)nstride, (int32_t)nib, (int32_t)mc, ncb, nb};
   bgtq_status s = ctx->use();
@@ -670,24 +690,30 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
     if (j.rows < 0 || j.dst_row0 < 0) return fail(BGTQ_ERR_RANGE, "encode job %zu: negative rows", i);
     if (j.rows && (!j.src || !j.packed || !j.norms)) return fail(BGTQ_ERR_RANGE, "encode job %zu: null buffer", i);
     if (j.src_row_stride < j.tables->info.dim) return fail(BGTQ_ERR_RANGE, "encode job %zu: row stride below dim", i);
+    if (j.src_row_stride > INT32_MAX) return fail(BGTQ_ERR_RANGE, "encode job %zu: row stride above 2^31 - 1", i);
   }
   if (bgtq_status s = ctx->use()) return s;
-  // Group jobs by dimension into launches of at most kEncodeJobsPerLaunch.
-  std::map<int, std::vector<size_t>> by_dim;
+  // Group jobs by dimension and bulk-encoder kind into launches of at most
+  // kEncodeJobsPerLaunch.
+  std::map<std::pair<int, int>, std::vector<size_t>> by_kind;
   for (size_t i = 0; i < n_jobs; ++i)
-    if (jobs[i].rows > 0) by_dim[jobs[i].tables->info.dim].push_back(i);
-  for (auto &kv : by_dim) {
+    if (jobs[i].rows > 0) {
+      const bgtq_tables *t = jobs[i].tables;
+      by_kind[{t->info.dim, encode_bulk_kind(t->h())}].push_back(i);
+    }
+  for (auto &kv : by_kind) {
+    const int dim = kv.first.first, kind = kv.first.second;
     const std::vector<size_t> &idx = kv.second;
     for (size_t b = 0; b < idx.size(); b += kEncodeJobsPerLaunch) {
       EncodeLaunch L{};
       int64_t max_rows = 0, total_rows = 0;
-      int lds = 0;
+      int lds = 0, lut_max = 0, books_max = 0;
       for (size_t k = b; k < std::min(idx.size(), b + kEncodeJobsPerLaunch); ++k) {
         const bgtq_encode_job &j = jobs[idx[k]];
         EncodeJobDev &J = L.jobs[L.n_jobs++];
         J.t = j.tables->dev();
         J.src = j.src;
-        J.src_stride = j.src_row_stride;
+        J.src_stride = (int32_t)j.src_row_stride;
         J.rows = j.rows;
         J.packed = j.packed;
         J.norms = j.norms;
@@ -696,20 +722,25 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
         max_rows = std::max(max_rows, j.rows);
         total_rows += j.rows;
         const bgtq_tables_info &ti = j.tables->info;
-        lds = std::max(lds, encode_wave_lds_bytes(kv.first, ti.n_codebooks * 256, ti.n_books * ti.max_centroids));
+        lds = std::max(lds, encode_wave_lds_bytes(dim, ti.n_codebooks * 256, ti.n_books * ti.max_centroids));
+        lut_max = std::max(lut_max, ti.n_codebooks * 256);
+        books_max = std::max(books_max, ti.n_books * ti.max_centroids);
       }
+      const bool src_f32 = src_dtype == BGTQ_DTYPE_F32;
       if (lds <= 160 * 1024 && total_rows < kEncodeWaveMaxRows) {
         // Few rows (a decode step's appended tokens): one wave per row, each
         // wave striding over enough rows to keep about sixteen waves per
-        // compute unit busy. Bulk encodes keep one thread per row.
+        // compute unit busy.
         const int64_t target_waves = 16 * (int64_t)device_cus();
         const int64_t rows_per_wave = std::max<int64_t>(1, (total_rows + target_waves - 1) / target_waves);
         const int64_t wgs = std::max<int64_t>(1, (max_rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave));
-        HIP_TRY(launch_encode_wave(L, kv.first, src_dtype == BGTQ_DTYPE_F32, (int)std::min<int64_t>(wgs, 65535), lds,
-                                   ctx->stream),
+        HIP_TRY(launch_encode_wave(L, dim, src_f32, (int)std::min<int64_t>(wgs, 65535), lds, ctx->stream),
                 "encode launch");
+      } else if (kind && encode_bulk_lds_bytes(kind, lut_max, books_max) <= 64 * 1024) {
+        // Bulk encodes of layout-B-shaped tables: thread per row, structure at compile time.
+        HIP_TRY(launch_encode_bulk(L, kind, src_f32, max_rows, lut_max, books_max, ctx->stream), "encode launch");
       } else {
-        HIP_TRY(launch_encode(L, kv.first, src_dtype == BGTQ_DTYPE_F32, max_rows, ctx->stream), "encode launch");
+        HIP_TRY(launch_encode(L, dim, src_f32, max_rows, ctx->stream), "encode launch");
       }
     }
   }
@@ -891,27 +922,17 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) {
 }
 
 // ---------------------------------------------------------------- chunked prefill
-struct PrefillWorkspace {
-  size_t counters, qr, part, total;
-};
-
-static PrefillWorkspace prefill_ws(int64_t counters, int64_t queries, int dim, int splits) {
-  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
-  PrefillWorkspace w;
-  w.counters = 0;
-  w.qr = al(sizeof(uint32_t) * counters);
-  w.part = w.qr + al(sizeof(float) * queries * dim);
-  w.total = w.part + (splits > 1 ? al(sizeof(float) * queries * splits * (dim + 2)) : 0);
-  return w;
-}
-
 struct PrefillPlan {
-  int tiles, split_tokens, splits;
+  int tiles, tile_queries, split_tokens, splits;
+  size_t workspace;  // split partials: (m, l) then o per (query, split)
 };
 
-// Token splits: enough (tile, split) workgroups for about four per compute
-// unit over the causal half of the history, at least 128 tokens each and at
-// most kPrefillMaxSplits splits (the merge holds one split per lane).
+// Query tiles: four waves of one 16-query block each for small chunks (more
+// tiles to spread), of prefill_column_blocks(dim) blocks each for long ones
+// (the K operand rebuilt once per block serves more queries). Token splits:
+// enough (tile, split) workgroups for about two per compute unit over the
+// causal half of the history, at least 64 tokens each and at most
+// kPrefillMaxSplits splits.
 static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   if (!d) return fail(BGTQ_ERR_RANGE, "null descriptor");
   if (d->batch < 1 || d->rows < 1 || d->kv_heads < 1 || d->kv_heads > kMaxKvHeads || d->q_heads < d->kv_heads ||
@@ -933,18 +954,21 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   }
   if (!d->v || !d->q || !d->out || !d->starts) return fail(BGTQ_ERR_RANGE, "null v/q/out/starts");
   if (d->split_tokens < 0) return fail(BGTQ_ERR_RANGE, "negative split_tokens");
-  const int64_t G = d->q_heads / d->kv_heads;
-  plan->tiles = (int)((d->rows * G + prefill_tile_queries(d->dim) - 1) / prefill_tile_queries(d->dim));
+  const int64_t G = d->q_heads / d->kv_heads, nq = (int64_t)d->rows * G;
+  plan->tile_queries = nq >= 2048 ? 64 * prefill_column_blocks(d->dim) : 64;
+  plan->tiles = (int)((nq + plan->tile_queries - 1) / plan->tile_queries);
   const int64_t L = d->max_length;
   int64_t sp = d->split_tokens;
   if (sp == 0) {
     const int64_t units = (int64_t)d->batch * d->kv_heads * plan->tiles;
-    sp = std::max<int64_t>(128, units * (L / 2 + 1) / (4 * (int64_t)device_cus()));
+    sp = std::max<int64_t>(64, units * (L / 2 + 1) / (2 * (int64_t)device_cus()));
   }
   sp = std::max<int64_t>(sp, (L + kPrefillMaxSplits - 1) / kPrefillMaxSplits);
   sp = std::min<int64_t>((sp + 31) / 32 * 32, (L + 31) / 32 * 32);
   plan->split_tokens = (int)sp;
   plan->splits = (int)((L + sp - 1) / sp);
+  const int64_t queries = (int64_t)d->batch * d->rows * d->q_heads;
+  plan->workspace = plan->splits > 1 ? sizeof(float) * (size_t)(queries * plan->splits * (d->dim + 2)) : 0;
   return BGTQ_OK;
 }
 
@@ -952,8 +976,7 @@ bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *byte
   PrefillPlan plan{};
   if (bgtq_status s = plan_prefill(d, &plan)) return s;
   if (!bytes) return fail(BGTQ_ERR_RANGE, "null output");
-  const int64_t queries = (int64_t)d->batch * d->rows * d->q_heads;
-  *bytes = prefill_ws((int64_t)d->batch * d->kv_heads * plan.tiles, queries, d->dim, plan.splits).total;
+  *bytes = std::max<size_t>(plan.workspace, 256);
   return BGTQ_OK;
 }
 
@@ -961,15 +984,12 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
   PrefillPlan plan{};
   if (bgtq_status s = plan_prefill(d, &plan)) return s;
-  const int64_t queries = (int64_t)d->batch * d->rows * d->q_heads;
-  const PrefillWorkspace w = prefill_ws((int64_t)d->batch * d->kv_heads * plan.tiles, queries, d->dim, plan.splits);
-  if (!d->workspace || d->workspace_bytes < w.total)
-    return fail(BGTQ_ERR_RANGE, "workspace of %zu bytes required", w.total);
-  // The layout check and the query rotation use the decode parameter block:
-  // the chunk's rows act as batch * rows query sets of Hq heads.
+  if (plan.workspace && (!d->workspace || d->workspace_bytes < plan.workspace))
+    return fail(BGTQ_ERR_RANGE, "workspace of %zu bytes required", plan.workspace);
+  // The layout check shares the fused decode's requirements.
   DecodeParams dp{};
   for (int h = 0; h < d->kv_heads; ++h) dp.tables[h] = d->key_format == BGTQ_KEYS_PACKED ? d->tables[h]->dev() : nullptr;
-  dp.batch = d->batch * d->rows;
+  dp.batch = d->batch;
   dp.q_heads = d->q_heads;
   dp.kv_heads = d->kv_heads;
   dp.dim = d->dim;
@@ -993,10 +1013,8 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   if (!fast_layout(dp, d->tables, &fl, &nn, &sg))
     return fail(BGTQ_ERR_UNSUPPORTED, "prefill needs 16-byte aligned FP16 V/K/scales and a layout whose 32-dim "
                                       "K-steps each lie in one group and book (at most two groups)");
+  if (reinterpret_cast<uintptr_t>(d->q) & 15) return fail(BGTQ_ERR_RANGE, "q must be 16-byte aligned");
   if (bgtq_status s = ctx->use()) return s;
-  uint8_t *ws = static_cast<uint8_t *>(d->workspace);
-  float *qr = reinterpret_cast<float *>(ws + w.qr);
-  HIP_TRY(launch_rotate_q(dp, d->q, qr, ctx->stream), "rotate_q launch");
   PrefillParams p{};
   for (int h = 0; h < d->kv_heads; ++h) p.tables[h] = dp.tables[h];
   p.batch = d->batch;
@@ -1018,14 +1036,15 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   p.v = d->v;
   p.v_seq_stride = d->v_seq_stride;
   p.v_head_stride = d->v_head_stride;
-  p.qr = qr;
+  p.q = d->q;
+  p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
   p.starts = d->starts;
   p.max_length = (int32_t)d->max_length;
   p.split_tokens = plan.split_tokens;
   p.splits = plan.splits;
   p.tiles = plan.tiles;
-  p.counters = reinterpret_cast<uint32_t *>(ws + w.counters);
-  p.part = reinterpret_cast<float *>(ws + w.part);
+  p.tile_queries = plan.tile_queries;
+  p.part = static_cast<float *>(d->workspace);
   p.out = d->out;
   HIP_TRY(launch_prefill(p, fl, nn, sg, ctx->stream), "prefill launch");
   return BGTQ_OK;

@@ -9,7 +9,7 @@ namespace bgtq {
 constexpr int kMaxDim = 128;
 constexpr int kMaxGroups = 8;
 constexpr int kMaxKvHeads = 16;
-constexpr int kEncodeJobsPerLaunch = 24;
+constexpr int kEncodeJobsPerLaunch = 60;  // 56-byte jobs: the launch stays under 4 KB of kernel arguments
 
 // Device-resident calibration tables, built once on the host from the
 // reference's serialized tables (src/webgpu/layout.ts:24-31). Fixed header,
@@ -17,7 +17,7 @@ constexpr int kEncodeJobsPerLaunch = 24;
 struct DevTables {
   int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids, n_books, n_codebooks;
   int32_t gstart[kMaxGroups], gend[kMaxGroups], gsize[kMaxGroups];  // group ranges (head-perm order)
-  uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, total_bytes;
+  uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, off_rot_q, total_bytes;
   int32_t cent_exp;  // 2^cent_exp * max|centroid| <= 2^14: fp16 hi/lo split range for MFMA operands
   uint8_t perm[kMaxDim];      // head_perm
   uint8_t group_of[kMaxDim];
@@ -34,8 +34,14 @@ struct DevTables {
   //             uint32 pair_hi[256], pair_lo[256]  (entry = packed nibble byte:
   //                                                 low nibble in the low half)
   //             uint16 code_hi[256], code_lo[256]  (entry = byte code)
+  // [off_rot_q] the rotation with the head permutation folded in,
+  //             Rq[j][c] = R[j][i] for c = perm[i] (qr = Rq q), as fp16
+  //             (hi, lo) MFMA A operands: for 16-row tile n, 32-column step
+  //             s and lane l, 8 hi then 8 lo halves of
+  //             Rq[16 n + l % 16][32 s + 8 (l / 16) + 0..7] (kRotQBytes).
 };
 constexpr int kMfmaTableBytes = 3072;
+__host__ __device__ constexpr int rot_q_bytes(int dim) { return dim * dim * 4; }
 
 __host__ __device__ inline const uint8_t *tables_lut(const DevTables *t) {
   return reinterpret_cast<const uint8_t *>(t) + t->off_lut;
@@ -52,17 +58,21 @@ __host__ __device__ inline const float *tables_rot_t(const DevTables *t) {
 __host__ __device__ inline const uint8_t *tables_mfma(const DevTables *t) {
   return reinterpret_cast<const uint8_t *>(t) + t->off_mfma;
 }
+__host__ __device__ inline const uint8_t *tables_rot_q(const DevTables *t) {
+  return reinterpret_cast<const uint8_t *>(t) + t->off_rot_q;
+}
 
 struct EncodeJobDev {
   const DevTables *t;
   const void *src;
-  int64_t src_stride;  // elements
-  int64_t rows;
   uint8_t *packed;
   uint16_t *norms;
+  int64_t rows;
   int64_t dst_row0;
-  int64_t dst_step;  // destination row step per source row (>= 1)
+  int32_t src_stride;  // elements
+  int32_t dst_step;    // destination row step per source row (>= 1)
 };
+static_assert(sizeof(EncodeJobDev) == 56, "encode job layout");
 
 struct EncodeLaunch {
   EncodeJobDev jobs[kEncodeJobsPerLaunch];
@@ -103,7 +113,7 @@ struct DecodeParams {
 
 // Chunked-prefill attention of one layer (prefill.hip). Units are (sequence,
 // KV head); a unit's queries are its chunk's rows x G heads (qi = row*G + h),
-// tiled by prefill_tile_queries(dim) and split over token ranges.
+// tiled by tile_queries and split over token ranges.
 struct PrefillParams {
   const DevTables *tables[kMaxKvHeads];
   int32_t batch, rows, q_heads, kv_heads, dim, G;
@@ -116,19 +126,19 @@ struct PrefillParams {
   int64_t k_seq_stride, k_head_stride;  // elements
   const void *v;                        // FP16
   int64_t v_seq_stride, v_head_stride;  // elements
-  const float *qr;          // [B*rows*Hq*dim] rotated, permuted, scaled by 1/sqrt(dim)
+  const float *q;           // [B*rows*Hq*dim] queries
+  float inv_sqrt_d;
   const uint32_t *starts;   // [B] position of each chunk's first row
   int32_t max_length;       // tokens every K/V buffer holds; kernels clamp starts to max_length - rows
   int32_t split_tokens;     // multiple of 32
-  int32_t splits;           // ceil(max_length / split_tokens) <= 64
+  int32_t splits;           // ceil(max_length / split_tokens) <= kPrefillMaxSplits
   int32_t tiles;            // query tiles per unit
-  uint32_t *counters;       // [B*Hkv*tiles] split arrival counters: zero between launches
-  float *part;              // [B*rows*Hq*splits*(dim+2)] (m, l, o[dim])
+  int32_t tile_queries;     // 64 or 64 * prefill_column_blocks(dim)
+  float *part;              // (m, l) [B*rows*Hq*splits*2], then o [B*rows*Hq*splits*dim]
   float *out;               // [B*rows*Hq*dim]
 };
-// 16-query MFMA column blocks per wave of the prefill kernel, and queries per tile (four waves).
+// Most 16-query MFMA column blocks per wave of the prefill kernel (four waves per tile).
 __host__ __device__ constexpr int prefill_column_blocks(int dim) { return dim == 64 ? 4 : 2; }
-__host__ __device__ constexpr int prefill_tile_queries(int dim) { return 4 * 16 * prefill_column_blocks(dim); }
 constexpr int kPrefillMaxSplits = 64;
 
 // Structure of a layout the fused matrix-core decode handles: every 32-dim
@@ -148,6 +158,15 @@ hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64
 int encode_wave_lds_bytes(int dim, int lut_bytes, int book_floats);
 hipError_t launch_encode_wave(const EncodeLaunch &launch, int dim, int src_f32, int wgs_per_job, int lds_bytes,
                               hipStream_t stream);
+// Bulk thread-per-row encode (encode_bulk.hip) for layouts of two equal
+// contiguous groups with nibble codes in the first (layout B at d 64 / 128):
+// kind 1 (d=64) or 2 (d=128), 0 when the layout does not qualify. The launch
+// needs encode_bulk_lds_bytes of dynamic LDS for the largest LUT (bytes) and
+// book set (floats) among its jobs.
+int encode_bulk_kind(const DevTables *T);
+int encode_bulk_lds_bytes(int kind, int lut_bytes, int book_floats);
+hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int src_f32, int64_t max_rows, int lut_bytes,
+                              int book_floats, hipStream_t stream);
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
 int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_bytes, int norm_stride);
 hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream);
@@ -160,7 +179,8 @@ bool decode_fast_supported(int dim, int key_format, int nn, int sg);
 // Row bytes of the packed layout with nn leading nibble K-steps (no padding).
 int decode_fast_row_bytes(int dim, int nn);
 hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
-// Chunked prefill (prefill.hip), same layout requirements as the fused decode.
+// Chunked prefill (prefill.hip, the kernel and, with several splits, the
+// merge), same layout requirements as the fused decode.
 hipError_t launch_prefill(const PrefillParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
 hipError_t launch_reconstruct(const DevTables *t, const uint8_t *packed, const uint16_t *norms,
                               int64_t rows, float *out, hipStream_t stream);

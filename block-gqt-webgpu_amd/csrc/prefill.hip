@@ -13,21 +13,28 @@
 // LDS buffers shared by the four waves: packed codes, FP16 scales and FP16 V
 // go HBM -> LDS with buffer_load ... lds, each wave issuing a quarter of every
 // buffer, four buffers ahead of the one computed on, one barrier per 32-token
-// block. Each wave rebuilds the K operand from LDS lookup tables of fp16
-// (hi, lo) centroid splits once per 16-token x 32-dim step and reuses it for
-// its NCB column blocks: QK as 16x16x32 f16 MFMAs (hi*hi + lo*hi + hi*lo),
-// per-token group scales, the causal mask, an online softmax in the log2
-// domain and PV as MFMAs with V read transposed (ds_read_b64_tr_b16).
-// Splits whose tokens lie past every query of the tile exit at once; a tile
-// with one active split writes its output directly, otherwise the last
-// workgroup of the tile to arrive merges the (m, l, o) partials by
-// log-sum-exp.
+// block.
 //
-// Queries arrive rotated into the code domain and scaled by 1/sqrt(d)
-// (rotate_q_kernel): with k = ((c*s) @ R)[inv_perm] (the reconstruction of
+// The queries are rotated into the code domain in the prologue, on the matrix
+// cores: with k = ((c*s) @ R)[inv_perm] (the reconstruction of
 // src/reference/production_math.py:27-31), q.k = sum_g s_g sum_{j in g}
-// c_j[code_j] (R q[perm])_j. The arithmetic is that of
-// src/reference/attention.py:5-22 with causal positions.
+// c_j[code_j] qr_j where qr = Rq q and Rq is R with the head permutation
+// folded into its columns. qr^T = Rq q^T comes out of the MFMAs with lane
+// (gq, col) holding dims 16 n + 4 gq + r of query col; the QK K-steps use
+// that order (MFMA k = 8 gq + jv <-> dim 32 s + 16 (jv / 4) + 4 gq + jv % 4),
+// so the rotated queries are QK operands as they stand and the K operand is
+// gathered in the same order.
+//
+// Per 32-token block each wave rebuilds the K operand from LDS lookup tables
+// of fp16 (hi, lo) centroid splits once per 16-token x 32-dim step and reuses
+// it for its NCB column blocks: QK as 16x16x32 f16 MFMAs (hi*hi + lo*hi +
+// hi*lo), per-token group scales, the causal mask, an online softmax in the
+// log2 domain and PV as MFMAs with V read transposed (ds_read_b64_tr_b16).
+// Splits whose tokens lie past every query of the tile exit at once; a tile
+// with one active split writes its output directly, otherwise each split
+// stores an (m, l, o) partial and prefill_merge_kernel combines them by
+// log-sum-exp. The arithmetic is that of src/reference/attention.py:5-22 with
+// causal positions.
 #include <hip/hip_fp16.h>
 
 #include "bgtq_internal.h"
@@ -82,13 +89,36 @@ __device__ __forceinline__ void wait_blocks(int newer) {
   }
 }
 
+// Split of x * sc (sc a power of two) into fp16 hi (rounded toward zero) and lo halves.
+__device__ __forceinline__ void split_scaled(const float *x, float sc, half8 &hi, half8 &lo) {
+  u32x4 h4, l4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t h, l;
+    split2(x[2 * k] * sc, x[2 * k + 1] * sc, h, l);
+    h4[k] = h;
+    l4[k] = l;
+  }
+  hi = __builtin_bit_cast(half8, h4);
+  lo = __builtin_bit_cast(half8, l4);
+}
+
+// Exponent e with max * 2^e near 2^14 (fp16 hi/lo split range); 0 for max 0.
+__device__ __forceinline__ int split_exp(float mx) { return mx > 0.0f ? 14 - (int)ceilf(__builtin_log2f(mx)) : 0; }
+
+// The query's row of [B, rows, Hq] (outputs, partials).
+__device__ __forceinline__ int64_t query_row(int b, int rows, int Hq, int kv, int G, int qi) {
+  const int row = qi / G, h = qi - row * G;
+  return ((int64_t)b * rows + row) * Hq + kv * G + h;
+}
+
 // KF: 1 = packed codes, 0 = FP16 K rows. NN: leading nibble K-steps. SG:
-// K-steps in group 0. NCB: 16-query column blocks per wave.
-// Two waves per SIMD (at most 256 registers each): one wave's softmax overlaps
-// the other's matrix-core work.
+// K-steps in group 0. NCB: 16-query column blocks per wave. At least two
+// waves per SIMD (at most 256 registers each), so that one wave's softmax
+// overlaps another's matrix-core work; up to four for single-block tiles.
 template <int D, int KF, int NN, int SG, int NCB>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
-    PrefillParams p, FastLayout fl) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, NCB == 1 ? 4 : 2))) void
+prefill_kernel(PrefillParams p, FastLayout fl) {
   using Sl = PSlot<D, KF, NN>;
   constexpr int KS = Sl::KS, DT = Sl::DT, PR = Sl::PR, RB = Sl::RB, AHEAD = Sl::AHEAD;
   constexpr int QW = NCB * 16, QT = kWaves * QW;
@@ -131,9 +161,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int P = 64 * (wave * Sl::VW + kk) + lane, r = P / PR, c = P % PR;
     voff_rows[kk] = r * (2 * D) + ((c ^ swz<D>(r)) * 16);
   }
+  // Block i's descriptors start at its first token and cover its tokens inside
+  // the history: the hardware range check returns zeros past the end.
   auto issue = [&](int i) {
     const int c0 = t_lo + i * kChunk;
-    const uint32_t rest = (uint32_t)min(T_b - c0, kChunk);  // tokens of the block inside the history (> 0)
+    const uint32_t rest = (uint32_t)min(T_b - c0, kChunk);  // > 0: c0 < t_hi <= T_b
     uint8_t *sb = smem + (i % Sl::RING) * Sl::BYTES;
     const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
 #pragma unroll
@@ -159,8 +191,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     if (i < n_blocks) issue(i);
 
   // ---------------- prologue ----------------
-  // MFMA lookup tables of the K-steps' books into LDS (wave 0), this wave's
-  // query operands into registers, then one wait for everything.
+  // MFMA lookup tables of the K-steps' books into LDS (wave 0); this wave's
+  // queries rotated and split into QK operands. B operand of QK step s for
+  // column block cb: lane holds query col's dims 32 s + 4 gq + 0..3 and
+  // 32 s + 16 + 4 gq + 0..3.
   if (KF == 1 && wave == 0) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -170,48 +204,76 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       if (s < NN) dma16(rt, tabs + s * 2048 + 1024, 1024 + lane * 16, 0);
     }
   }
-  // B operand of QK for column block cb: lane holds qr[query col][32 s + 8 gq + 0..7].
   bool valid[NCB];
-  int64_t gqi[NCB];  // global query row of this lane's column query
-  f32x4 qv[NCB][KS][2];
-#pragma unroll
-  for (int cb = 0; cb < NCB; ++cb) {
-    const int qi = q0 + wave * QW + cb * 16 + col;
-    valid[cb] = qi < nq;
-    const int row = valid[cb] ? qi / G : 0, h = valid[cb] ? qi - row * G : 0;
-    gqi[cb] = ((int64_t)b * rows + row) * Hq + kv * G + h;
-    const f32x4 *src = reinterpret_cast<const f32x4 *>(p.qr + gqi[cb] * D);
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      qv[cb][s][0] = valid[cb] ? src[8 * s + 2 * gq] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      qv[cb][s][1] = valid[cb] ? src[8 * s + 2 * gq + 1] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-  }
-  const int ec = KF == 1 ? T->cent_exp : 0;
   half8 qhi[NCB][KS], qlo[NCB][KS];
   float kq[NCB];  // log2-domain logit = (sum_g s_g acc_g) * kq
   int lim[NCB];   // exclusive token end of this lane's column query inside the split
   int lim_min = t_hi;
+  const int ec = KF == 1 ? T->cent_exp : 0;
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
+    const int qi = q0 + wave * QW + cb * 16 + col;
+    valid[cb] = qi < nq;
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + query_row(b, rows, Hq, kv, G, valid[cb] ? qi : 0) * D);
+    float qv[D / 4];  // this lane's share of the query row
     float qmax = 0.0f;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) qmax = fmaxf(qmax, fmaxf(fabsf(qv[cb][s][0][k]), fabsf(qv[cb][s][1][k])));
-    qmax = col_max(qmax);
-    const int eq = qmax > 0.0f ? 14 - (int)ceilf(__builtin_log2f(qmax)) : 0;
-    const float qsc = __builtin_ldexpf(1.0f, eq);
+      for (int hh = 0; hh < 2; ++hh) {
+        // KF 1: natural order 32 s + 8 gq + 4 hh + 0..3 (the rotation's k order);
+        // KF 0: QK order 32 s + 16 hh + 4 gq + 0..3.
+        const f32x4 v = valid[cb] ? src[KF == 1 ? 8 * s + 2 * gq + hh : 8 * s + 4 * hh + gq]
+                                  : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-#pragma unroll
-      for (int jv = 0; jv < 8; ++jv) {
-        const float x = qv[cb][s][jv >> 2][jv & 3] * qsc;
-        qhi[cb][s][jv] = (_Float16)x;
-        qlo[cb][s][jv] = (_Float16)(x - (float)qhi[cb][s][jv]);
+        for (int k = 0; k < 4; ++k) {
+          qv[8 * s + 4 * hh + k] = v[k];
+          qmax = fmaxf(qmax, fabsf(v[k]));
+        }
       }
-    kq[cb] = __builtin_ldexpf(kLog2e, -(eq + ec));
-    const int qi = q0 + wave * QW + cb * 16 + col;
+    int eq = split_exp(col_max(qmax));
+    if (KF == 1) {
+      // qr^T = Rq q^T on the matrix cores (q and Rq split hi/lo, three MFMAs
+      // per step): D layout, lane holds rows j = 16 n + 4 gq + r of query col.
+      half8 bh[KS], bl[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) split_scaled(qv + 8 * s, __builtin_ldexpf(1.0f, eq), bh[s], bl[s]);
+      const u32x4 *rq = reinterpret_cast<const u32x4 *>(tables_rot_q(T));
+      f32x4 qr[DT];
+#pragma unroll
+      for (int n = 0; n < DT; ++n) {
+        qr[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const u32x4 *op = rq + ((n * KS + s) * 64 + lane) * 2;
+          const half8 ah = __builtin_bit_cast(half8, op[0]), al = __builtin_bit_cast(half8, op[1]);
+          qr[n] = mfma(ah, bh[s], qr[n]);
+          qr[n] = mfma(al, bh[s], qr[n]);
+          qr[n] = mfma(ah, bl[s], qr[n]);
+        }
+      }
+      float rmax = 0.0f;
+#pragma unroll
+      for (int n = 0; n < DT; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rmax = fmaxf(rmax, fabsf(qr[n][r]));
+      const int e2 = split_exp(col_max(rmax));
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        float x[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[r] = qr[2 * s][r];
+          x[4 + r] = qr[2 * s + 1][r];
+        }
+        split_scaled(x, __builtin_ldexpf(1.0f, e2), qhi[cb][s], qlo[cb][s]);
+      }
+      eq += e2;
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) split_scaled(qv + 8 * s, __builtin_ldexpf(1.0f, eq), qhi[cb][s], qlo[cb][s]);
+    }
+    kq[cb] = __builtin_ldexpf(kLog2e * p.inv_sqrt_d, -(eq + ec));
     lim[cb] = valid[cb] ? min(start + qi / G + 1, t_hi) : t_hi;
     lim_min = min(lim_min, lim[cb]);
   }
@@ -222,7 +284,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   __syncthreads();
 
   const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
-  const _Float16 *tb = reinterpret_cast<const _Float16 *>(tabs);
+  const uint16_t *tb = reinterpret_cast<const uint16_t *>(tabs);
   float m_run[NCB], l_run[NCB];
   f32x4 O[NCB][DT];
 #pragma unroll
@@ -258,10 +320,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const int g = s < SG ? 0 : 1;
+        // K operand, dims 32 s + 4 gq + 0..3 then 32 s + 16 + 4 gq + 0..3.
         if (KF == 1) {
           u32x4 hi, lo;
           if (s < NN) {
-            const uint32_t w = *reinterpret_cast<const uint32_t *>(kbuf + t * RB + 16 * s + 4 * gq);
+            // nibble step: packed bytes 2 gq, 2 gq + 1 and 8 + 2 gq, 9 + 2 gq (two dims each)
+            const uint8_t *row = kbuf + t * RB + 16 * s + 2 * gq;
+            const uint32_t w = (uint32_t)*reinterpret_cast<const uint16_t *>(row) |
+                               ((uint32_t)*reinterpret_cast<const uint16_t *>(row + 8) << 16);
             const uint32_t *t32 = tn + s * 512;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -270,17 +336,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
               lo[k] = t32[256 + e];
             }
           } else {
-            const u32x2 w = *reinterpret_cast<const u32x2 *>(kbuf + t * RB + 16 * NN + 32 * (s - NN) + 8 * gq);
-            const _Float16 *t16 = tb + s * 1024;
-            half8 h8, l8;
+            // byte step: codes 4 gq + 0..3 and 16 + 4 gq + 0..3
+            const uint8_t *row = kbuf + t * RB + 16 * NN + 32 * (s - NN) + 4 * gq;
+            const u32x2 w{*reinterpret_cast<const uint32_t *>(row), *reinterpret_cast<const uint32_t *>(row + 16)};
+            const uint16_t *t16 = tb + s * 1024;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              const uint32_t e = (w[k >> 2] >> (8 * (k & 3))) & 255u;
-              h8[k] = t16[e];
-              l8[k] = t16[256 + e];
+            for (int k = 0; k < 4; ++k) {
+              const uint32_t e0 = (w[k >> 1] >> (16 * (k & 1))) & 255u;
+              const uint32_t e1 = (w[k >> 1] >> (16 * (k & 1) + 8)) & 255u;
+              hi[k] = (uint32_t)t16[e0] | ((uint32_t)t16[e1] << 16);
+              lo[k] = (uint32_t)t16[256 + e0] | ((uint32_t)t16[256 + e1] << 16);
             }
-            hi = __builtin_bit_cast(u32x4, h8);
-            lo = __builtin_bit_cast(u32x4, l8);
           }
           const half8 ah = __builtin_bit_cast(half8, hi), al = __builtin_bit_cast(half8, lo);
 #pragma unroll
@@ -290,12 +356,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             acc[cb][g] = mfma(ah, qlo[cb][s], acc[cb][g]);
           }
         } else {
-          const int piece = 4 * s + gq;
-          const half8 a = *reinterpret_cast<const half8 *>(kbuf + t * (2 * D) + ((piece ^ swz<D>(t)) * 16));
+          // FP16 K rows: 8-byte halves of swizzled 16-byte pieces
+          const int p0 = 4 * s + (gq >> 1), p1 = p0 + 2, off = (gq & 1) * 8;
+          const u32x2 a0 = *reinterpret_cast<const u32x2 *>(kbuf + t * (2 * D) + ((p0 ^ swz<D>(t)) * 16) + off);
+          const u32x2 a1 = *reinterpret_cast<const u32x2 *>(kbuf + t * (2 * D) + ((p1 ^ swz<D>(t)) * 16) + off);
+          const half8 ah = __builtin_bit_cast(half8, u32x4{a0[0], a0[1], a1[0], a1[1]});
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) {
-            acc[cb][0] = mfma(a, qhi[cb][s], acc[cb][0]);
-            acc[cb][0] = mfma(a, qlo[cb][s], acc[cb][0]);
+            acc[cb][0] = mfma(ah, qhi[cb][s], acc[cb][0]);
+            acc[cb][0] = mfma(ah, qlo[cb][s], acc[cb][0]);
           }
         }
       }
@@ -384,8 +453,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   // ---------------- epilogue ----------------
   // O row 4 gq + r of block cb is query (cb, 4 gq + r); its (m, l) live in
-  // column lane 4 gq + r.
+  // column lane 4 gq + r. One active split: the output; else the partial
+  // (m, l) at part[(row * S + split) * 2] and o at part_o[(row * S + split) * D].
   const int S = p.splits;
+  float *part_o = p.part + (int64_t)p.batch * rows * Hq * S * 2;
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     const float l_tot = col_sum(l_run[cb]);
@@ -393,89 +464,105 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int r = 0; r < 4; ++r) {
       const int qr_lane = 4 * gq + r;
       const float lr = __shfl(l_tot, qr_lane, 64);
-      const bool ok = __shfl((int)valid[cb], qr_lane, 64) != 0;
-      const int64_t g_row = __shfl(gqi[cb], qr_lane, 64);
-      if (!ok) continue;
+      const int qi = q0 + wave * QW + cb * 16 + qr_lane;
+      if (qi >= nq) continue;
+      const int64_t g_row = query_row(b, rows, Hq, kv, G, qi);
       if (n_act == 1) {
         const float inv = 1.0f / lr;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) p.out[g_row * D + 16 * dt + col] = O[cb][dt][r] * inv;
       } else {
-        float *pp = p.part + (g_row * S + split) * (D + 2);
+        float *po = part_o + (g_row * S + split) * D;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) coherent_store(pp + 2 + 16 * dt + col, O[cb][dt][r] * (1.0f / kPScale));
+        for (int dt = 0; dt < DT; ++dt) po[16 * dt + col] = O[cb][dt][r] * (1.0f / kPScale);
       }
     }
     if (n_act > 1 && gq == 0 && valid[cb]) {
-      float *pp = p.part + (gqi[cb] * S + split) * (D + 2);
-      coherent_store(pp, m_run[cb]);
-      coherent_store(pp + 1, l_tot * (1.0f / kPScale));
+      const int64_t g_row = query_row(b, rows, Hq, kv, G, q0 + wave * QW + cb * 16 + col);
+      float *pm = p.part + (g_row * S + split) * 2;
+      pm[0] = m_run[cb];
+      pm[1] = l_tot * (1.0f / kPScale);
     }
   }
+}
+
+// LSE merge of the split partials of tiles with more than one active split:
+// one wave per query, lane s holding split s's (m, l), the o rows read
+// coalesced eight splits at a time.
+template <int D>
+__global__ __launch_bounds__(kThreads) void prefill_merge_kernel(PrefillParams p, int tile_queries) {
+  const int unit = blockIdx.y;
+  const int b = unit / p.kv_heads, kv = unit - b * p.kv_heads;
+  const int G = p.G, Hq = p.q_heads, rows = p.rows, nq = rows * G;
+  const int lane = threadIdx.x & 63;
+  const int qi = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (qi >= nq) return;
+  const int start = (int)min(p.starts[b], (uint32_t)(p.max_length - rows));
+  const int tile = qi / tile_queries;
+  const int q_last = min(nq, (tile + 1) * tile_queries) - 1;
+  const int e_tile = start + q_last / G + 1;
+  const int n_act = (e_tile + p.split_tokens - 1) / p.split_tokens;
   if (n_act == 1) return;
-  // Last workgroup of this tile to finish merges its splits. Every thread
-  // waits for its partial stores before the arrival is counted.
-  __shared__ int last;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  uint32_t *counter = p.counters + (int64_t)unit * p.tiles + tile;
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(n_act - 1);
-  __syncthreads();
-  if (!last) return;
-  // One wave per query: lane s holds split s's (m, l); the o rows are read
-  // coalesced, eight splits at a time.
+  const int S = p.splits;
+  const int64_t g_row = query_row(b, rows, Hq, kv, G, qi);
+  const float *part_o = p.part + (int64_t)p.batch * rows * Hq * S * 2 + g_row * S * D;
+  const float2 ml = lane < n_act ? reinterpret_cast<const float2 *>(p.part)[g_row * S + lane]
+                                 : float2{-INFINITY, 0.0f};
+  float M = ml.x;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  float w = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - M);
+  float L = w * ml.y;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
+  w = w / L;
   constexpr int DL = D / 64;  // output dims per lane
-  for (int qq = wave; qq < n_valid; qq += kWaves) {
-    const int qi = q0 + qq, row = qi / G, h = qi - row * G;
-    const int64_t g_row = ((int64_t)b * rows + row) * Hq + kv * G + h;
-    float *pp = p.part + g_row * S * (D + 2);
-    const float ms = lane < n_act ? coherent_load(pp + lane * (D + 2)) : -INFINITY;
-    const float ls = lane < n_act ? coherent_load(pp + lane * (D + 2) + 1) : 0.0f;
-    float M = ms;
+  float acc[DL];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    float w = ms == -INFINITY ? 0.0f : exp2f(ms - M);
-    float L = w * ls;
+  for (int e = 0; e < DL; ++e) acc[e] = 0.0f;
+  for (int s0 = 0; s0 < n_act; s0 += 8) {
+    float o[8][DL];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
-    w = w / L;
-    float acc[DL];
+    for (int k = 0; k < 8; ++k)
 #pragma unroll
-    for (int k = 0; k < DL; ++k) acc[k] = 0.0f;
-    for (int s0 = 0; s0 < n_act; s0 += 8) {
-      float o[8][DL];
+      for (int e = 0; e < DL; ++e) o[k][e] = s0 + k < n_act ? part_o[(s0 + k) * D + lane + 64 * e] : 0.0f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < 8; ++k) {
+      const float wk = __shfl(w, min(s0 + k, 63), 64);
 #pragma unroll
-        for (int e = 0; e < DL; ++e)
-          o[k][e] = s0 + k < n_act ? coherent_load(pp + (s0 + k) * (D + 2) + 2 + lane + 64 * e) : 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float wk = __shfl(w, min(s0 + k, 63), 64);
-#pragma unroll
-        for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[k][e], s0 + k < n_act ? wk : 0.0f, acc[e]);
-      }
+      for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[k][e], wk, acc[e]);
     }
-#pragma unroll
-    for (int e = 0; e < DL; ++e) p.out[g_row * D + lane + 64 * e] = acc[e];
   }
-  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int e = 0; e < DL; ++e) p.out[g_row * D + lane + 64 * e] = acc[e];
+}
+
+template <int D, int KF, int NN, int SG, int NCB>
+hipError_t launch_ncb(const PrefillParams &p, const FastLayout &fl, hipStream_t stream) {
+  constexpr int lds = PSlot<D, KF, NN>::LDS;
+  static const hipError_t allowed = hipFuncSetAttribute((const void *)prefill_kernel<D, KF, NN, SG, NCB>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (allowed != hipSuccess) {
+    (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
+    return allowed;
+  }
+  const unsigned units = (unsigned)(p.batch * p.kv_heads);
+  hipLaunchKernelGGL((prefill_kernel<D, KF, NN, SG, NCB>), dim3((unsigned)p.splits, (unsigned)p.tiles, units),
+                     dim3(kThreads), lds, stream, p, fl);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  const int nq = p.rows * p.G;
+  hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((nq + kWaves - 1) / kWaves), units), dim3(kThreads),
+                     0, stream, p, kWaves * 16 * NCB);
+  return hipGetLastError();
 }
 
 template <int D, int KF, int NN, int SG>
 hipError_t launch_one(const PrefillParams &p, const FastLayout &fl, hipStream_t stream) {
   constexpr int NCB = prefill_column_blocks(D);
-  constexpr int lds = PSlot<D, KF, NN>::LDS;
-  static const hipError_t allowed = hipFuncSetAttribute((const void *)prefill_kernel<D, KF, NN, SG, NCB>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  if (allowed != hipSuccess) {
-    (void)hipGetLastError();
-    return allowed;
-  }
-  dim3 grid((unsigned)p.splits, (unsigned)p.tiles, (unsigned)(p.batch * p.kv_heads));
-  hipLaunchKernelGGL((prefill_kernel<D, KF, NN, SG, NCB>), grid, dim3(kThreads), lds, stream, p, fl);
-  return hipGetLastError();
+  if (p.tile_queries == kWaves * 16) return launch_ncb<D, KF, NN, SG, 1>(p, fl, stream);
+  if (p.tile_queries == kWaves * 16 * NCB) return launch_ncb<D, KF, NN, SG, NCB>(p, fl, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace

@@ -214,9 +214,10 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d);
  * buffers already hold the chunk's own tokens (encode them first).
  *   q, out: [B, rows, Hq, dim] FP32 contiguous; query head h uses KV head h / G.
  *   starts: device uint32 [B], starts[b] + rows <= max_length (kernels clamp).
- *   v: FP16. Key formats, strides and the workspace contract (zero-filled
- *   before first use, left zeroed by every call, one stream per workspace)
- *   are those of bgtq_decode.
+ *   v: FP16. Key formats and strides are those of bgtq_decode.
+ *   workspace: device memory of at least bgtq_prefill_workspace_size() bytes
+ *   for the token splits' partial results (no initial contents needed);
+ *   calls sharing a workspace must be ordered on one stream.
  * Layouts: d 64 or 128, every 32-dim K-step of the head-perm order in one
  * group and one centroid book, at most two groups (layout B and FP16 K);
  * others return BGTQ_ERR_UNSUPPORTED. */

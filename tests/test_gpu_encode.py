@@ -194,3 +194,53 @@ def test_bulk_encode_bit_exact(device, oracle):
         bad = np.nonzero(np.any(got_p != ref_p, axis=1) | np.any(got_n != ref_n, axis=1))[0]
         assert bad.size == 0, f"{name}: {bad.size} rows differ, first {bad[:5]}"
         tables.destroy()
+
+
+def test_bulk_layout_b_encoder_bit_exact(device, oracle):
+    """Layout B tables (two equal groups, nibbles first) take the bulk encoder with the layout's structure
+    compiled in: FP16 and FP32 sources, interleaved heads (row stride above dim), an offset destination,
+    and a launch that also carries a job of another layout kind."""
+    import torch
+    import bgtq
+    from bgtq import batched, calibrate
+    rng = np.random.default_rng(123)
+    other = _layouts(oracle)[2][1]  # mixed_d64: the generic encoder in the same call
+    for dim in (64, 128):
+        p = calibrate.layout_b(dim)
+        print("bulk layout B", dim, flush=True)
+        rows, heads, row0 = 20000, 3, 5
+        k = _random_half_rows(rng, rows * heads, dim).reshape(rows, heads, dim)
+        tables = bgtq.Tables(device, p)
+        t_other = bgtq.Tables(device, other) if dim == 64 else None
+        try:
+            for src_kind in ("f16", "f32"):
+                if src_kind == "f16":
+                    src = torch.from_numpy(k.view(np.int16)).cuda()
+                else:
+                    src = torch.from_numpy(k.view(np.float16).astype(np.float32)).cuda()
+                packed = torch.zeros((heads, row0 + rows, p.rowBytes), dtype=torch.uint8, device="cuda")
+                norms = torch.zeros((heads, row0 + rows, p.normStride), dtype=torch.int16, device="cuda")
+                jobs = [dict(tables=tables, src=src[:, h], src_row_stride=heads * dim, rows=rows, packed=packed[h],
+                             norms=norms[h], dst_row0=row0) for h in range(heads)]
+                if t_other is not None:
+                    po = torch.zeros((rows, other.rowBytes), dtype=torch.uint8, device="cuda")
+                    no = torch.zeros((rows, other.normStride), dtype=torch.int16, device="cuda")
+                    jobs.append(dict(tables=t_other, src=src[:, 0], src_row_stride=heads * dim, rows=rows, packed=po,
+                                     norms=no))
+                batched.encode(device, jobs, src_kind)
+                device.synchronize()
+                for h in range(heads):
+                    ref_p, ref_n = oracle.encode_pack(_olayout(oracle, p), np.ascontiguousarray(k[:, h]))
+                    got_p = packed[h].cpu().numpy()
+                    got_n = norms[h].cpu().numpy().view(np.uint16)
+                    assert not got_p[:row0].any() and not got_n[:row0].any(), "rows before dst_row0 written"
+                    bad = np.nonzero(np.any(got_p[row0:] != ref_p, axis=1) | np.any(got_n[row0:] != ref_n, axis=1))[0]
+                    assert bad.size == 0, f"d={dim} {src_kind} head {h}: {bad.size} rows differ, first {bad[:5]}"
+                if t_other is not None:
+                    ref_p, ref_n = oracle.encode_pack(_olayout(oracle, other), np.ascontiguousarray(k[:, 0]))
+                    assert np.array_equal(po.cpu().numpy(), ref_p)
+                    assert np.array_equal(no.cpu().numpy().view(np.uint16), ref_n)
+        finally:
+            tables.destroy()
+            if t_other is not None:
+                t_other.destroy()
