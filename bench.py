@@ -360,6 +360,7 @@ def main():
     ap.add_argument("--sweep-splits", default="", help="comma list: time the decode at each split count and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the Qwen prompt-prefill measurements")
     ap.add_argument("--encode-only", action="store_true", help="only the SmolLM2 bulk K-encode measurement")
+    ap.add_argument("--prefill-chunks", default="0,32", help="with --prefill-only: chunk sizes (0 = whole prompt)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (HBM counter calibration)")
     a = ap.parse_args()
@@ -384,8 +385,11 @@ def main():
         print(json.dumps({"encode_smollm2_prefill": encode_throughput(dev, a.layout, max(a.steps, 5))}))
         return
     if a.prefill_only:
-        print(json.dumps({"qwen_prefill_4096": qwen_prefill(dev, a.steps, a.layout),
-                          "qwen_prefill_4096_chunk32": qwen_prefill(dev, 2, a.layout, chunk=32)}))
+        out = {}
+        for c in [int(x) for x in a.prefill_chunks.split(",")]:
+            out["qwen_prefill_4096" + (f"_chunk{c}" if c else "")] = qwen_prefill(dev, a.steps if not c else 2,
+                                                                                 a.layout, chunk=c)
+        print(json.dumps(out))
         return
     log("building workload ...")
     w = DecodeWorkload(dev, a.layout, splits=a.splits)

@@ -672,9 +672,9 @@ static int device_cus() {
   return cached[dev];
 }
 
-// Up to this many rows per launch the wave-per-row encoder (short latency per
-// row) runs; larger launches use the thread-per-row encoder (more rows per
-// instruction).
+// Below this many rows per launch the wave-per-row encoder (short latency per
+// row) runs; larger launches use a thread-per-row encoder (more rows per
+// instruction): the bulk one where the layout qualifies, else the generic one.
 constexpr int64_t kEncodeWaveMaxRows = 16384;
 
 // ---------------------------------------------------------------- batched entry points
@@ -727,6 +727,8 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
         books_max = std::max(books_max, ti.n_books * ti.max_centroids);
       }
       const bool src_f32 = src_dtype == BGTQ_DTYPE_F32;
+      const int wg = kind == 1 ? 256 : 128;
+      const bool bulk_ok = kind && encode_bulk_lds_bytes(kind, wg, lut_max, books_max) <= 64 * 1024;
       if (lds <= 160 * 1024 && total_rows < kEncodeWaveMaxRows) {
         // Few rows (a decode step's appended tokens): one wave per row, each
         // wave striding over enough rows to keep about sixteen waves per
@@ -736,9 +738,9 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
         const int64_t wgs = std::max<int64_t>(1, (max_rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave));
         HIP_TRY(launch_encode_wave(L, dim, src_f32, (int)std::min<int64_t>(wgs, 65535), lds, ctx->stream),
                 "encode launch");
-      } else if (kind && encode_bulk_lds_bytes(kind, lut_max, books_max) <= 64 * 1024) {
+      } else if (bulk_ok) {
         // Bulk encodes of layout-B-shaped tables: thread per row, structure at compile time.
-        HIP_TRY(launch_encode_bulk(L, kind, src_f32, max_rows, lut_max, books_max, ctx->stream), "encode launch");
+        HIP_TRY(launch_encode_bulk(L, kind, wg, src_f32, max_rows, lut_max, books_max, ctx->stream), "encode launch");
       } else {
         HIP_TRY(launch_encode(L, dim, src_f32, max_rows, ctx->stream), "encode launch");
       }

@@ -160,13 +160,14 @@ hipError_t launch_encode_wave(const EncodeLaunch &launch, int dim, int src_f32, 
                               hipStream_t stream);
 // Bulk thread-per-row encode (encode_bulk.hip) for layouts of two equal
 // contiguous groups with nibble codes in the first (layout B at d 64 / 128):
-// kind 1 (d=64) or 2 (d=128), 0 when the layout does not qualify. The launch
-// needs encode_bulk_lds_bytes of dynamic LDS for the largest LUT (bytes) and
-// book set (floats) among its jobs.
+// kind 1 (d=64) or 2 (d=128), 0 when the layout does not qualify. wg rows per
+// workgroup: 256 (d=64) or 128 (d=128). The launch needs
+// encode_bulk_lds_bytes of dynamic LDS for the largest LUT (bytes) and book
+// set (floats) among its jobs.
 int encode_bulk_kind(const DevTables *T);
-int encode_bulk_lds_bytes(int kind, int lut_bytes, int book_floats);
-hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int src_f32, int64_t max_rows, int lut_bytes,
-                              int book_floats, hipStream_t stream);
+int encode_bulk_lds_bytes(int kind, int wg, int lut_bytes, int book_floats);
+hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int wg, int src_f32, int64_t max_rows,
+                              int lut_bytes, int book_floats, hipStream_t stream);
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
 int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_bytes, int norm_stride);
 hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream);

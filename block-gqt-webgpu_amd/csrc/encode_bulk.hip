@@ -38,10 +38,10 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
-template <int D>
+template <int D, int WG>
 struct Bulk {
-  static constexpr int ROWS = D == 128 ? 128 : 256;  // rows (threads) per workgroup
-  static constexpr int SSTR = D + 2;                 // staged halfs per row: odd dword stride
+  static constexpr int ROWS = WG;     // rows (threads) per workgroup
+  static constexpr int SSTR = D + 2;  // staged halfs per row: odd dword stride
   static constexpr int STAGE = ROWS * SSTR * 2;
 };
 
@@ -78,14 +78,14 @@ __device__ __forceinline__ float tree_sum(F &&leaf) {
   return total;
 }
 
-template <int D, int NG, int NS, bool SRC_F32>
-__global__ __launch_bounds__(Bulk<D>::ROWS) void encode_bulk_kernel(EncodeLaunch launch, int lut_area) {
-  constexpr int ROWS = Bulk<D>::ROWS, SSTR = Bulk<D>::SSTR, GW = D / NG;
+template <int D, int NG, int NS, bool SRC_F32, int WG>
+__global__ __launch_bounds__(WG) void encode_bulk_kernel(EncodeLaunch launch, int lut_area) {
+  constexpr int ROWS = Bulk<D, WG>::ROWS, SSTR = Bulk<D, WG>::SSTR, GW = D / NG;
   constexpr int LOGICAL = NS / 2 + D - NS;  // packed bytes before padding
   static_assert(GW % 8 == 0 && NS % 8 == 0 && NS <= D && LOGICAL % 4 == 0, "layout");
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t *stage = reinterpret_cast<uint16_t *>(smem);
-  uint8_t *lut = smem + Bulk<D>::STAGE;
+  uint8_t *lut = smem + Bulk<D, WG>::STAGE;
   float *books = reinterpret_cast<float *>(lut + lut_area);
 
   const EncodeJobDev job = launch.jobs[blockIdx.y];
@@ -170,16 +170,15 @@ __global__ __launch_bounds__(Bulk<D>::ROWS) void encode_bulk_kernel(EncodeLaunch
   for (int g = NG; g < NSTR; ++g) nrow[g] = 0;
 }
 
-template <int D, int NG, int NS>
+template <int D, int NG, int NS, int WG>
 hipError_t launch_kind(const EncodeLaunch &launch, int src_f32, int64_t max_rows, int lut_area, int book_floats,
                        hipStream_t stream) {
-  const int lds = Bulk<D>::STAGE + lut_area + book_floats * 4;
-  dim3 grid((unsigned)((max_rows + Bulk<D>::ROWS - 1) / Bulk<D>::ROWS), (unsigned)launch.n_jobs);
+  const int lds = Bulk<D, WG>::STAGE + lut_area + book_floats * 4;
+  dim3 grid((unsigned)((max_rows + WG - 1) / WG), (unsigned)launch.n_jobs);
   if (src_f32)
-    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, true>), grid, dim3(Bulk<D>::ROWS), lds, stream, launch, lut_area);
+    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, true, WG>), grid, dim3(WG), lds, stream, launch, lut_area);
   else
-    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, false>), grid, dim3(Bulk<D>::ROWS), lds, stream, launch,
-                       lut_area);
+    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, false, WG>), grid, dim3(WG), lds, stream, launch, lut_area);
   return hipGetLastError();
 }
 
@@ -193,16 +192,19 @@ int encode_bulk_kind(const DevTables *T) {
   return d == 64 ? 1 : 2;
 }
 
-int encode_bulk_lds_bytes(int kind, int lut_bytes, int book_floats) {
+int encode_bulk_lds_bytes(int kind, int wg, int lut_bytes, int book_floats) {
   const int d = kind == 1 ? 64 : 128;
-  return (d == 64 ? Bulk<64>::STAGE : Bulk<128>::STAGE) + ((lut_bytes + 15) & ~15) + book_floats * 4;
+  return wg * (d + 2) * 2 + ((lut_bytes + 15) & ~15) + book_floats * 4;
 }
 
-hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int src_f32, int64_t max_rows, int lut_bytes,
-                              int book_floats, hipStream_t stream) {
+hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int wg, int src_f32, int64_t max_rows,
+                              int lut_bytes, int book_floats, hipStream_t stream) {
   const int lut_area = (lut_bytes + 15) & ~15;
-  if (kind == 1) return launch_kind<64, 2, 32>(launch, src_f32, max_rows, lut_area, book_floats, stream);
-  if (kind == 2) return launch_kind<128, 2, 64>(launch, src_f32, max_rows, lut_area, book_floats, stream);
+#define BGTQ_BULK(K, DD, NS, W) \
+  if (kind == K && wg == W) return launch_kind<DD, 2, NS, W>(launch, src_f32, max_rows, lut_area, book_floats, stream);
+  BGTQ_BULK(1, 64, 32, 256)
+  BGTQ_BULK(2, 128, 64, 128)
+#undef BGTQ_BULK
   return hipErrorInvalidValue;
 }
 

@@ -37,6 +37,8 @@
 // causal positions.
 #include <hip/hip_fp16.h>
 
+#include <type_traits>
+
 #include "bgtq_internal.h"
 #include "gfx950_common.h"
 
@@ -51,6 +53,9 @@ constexpr int kChunk = 32;  // tokens per block: two 16-token MFMA tiles
 constexpr int kRing = 6;    // shared LDS buffers: compute one, four in flight, one draining
 
 // One ring buffer: V block, K block, FP16 scales; every wave DMAs a quarter.
+// Packed-code kernels also hold the K-steps' centroid books (fp32) and two
+// buffers of built K operands. The ring is as deep as lets two workgroups
+// share a compute unit.
 template <int D, int KF, int NN>
 struct PSlot {
   static constexpr int KS = D / 32, DT = D / 16, PR = D / 8;
@@ -65,10 +70,12 @@ struct PSlot {
   static constexpr int NBYTES = KF == 1 ? kChunk * 4 : 0;
   static constexpr int BYTES = VBYTES + KBYTES + NBYTES;
   static constexpr int LW = VW + KW + (KF == 1 ? 1 : 0);  // DMA instructions per wave per block
-  static constexpr int RING = kRing;
+  static constexpr int BOOKS = KF == 1 ? KS * 1024 : 0;    // 256 fp32 centroids per K-step
+  static constexpr int KOP = KF == 1 ? 2 * 2 * KS * 2048 : 0;  // [buffer][u][s]: hi 1 KB, lo 1 KB
+  static constexpr int FIXED = BOOKS + KOP;
+  static constexpr int RING = 6 * BYTES + FIXED <= kLdsLimit / 2 ? 6 : 4 * BYTES + FIXED <= kLdsLimit / 2 ? 4 : 3;
   static constexpr int AHEAD = RING - 2;
-  static constexpr int TABLES = KF == 1 ? KS * 2048 : 0;
-  static constexpr int LDS = RING * BYTES + TABLES;
+  static constexpr int LDS = RING * BYTES + FIXED;
   static_assert(VI % kWaves == 0 && KQ % 16 == 0 && KBYTES % 16 == 0, "DMA split over four waves");
   static_assert(LDS <= kLdsLimit, "LDS of one workgroup");
   static_assert(AHEAD * LW < 64, "vmcnt range");
@@ -106,6 +113,15 @@ __device__ __forceinline__ void split_scaled(const float *x, float sc, half8 &hi
 // Exponent e with max * 2^e near 2^14 (fp16 hi/lo split range); 0 for max 0.
 __device__ __forceinline__ int split_exp(float mx) { return mx > 0.0f ? 14 - (int)ceilf(__builtin_log2f(mx)) : 0; }
 
+__device__ __forceinline__ float wave_max(float v) {
+  v = col_max(v);
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((uint16_t)bits)); }
+
 // The query's row of [B, rows, Hq] (outputs, partials).
 __device__ __forceinline__ int64_t query_row(int b, int rows, int Hq, int kv, int G, int qi) {
   const int row = qi / G, h = qi - row * G;
@@ -116,6 +132,13 @@ __device__ __forceinline__ int64_t query_row(int b, int rows, int Hq, int kv, in
 // K-steps in group 0. NCB: 16-query column blocks per wave. At least two
 // waves per SIMD (at most 256 registers each), so that one wave's softmax
 // overlaps another's matrix-core work; up to four for single-block tiles.
+//
+// Packed codes: the four waves build each block's K operand once, in LDS,
+// one block ahead of the one computed on: K'[t][d] = c_d * s_g(d)(t) *
+// 2^(ec - E) with 2^E bounding the block's FP16 scales, split into fp16 hi/lo
+// in the MFMA A-operand order. The group scales then ride inside the product
+// and a logit is acc * 2^(E - ec - eq) in the log2 domain (the queries carry
+// log2(e) / sqrt(d)).
 template <int D, int KF, int NN, int SG, int NCB>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, NCB == 1 ? 4 : 2))) void
 prefill_kernel(PrefillParams p, FastLayout fl) {
@@ -144,7 +167,9 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   const int t_lo = split * SP, t_hi = min(t_lo + SP, e_tile);
   const int n_blocks = (t_hi - t_lo + kChunk - 1) / kChunk;
   const DevTables *T = KF == 1 ? p.tables[kv] : nullptr;
-  uint8_t *tabs = smem + Sl::RING * Sl::BYTES;
+  float *books = reinterpret_cast<float *>(smem + Sl::RING * Sl::BYTES);
+  uint8_t *kop = smem + Sl::RING * Sl::BYTES + Sl::BOOKS;
+  auto slot = [&](int i) { return smem + (i % Sl::RING) * Sl::BYTES; };
 
   // ---------------- streams of this unit ----------------
   const _Float16 *v_base = static_cast<const _Float16 *>(p.v) + b * p.v_seq_stride + kv * p.v_head_stride;
@@ -166,7 +191,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   auto issue = [&](int i) {
     const int c0 = t_lo + i * kChunk;
     const uint32_t rest = (uint32_t)min(T_b - c0, kChunk);  // > 0: c0 < t_hi <= T_b
-    uint8_t *sb = smem + (i % Sl::RING) * Sl::BYTES;
+    uint8_t *sb = slot(i);
     const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
 #pragma unroll
     for (int kk = 0; kk < Sl::VW; ++kk) dma16(rV, sb + (wave * Sl::VW + kk) * 1024, voff_rows[kk], 0);
@@ -191,25 +216,26 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     if (i < n_blocks) issue(i);
 
   // ---------------- prologue ----------------
-  // MFMA lookup tables of the K-steps' books into LDS (wave 0); this wave's
-  // queries rotated and split into QK operands. B operand of QK step s for
-  // column block cb: lane holds query col's dims 32 s + 4 gq + 0..3 and
-  // 32 s + 16 + 4 gq + 0..3.
+  // Centroid books of the K-steps into LDS (wave 0, 256 floats per step);
+  // this wave's queries rotated, scaled by log2(e) / sqrt(d) and split into QK
+  // operands. B operand of QK step s for column block cb: lane holds query
+  // col's dims 32 s + 4 gq + 0..3 and 32 s + 16 + 4 gq + 0..3.
+  const int ec = KF == 1 ? T->cent_exp : 0;
   if (KF == 1 && wave == 0) {
+    const int mc = T->max_centroids;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const uint8_t *src = tables_mfma(T) + fl.book[s] * kMfmaTableBytes + (s < NN ? 0 : 2048);
-      const __amdgpu_buffer_rsrc_t rt = rsrc(src, s < NN ? 2048 : 1024);
-      dma16(rt, tabs + s * 2048, lane * 16, 0);
-      if (s < NN) dma16(rt, tabs + s * 2048 + 1024, 1024 + lane * 16, 0);
+      const __amdgpu_buffer_rsrc_t rb = rsrc(tables_books(T) + fl.book[s] * mc, (uint32_t)(min(mc, 256) * 4));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dma4(rb, reinterpret_cast<uint8_t *>(books + s * 256 + 64 * k), 256 * k + lane * 4, 0);
     }
   }
+  const float qscale = kLog2e * p.inv_sqrt_d;
   bool valid[NCB];
   half8 qhi[NCB][KS], qlo[NCB][KS];
-  float kq[NCB];  // log2-domain logit = (sum_g s_g acc_g) * kq
+  int eqs[NCB];   // logit = acc * 2^(E - ec - eqs)
   int lim[NCB];   // exclusive token end of this lane's column query inside the split
   int lim_min = t_hi;
-  const int ec = KF == 1 ? T->cent_exp : 0;
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     const int qi = q0 + wave * QW + cb * 16 + col;
@@ -227,8 +253,8 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          qv[8 * s + 4 * hh + k] = v[k];
-          qmax = fmaxf(qmax, fabsf(v[k]));
+          qv[8 * s + 4 * hh + k] = v[k] * qscale;
+          qmax = fmaxf(qmax, fabsf(qv[8 * s + 4 * hh + k]));
         }
       }
     int eq = split_exp(col_max(qmax));
@@ -273,7 +299,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) split_scaled(qv + 8 * s, __builtin_ldexpf(1.0f, eq), qhi[cb][s], qlo[cb][s]);
     }
-    kq[cb] = __builtin_ldexpf(kLog2e * p.inv_sqrt_d, -(eq + ec));
+    eqs[cb] = eq + ec;
     lim[cb] = valid[cb] ? min(start + qi / G + 1, t_hi) : t_hi;
     lim_min = min(lim_min, lim[cb]);
   }
@@ -283,8 +309,55 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   wait_vm<0>();
   __syncthreads();
 
-  const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
-  const uint16_t *tb = reinterpret_cast<const uint16_t *>(tabs);
+  // Builds block i's K operand into buffer i & 1; returns E (2^E >= every
+  // FP16 scale of the block). Thread (wave w, lane) builds the (u, s) steps
+  // w + 4 k: token 16 u + col, dims 32 s + 4 gq + 0..3 and 32 s + 16 + 4 gq + 0..3.
+  auto build = [&](int i) -> int {
+    if constexpr (KF == 1) {
+      const uint8_t *kraw = slot(i) + Sl::VBYTES;
+      const uint32_t *nrm = reinterpret_cast<const uint32_t *>(kraw + Sl::KBYTES);
+      const uint32_t nw = nrm[lane & 31];
+      const float smax = wave_max(SG < KS ? fmaxf(h2f(nw & 0xffffu), h2f(nw >> 16)) : h2f(nw & 0xffffu));
+      const int E = smax > 0.0f ? (int)ceilf(__builtin_log2f(smax)) : 0;
+      uint8_t *kb = kop + (i & 1) * (2 * KS * 2048);
+#pragma unroll
+      for (int k = 0; k < 2 * KS / kWaves; ++k) {
+        const int combo = wave + kWaves * k, u = combo / KS, s = combo - u * KS;
+        const int t = 16 * u + col;
+        const uint32_t nt = nrm[t];
+        const float F = __builtin_ldexpf(s < SG ? h2f(nt & 0xffffu) : h2f(nt >> 16), ec - E);
+        uint32_t e[8];
+        if (s < NN) {
+          const uint8_t *row = kraw + t * RB + 16 * s + 2 * gq;
+          const uint32_t w = (uint32_t)*reinterpret_cast<const uint16_t *>(row) |
+                             ((uint32_t)*reinterpret_cast<const uint16_t *>(row + 8) << 16);
+#pragma unroll
+          for (int k2 = 0; k2 < 8; ++k2) e[k2] = (w >> (4 * k2)) & 15u;
+        } else {
+          const uint8_t *row = kraw + t * RB + 16 * NN + 32 * (s - NN) + 4 * gq;
+          const uint32_t w0 = *reinterpret_cast<const uint32_t *>(row), w1 = *reinterpret_cast<const uint32_t *>(row + 16);
+#pragma unroll
+          for (int k2 = 0; k2 < 4; ++k2) {
+            e[k2] = (w0 >> (8 * k2)) & 255u;
+            e[4 + k2] = (w1 >> (8 * k2)) & 255u;
+          }
+        }
+        float v[8];
+#pragma unroll
+        for (int k2 = 0; k2 < 8; ++k2) v[k2] = books[s * 256 + e[k2]] * F;
+        half8 hi, lo;
+        split_scaled(v, 1.0f, hi, lo);
+        uint8_t *dst = kb + (u * KS + s) * 2048 + lane * 16;
+        *reinterpret_cast<half8 *>(dst) = hi;
+        *reinterpret_cast<half8 *>(dst + 1024) = lo;
+      }
+      return E;
+    } else {
+      return 0;
+    }
+  };
+  int E_cur = n_blocks > 0 ? build(0) : 0;
+
   float m_run[NCB], l_run[NCB];
   f32x4 O[NCB][DT];
 #pragma unroll
@@ -297,119 +370,66 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   const int trow = 4 * gq + (col >> 2);
   const int tpiece = (col & 3) >> 1, thalf = (col & 1) * 8;
 
-  for (int i = 0; i < n_blocks; ++i) {
+  // One 32-token block: QK, mask (tail blocks only), online softmax, PV.
+  auto compute = [&](int i, auto masked) {
+    constexpr bool MASK = decltype(masked)::value;
     const int c0 = t_lo + i * kChunk;
-    // Block i + AHEAD goes to the buffer of block i - 2, which every wave
-    // finished before the barrier of iteration i - 1.
-    if (i + AHEAD < n_blocks) issue(i + AHEAD);
-    wait_blocks<Sl::LW, AHEAD>(min(n_blocks - 1 - i, AHEAD));
-    __syncthreads();  // every wave's quarter of block i has landed
-    const uint8_t *sb = smem + (i % Sl::RING) * Sl::BYTES;
-    const uint8_t *kbuf = sb + Sl::VBYTES;
-
-    float x[NCB][8];
+    const uint8_t *sb = slot(i);
+    f32x4 acc[NCB][2];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) acc[cb][0] = acc[cb][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      f32x4 acc[NCB][2];
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) {
-        acc[cb][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        acc[cb][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-      const int t = 16 * u + col;  // A-operand row (token) of this lane
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const int g = s < SG ? 0 : 1;
-        // K operand, dims 32 s + 4 gq + 0..3 then 32 s + 16 + 4 gq + 0..3.
-        if (KF == 1) {
-          u32x4 hi, lo;
-          if (s < NN) {
-            // nibble step: packed bytes 2 gq, 2 gq + 1 and 8 + 2 gq, 9 + 2 gq (two dims each)
-            const uint8_t *row = kbuf + t * RB + 16 * s + 2 * gq;
-            const uint32_t w = (uint32_t)*reinterpret_cast<const uint16_t *>(row) |
-                               ((uint32_t)*reinterpret_cast<const uint16_t *>(row + 8) << 16);
-            const uint32_t *t32 = tn + s * 512;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              const uint32_t e = (w >> (8 * k)) & 255u;
-              hi[k] = t32[e];
-              lo[k] = t32[256 + e];
-            }
-          } else {
-            // byte step: codes 4 gq + 0..3 and 16 + 4 gq + 0..3
-            const uint8_t *row = kbuf + t * RB + 16 * NN + 32 * (s - NN) + 4 * gq;
-            const u32x2 w{*reinterpret_cast<const uint32_t *>(row), *reinterpret_cast<const uint32_t *>(row + 16)};
-            const uint16_t *t16 = tb + s * 1024;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              const uint32_t e0 = (w[k >> 1] >> (16 * (k & 1))) & 255u;
-              const uint32_t e1 = (w[k >> 1] >> (16 * (k & 1) + 8)) & 255u;
-              hi[k] = (uint32_t)t16[e0] | ((uint32_t)t16[e1] << 16);
-              lo[k] = (uint32_t)t16[256 + e0] | ((uint32_t)t16[256 + e1] << 16);
-            }
-          }
-          const half8 ah = __builtin_bit_cast(half8, hi), al = __builtin_bit_cast(half8, lo);
+        if constexpr (KF == 1) {
+          const uint8_t *src = kop + (i & 1) * (2 * KS * 2048) + (u * KS + s) * 2048 + lane * 16;
+          const half8 ah = *reinterpret_cast<const half8 *>(src), al = *reinterpret_cast<const half8 *>(src + 1024);
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) {
-            acc[cb][g] = mfma(ah, qhi[cb][s], acc[cb][g]);
-            acc[cb][g] = mfma(al, qhi[cb][s], acc[cb][g]);
-            acc[cb][g] = mfma(ah, qlo[cb][s], acc[cb][g]);
+            acc[cb][u] = mfma(ah, qhi[cb][s], acc[cb][u]);
+            acc[cb][u] = mfma(al, qhi[cb][s], acc[cb][u]);
+            acc[cb][u] = mfma(ah, qlo[cb][s], acc[cb][u]);
           }
         } else {
           // FP16 K rows: 8-byte halves of swizzled 16-byte pieces
+          const uint8_t *kbuf = sb + Sl::VBYTES;
+          const int t = 16 * u + col;
           const int p0 = 4 * s + (gq >> 1), p1 = p0 + 2, off = (gq & 1) * 8;
           const u32x2 a0 = *reinterpret_cast<const u32x2 *>(kbuf + t * (2 * D) + ((p0 ^ swz<D>(t)) * 16) + off);
           const u32x2 a1 = *reinterpret_cast<const u32x2 *>(kbuf + t * (2 * D) + ((p1 ^ swz<D>(t)) * 16) + off);
           const half8 ah = __builtin_bit_cast(half8, u32x4{a0[0], a0[1], a1[0], a1[1]});
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) {
-            acc[cb][0] = mfma(ah, qhi[cb][s], acc[cb][0]);
-            acc[cb][0] = mfma(ah, qlo[cb][s], acc[cb][0]);
+            acc[cb][u] = mfma(ah, qhi[cb][s], acc[cb][u]);
+            acc[cb][u] = mfma(ah, qlo[cb][s], acc[cb][u]);
           }
         }
       }
-      // logits of this lane: query col of each block, tokens c0 + 16u + 4gq + r
-      u32x4 nr{0u, 0u, 0u, 0u};
-      if (KF == 1) nr = *reinterpret_cast<const u32x4 *>(kbuf + Sl::KBYTES + (16 * u + 4 * gq) * 4);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s0 = 1.0f, s1 = 1.0f;
-        if (KF == 1) {
-          s0 = __half2float(__ushort_as_half((uint16_t)(nr[r] & 0xffffu)));
-          s1 = __half2float(__ushort_as_half((uint16_t)(nr[r] >> 16)));
-        }
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-          float v;
-          if (KF == 1 && SG < KS) v = __builtin_fmaf(s1, acc[cb][1][r], s0 * acc[cb][0][r]);
-          else v = s0 * acc[cb][0][r];
-          x[cb][4 * u + r] = v * kq[cb];
-        }
-      }
     }
-    if (c0 + kChunk > lim_min) {
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
-          x[cb][j] = tok < lim[cb] ? x[cb][j] : -INFINITY;
-        }
-    }
-    // online softmax (log2 domain) per column query, then P as hi/lo A operands
     half8 pha[NCB], pla[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
-      const float *xc = x[cb];
-      const float mloc = fmaxf(fmaxf(fmaxf(xc[0], xc[1]), fmaxf(xc[2], xc[3])),
-                               fmaxf(fmaxf(xc[4], xc[5]), fmaxf(xc[6], xc[7])));
-      const float m_new = fmaxf(m_run[cb], col_max(mloc));
+      // raw logits of query col: tokens c0 + 16u + 4gq + r
+      float xr[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xr[j] = acc[cb][j >> 2][j & 3];
+        if constexpr (MASK) {
+          const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
+          xr[j] = tok < lim[cb] ? xr[j] : -INFINITY;
+        }
+      }
+      const float C = __builtin_ldexpf(1.0f, E_cur - eqs[cb]);
+      const float mloc = fmaxf(fmaxf(fmaxf(xr[0], xr[1]), fmaxf(xr[2], xr[3])),
+                               fmaxf(fmaxf(xr[4], xr[5]), fmaxf(xr[6], xr[7])));
+      const float m_new = fmaxf(m_run[cb], col_max(mloc) * C);
       const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[cb] - m_new);
-      const float mb = (m_new == -INFINITY ? 0.0f : m_new) - 15.0f;
+      const float nmb = 15.0f - (m_new == -INFINITY ? 0.0f : m_new);
       float pr[8], psum = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        pr[j] = __builtin_amdgcn_exp2f(xc[j] - mb);
+        pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(xr[j], C, nmb));
         psum += pr[j];
       }
       l_run[cb] = __builtin_fmaf(l_run[cb], alpha, psum);
@@ -449,6 +469,21 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         O[cb][dt] = mfma(pla[cb], vb, O[cb][dt]);
       }
     }
+  };
+
+  for (int i = 0; i < n_blocks; ++i) {
+    // Block i + AHEAD goes to the buffer of block i - 2, whose V every wave
+    // read before the barrier of iteration i - 1. Wait for block i + 1
+    // (built below); block i has landed already.
+    if (i + AHEAD < n_blocks) issue(i + AHEAD);
+    if (i + 1 < n_blocks) wait_blocks<Sl::LW, AHEAD - 1>(min(n_blocks - 2 - i, AHEAD - 1));
+    // Block i + 1 visible to all waves; block i's K operand (built last
+    // iteration) complete; every wave done with the operand buffer of i - 1.
+    __syncthreads();
+    const int E_next = i + 1 < n_blocks ? build(i + 1) : 0;
+    if (t_lo + i * kChunk + kChunk > lim_min) compute(i, std::true_type{});
+    else compute(i, std::false_type{});
+    E_cur = E_next;
   }
 
   // ---------------- epilogue ----------------

@@ -199,7 +199,8 @@ def test_bulk_encode_bit_exact(device, oracle):
 def test_bulk_layout_b_encoder_bit_exact(device, oracle):
     """Layout B tables (two equal groups, nibbles first) take the bulk encoder with the layout's structure
     compiled in: FP16 and FP32 sources, interleaved heads (row stride above dim), an offset destination,
-    and a launch that also carries a job of another layout kind."""
+    a launch that also carries a job of another layout kind, and at d=64 a launch large enough for
+    the wide (256-row) workgroups."""
     import torch
     import bgtq
     from bgtq import batched, calibrate
@@ -208,7 +209,7 @@ def test_bulk_layout_b_encoder_bit_exact(device, oracle):
     for dim in (64, 128):
         p = calibrate.layout_b(dim)
         print("bulk layout B", dim, flush=True)
-        rows, heads, row0 = 20000, 3, 5
+        rows, heads, row0 = (90000 if dim == 64 else 20000), 3, 5
         k = _random_half_rows(rng, rows * heads, dim).reshape(rows, heads, dim)
         tables = bgtq.Tables(device, p)
         t_other = bgtq.Tables(device, other) if dim == 64 else None
