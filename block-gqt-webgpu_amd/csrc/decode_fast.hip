@@ -10,10 +10,11 @@
 //             packed byte (two dims), for byte K-steps one entry per code.
 //   main loop each wave streams 32-token chunks of packed codes, FP16 scales
 //             and FP16 V straight from HBM into a three-deep ring of LDS
-//             buffers with buffer_load ... lds (no VGPR staging), two chunks
-//             ahead of the one it computes on. Reads past the sequence's
-//             length return zeros, so the tail needs no clamping. From LDS it
-//             rebuilds the K operand through the tables, runs QK as 16x16x32
+//             buffers with buffer_load ... lds (no VGPR staging, non-temporal:
+//             every byte is read once), two chunks ahead of the one it
+//             computes on. Reads past the sequence's length return zeros, so
+//             the tail needs no clamping. From LDS it rebuilds the K
+//             operand through the tables, runs QK as 16x16x32
 //             f16 MFMAs (hi*hi + lo*hi + hi*lo, FP32-level logits), an online
 //             softmax in the log2 domain, and PV as MFMAs with the V operand
 //             read transposed by ds_read_b64_tr_b16. V rows (and FP16 K rows)
@@ -131,20 +132,20 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     uint8_t *sb = slot_base(i % Sl::RING);
     const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
 #pragma unroll
-    for (int k = 0; k < VI; ++k) dma16(rV, sb + k * 1024, voff_rows[k], 0);
+    for (int k = 0; k < VI; ++k) dma16<kStream>(rV, sb + k * 1024, voff_rows[k], 0);
     uint8_t *kb = sb + Gm::VBYTES;
     if (KF == 1) {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * RB, rest * RB);
       const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * 2, rest * 4);
 #pragma unroll
       for (int k = 0; k < KI; ++k) {
-        if (k + 1 < KI || Sl::KLAST == 64 || lane < Sl::KLAST) dma16(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+        if (k + 1 < KI || Sl::KLAST == 64 || lane < Sl::KLAST) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
       }
-      if (lane < kChunk) dma4(rN, kb + Sl::KBYTES, lane * 4, 0);
+      if (lane < kChunk) dma4<kStream>(rN, kb + Sl::KBYTES, lane * 4, 0);
     } else {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
 #pragma unroll
-      for (int k = 0; k < KI; ++k) dma16(rK, kb + k * 1024, voff_rows[k], 0);
+      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, voff_rows[k], 0);
     }
   };
   // The first AHEAD chunks stream in while the prologue runs; the last ring

@@ -28,13 +28,20 @@ constexpr int kRsrcWord3 = 0x00020000;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kRsrcWord3);
 }
+// Cache policy of a load: kStream marks data read once (the non-temporal
+// bit), so streaming K/V does not displace what the caches hold.
+constexpr int kCached = 0;
+constexpr int kStream = 2;
+
 // HBM -> LDS without VGPRs: lane i writes 16 (4) bytes at lds + 16 i (4 i).
 // Lanes whose offset lies past the descriptor's size write zeros.
+template <int POLICY = kCached>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, (int)voff, (int)soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, (int)voff, (int)soff, 0, POLICY);
 }
+template <int POLICY = kCached>
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, (int)voff, (int)soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, (int)voff, (int)soff, 0, POLICY);
 }
 
 // Reductions over the four 16-lane rows that share a column (lane % 16).
