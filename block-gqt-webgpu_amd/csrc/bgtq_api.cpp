@@ -369,8 +369,8 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   for (int b = 0; b < nb; ++b) {
     const float *c = cent + book_rows[b] * mc;
     uint8_t *tb = h + off_mfma + (size_t)kMfmaTableBytes * b;
-    uint32_t *pair_hi = reinterpret_cast<uint32_t *>(tb), *pair_lo = pair_hi + 256;
-    uint16_t *code_hi = reinterpret_cast<uint16_t *>(tb + 2048), *code_lo = code_hi + 256;
+    uint32_t *pair = reinterpret_cast<uint32_t *>(tb);         // [256][hi pair, lo pair]
+    uint32_t *code = reinterpret_cast<uint32_t *>(tb + 2048);  // [256] hi | lo << 16
     auto split = [&](int e, uint16_t *hi, uint16_t *lo) {
       const float x = e < mc ? c[e] * csc : 0.0f;
       *hi = f32_to_f16_rtz(x);
@@ -380,9 +380,11 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
       uint16_t h0, l0, h1, l1;
       split(e & 15, &h0, &l0);
       split(e >> 4, &h1, &l1);
-      pair_hi[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-      pair_lo[e] = (uint32_t)l0 | ((uint32_t)l1 << 16);
-      split(e, &code_hi[e], &code_lo[e]);
+      pair[2 * e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+      pair[2 * e + 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+      uint16_t ch, cl;
+      split(e, &ch, &cl);
+      code[e] = (uint32_t)ch | ((uint32_t)cl << 16);
     }
   }
   // Query rotation operands (prefill): Rq[j][perm[i]] = R[j][i], split like

@@ -31,9 +31,9 @@ struct DevTables {
   // [off_rot_t] float rotation transposed, Rt[i*dim+j] = R[j*dim+i]
   // [off_mfma]  per book, kMfmaTableBytes: the fp16 (hi, lo) split of
   //             centroid * 2^cent_exp as MFMA lookup tables,
-  //             uint32 pair_hi[256], pair_lo[256]  (entry = packed nibble byte:
-  //                                                 low nibble in the low half)
-  //             uint16 code_hi[256], code_lo[256]  (entry = byte code)
+  //             uint32 pair[256][2]: hi pair, lo pair (entry = packed
+  //                    nibble byte, low nibble in the low half of each pair)
+  //             uint32 code[256]: hi | lo << 16 (entry = byte code)
   // [off_rot_q] the rotation with the head permutation folded in,
   //             Rq[j][c] = R[j][i] for c = perm[i] (qr = Rq q), as fp16
   //             (hi, lo) MFMA A operands: for 16-row tile n, 32-column step

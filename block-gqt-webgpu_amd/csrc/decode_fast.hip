@@ -253,7 +253,6 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   __syncthreads();  // q staging (last ring slot) is dead
 
   const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
-  const _Float16 *tb = reinterpret_cast<const _Float16 *>(tabs);
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 O[DT];
 #pragma unroll
@@ -293,25 +292,23 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
           u32x4 hi, lo;
           if (s < NN) {
             const uint32_t w = *reinterpret_cast<const uint32_t *>(kbuf + t * RB + 16 * s + 4 * gq);
-            const uint32_t *t32 = tn + s * 512;
+            const u32x2 *t64 = reinterpret_cast<const u32x2 *>(tn + s * 512);  // [byte]: hi pair, lo pair
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              const uint32_t e = (w >> (8 * k)) & 255u;
-              hi[k] = t32[e];
-              lo[k] = t32[256 + e];
+              const u32x2 v = t64[(w >> (8 * k)) & 255u];
+              hi[k] = v[0];
+              lo[k] = v[1];
             }
           } else {
             const u32x2 w = *reinterpret_cast<const u32x2 *>(kbuf + t * RB + 16 * NN + 32 * (s - NN) + 8 * gq);
-            const _Float16 *t16 = tb + s * 1024;
-            half8 h8, l8;
+            const uint32_t *t32 = tn + s * 512;  // [code]: hi | lo << 16
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              const uint32_t e = (w[k >> 2] >> (8 * (k & 3))) & 255u;
-              h8[k] = t16[e];
-              l8[k] = t16[256 + e];
+            for (int k = 0; k < 4; ++k) {
+              const uint32_t c0 = t32[(w[k >> 1] >> (16 * (k & 1))) & 255u];
+              const uint32_t c1 = t32[(w[k >> 1] >> (16 * (k & 1) + 8)) & 255u];
+              hi[k] = __builtin_amdgcn_perm(c1, c0, 0x05040100u);  // c0.hi, c1.hi
+              lo[k] = __builtin_amdgcn_perm(c1, c0, 0x07060302u);  // c0.lo, c1.lo
             }
-            hi = __builtin_bit_cast(u32x4, h8);
-            lo = __builtin_bit_cast(u32x4, l8);
           }
           const half8 ah = __builtin_bit_cast(half8, hi), al = __builtin_bit_cast(half8, lo);
           acc[u][g] = mfma(ah, qhi[s], acc[u][g]);
