@@ -8,9 +8,10 @@ from ._lib import (DeviceError, RangeError, StateError, UnsupportedError, LIB_PA
 from .layout import BlockGTQParameters, tables, validate_layout
 from .runtime import (CompressedKeys, Device, FP16Keys, PackedKeys, Tables, Values, append_count)
 from .attention import AttentionEngine, AttentionSession, OptimizedAttention
+from .calibration import Calibration
 
 lib()  # fail loudly at import when the native library is missing
 
 __all__ = ["BlockGTQParameters", "tables", "validate_layout", "Device", "Tables", "FP16Keys", "PackedKeys",
            "CompressedKeys", "Values", "append_count", "AttentionEngine", "AttentionSession",
-           "OptimizedAttention", "RangeError", "StateError", "DeviceError", "UnsupportedError", "LIB_PATH"]
+           "OptimizedAttention", "Calibration", "RangeError", "StateError", "DeviceError", "UnsupportedError", "LIB_PATH"]

@@ -35,7 +35,8 @@ class UnsupportedError(NotImplementedError):
 
 class TablesInfo(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("dim", "groups", "row_bytes", "norm_stride", "nibble_dims",
-                                             "max_centroids", "n_codebooks", "n_books")]
+                                             "max_centroids", "n_codebooks", "n_books")] + [
+        ("device_bytes", ctypes.c_uint64)]
 
 
 class Allocation(ctypes.Structure):

@@ -195,7 +195,7 @@ struct bgtq_attention {
 extern "C" {
 
 const char *bgtq_last_error(void) { return g_error.c_str(); }
-int32_t bgtq_abi_version(void) { return 1; }
+int32_t bgtq_abi_version(void) { return 2; }
 
 // ---------------------------------------------------------------- context
 bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
@@ -405,7 +405,8 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
           }
         }
   }
-  t->info = bgtq_tables_info{(int32_t)d, (int32_t)ng, (int32_t)rb, (int32_t)nstride, (int32_t)nib, (int32_t)mc, ncb, nb};
+  t->info = bgtq_tables_info{(int32_t)d, (int32_t)ng, (int32_t)rb, (int32_t)nstride, (int32_t)nib, (int32_t)mc, ncb, nb,
+                             (uint64_t)total};
   bgtq_status s = ctx->use();
   if (!s) s = t->blob.alloc(total, "K tables");
   if (!s) {

@@ -97,3 +97,17 @@ export class AttentionEngine {
   readonly device: Device;
   session(keys: KeyStore, values: Values, maxQueries?: number): AttentionSession;
 }
+
+/** src/model/calibration.ts: base is a directory with calibration.json and its payload. */
+export type CalibrationHead = {
+  tables: unknown; config: Uint32Array; table: Float32Array; ranges: Uint32Array; rowBytes: number; normStride: number;
+};
+export class Calibration {
+  static load(device: Device, adapter?: { layers: number; kvHeads: number }, base?: string,
+              modelRevision?: string): Promise<Calibration>;
+  readonly device: Device;
+  readonly sha256: string;
+  readonly heads: CalibrationHead[];
+  readonly allocations: { name: string; role: "tables"; bytes: number }[];
+  destroy(): void;
+}

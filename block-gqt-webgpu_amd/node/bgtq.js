@@ -212,7 +212,64 @@ class AttentionEngine {
   }
 }
 
+// ---- model calibration (src/model/calibration.ts:4-24) ---------------------
+// base is a directory holding calibration.json and its payload. Each head
+// keeps its host arrays and a device table set (tables) for the batched entry
+// points; the checks and messages are the reference's.
+class Calibration {
+  constructor(device, sha256) {
+    this.device = device; this.sha256 = sha256; this.heads = []; this.allocations = [];
+  }
+  static async load(device, adapter, base, modelRevision) {
+    const fs = require('fs');
+    const crypto = require('crypto');
+    base = base === undefined ? path.join(process.cwd(), 'fixtures', 'model') : base;
+    const m = JSON.parse(fs.readFileSync(path.join(base, 'calibration.json'), 'utf8'));
+    const file = fs.readFileSync(path.join(base, m.binary));
+    const payload = file.buffer.slice(file.byteOffset, file.byteOffset + file.byteLength);
+    const sha = crypto.createHash('sha256').update(file).digest('hex');
+    const expected = adapter ? adapter.layers * adapter.kvHeads : 90;
+    const expectedRevision = modelRevision !== undefined ? modelRevision
+      : (adapter ? undefined : '12fd25f77366fa6b3b4b768ec3050bf629380bac');
+    if (sha !== m.sha256 || m.heads.length !== expected || (expectedRevision && m.model_revision !== expectedRevision) ||
+        m.upstream_commit !== '3fe14e7d4b8a6c85402818f7e22052527ed42e93') {
+      throw new Error('Calibration mismatch');
+    }
+    const c = new Calibration(device, sha);
+    try {
+      for (let i = 0; i < expected; i++) {
+        const read = (name) => {
+          const a = m.arrays[`h${i}_${name}`];
+          if (!a || a.offset % 4 || a.offset + a.nbytes > payload.byteLength) throw new Error('Bad calibration descriptor');
+          return payload.slice(a.offset, a.offset + a.nbytes);
+        };
+        const config = new Uint32Array(read('config')), table = new Float32Array(read('table'));
+        const ranges = new Uint32Array(read('ranges'));
+        if (config[0] !== 64 || config[1] > 8 || ranges.length !== 128 || table.some((x) => !Number.isFinite(x))) {
+          throw new Error('Unsupported calibration');
+        }
+        for (let j = 0; j < 64; j++) {
+          for (let k = 0; k < 64; k++) {
+            if ((k < ranges[j * 2] || k >= ranges[j * 2 + 1]) && table[k * 64 + j] !== 0) throw new Error('Off-group rotation');
+          }
+        }
+        const handle = native.tablesCreate(device.handle, config, table);
+        c.heads.push({ tables: handle, config, table, ranges, rowBytes: config[2], normStride: config[3] });
+        c.allocations.push({ name: `head ${i} tables`, role: 'tables', bytes: native.tablesDeviceBytes(handle) });
+      }
+    } catch (e) {
+      c.destroy();
+      throw e;
+    }
+    return c;
+  }
+  destroy() {
+    for (const h of this.heads) if (h.tables) native.tablesDestroy(h.tables);
+    this.heads.forEach((h) => { h.tables = null; });
+  }
+}
+
 module.exports = {
   native, Device, requestDevice, DeviceView, readBuffer, validateLayout, tables, appendCount,
-  FP16Keys, PackedKeys, CompressedKeys, Values, OptimizedAttention, AttentionEngine, AttentionSession,
+  FP16Keys, PackedKeys, CompressedKeys, Values, OptimizedAttention, AttentionEngine, AttentionSession, Calibration,
 };

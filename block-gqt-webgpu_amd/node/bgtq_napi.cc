@@ -175,6 +175,15 @@ napi_value TablesCreate(napi_env env, napi_callback_info info) {
   BGTQ_TRY(env, bgtq_tables_create(static_cast<bgtq_context *>(handle(env, a.v[0])), ints, ni, fl, nf, &t));
   return wrap(env, t);
 }
+napi_value TablesDeviceBytes(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  bgtq_tables_info ti{};
+  BGTQ_TRY(env, bgtq_tables_info_get(static_cast<bgtq_tables *>(handle(env, a.v[0])), &ti));
+  napi_value v;
+  NAPI_TRY(env, napi_create_double(env, (double)ti.device_bytes, &v));
+  return v;
+}
 napi_value TablesDestroy(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 1)) return nullptr;
@@ -375,7 +384,8 @@ napi_value Init(napi_env env, napi_value exports) {
   } fns[] = {
       {"contextCreate", ContextCreate},       {"contextDestroy", ContextDestroy},
       {"contextSynchronize", ContextSynchronize}, {"tablesCreate", TablesCreate},
-      {"tablesDestroy", TablesDestroy},       {"fp16KeysCreate", Fp16KeysCreate},
+      {"tablesDestroy", TablesDestroy},       {"tablesDeviceBytes", TablesDeviceBytes},
+      {"fp16KeysCreate", Fp16KeysCreate},
       {"packedKeysCreate", PackedKeysCreate}, {"keysAppend", KeysAppend},
       {"keysReady", KeysReady},               {"keysLength", KeysLength},
       {"keysRead", KeysRead},                 {"keysReadFp16", KeysReadFp16},

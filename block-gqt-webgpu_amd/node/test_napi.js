@@ -92,6 +92,13 @@ async function main() {
   try { keys.ready(); } catch (e) { threw = e.message === 'K storage not ready'; }
   check(threw, 'empty store is not ready');
   keys.destroy();
+  // Model calibration (src/model/calibration.ts:7-21): 90 SmolLM2 heads on the device.
+  const cal = await bgtq.Calibration.load(device, undefined, path.join(FIXTURES, 'model'));
+  check(cal.heads.length === 90 && cal.allocations.every((x) => x.bytes > 0), 'calibration: 90 heads on the device');
+  check(cal.heads[1].rowBytes === 37 && cal.heads[1].normStride === 4, 'calibration: head 1 row geometry');
+  cal.destroy();
+  await rejects(() => bgtq.Calibration.load(device, { layers: 2, kvHeads: 3 }, path.join(FIXTURES, 'model')), Error,
+    'Calibration mismatch', 'calibration: wrong model geometry');
   device.destroy();
   console.log(failures ? `${failures} check(s) failed` : 'all N-API checks passed');
   process.exit(failures ? 1 : 0);

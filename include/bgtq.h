@@ -50,6 +50,7 @@ typedef struct {
 
 /* Thread-local message of the last failing call on this thread. */
 const char *bgtq_last_error(void);
+/* 2: bgtq_tables_info gained device_bytes. */
 int32_t bgtq_abi_version(void);
 
 /* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
@@ -77,6 +78,7 @@ typedef struct bgtq_tables bgtq_tables;
 typedef struct {
   int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids;
   int32_t n_codebooks, n_books; /* LUT rows; distinct centroid rows */
+  uint64_t device_bytes;        /* device memory the tables hold */
 } bgtq_tables_info;
 bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_t n_integer,
                                const float *floating, size_t n_floating, bgtq_tables **out);

@@ -245,3 +245,41 @@ def test_bulk_layout_b_encoder_bit_exact(device, oracle):
             tables.destroy()
             if t_other is not None:
                 t_other.destroy()
+
+
+def test_calibration_load_encodes_every_head(device, oracle):
+    """Calibration.load (src/model/calibration.ts:7-21) puts the 90 SmolLM2 heads on the device;
+    each head's tables then encode its KV head's post-RoPE rows bit for bit as the oracle does
+    with the same blob (the reference's tests/webgpu/model-codec-test.ts:13-21 on 3 rows per
+    head; here 37 rows, FP32 model-path source)."""
+    import torch
+    import bgtq
+    from bgtq import batched
+    cal = bgtq.Calibration.load(device, REF / "model")
+    try:
+        assert len(cal.heads) == 90 and len(cal.allocations) == 90
+        assert all(x["bytes"] > 0 for x in cal.allocations)
+        m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+        rng = np.random.default_rng(90)
+        rows, kvh = 37, 3
+        kr = (rng.standard_normal((rows, kvh, 64)) * 2.3).astype(np.float32)
+        src = torch.from_numpy(kr).cuda()
+        outs, jobs = [], []
+        for h, head in enumerate(cal.heads):
+            p = bgtq.BlockGTQParameters.from_serialized(a[f"h{h}_config"], a[f"h{h}_table"])
+            info = head.tables.info
+            assert (info["dim"], info["groups"], info["row_bytes"], info["norm_stride"]) == \
+                (64, p.groups, p.rowBytes, p.normStride) == (64, p.groups, head.row_bytes, head.norm_stride)
+            packed = torch.zeros((rows, p.rowBytes), dtype=torch.uint8, device="cuda")
+            norms = torch.zeros((rows, p.normStride), dtype=torch.int16, device="cuda")
+            outs.append((p, packed, norms))
+            jobs.append(dict(tables=head.tables, src=src[:, h % kvh], src_row_stride=kvh * 64, rows=rows,
+                             packed=packed, norms=norms, dst_row0=0))
+        batched.encode(device, jobs, "f32")
+        device.synchronize()
+        for h, (p, packed, norms) in enumerate(outs):
+            ref_p, ref_n = oracle.encode_pack(_olayout(oracle, p), kr[:, h % kvh].astype(np.float16).view(np.uint16))
+            np.testing.assert_array_equal(packed.cpu().numpy(), ref_p, err_msg=f"head {h}")
+            np.testing.assert_array_equal(norms.cpu().numpy().view(np.uint16), ref_n, err_msg=f"head {h}")
+    finally:
+        cal.destroy()

@@ -18,7 +18,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(bgtq.LIB_PATH))
     missing = [name for name in sorted(declared) if not hasattr(lib, name)]
     assert not missing, missing
-    assert lib.bgtq_abi_version() == 1
+    assert lib.bgtq_abi_version() == 2
 
 
 def test_no_device_is_reported_cleanly():
@@ -161,4 +161,115 @@ def test_node_addon_loads_without_a_device():
     assert r.returncode == 0, r.stderr
     import json
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert out == {"abi": 1, "miss": [], "missc": []}, out
+    assert out == {"abi": 2, "miss": [], "missc": []}, out
+
+
+def _tampered_calibration(tmp_path, edit_manifest=None, edit_payload=None):
+    """A copy of the committed SmolLM2 calibration with the manifest and/or payload changed
+    (the payload's sha256 is rewritten unless the manifest edit says otherwise)."""
+    import hashlib
+    import json
+    m = json.loads((REF / "model" / "calibration.json").read_text())
+    payload = bytearray((REF / "model" / m["binary"]).read_bytes())
+    if edit_payload:
+        edit_payload(m, payload)
+        m["sha256"] = hashlib.sha256(payload).hexdigest()
+    if edit_manifest:
+        edit_manifest(m)
+    (tmp_path / m["binary"]).write_bytes(bytes(payload))
+    (tmp_path / "calibration.json").write_text(json.dumps(m))
+    return tmp_path
+
+
+def test_calibration_loader_checks(oracle, tmp_path):
+    """Calibration.load's manifest and per-head checks (src/model/calibration.ts:8-18), with the
+    reference's messages, on the committed SmolLM2 calibration and tampered copies of it."""
+    import bgtq
+    from bgtq import calibration
+    m, sha, blobs = calibration.read(REF / "model")
+    _, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    assert len(blobs) == 90 and sha == m["sha256"]
+    for i, b in enumerate(blobs):
+        np.testing.assert_array_equal(b.config, a[f"h{i}_config"])
+        np.testing.assert_array_equal(b.table.view(np.uint32), a[f"h{i}_table"].view(np.uint32))
+        assert (b.row_bytes, b.norm_stride) == (m["heads"][i]["row_bytes"], m["heads"][i]["norm_stride"])
+    # The model geometry given explicitly (30 layers x 3 KV heads) needs no pinned revision.
+    assert len(calibration.read(REF / "model", layers=30, kv_heads=3, model_revision=m["model_revision"])[2]) == 90
+
+    def f32_offset(mm, head, index):
+        return mm["arrays"][f"h{head}_table"]["offset"] + 4 * index
+
+    def poke(head, index, value):
+        def edit(mm, payload):
+            payload[f32_offset(mm, head, index):f32_offset(mm, head, index) + 4] = np.float32(value).tobytes()
+        return edit
+
+    r0 = a["h5_ranges"].reshape(64, 2)
+    j = 0
+    k = int(r0[j, 1]) if r0[j, 1] < 64 else int(r0[j, 0]) - 1  # a row outside position j's group
+    assert 0 <= k < 64 and not (r0[j, 0] <= k < r0[j, 1])
+    cases = [
+        (dict(edit_manifest=lambda mm: mm.update(sha256="0" * 64)), {}, "Calibration mismatch"),
+        (dict(edit_manifest=lambda mm: mm.update(model_revision="other")), {}, "Calibration mismatch"),
+        (dict(edit_manifest=lambda mm: mm.update(upstream_commit="other")), {}, "Calibration mismatch"),
+        (dict(edit_manifest=lambda mm: mm["heads"].pop()), {}, "Calibration mismatch"),
+        (dict(), dict(layers=2, kv_heads=3), "Calibration mismatch"),
+        (dict(edit_manifest=lambda mm: mm["arrays"].pop("h7_ranges")), {}, "Bad calibration descriptor"),
+        (dict(edit_manifest=lambda mm: mm["arrays"]["h3_table"].update(offset=mm["arrays"]["h3_table"]["offset"] + 2)),
+         {}, "Bad calibration descriptor"),
+        (dict(edit_manifest=lambda mm: mm["arrays"]["h89_table"].update(nbytes=1 << 30)), {}, "Bad calibration descriptor"),
+        (dict(edit_payload=poke(4, 5000, np.inf)), {}, "Unsupported calibration"),
+        (dict(edit_payload=poke(5, k * 64 + j, 0.25)), {}, "Off-group rotation"),
+    ]
+    for n, (edit, kw, msg) in enumerate(cases):
+        d = tmp_path / f"c{n}"
+        d.mkdir()
+        with pytest.raises(bgtq.StateError, match=msg):
+            calibration.read(_tampered_calibration(d, **edit), **kw)
+    # An in-group entry may change freely.
+    lo = int(r0[j, 0])
+    d = tmp_path / "ingroup"
+    d.mkdir()
+    assert len(calibration.read(_tampered_calibration(d, edit_payload=poke(5, lo * 64 + j, 0.25)))[2]) == 90
+
+
+def test_node_calibration_checks(oracle, tmp_path):
+    """The Node Calibration.load runs the same checks with the same messages (on head 0, before any
+    device work: later heads are checked after the earlier heads' tables are on the device)."""
+    import json
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    addon = ROOT / "block-gqt-webgpu_amd" / "node" / "bgtq_napi.node"
+    if node is None or not addon.exists():
+        pytest.skip("node or the built addon is absent")
+    _, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    r0 = a["h0_ranges"].reshape(64, 2)
+    k = int(r0[0, 1]) if r0[0, 1] < 64 else int(r0[0, 0]) - 1
+
+    def poke(head, index, value):
+        def edit(mm, payload):
+            off = mm["arrays"][f"h{head}_table"]["offset"] + 4 * index
+            payload[off:off + 4] = np.float32(value).tobytes()
+        return edit
+
+    cases = {
+        "Calibration mismatch": dict(edit_manifest=lambda mm: mm.update(model_revision="other")),
+        "Bad calibration descriptor": dict(edit_manifest=lambda mm: mm["arrays"].pop("h0_ranges")),
+        "Unsupported calibration": dict(edit_payload=poke(0, 5000, np.nan)),
+        "Off-group rotation": dict(edit_payload=poke(0, k * 64, 0.25)),
+    }
+    dirs = {}
+    for n, (msg, edit) in enumerate(cases.items()):
+        d = tmp_path / f"c{n}"
+        d.mkdir()
+        dirs[msg] = str(_tampered_calibration(d, **edit))
+    script = ("const b=require(process.argv[1]);const dirs=JSON.parse(process.argv[2]);const out={};"
+              "(async()=>{for(const [want,dir] of Object.entries(dirs)){"
+              "try{await b.Calibration.load({handle:null},undefined,dir);out[want]='no error';}"
+              "catch(e){out[want]=e.message;}}console.log(JSON.stringify(out));})();")
+    r = subprocess.run([node, "-e", script, str(addon.parent / "bgtq.js"), json.dumps(dirs)],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out == {m: m for m in cases}, out
