@@ -152,9 +152,9 @@ def test_node_addon_loads_without_a_device():
         pytest.skip("node or the built addon is absent")
     script = ("const b=require(process.argv[1]);"
               "const want=['contextCreate','tablesCreate','packedKeysCreate','keysAppend','keysRead','valuesCreate',"
-              "'valuesAppend','attentionCreate','attentionSetQueries','attentionRecord','attentionRead'];"
+              "'valuesAppend','attentionCreate','attentionSetQueries','attentionRecord','attentionRead','tablesDeviceBytes'];"
               "const miss=want.filter(k=>typeof b.native[k]!=='function');"
-              "const cls=['PackedKeys','CompressedKeys','FP16Keys','Values','OptimizedAttention','AttentionEngine','tables'];"
+              "const cls=['PackedKeys','CompressedKeys','FP16Keys','Values','OptimizedAttention','AttentionEngine','tables','Calibration'];"
               "const missc=cls.filter(k=>!b[k]);"
               "console.log(JSON.stringify({abi:b.native.abiVersion,miss,missc}));")
     r = subprocess.run([node, "-e", script, str(addon.parent / "bgtq.js")], capture_output=True, text=True, timeout=60)
