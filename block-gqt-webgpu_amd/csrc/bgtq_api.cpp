@@ -843,6 +843,10 @@ static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables,
       if (h == 0) fl->book[s] = bk;
       else if (fl->book[s] != bk) return false;
     }
+    const uint8_t *base = reinterpret_cast<const uint8_t *>(tables[h]->dev());
+    fl->mfma[h] = base + T->off_mfma;
+    fl->rot_q[h] = base + T->off_rot_q;
+    fl->cent_exp[h] = T->cent_exp;
     const int sgv = T->groups == 1 ? ks : g0;
     if (h == 0) {
       *nn = n;

@@ -147,6 +147,12 @@ constexpr int kPrefillMaxSplits = 64;
 // groups (norm_stride 2), group 0 first; rows 8-byte aligned.
 struct FastLayout {
   int32_t book[4];  // centroid book of each K-step
+  // Per KV head, resolved on the host so the kernel's first loads need no
+  // dependent read of the tables' header: the MFMA lookup tables, the
+  // permuted rotation's MFMA operands and cent_exp.
+  const uint8_t *mfma[kMaxKvHeads];
+  const uint8_t *rot_q[kMaxKvHeads];
+  int32_t cent_exp[kMaxKvHeads];
 };
 
 // Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).

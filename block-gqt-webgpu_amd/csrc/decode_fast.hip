@@ -56,17 +56,22 @@ struct Geo {
   static constexpr int VI = VBYTES / 1024;  // 16-byte DMA instructions per V chunk
 };
 
-// One ring buffer: V chunk, K chunk, FP16 scales (32 x 4 bytes), packed tight
-// so two workgroups of the layout-B d=64 kernel fit one CU's 160 KB.
+// One ring buffer: V chunk, FP16 scales (32 x 4 bytes), K chunk. Every DMA
+// instruction runs on all 64 lanes (lanes past the data read zeros into the
+// padding: scales to 256 bytes, K to whole 1 KB pieces), so the compiler's
+// count of loads in flight matches the hardware's and its own waits for
+// register loads never wait for ring data. Two workgroups of the layout-B
+// d=64 kernel still fit one CU's 160 KB.
 template <int D, int KF, int NN>
 struct Slot {
   static constexpr int KS = D / 32;
   static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : 2 * D;  // K row bytes
   static constexpr int KBYTES = kChunk * RB;
-  static constexpr int KI = (KBYTES + 1023) / 1024;              // 16-byte DMA instructions per K chunk
-  static constexpr int KLAST = (KBYTES - (KI - 1) * 1024) / 16;  // lanes of the last one
-  static constexpr int NBYTES = KF == 1 ? kChunk * 4 : 0;
-  static constexpr int BYTES = Geo<D>::VBYTES + KBYTES + NBYTES;
+  static constexpr int KI = (KBYTES + 1023) / 1024;  // 16-byte DMA instructions per K chunk
+  static constexpr int NBYTES = KF == 1 ? 64 * 4 : 0;
+  static constexpr int NOFF = Geo<D>::VBYTES;         // scales
+  static constexpr int KOFF = NOFF + NBYTES;          // K
+  static constexpr int BYTES = KOFF + KI * 1024;
   static constexpr int L = Geo<D>::VI + KI + (KF == 1 ? 1 : 0);  // DMA instructions per chunk
   static constexpr int TABLES = KF == 1 ? KS * 2048 : 0;
   // Three buffers per wave where they fit the CU, else two (FP16 K at d=128).
@@ -86,7 +91,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   constexpr int KS = Gm::KS, DT = Gm::DT, PR = Gm::PR, VI = Gm::VI;
   constexpr int RB = Sl::RB, KI = Sl::KI, L = Sl::L, AHEAD = Sl::AHEAD;
   static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
-  static_assert(kWaves * Sl::BYTES >= 5 * 16 * D * 4, "q staging fits one ring slot of all waves");
+  static_assert(kWaves * Sl::BYTES >= 16 * (D + 4) * 4, "q staging fits one ring slot of all waves");
+  static_assert(KF == 0 || Gm::DT % kWaves == 0, "rotation tiles split evenly over the waves");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= kWaves * 16 * (D + 2) * 4, "wave merge fits the ring");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
   extern __shared__ __align__(16) uint8_t smem[];
@@ -102,7 +108,6 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // sequence at any moment sweep adjacent memory.
   const int t_end = kInterleaved ? T_b : min(T_b, split * p.split_tokens + p.split_tokens);
   const int stride = kInterleaved ? p.splits * kWaves * kChunk : kWaves * kChunk;
-  const DevTables *T = KF == 1 ? p.tables[kv] : nullptr;
   uint8_t *tabs = smem + Sl::RING * kWaves * Sl::BYTES;
   auto slot_base = [&](int s) { return smem + (s * kWaves + wave) * Sl::BYTES; };
 
@@ -128,106 +133,137 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
   auto issue = [&](int i) {
     const int c0 = first + i * stride;
-    const uint32_t rest = (uint32_t)min(T_b - c0, kChunk);  // tokens of the chunk inside the sequence (> 0)
+    // Tokens of the chunk inside the sequence; none for a chunk past the end
+    // (a zero-sized descriptor: the DMA only writes zeros to LDS).
+    const int in_seq = min(T_b - c0, kChunk);
+    const uint32_t rest = __builtin_amdgcn_readfirstlane(in_seq > 0 ? in_seq : 0);  // wave-uniform: SGPR descriptor
     uint8_t *sb = slot_base(i % Sl::RING);
     const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
 #pragma unroll
     for (int k = 0; k < VI; ++k) dma16<kStream>(rV, sb + k * 1024, voff_rows[k], 0);
-    uint8_t *kb = sb + Gm::VBYTES;
+    uint8_t *kb = sb + Sl::KOFF;
     if (KF == 1) {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * RB, rest * RB);
       const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * 2, rest * 4);
 #pragma unroll
-      for (int k = 0; k < KI; ++k) {
-        if (k + 1 < KI || Sl::KLAST == 64 || lane < Sl::KLAST) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
-      }
-      if (lane < kChunk) dma4<kStream>(rN, kb + Sl::KBYTES, lane * 4, 0);
+      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+      dma4<kStream>(rN, sb + Sl::NOFF, lane * 4, 0);
     } else {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
 #pragma unroll
       for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, voff_rows[k], 0);
     }
   };
-  // The first AHEAD chunks stream in while the prologue runs; the last ring
-  // slot holds the prologue's q staging.
+  // Per-head causal limits (read before the ring's loads are in flight).
+  const bool head_ok = col < G;
+  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)b * Hq + hq0 + col], T_b) : T_b) : 0;
+  const int lim = min(end_h, t_end);
+  // Wave-uniform: chunks reaching past lim_min need the per-head mask.
+  int lim_min = head_ok ? lim : t_end;
 #pragma unroll
-  for (int i = 0; i < AHEAD; ++i)
-    if (i < n_chunks) issue(i);
+  for (int o = 32; o >= 1; o >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o, 64));
 
   // ---------------- prologue ----------------
-  // One round trip: the MFMA lookup tables of the K-steps' books and the G
-  // query rows go HBM -> LDS by DMA (query rows past G read as zeros), the
-  // wave's quarter of the transposed rotation goes to registers.
-  float *q_raw = reinterpret_cast<float *>(smem + (Sl::RING - 1) * kWaves * Sl::BYTES);  // [16][D]
-  float *q_part = q_raw + 16 * D;                                                     // [4][16][D]
+  // One round trip: wave 0 DMAs the MFMA lookup tables of the K-steps' books
+  // into LDS; every wave loads its lanes' query values (lane (gq, col): head
+  // col, dims 32 s + 8 gq + 0..7) and, for packed K, the MFMA operands of its
+  // tiles of the permuted rotation. The first AHEAD chunks are issued behind
+  // these loads and stay in flight through the prologue.
   if (KF == 1 && wave == 0) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const uint8_t *src = tables_mfma(T) + fl.book[s] * kMfmaTableBytes + (s < NN ? 0 : 2048);
+      const uint8_t *src = fl.mfma[kv] + fl.book[s] * kMfmaTableBytes + (s < NN ? 0 : 2048);
       const __amdgpu_buffer_rsrc_t rt = rsrc(src, s < NN ? 2048 : 1024);
       dma16(rt, tabs + s * 2048, lane * 16, 0);
       if (s < NN) dma16(rt, tabs + s * 2048 + 1024, 1024 + lane * 16, 0);
     }
   }
-  if (wave == kWaves - 1) {
-    const __amdgpu_buffer_rsrc_t rq = rsrc(p.q + ((int64_t)b * Hq + hq0) * D, (uint32_t)(G * D * 4));
+  f32x4 qload[KS][2];  // unconditional loads of a valid row; heads past G are zeroed after the chunk issue
+  {
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + ((int64_t)b * Hq + hq0 + (head_ok ? col : 0)) * D);
 #pragma unroll
-    for (int k = 0; k < 16 * D * 4 / 1024; ++k) dma16(rq, reinterpret_cast<uint8_t *>(q_raw) + k * 1024, k * 1024 + lane * 16, 0);
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) qload[s][hh] = src[8 * s + 2 * gq + hh];
   }
-  constexpr int IQ = D / kWaves;  // rotation rows i of this wave: wave * IQ + ii
-  constexpr int JL = D / 64;      // output dims j of this lane: lane + 64 jl
-  float rt[KF == 1 ? IQ * JL : 1];
-  int src_i[KF == 1 ? IQ : 1];
+  constexpr int NT = KF == 1 ? DT / kWaves : 1;  // 16-row tiles of the rotation per wave
+  u32x4 rq[NT][KS][2];
   if (KF == 1) {
-    const float *Rt = tables_rot_t(T);  // Rt[i*D + j] = R[j][i]
+    const u32x4 *op = reinterpret_cast<const u32x4 *>(fl.rot_q[kv]);  // [tile][K-step][lane][hi, lo]
 #pragma unroll
-    for (int ii = 0; ii < IQ; ++ii) {
-      src_i[ii] = T->perm[wave * IQ + ii];
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int jl = 0; jl < JL; ++jl) rt[ii * JL + jl] = Rt[(wave * IQ + ii) * D + lane + 64 * jl];
-    }
+      for (int s = 0; s < KS; ++s) {
+        const int at = (((wave * NT + t) * KS + s) * 64 + lane) * 2;
+        rq[t][s][0] = op[at];
+        rq[t][s][1] = op[at + 1];
+      }
   }
-  const int ec = KF == 1 ? T->cent_exp : 0;
-  wait_vm<0>();
-  __syncthreads();
-  // qr[h][j] = sum_i R[j][i] q[h][perm[i]]: wave w sums i in its quarter
-  // (off-group entries of R are exact zeros).
+  const int ec = KF == 1 ? fl.cent_exp[kv] : 0;
+  // Unconditional, so every wave has exactly AHEAD * L chunk loads in flight
+  // behind its prologue loads (chunks past the end are zero-sized). The
+  // scheduling barriers keep the prologue's loads ahead of them, so waiting
+  // for those loads never waits for the chunks.
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int jl = 0; jl < JL; ++jl) {
-    const int jj = lane + 64 * jl;
-    float acc[16];
+  for (int i = 0; i < AHEAD; ++i) issue(i);
+  __builtin_amdgcn_sched_barrier(0);
+  float qv[KS][8];
 #pragma unroll
-    for (int h = 0; h < 16; ++h) acc[h] = 0.0f;
-    if (KF == 1) {
+  for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int ii = 0; ii < IQ; ++ii)
+    for (int k = 0; k < 8; ++k) qv[s][k] = head_ok ? qload[s][k >> 2][k & 3] : 0.0f;
+  if (KF == 1) {
+    // qr^T = Rq q^T, Rq = R with the head permutation folded into its
+    // columns, on the matrix cores (q and Rq split hi/lo, three MFMAs per
+    // K-step, off-group entries exact zeros). Tile n leaves rows
+    // j = 16 n + 4 gq + 0..3 of head col in this lane; they go through LDS
+    // (the last ring slot, rows padded to D + 4 floats) to the QK layout.
+    float qmax = 0.0f;
 #pragma unroll
-        for (int h = 0; h < 16; ++h) acc[h] = __builtin_fmaf(rt[ii * JL + jl], q_raw[h * D + src_i[ii]], acc[h]);
-    } else if (wave == 0) {
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int h = 0; h < 16; ++h) acc[h] = q_raw[h * D + jj];
+      for (int jv = 0; jv < 8; ++jv) qmax = fmaxf(qmax, fabsf(qv[s][jv]));
+    const int e0 = split_exp(col_max(qmax));
+    half8 bh[KS], bl[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) split_scaled(qv[s], __builtin_ldexpf(1.0f, e0), bh[s], bl[s]);
+    float *qs = reinterpret_cast<float *>(smem + (Sl::RING - 1) * kWaves * Sl::BYTES);  // [16][D + 4]
+    const float unscale = __builtin_ldexpf(1.0f, -e0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const half8 ah = __builtin_bit_cast(half8, rq[t][s][0]), al = __builtin_bit_cast(half8, rq[t][s][1]);
+        acc = mfma(ah, bh[s], acc);
+        acc = mfma(al, bh[s], acc);
+        acc = mfma(ah, bl[s], acc);
+      }
+      *reinterpret_cast<f32x4 *>(qs + col * (D + 4) + 16 * (wave * NT + t) + 4 * gq) = acc * unscale;
     }
+    wait_vm<AHEAD * L>();  // wave 0's table DMAs, which precede the chunks
+    lds_barrier();
 #pragma unroll
-    for (int h = 0; h < 16; ++h) q_part[(wave * 16 + h) * D + jj] = acc[h];
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(qs + col * (D + 4) + 32 * s + 8 * gq + 4 * hh);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) qv[s][4 * hh + k] = v[k];
+      }
   }
-  __syncthreads();
   // B operand of QK: lane holds qr[head = col][32 s + 8 gq + 0..7], split hi/lo
   // after scaling the head's row so its largest entry is near 2^14.
-  const bool head_ok = col < G;
   half8 qhi[KS], qlo[KS];
   float kq;  // log2-domain logit = (sum_g s_g acc_g) * kq
   {
-    float qv[KS][8];
     float qmax = 0.0f;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int jv = 0; jv < 8; ++jv) {
-        const int jj = 32 * s + 8 * gq + jv;
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) v += q_part[(w * 16 + col) * D + jj];
-        v = head_ok ? v * p.inv_sqrt_d : 0.0f;
+        const float v = head_ok ? qv[s][jv] * p.inv_sqrt_d : 0.0f;
         qv[s][jv] = v;
         qmax = fmaxf(qmax, fabsf(v));
       }
@@ -244,13 +280,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       }
     kq = __builtin_ldexpf(kLog2e, -(eq + ec));
   }
-  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)b * Hq + hq0 + col], T_b) : T_b) : 0;
-  const int lim = min(end_h, t_end);
-  // Wave-uniform: chunks reaching past lim_min need the per-head mask.
-  int lim_min = head_ok ? lim : t_end;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o, 64));
-  __syncthreads();  // q staging (last ring slot) is dead
+  if (KF == 1) lds_barrier();  // q staging (last ring slot) is dead
 
   const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
   float m_run = -INFINITY, l_run = 0.0f;
@@ -276,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     else if (newer >= 1) wait_vm<L>();
     else wait_vm<0>();
     const uint8_t *sb = slot_base(i % Sl::RING);
-    const uint8_t *kbuf = sb + Gm::VBYTES;
+    const uint8_t *kbuf = sb + Sl::KOFF;
 
     // QK: acc[u][g] = sum over the K-steps of group g.
     f32x4 acc[2][2];
@@ -327,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       u32x4 nr{0u, 0u, 0u, 0u};
-      if (KF == 1) nr = *reinterpret_cast<const u32x4 *>(kbuf + Sl::KBYTES + (16 * u + 4 * gq) * 4);
+      if (KF == 1) nr = *reinterpret_cast<const u32x4 *>(sb + Sl::NOFF + (16 * u + 4 * gq) * 4);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float v;
@@ -407,6 +437,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 
   // ---------------- epilogue ----------------
   const float l_tot = col_sum(l_run) * (1.0f / kPScale);
+  wait_vm<0>();     // a wave without chunks still has its prologue's zero-sized chunk loads to retire
   __syncthreads();  // every wave is done with the ring
   float *comb = reinterpret_cast<float *>(smem);  // [wave][16 heads][2 + D]
   if (gq == 0) {

@@ -72,6 +72,23 @@ __device__ __forceinline__ void split2(float x0, float x1, uint32_t &hi, uint32_
   lo = __builtin_bit_cast(uint32_t, l);
 }
 
+// Split of x * sc (sc a power of two) into fp16 hi (rounded toward zero) and lo halves.
+__device__ __forceinline__ void split_scaled(const float *x, float sc, half8 &hi, half8 &lo) {
+  u32x4 h4, l4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t h, l;
+    split2(x[2 * k] * sc, x[2 * k + 1] * sc, h, l);
+    h4[k] = h;
+    l4[k] = l;
+  }
+  hi = __builtin_bit_cast(half8, h4);
+  lo = __builtin_bit_cast(half8, l4);
+}
+
+// Exponent e with max * 2^e near 2^14 (fp16 hi/lo split range); 0 for max 0.
+__device__ __forceinline__ int split_exp(float mx) { return mx > 0.0f ? 14 - (int)ceilf(__builtin_log2f(mx)) : 0; }
+
 // Relaxed atomics at device scope: on gfx950 they go to the device-coherent
 // level (system-coherent bit) instead of this XCD's L2.
 __device__ __forceinline__ void coherent_store(float *ptr, float v) {
@@ -90,6 +107,16 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Workgroup barrier for LDS traffic only. __syncthreads() also waits for every
+// outstanding global load of the wave (its release fence), which would drain
+// the HBM -> LDS ring; here the caller has already waited for the DMAs whose
+// LDS data the other waves read.
+__device__ __forceinline__ void lds_barrier() {
+  wait_lds();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // 16-byte piece swizzle of an FP16 row of D values in LDS: conflict-free
 // transposed (ds_read_b64_tr_b16) and row reads.

@@ -96,23 +96,6 @@ __device__ __forceinline__ void wait_blocks(int newer) {
   }
 }
 
-// Split of x * sc (sc a power of two) into fp16 hi (rounded toward zero) and lo halves.
-__device__ __forceinline__ void split_scaled(const float *x, float sc, half8 &hi, half8 &lo) {
-  u32x4 h4, l4;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    uint32_t h, l;
-    split2(x[2 * k] * sc, x[2 * k + 1] * sc, h, l);
-    h4[k] = h;
-    l4[k] = l;
-  }
-  hi = __builtin_bit_cast(half8, h4);
-  lo = __builtin_bit_cast(half8, l4);
-}
-
-// Exponent e with max * 2^e near 2^14 (fp16 hi/lo split range); 0 for max 0.
-__device__ __forceinline__ int split_exp(float mx) { return mx > 0.0f ? 14 - (int)ceilf(__builtin_log2f(mx)) : 0; }
-
 __device__ __forceinline__ float wave_max(float v) {
   v = col_max(v);
 #pragma unroll
