@@ -30,9 +30,12 @@ DEVICE_SOURCES = ["encode.hip", "encode_bulk.hip", "encode_wave.hip", "decode.hi
 HOST_SOURCES = ["bgtq_api.cpp"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}"]
+# -amdgpu-mfma-vgpr-form: matrix-core accumulators in ordinary VGPRs (gfx950's
+# unified register file), so the softmax rescale of the output accumulators
+# needs no copies between accumulation and architectural registers.
 DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
                 "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang",
-                "-packed-fp32-ops"]
+                "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def hipcc():

@@ -77,8 +77,8 @@ struct Slot {
   // Three buffers per wave where they fit the CU, else two (FP16 K at d=128).
   static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
   static constexpr int AHEAD = RING - 1;
-  static constexpr int LDS = RING * kWaves * BYTES + TABLES;
-  static_assert(LDS <= kLdsLimit, "LDS of one workgroup");
+  static constexpr int DYN = RING * kWaves * BYTES;  // dynamic LDS: the ring (the tables are static)
+  static_assert(DYN + TABLES <= kLdsLimit, "LDS of one workgroup");
   static_assert(AHEAD >= 1 && AHEAD <= 3, "ring waits cover up to three chunks in flight");
 };
 
@@ -108,8 +108,12 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // sequence at any moment sweep adjacent memory.
   const int t_end = kInterleaved ? T_b : min(T_b, split * p.split_tokens + p.split_tokens);
   const int stride = kInterleaved ? p.splits * kWaves * kChunk : kWaves * kChunk;
-  uint8_t *tabs = smem + Sl::RING * kWaves * Sl::BYTES;
-  auto slot_base = [&](int s) { return smem + (s * kWaves + wave) * Sl::BYTES; };
+  // The K-steps' lookup tables are static LDS (an address fixed at compile
+  // time, so a lookup's address is the code byte shifted: one instruction);
+  // the ring is the dynamic LDS.
+  __shared__ __align__(16) uint8_t tabs[KF == 1 ? Sl::TABLES : 16];
+  uint8_t *ring = smem;
+  auto slot_base = [&](int s) { return ring + (s * kWaves + wave) * Sl::BYTES; };
 
   // ---------------- streams of this (sequence, KV head) ----------------
   // Each chunk's loads use buffer descriptors based at the chunk's first token
@@ -228,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     half8 bh[KS], bl[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) split_scaled(qv[s], __builtin_ldexpf(1.0f, e0), bh[s], bl[s]);
-    float *qs = reinterpret_cast<float *>(smem + (Sl::RING - 1) * kWaves * Sl::BYTES);  // [16][D + 4]
+    float *qs = reinterpret_cast<float *>(ring + (Sl::RING - 1) * kWaves * Sl::BYTES);  // [16][D + 4]
     const float unscale = __builtin_ldexpf(1.0f, -e0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -549,12 +553,12 @@ template <int D, int KF, int NN, int SG>
 hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
   static const hipError_t allowed = hipFuncSetAttribute(
-      (const void *)decode_fast_kernel<D, KF, NN, SG>, hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN>::LDS);
+      (const void *)decode_fast_kernel<D, KF, NN, SG>, hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN>::DYN);
   if (allowed != hipSuccess) {
     (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
     return allowed;
   }
-  constexpr int lds = Slot<D, KF, NN>::LDS;
+  constexpr int lds = Slot<D, KF, NN>::DYN;
   dim3 grid((unsigned)p.splits, (unsigned)(p.batch * p.kv_heads));
   hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG>), grid, dim3(kThreads), lds, stream, p, fl);
   return hipGetLastError();
