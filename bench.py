@@ -182,7 +182,7 @@ def encode_throughput(dev, layout="B", reps=10):
             "gbs_algorithmic": round(rows * (128 + p.rowBytes + 2 * p.normStride) / (ms / 1e3) / 1e9, 1)}
 
 
-def smollm2_decode_step(dev, steps, layout="B"):
+def smollm2_decode_step(dev, steps, layout="B", splits=0):
     """SmolLM2-135M geometry at batch 1: per layer, encode the new token's K for
     3 KV heads, then attend 9 query heads over the 4096 + 1 cached tokens."""
     import torch
@@ -212,7 +212,7 @@ def smollm2_decode_step(dev, steps, layout="B"):
                     max_length=T + 1, v=v[l], v_seq_stride=v.stride(1), v_head_stride=v.stride(2),
                     tables=tabs[l * HKV2:(l + 1) * HKV2], packed=packed[l], packed_seq_stride=packed.stride(1),
                     packed_head_stride=packed.stride(2), norms=norms[l], norms_seq_stride=norms.stride(1),
-                    norms_head_stride=norms.stride(2))
+                    norms_head_stride=norms.stride(2), splits=splits)
         if ws is None:
             ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8, device="cuda")
         descs.append(batched.decode_desc(workspace=ws, **args))
@@ -236,6 +236,31 @@ def smollm2_decode_step(dev, steps, layout="B"):
 def prefill_flops(prompt, hq, dim, layers):
     """Algorithmic causal attention FLOPs of a prompt: QK and PV, 2 * dim each per (query, visible token)."""
     return layers * hq * (prompt * (prompt + 1) // 2) * dim * 4
+
+
+def device_ceilings():
+    """Achievable ceilings of this GPU, measured now: a streaming non-temporal read of the decode step's
+    byte count (one layer, 754,974,720 B) and a dense fp16 16x16x32 matrix-core loop on every CU."""
+    import torch
+    lib = ctypes.CDLL(str(ROOT / "block-gqt-webgpu_amd" / "lib" / "libbgtq_probes.so"))
+    lib.bgtq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    lib.bgtq_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(ctypes.c_double)]
+    nbytes = BATCH * HKV * CTX * 180
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    us = ctypes.c_double()
+    if lib.bgtq_probe_read(buf.data_ptr(), nbytes, 20, ctypes.byref(us)) != 0:
+        raise RuntimeError("read probe failed")
+    del buf
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    flops, us2 = ctypes.c_double(), ctypes.c_double()
+    if lib.bgtq_probe_mfma(cus, 4096, 5, ctypes.byref(flops), ctypes.byref(us2)) != 0:
+        raise RuntimeError("matrix-core probe failed")
+    return {"hbm_read_gbs": round(nbytes / us.value / 1e3, 1), "hbm_read_us": round(us.value, 2),
+            "hbm_read_bytes": nbytes, "mfma_f16_tflops": round(flops.value / us2.value / 1e6, 1),
+            "probes": "libbgtq_probes.so: grid-stride 16-byte non-temporal loads (4096 x 256 threads); "
+                      "8 chains of v_mfma_f32_16x16x32_f16 per wave, 8 waves per CU"}
 
 
 def qwen_prefill(dev, steps, layout="B", chunk=0, prompt=4096, layers=LAYERS):
@@ -360,6 +385,7 @@ def main():
     ap.add_argument("--sweep-splits", default="", help="comma list: time the decode at each split count and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the Qwen prompt-prefill measurements")
     ap.add_argument("--encode-only", action="store_true", help="only the SmolLM2 bulk K-encode measurement")
+    ap.add_argument("--smollm2-step-only", action="store_true", help="only the SmolLM2 batch-1 decode step")
     ap.add_argument("--prefill-chunks", default="0,32", help="with --prefill-only: chunk sizes (0 = whole prompt)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (HBM counter calibration)")
@@ -383,6 +409,11 @@ def main():
     batched.bind_torch_stream(dev)
     if a.encode_only:
         print(json.dumps({"encode_smollm2_prefill": encode_throughput(dev, a.layout, max(a.steps, 5))}))
+        return
+    if a.smollm2_step_only:
+        for sp in [int(x) for x in (a.sweep_splits or str(a.splits)).split(",")]:
+            print(json.dumps({"splits": sp, "smollm2_decode_step_b1": smollm2_decode_step(dev, a.steps, a.layout, sp)}),
+                  flush=True)
         return
     if a.prefill_only:
         out = {}
@@ -412,6 +443,9 @@ def main():
     ms_launch = ms_step / LAYERS  # one decode launch per layer, back to back in the graph
     achieved = bytes_layer / (ms_launch / 1e3) / 1e9
     extra = {"eager_ms_per_step": round(ms_eager, 4)}
+    log("device ceilings ...")
+    ceil = device_ceilings()
+    extra["ceilings"] = ceil
     if not a.no_extra:
         del w
         torch.cuda.empty_cache()
@@ -432,6 +466,9 @@ def main():
         extra["qwen_prefill_4096"] = qwen_prefill(dev, max(2, a.steps // 2), a.layout)
         log("Qwen prefill, chunks of 32 ...")
         extra["qwen_prefill_4096_chunk32"] = qwen_prefill(dev, 2, a.layout, chunk=32)
+        for k in ("qwen_prefill_4096", "qwen_prefill_4096_chunk32"):
+            extra[k]["mfma_frac_of_measured_ceiling"] = round(
+                extra[k]["attention_tflops_algorithmic"] / ceil["mfma_f16_tflops"], 4)
     cpu = None if a.no_cpu else cpu_baseline(a.layout)
     rec = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -445,6 +482,7 @@ def main():
                    "launch": "eager" if a.eager else "hip graph of 24 per-layer launches"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "frac_of_measured_read_ceiling": round(achieved / ceil["hbm_read_gbs"], 4),
                      "kernel": "decode_fast_kernel<64,1,1,1> (one launch per layer)", "bytes_per_launch": bytes_layer},
         "cpu_baseline": cpu,
         **extra,

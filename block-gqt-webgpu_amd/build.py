@@ -75,6 +75,16 @@ def build_library(verbose=False) -> Path:
     return target
 
 
+def build_probes() -> Path:
+    """libbgtq_probes.so: the benchmark's streaming-read and matrix-core ceiling kernels."""
+    LIB_DIR.mkdir(exist_ok=True)
+    target = LIB_DIR / "libbgtq_probes.so"
+    tmp = LIB_DIR / "libbgtq_probes.so.tmp"
+    _run([hipcc(), *COMMON, *DEVICE_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "probes.hip")])
+    os.replace(tmp, target)
+    return target
+
+
 def build_napi() -> Path:
     """Node N-API addon over libbgtq.so (headers from the image's Node)."""
     node_inc = None
@@ -96,6 +106,7 @@ def main():
     ap.add_argument("-v", "--verbose", action="store_true")
     a = ap.parse_args()
     print(build_library(a.verbose))
+    print(build_probes())
     if a.napi:
         print(build_napi())
 
