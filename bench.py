@@ -199,14 +199,15 @@ def smollm2_decode_step(dev, steps, layout="B", splits=0):
         batched.encode(dev, [dict(tables=tabs[l * HKV2 + h], src=hist[l, h], src_row_stride=64, rows=T,
                                   packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=0) for h in range(HKV2)], "f16")
     del hist
-    knew = torch.randn((L, HKV2, 64), device="cuda")  # post-RoPE FP32 K of the new token
+    knew = torch.randn((L, 1, HKV2, 64), device="cuda")  # post-RoPE FP32 K of the new token
+    vnew = torch.randn((L, 1, HKV2, 64), device="cuda")  # its FP32 V
     v = torch.randn((L, 1, HKV2, T + 1, 64), device="cuda").half()
     q = torch.randn((L, 1, HQ2, 64), device="cuda")
     out = torch.empty((L, 1, HQ2, 64), device="cuda")
     lengths = torch.full((1,), T + 1, dtype=torch.int32, device="cuda")
     jobs, descs, ws = [], [], None
     for l in range(L):
-        jobs.append([dict(tables=tabs[l * HKV2 + h], src=knew[l, h], src_row_stride=64, rows=1,
+        jobs.append([dict(tables=tabs[l * HKV2 + h], src=knew[l, 0, h], src_row_stride=64, rows=1,
                           packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=T) for h in range(HKV2)])
         args = dict(batch=1, q_heads=HQ2, kv_heads=HKV2, dim=64, q=q[l], out=out[l], lengths=lengths,
                     max_length=T + 1, v=v[l], v_seq_stride=v.stride(1), v_head_stride=v.stride(2),
@@ -217,20 +218,27 @@ def smollm2_decode_step(dev, steps, layout="B", splits=0):
             ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8, device="cuda")
         descs.append(batched.decode_desc(workspace=ws, **args))
 
-    def step():
+    appends = [batched.append_desc(k_new=knew[l], v_new=vnew[l]) for l in range(L)]
+
+    def step():  # one launch per layer: encode the new K and append its V inside the attention launch
+        for l in range(L):
+            batched.decode_append(dev, descs[l], appends[l])
+
+    def step_two_calls():  # the same step as two launches per layer (the V row is not written here)
         for l in range(L):
             batched.encode(dev, jobs[l], "f32")
             batched.decode(dev, descs[l])
 
-    g = graph_of(torch, dev, step)
-    ms = time_graph(torch, g, steps, 3)
+    ms = time_graph(torch, graph_of(torch, dev, step), steps, 3)
+    ms2 = time_graph(torch, graph_of(torch, dev, step_two_calls), steps, 3)
     per_token = p.rowBytes + 2 * p.normStride + 128
     bytes_step = L * HKV2 * (T + 1) * per_token
     for t in tabs:
         t.destroy()
     return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(bytes_step / (ms / 1e3) / 1e9, 1),
-            "workload": "30 layers x (encode 1 token x 3 KV heads + attend 9 q heads over 4097 tokens), d=64, "
-                        "batch 1, layout B, FP16 V"}
+            "two_launches_per_layer_us_per_step": round(ms2 * 1e3, 2),
+            "workload": "30 layers x (encode 1 token x 3 KV heads, append its V, attend 9 q heads over 4097 "
+                        "tokens), d=64, batch 1, layout B, FP16 V; one bgtq_decode_append launch per layer"}
 
 
 def prefill_flops(prompt, hq, dim, layers):

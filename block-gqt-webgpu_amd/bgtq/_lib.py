@@ -63,6 +63,12 @@ class DecodeDesc(ctypes.Structure):
 
 
 
+class AppendDesc(ctypes.Structure):
+    _fields_ = [("k_new", ctypes.c_void_p), ("k_new_dtype", ctypes.c_int32), ("k_new_seq_stride", ctypes.c_int64),
+                ("k_new_head_stride", ctypes.c_int64), ("v_new", ctypes.c_void_p), ("v_new_dtype", ctypes.c_int32),
+                ("v_new_seq_stride", ctypes.c_int64), ("v_new_head_stride", ctypes.c_int64)]
+
+
 class PrefillDesc(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("rows", ctypes.c_int32), ("q_heads", ctypes.c_int32),
                 ("kv_heads", ctypes.c_int32), ("dim", ctypes.c_int32), ("key_format", ctypes.c_int32),
@@ -119,6 +125,7 @@ SIGNATURES = {
     "bgtq_encode_batched": (_I32, [_VP, _I32, ctypes.POINTER(EncodeJob), _SZ]),
     "bgtq_decode_workspace_size": (_I32, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_decode": (_I32, [_VP, ctypes.POINTER(DecodeDesc)]),
+    "bgtq_decode_append": (_I32, [_VP, ctypes.POINTER(DecodeDesc), ctypes.POINTER(AppendDesc)]),
     "bgtq_prefill_workspace_size": (_I32, [ctypes.POINTER(PrefillDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_prefill": (_I32, [_VP, ctypes.POINTER(PrefillDesc)]),
 }

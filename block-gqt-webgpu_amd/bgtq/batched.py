@@ -66,6 +66,22 @@ def decode(device, desc) -> None:
     check(lib().bgtq_decode(device.handle, ctypes.byref(desc)))
 
 
+def append_desc(*, k_new, v_new):
+    """bgtq_append_desc over device tensors [B, Hkv, dim] (FP32 or FP16, any strides in elements)."""
+    a = _lib.AppendDesc()
+    dt = {"torch.float32": _lib.DTYPE_F32, "torch.float16": _lib.DTYPE_F16}
+    a.k_new, a.k_new_dtype = _addr(k_new), dt[str(k_new.dtype)]
+    a.k_new_seq_stride, a.k_new_head_stride = k_new.stride(0), k_new.stride(1)
+    a.v_new, a.v_new_dtype = _addr(v_new), dt[str(v_new.dtype)]
+    a.v_new_seq_stride, a.v_new_head_stride = v_new.stride(0), v_new.stride(1)
+    return a
+
+
+def decode_append(device, desc, append) -> None:
+    """The decode step with its new token (bgtq_decode_append): row lengths[b] - 1 of the caches."""
+    check(lib().bgtq_decode_append(device.handle, ctypes.byref(desc), ctypes.byref(append)))
+
+
 def prefill_desc(*, batch, rows, q_heads, kv_heads, dim, q, out, starts, max_length, v, v_seq_stride,
                  v_head_stride, tables=None, packed=None, packed_seq_stride=0, packed_head_stride=0, norms=None,
                  norms_seq_stride=0, norms_head_stride=0, k_f16=None, k_seq_stride=0, k_head_stride=0,

@@ -846,6 +846,9 @@ static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables,
     const uint8_t *base = reinterpret_cast<const uint8_t *>(tables[h]->dev());
     fl->mfma[h] = base + T->off_mfma;
     fl->rot_q[h] = base + T->off_rot_q;
+    fl->rot_t[h] = reinterpret_cast<const float *>(base + T->off_rot_t);
+    fl->lut[h] = base + T->off_lut;
+    fl->books[h] = reinterpret_cast<const float *>(base + T->off_books);
     fl->cent_exp[h] = T->cent_exp;
     const int sgv = T->groups == 1 ? ks : g0;
     if (h == 0) {
@@ -881,7 +884,21 @@ static bgtq_status launch_decode_common(bgtq_context *ctx, DecodeParams &p, cons
   return BGTQ_OK;
 }
 
-bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) {
+static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, const bgtq_append_desc *a);
+
+bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) { return decode_impl(ctx, d, nullptr); }
+
+bgtq_status bgtq_decode_append(bgtq_context *ctx, const bgtq_decode_desc *d, const bgtq_append_desc *a) {
+  if (!a) return fail(BGTQ_ERR_RANGE, "null append descriptor");
+  if (!a->k_new || !a->v_new) return fail(BGTQ_ERR_RANGE, "null new K or V");
+  for (int32_t t : {a->k_new_dtype, a->v_new_dtype})
+    if (t != BGTQ_DTYPE_F16 && t != BGTQ_DTYPE_F32) return fail(BGTQ_ERR_RANGE, "invalid new K/V dtype");
+  if (d && (a->k_new_seq_stride < 0 || a->k_new_head_stride < 0 || a->v_new_seq_stride < 0 || a->v_new_head_stride < 0))
+    return fail(BGTQ_ERR_RANGE, "negative new K/V stride");
+  return decode_impl(ctx, d, a);
+}
+
+static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, const bgtq_append_desc *a) {
   if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
   int splits = 1;
   if (bgtq_status s = validate_decode(d, &splits)) return s;
@@ -927,6 +944,24 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d) {
   p.logits = nullptr;
   p.probs = nullptr;
   p.logit_stride = 0;
+  if (a) {
+    p.k_new = a->k_new;
+    p.k_new_f32 = a->k_new_dtype == BGTQ_DTYPE_F32;
+    p.k_new_seq_stride = a->k_new_seq_stride;
+    p.k_new_head_stride = a->k_new_head_stride;
+    p.v_new = a->v_new;
+    p.v_new_f32 = a->v_new_dtype == BGTQ_DTYPE_F32;
+    p.v_new_seq_stride = a->v_new_seq_stride;
+    p.v_new_head_stride = a->v_new_head_stride;
+    FastLayout fl{};
+    int nn = 0, sg = 0;
+    p.q = d->q;
+    if (!fast_layout(p, d->tables, &fl, &nn, &sg))
+      return fail(BGTQ_ERR_UNSUPPORTED,
+                  "decode_append needs the fused kernel's layouts; use bgtq_encode_batched and bgtq_decode");
+    HIP_TRY(launch_decode_fast(p, fl, nn, sg, ctx->stream), "decode append launch");
+    return BGTQ_OK;
+  }
   return launch_decode_common(ctx, p, d->q, d->tables);
 }
 

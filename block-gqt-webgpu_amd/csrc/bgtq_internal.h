@@ -109,6 +109,13 @@ struct DecodeParams {
   float *probs;   // optional [B*Hq*logit_stride]
   int64_t logit_stride;
   int32_t lds_bytes;  // dynamic LDS of the split kernel
+  // Decode-step append (fused kernel only), null otherwise: the newest token
+  // of sequence b sits at row lengths[b] - 1 of the caches; its post-RoPE K
+  // [b][kv][dim] is encoded into packed/norms (or converted into the FP16 K
+  // rows) and its V converted into the FP16 V rows within the launch.
+  const void *k_new, *v_new;
+  int32_t k_new_f32, v_new_f32;
+  int64_t k_new_seq_stride, k_new_head_stride, v_new_seq_stride, v_new_head_stride;  // elements
 };
 
 // Chunked-prefill attention of one layer (prefill.hip). Units are (sequence,
@@ -153,6 +160,10 @@ struct FastLayout {
   const uint8_t *mfma[kMaxKvHeads];
   const uint8_t *rot_q[kMaxKvHeads];
   int32_t cent_exp[kMaxKvHeads];
+  // The decode-step append's encoder tables: transposed rotation, code LUT, books.
+  const float *rot_t[kMaxKvHeads];
+  const uint8_t *lut[kMaxKvHeads];
+  const float *books[kMaxKvHeads];
 };
 
 // Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).

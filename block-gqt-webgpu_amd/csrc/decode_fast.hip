@@ -34,6 +34,7 @@
 #include <hip/hip_fp16.h>
 
 #include "bgtq_internal.h"
+#include "encode_row.h"
 #include "gfx950_common.h"
 
 namespace bgtq {
@@ -88,6 +89,7 @@ template <int D, int KF, int NN, int SG>
 __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
   using Sl = Slot<D, KF, NN>;
+  static_assert(KF == 0 || row_enc::scratch_bytes(D) <= Sl::BYTES, "append scratch fits a ring slot");
   constexpr int KS = Gm::KS, DT = Gm::DT, PR = Gm::PR, VI = Gm::VI;
   constexpr int RB = Sl::RB, KI = Sl::KI, L = Sl::L, AHEAD = Sl::AHEAD;
   static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
@@ -166,6 +168,62 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   int lim_min = head_ok ? lim : t_end;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o, 64));
+
+  // ---------------- decode-step append ----------------
+  // With p.k_new the sequence's newest token (row T_b - 1) arrives in this
+  // launch. The wave whose chunk holds it loads the new K and V rows (and,
+  // at d=64, its column of the transposed rotation) with the prologue's
+  // loads; after the prologue it encodes the K (packed K; FP16 K rows are
+  // converted) and converts the V, stores both rows to the caches for the
+  // later steps and keeps them in registers: after that chunk's loads land it
+  // writes them over the chunk's LDS copy, whose loads may have read the rows
+  // before they were stored.
+  constexpr int JL = D > 64 ? 2 : 1;
+  const int t_new = T_b - 1;
+  const int c_new = t_new >= 0 ? t_new / kChunk : 0;
+  const bool app = p.k_new != nullptr && t_new >= 0 && c_new % (p.splits * kWaves) == split * kWaves + wave;
+  const int i_new = app ? c_new / (p.splits * kWaves) : -1;  // the wave's loop iteration of that chunk
+  uint32_t pk_new[JL] = {};                    // packed K bytes lane, lane + 64
+  uint32_t h_new = 0;                          // FP16 scale bits (lanes below the norm stride)
+  u32x4 v_new16{0u, 0u, 0u, 0u}, k_new16{0u, 0u, 0u, 0u};  // FP16 pieces of the V / K row (lanes below D / 8)
+  uint32_t v_raw[8] = {}, k_raw[8] = {};       // lane's 8 values of the new V / K row: FP32 bits, or FP16 pairs
+  uint32_t k_nat[JL] = {};                     // packed K: new K element lane + 64 jl (FP32 or FP16 bits)
+  float rt_col[D == 64 ? D : 1];               // d=64: R[lane][i] for every i
+  row_enc::Lane<D> lc;
+  const int64_t v_off = (int64_t)b * p.v_new_seq_stride + kv * p.v_new_head_stride;
+  const int64_t k_off = (int64_t)b * p.k_new_seq_stride + kv * p.k_new_head_stride;
+  auto load_piece = [&](const void *src, int f32, int64_t off, uint32_t (&r)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (f32) r[k] = static_cast<const uint32_t *>(src)[off + 8 * lane + k];
+      else if (k < 4) r[k] = (uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k] |
+                             ((uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k + 1] << 16);
+    }
+  };
+  auto half_piece = [&](int f32, const uint32_t (&r)[8]) {
+    u32x4 h;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      h[k] = f32 ? (uint32_t)row_enc::f32_to_f16_bits(__uint_as_float(r[2 * k])) |
+                       ((uint32_t)row_enc::f32_to_f16_bits(__uint_as_float(r[2 * k + 1])) << 16)
+                 : r[k];
+    return h;
+  };
+  if (app) {
+    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
+    if (KF == 1) {
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl)
+        k_nat[jl] = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new)[k_off + lane + 64 * jl]
+                                : (uint32_t)static_cast<const uint16_t *>(p.k_new)[k_off + lane + 64 * jl];
+      if (D == 64) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) rt_col[i] = fl.rot_t[kv][i * D + lane];
+      }
+    } else if (lane < PR) {
+      load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
+    }
+  }
 
   // ---------------- prologue ----------------
   // One round trip: wave 0 DMAs the MFMA lookup tables of the K-steps' books
@@ -286,6 +344,53 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   }
   if (KF == 1) lds_barrier();  // q staging (last ring slot) is dead
 
+  if (app) {  // the new token's rows: convert / encode, store to the caches
+    if (lane < PR) {
+      v_new16 = half_piece(p.v_new_f32, v_raw);
+      *reinterpret_cast<u32x4 *>(const_cast<_Float16 *>(v_base) + (int64_t)t_new * D + 8 * lane) = v_new16;
+    }
+    if (KF == 1) {
+      // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
+      const DevTables *T = p.tables[kv];
+      lc.init(T, lane);  // here, not with the prologue loads: its byte loads would be waited for there
+      float x[JL];
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl) {
+        const int src = lc.perm[jl];
+        uint32_t raw = __shfl(k_nat[0], src & 63, 64);
+        if (JL > 1) {
+          const uint32_t hi = __shfl(k_nat[JL - 1], src & 63, 64);
+          raw = src >= 64 ? hi : raw;
+        }
+        const uint16_t h16 = p.k_new_f32 ? row_enc::f32_to_f16_bits(__uint_as_float(raw)) : (uint16_t)raw;
+        x[jl] = lc.own[jl] ? row_enc::f16_bits_to_f32(h16) : 0.0f;
+      }
+      // Scratch: this wave's last ring slot, loaded into only from the loop on.
+      const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
+      const float *rt = fl.rot_t[kv];
+      h_new = row_enc::encode_row<D>(
+          T, lc, x,
+          [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
+          fl.lut[kv], fl.books[kv], scr, lane);
+      const int logical = T->nibble_dims / 2 + D - T->nibble_dims;
+      uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * RB;
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl) {
+        const int bb = lane + 64 * jl;
+        if (bb < RB) {
+          pk_new[jl] = row_enc::packed_byte(scr.codes, bb, T->nibble_dims, logical);
+          prow[bb] = (uint8_t)pk_new[jl];
+        }
+      }
+      if (lane < 2) const_cast<uint16_t *>(n_base)[(int64_t)t_new * 2 + lane] = (uint16_t)h_new;
+      row_enc::wave_sync();  // scratch reads done before the slot's first load
+    } else if (lane < PR) {
+      k_new16 = half_piece(p.k_new_f32, k_raw);
+      *reinterpret_cast<u32x4 *>(reinterpret_cast<_Float16 *>(const_cast<uint8_t *>(k_base)) + (int64_t)t_new * D +
+                                 8 * lane) = k_new16;
+    }
+  }
+
   const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 O[DT];
@@ -311,6 +416,19 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     else wait_vm<0>();
     const uint8_t *sb = slot_base(i % Sl::RING);
     const uint8_t *kbuf = sb + Sl::KOFF;
+    if (i == i_new) {  // the appended row over the chunk's LDS copy (wave-uniform)
+      const int r = t_new % kChunk;
+      uint8_t *wsb = const_cast<uint8_t *>(sb);
+      if (lane < PR) *reinterpret_cast<u32x4 *>(wsb + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = v_new16;
+      if (KF == 1) {
+#pragma unroll
+        for (int jl = 0; jl < JL; ++jl)
+          if (lane + 64 * jl < RB) wsb[Sl::KOFF + r * RB + lane + 64 * jl] = (uint8_t)pk_new[jl];
+        if (lane < 2) reinterpret_cast<uint16_t *>(wsb + Sl::NOFF)[2 * r + lane] = (uint16_t)h_new;
+      } else if (lane < PR) {
+        *reinterpret_cast<u32x4 *>(wsb + Sl::KOFF + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = k_new16;
+      }
+    }
 
     // QK: acc[u][g] = sum over the K-steps of group g.
     f32x4 acc[2][2];

@@ -1,0 +1,204 @@
+// One K row encoded by one wave (lane j owns dimension j, and j + 64 at
+// d=128): the arithmetic of src/reference/production_math.py:4-24 as its
+// torch code evaluates on the CPU, bit for bit. Shared by the wave encoder
+// (encode_wave.hip) and the decode-step append inside the fused decode
+// kernel (decode_fast.hip).
+//  * the FP32 sums of production_math.py:12, :14 and :23 follow ATen's 8-lane
+//    inner-sum tree: lane (l, g) forms partial l of group g from the four
+//    interleaved accumulators in the tree's order, lane g then adds the eight
+//    partials in order; masked-out leaves are exact zeros and are skipped
+//    (a + 0 = a for the never-negative-zero accumulators), all groups at once;
+//  * y_j = sum_i xn_i R[j][i] (production_math.py:16) is one FMA chain per
+//    lane over all i in ascending order from +0, the order of the CPU sgemm;
+//    off-group rotation entries are exact zeros, so adding their products
+//    changes nothing;
+//  * division and square root are IEEE (built with -ffp-contract=off and
+//    correctly rounded fp32 division/sqrt).
+#pragma once
+
+#include <hip/hip_fp16.h>
+
+#include "bgtq_internal.h"
+
+namespace bgtq {
+namespace row_enc {
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Per-wave LDS scratch of one row: leaf[D] f32, xn[D] f32, part[64] f32,
+// tot[8] f32, codes[D] u8.
+__host__ __device__ constexpr int scratch_bytes(int D) { return ((D * 4 * 2 + 64 * 4 + 8 * 4 + D) + 15) & ~15; }
+
+template <int D>
+struct Scratch {
+  float *leaf, *xn, *part, *tot;
+  uint8_t *codes;
+  __device__ explicit Scratch(uint8_t *base) {
+    leaf = reinterpret_cast<float *>(base);
+    xn = leaf + D;
+    part = xn + D;
+    tot = part + 64;
+    codes = reinterpret_cast<uint8_t *>(tot + 8);
+  }
+};
+
+// ATen's 8-lane inner sum over leaf[0..D) restricted to each group's positions,
+// for all ng groups; lane (l, g) = 8 g + l passes its group's range [gs, ge).
+// Every lane then reads tot[g].
+template <int D>
+__device__ __forceinline__ void group_sums(const float *leaf, float *part, float *tot, int lane, int ng, int gs,
+                                           int ge) {
+  constexpr int NV = D / 8, SI = NV / 4;
+  if (lane < 8 * ng) {
+    const int l = lane & 7, g = lane >> 3;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SI; ++i) {
+      const int p0 = (4 * i + 0) * 8 + l, p1 = (4 * i + 1) * 8 + l, p2 = (4 * i + 2) * 8 + l, p3 = (4 * i + 3) * 8 + l;
+      if (p0 >= gs && p0 < ge) a0 += leaf[p0];
+      if (p1 >= gs && p1 < ge) a1 += leaf[p1];
+      if (p2 >= gs && p2 < ge) a2 += leaf[p2];
+      if (p3 >= gs && p3 < ge) a3 += leaf[p3];
+    }
+#pragma unroll
+    for (int v = SI * 4; v < NV; ++v) {
+      const int p = v * 8 + l;
+      if (p >= gs && p < ge) a0 += leaf[p];
+    }
+    a0 += a1;
+    a0 += a2;
+    a0 += a3;
+    part[g * 8 + l] = a0;
+  }
+  wave_sync();
+  if (lane < ng) {
+    float t = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) t += part[lane * 8 + l];
+    tot[lane] = t;
+  }
+  wave_sync();
+}
+
+// Per-lane constants of the dimensions a lane owns, from the tables.
+template <int D>
+struct Lane {
+  static constexpr int JL = D > 64 ? 2 : 1;  // dimensions per lane
+  int perm[JL], grp[JL], cb[JL], bk[JL];
+  float off[JL], inv[JL];
+  bool own[JL];
+  int gs, ge;  // group range of this lane's tree partial (lane = 8 g + l)
+  __device__ void init(const DevTables *T, int lane) {
+    gs = T->gstart[(lane >> 3) & (kMaxGroups - 1)];
+    ge = T->gend[(lane >> 3) & (kMaxGroups - 1)];
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl) {
+      const int j = lane + 64 * jl;
+      own[jl] = j < D;
+      const int jj = own[jl] ? j : 0;
+      perm[jl] = T->perm[jj];
+      grp[jl] = T->group_of[jj];
+      cb[jl] = T->pos_cb[jj];
+      bk[jl] = T->pos_book[jj];
+      off[jl] = T->lut_off[jj];
+      inv[jl] = T->lut_inv[jj];
+    }
+  }
+};
+
+// Encodes the row whose FP16-valued inputs x (head-perm order, lane's
+// dimensions) are given: codes land in s.codes[0..D); lanes below the norm
+// stride return their FP16 scale bits (zero past the groups), the others 0.
+// rot(i, jl) is R[j][i] for the lane's dimension j = lane + 64 jl (from LDS,
+// global memory or registers); lut and books may be in LDS or global memory.
+template <int D, typename Rot>
+__device__ __forceinline__ uint16_t encode_row(const DevTables *T, const Lane<D> &c, const float (&x)[Lane<D>::JL],
+                                               Rot rot, const uint8_t *lut, const float *books, const Scratch<D> &s,
+                                               int lane) {
+  constexpr int JL = Lane<D>::JL;
+  const int ng = T->groups, mc = T->max_centroids;
+  // production_math.py:12  n_g = sqrt(sum((x*x)*mask) + 1e-30)
+#pragma unroll
+  for (int jl = 0; jl < JL; ++jl)
+    if (c.own[jl]) s.leaf[lane + 64 * jl] = x[jl] * x[jl];
+  wave_sync();
+  group_sums<D>(s.leaf, s.part, s.tot, lane, ng, c.gs, c.ge);
+  float nrm[kMaxGroups];
+#pragma unroll
+  for (int g = 0; g < kMaxGroups; ++g) nrm[g] = g < ng ? __builtin_sqrtf(s.tot[g] + 1e-30f) : 1.0f;
+  // production_math.py:14  raw_g = sum(n_g*mask)/|g| (more than one group)
+  float raw[kMaxGroups];
+  if (ng > 1) {
+    wave_sync();
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl) {
+      float n = nrm[0];
+#pragma unroll
+      for (int g = 1; g < kMaxGroups; ++g) n = c.grp[jl] == g ? nrm[g] : n;
+      if (c.own[jl]) s.leaf[lane + 64 * jl] = n;
+    }
+    wave_sync();
+    group_sums<D>(s.leaf, s.part, s.tot, lane, ng, c.gs, c.ge);
+#pragma unroll
+    for (int g = 0; g < kMaxGroups; ++g) raw[g] = g < ng ? s.tot[g] / (float)T->gsize[g] : 0.0f;
+  } else {
+#pragma unroll
+    for (int g = 0; g < kMaxGroups; ++g) raw[g] = nrm[g];
+  }
+  // production_math.py:15  xn = x / where(n > 1e-10, n, 1)
+#pragma unroll
+  for (int jl = 0; jl < JL; ++jl) {
+    float n = nrm[0];
+#pragma unroll
+    for (int g = 1; g < kMaxGroups; ++g) n = c.grp[jl] == g ? nrm[g] : n;
+    if (c.own[jl]) s.xn[lane + 64 * jl] = x[jl] / (n > 1e-10f ? n : 1.0f);
+  }
+  wave_sync();
+  // production_math.py:16-18  y_j (FMA chain, i ascending), bin, code
+  float cent[JL];
+#pragma unroll
+  for (int jl = 0; jl < JL; ++jl) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D; ++i) acc = __builtin_fmaf(s.xn[i], rot(i, jl), acc);
+    float t = (acc - c.off[jl]) * c.inv[jl];
+    t = fminf(fmaxf(t, 0.0f), 255.0f);
+    const uint8_t code = lut[c.cb[jl] * 256 + (int)t];
+    if (c.own[jl]) s.codes[lane + 64 * jl] = code;
+    cent[jl] = books[c.bk[jl] * mc + code];
+  }
+  // production_math.py:20-23  corrected_g = raw_g / max(sqrt(sum((c*c)*mask)), 1e-10)
+  wave_sync();
+#pragma unroll
+  for (int jl = 0; jl < JL; ++jl)
+    if (c.own[jl]) s.leaf[lane + 64 * jl] = cent[jl] * cent[jl];
+  wave_sync();
+  group_sums<D>(s.leaf, s.part, s.tot, lane, ng, c.gs, c.ge);
+  uint16_t h = 0;
+  if (lane < T->norm_stride && lane < ng) {
+    const float cc = fmaxf(__builtin_sqrtf(s.tot[lane]), 1e-10f);
+    float rg = raw[0];
+#pragma unroll
+    for (int g = 1; g < kMaxGroups; ++g) rg = lane == g ? raw[g] : rg;
+    h = f32_to_f16_bits(rg / cc);
+  }
+  return h;
+}
+
+// Byte b of the packed row (src/reference/mixed_layout.py:21-27): nibble
+// bytes, then byte codes, then zero padding.
+__device__ __forceinline__ uint8_t packed_byte(const uint8_t *codes, int b, int nibble_dims, int logical) {
+  if (b < nibble_dims / 2) return (uint8_t)((codes[2 * b] & 15) | ((codes[2 * b + 1] & 15) << 4));
+  if (b < logical) return codes[nibble_dims + b - nibble_dims / 2];
+  return 0;
+}
+
+}  // namespace row_enc
+}  // namespace bgtq

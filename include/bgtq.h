@@ -206,6 +206,29 @@ typedef struct {
 bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes);
 bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d);
 
+/* One decode step of a layer with its new token, in one launch: the model
+ * step's encode_k (packed K) or append (FP16 K), the V append and the
+ * attention of src/model/decoder.ts:46-56 at rows = 1 (src/model/codec.wgsl,
+ * src/model/append.wgsl, then src/model/compressed-dot.wgsl:14-31 and
+ * src/model/attention.wgsl:24-39). The new token of sequence b is row
+ * lengths[b] - 1 of the caches: its post-RoPE K (k_new[b][kv][dim], FP32 is
+ * rounded to FP16 first) is encoded with tables[kv] into packed/norms (or
+ * converted into k_f16), its V (v_new) converted into the FP16 V rows, and
+ * the attention covers lengths[b] tokens including it. Same results as
+ * bgtq_encode_batched of those rows, the V rows written, then bgtq_decode.
+ * Needs the fused kernel's layouts (FP16 V, d 64 or 128, 32-dim K-steps within
+ * one group and book, norm_stride 2); other layouts return
+ * BGTQ_ERR_UNSUPPORTED (use the two calls). The workspace is the decode's. */
+typedef struct {
+  const void *k_new;
+  int32_t k_new_dtype; /* BGTQ_DTYPE_F32 or BGTQ_DTYPE_F16 */
+  int64_t k_new_seq_stride, k_new_head_stride; /* elements */
+  const void *v_new;
+  int32_t v_new_dtype;
+  int64_t v_new_seq_stride, v_new_head_stride;
+} bgtq_append_desc;
+bgtq_status bgtq_decode_append(bgtq_context *ctx, const bgtq_decode_desc *d, const bgtq_append_desc *a);
+
 /* Chunked-prefill attention for one layer: the model forward over a chunk of
  * prompt rows (src/model/decoder.ts:46-56 with rows > 1, called per chunk by
  * src/model/decoder.ts:82; the reference caps chunks at 32 rows,

@@ -1,0 +1,129 @@
+"""The decode step with its new token in one launch (bgtq_decode_append) against
+the two-call path of the reference's model step (src/model/decoder.ts:46-56 at
+rows = 1): bgtq_encode_batched of the new K rows, the V rows written, then
+bgtq_decode. Packed K rows, FP16 scales, K and V rows must be bit-identical and
+the outputs equal, for new tokens at every position inside a 32-token chunk,
+ragged batches and forced splits."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="f32", hkv=2, hq=14, seed=0):
+    import torch
+    import bgtq
+    from bgtq import batched, calibrate
+    print("append", dim, key_format, lengths, splits, k_dtype, v_dtype, flush=True)
+    B, cap = len(lengths), max(lengths)
+    g = torch.Generator().manual_seed(seed)
+    hist = torch.randn((B, hkv, cap, dim), generator=g).half().cuda()
+    v0 = torch.randn((B, hkv, cap, dim), generator=g).half().cuda()
+    q = torch.randn((B, hq, dim), generator=g).cuda()
+    tdt = {"f32": torch.float32, "f16": torch.float16}
+    k_new = torch.randn((B, hkv, dim), generator=g).to(tdt[k_dtype]).cuda()
+    v_new = torch.randn((B, hkv, dim), generator=g).to(tdt[v_dtype]).cuda()
+    lens = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    outs, caches, tabs = [], [], []
+    if key_format == "packed":
+        p = calibrate.layout_b(dim)
+        tabs = [bgtq.Tables(device, p) for _ in range(hkv)]
+        rb, ns = p.rowBytes, p.normStride
+        packed0 = torch.zeros((B, hkv, cap * rb + 64), dtype=torch.uint8, device="cuda")
+        # scale rows padded to 16 bytes: the fused kernel loads four tokens' scales at once
+        norms0 = torch.zeros((B, hkv, (cap * ns + 32 + 7) // 8 * 8), dtype=torch.int16, device="cuda")
+        batched.encode(device, [dict(tables=tabs[h], src=hist[b, h], src_row_stride=dim, rows=lengths[b] - 1,
+                                     packed=packed0[b, h], norms=norms0[b, h]) for b in range(B) for h in range(hkv)],
+                       "f16")
+    for mode in ("two calls", "fused"):
+        out = torch.full((B, hq, dim), float("nan"), device="cuda")
+        v = v0.clone()
+        if key_format == "packed":
+            packed, norms = packed0.clone(), norms0.clone()
+            kw = dict(tables=tabs, packed=packed, packed_seq_stride=packed.stride(0),
+                      packed_head_stride=packed.stride(1), norms=norms, norms_seq_stride=norms.stride(0),
+                      norms_head_stride=norms.stride(1))
+            cache = (packed, norms, v)
+        else:
+            k = hist.clone()
+            kw = dict(k_f16=k, k_seq_stride=k.stride(0), k_head_stride=k.stride(1))
+            cache = (k, v)
+        args = dict(batch=B, q_heads=hq, kv_heads=hkv, dim=dim, q=q, out=out, lengths=lens, max_length=cap, v=v,
+                    v_seq_stride=v.stride(0), v_head_stride=v.stride(1), splits=splits, **kw)
+        ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8, device="cuda")
+        desc = batched.decode_desc(workspace=ws, **args)
+        if mode == "two calls":
+            if key_format == "packed":
+                batched.encode(device, [dict(tables=tabs[h], src=k_new[b, h], src_row_stride=dim, rows=1,
+                                             packed=packed[b, h], norms=norms[b, h], dst_row0=lengths[b] - 1)
+                                        for b in range(B) for h in range(hkv)], k_dtype)
+            else:
+                for b in range(B):
+                    k[b, :, lengths[b] - 1] = k_new[b].half()
+            for b in range(B):
+                v[b, :, lengths[b] - 1] = v_new[b].half()
+            batched.decode(device, desc)
+        else:
+            batched.decode_append(device, desc, batched.append_desc(k_new=k_new, v_new=v_new))
+        torch.cuda.synchronize()
+        assert not ws[:4 * B * hkv].any(), "split counters left nonzero"
+        outs.append(out.cpu())
+        caches.append([c.cpu() for c in cache])
+    for a, b in zip(caches[0], caches[1]):
+        assert torch.equal(a, b), "caches differ"
+    assert not torch.isnan(outs[1]).any()
+    assert torch.equal(outs[0], outs[1]), float((outs[0] - outs[1]).abs().max())
+    for t in tabs:
+        t.destroy()
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_append_packed_every_chunk_position(device, dim):
+    _run(device, dim=dim, key_format="packed", lengths=[1, 32, 33, 64, 97, 1000, 4096])
+
+
+@pytest.mark.parametrize("splits", [1, 3, 16])
+def test_append_packed_forced_splits(device, splits):
+    _run(device, dim=64, key_format="packed", lengths=[2000, 31, 4095], splits=splits, hkv=3, hq=9)
+
+
+def test_append_fp16_sources(device):
+    _run(device, dim=64, key_format="packed", lengths=[513, 130], k_dtype="f16", v_dtype="f16")
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_append_fp16_keys(device, dim):
+    _run(device, dim=dim, key_format="fp16", lengths=[1, 40, 3000])
+
+
+def test_append_unsupported_layout_is_rejected(device, oracle):
+    """A layout outside the fused kernel (a real SmolLM2 head: K-steps mixing groups) is refused and
+    nothing is written; the two-call path serves it."""
+    import torch
+    import bgtq
+    from bgtq import batched
+    from conftest import REF
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    p = bgtq.BlockGTQParameters.from_serialized(a["h0_config"], a["h0_table"])
+    t = bgtq.Tables(device, p)
+    try:
+        T, dim = 100, 64
+        packed = torch.zeros((1, 1, T * p.rowBytes + 64), dtype=torch.uint8, device="cuda")
+        norms = torch.zeros((1, 1, T * p.normStride + 32), dtype=torch.int16, device="cuda")
+        v = torch.zeros((1, 1, T, dim), dtype=torch.float16, device="cuda")
+        q = torch.zeros((1, 3, dim), device="cuda")
+        out = torch.zeros((1, 3, dim), device="cuda")
+        args = dict(batch=1, q_heads=3, kv_heads=1, dim=dim, q=q, out=out,
+                    lengths=torch.tensor([T], dtype=torch.int32, device="cuda"), max_length=T, v=v,
+                    v_seq_stride=v.stride(0), v_head_stride=v.stride(1), tables=[t], packed=packed,
+                    packed_seq_stride=packed.stride(0), packed_head_stride=packed.stride(1), norms=norms,
+                    norms_seq_stride=norms.stride(0), norms_head_stride=norms.stride(1))
+        ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8, device="cuda")
+        desc = batched.decode_desc(workspace=ws, **args)
+        kn = torch.ones((1, 1, dim), device="cuda")
+        with pytest.raises(bgtq.UnsupportedError, match="decode_append"):
+            batched.decode_append(device, desc, batched.append_desc(k_new=kn, v_new=kn))
+        torch.cuda.synchronize()
+        assert not packed.any() and not v.any()
+    finally:
+        t.destroy()
