@@ -998,17 +998,43 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   }
   if (!d->v || !d->q || !d->out || !d->starts) return fail(BGTQ_ERR_RANGE, "null v/q/out/starts");
   if (d->split_tokens < 0) return fail(BGTQ_ERR_RANGE, "negative split_tokens");
+  if ((int64_t)d->batch * d->kv_heads > 65535) return fail(BGTQ_ERR_UNSUPPORTED, "prefill handles up to 65535 sequence x KV head units");
   const int64_t G = d->q_heads / d->kv_heads, nq = (int64_t)d->rows * G;
   plan->tile_queries = nq >= 2048 ? 64 * prefill_column_blocks(d->dim) : 64;
   plan->tiles = (int)((nq + plan->tile_queries - 1) / plan->tile_queries);
   const int64_t L = d->max_length;
+  const int64_t sp_min = std::max<int64_t>(32, ((L + kPrefillMaxSplits - 1) / kPrefillMaxSplits + 31) / 32 * 32);
+  const int64_t sp_max = (L + 31) / 32 * 32;
   int64_t sp = d->split_tokens;
   if (sp == 0) {
-    const int64_t units = (int64_t)d->batch * d->kv_heads * plan->tiles;
-    sp = std::max<int64_t>(64, units * (L / 2 + 1) / (2 * (int64_t)device_cus()));
+    // The shortest split length whose workgroups fit one round of two per
+    // compute unit, for a chunk at the end of the cache (the most history:
+    // the start is a device value). A second, partly filled round would leave
+    // most of the GPU idle behind the first one's tail.
+    const int64_t units = (int64_t)d->batch * d->kv_heads, slots = 2 * (int64_t)device_cus();
+    const int64_t start = L - d->rows, tq = plan->tile_queries;
+    auto workgroups = [&](int64_t s) {
+      int64_t n = 0;
+      for (int64_t t = 0; t < plan->tiles; ++t) {
+        const int64_t e = start + (std::min(nq, (t + 1) * tq) - 1) / G + 1;
+        n += (e + s - 1) / s;
+      }
+      return n * units;
+    };
+    if (workgroups(sp_max) > slots) {
+      sp = std::max<int64_t>(64, units * plan->tiles * (L / 2 + 1) / slots);  // several rounds anyway
+    } else {
+      int64_t lo = sp_min / 32, hi = sp_max / 32;  // in blocks; workgroups() does not grow with the length
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        if (workgroups(mid * 32) <= slots) hi = mid;
+        else lo = mid + 1;
+      }
+      sp = lo * 32;
+    }
   }
-  sp = std::max<int64_t>(sp, (L + kPrefillMaxSplits - 1) / kPrefillMaxSplits);
-  sp = std::min<int64_t>((sp + 31) / 32 * 32, (L + 31) / 32 * 32);
+  sp = std::max<int64_t>(sp, sp_min);
+  sp = std::min<int64_t>((sp + 31) / 32 * 32, sp_max);
   plan->split_tokens = (int)sp;
   plan->splits = (int)((L + sp - 1) / sp);
   const int64_t queries = (int64_t)d->batch * d->rows * d->q_heads;

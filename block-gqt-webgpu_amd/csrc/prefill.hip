@@ -131,7 +131,13 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
   extern __shared__ __align__(16) uint8_t smem[];
 
-  const int split = blockIdx.x, tile = blockIdx.y, unit = blockIdx.z;
+  // Grid (tile, unit, split), tiles in reverse. Consecutive workgroup ids go
+  // to consecutive XCDs, so with the tile fastest every XCD gets an even
+  // share of each split's tiles (a split index in the low bits would pin each
+  // split to fixed XCDs, and the first splits, active in every tile, would
+  // crowd theirs); within a split the heaviest tiles (the last queries, which
+  // see the most history) are dispatched first.
+  const int tile = p.tiles - 1 - (int)blockIdx.x, unit = blockIdx.y, split = blockIdx.z;
   const int b = unit / p.kv_heads, kv = unit - b * p.kv_heads;
   const int G = p.G, Hq = p.q_heads, rows = p.rows;
   const int tid = threadIdx.x, lane = tid & 63, gq = lane >> 4, col = lane & 15;
@@ -147,7 +153,11 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   const int SP = p.split_tokens;
   const int n_act = (e_tile + SP - 1) / SP;
   if (split >= n_act) return;  // workgroup-uniform: before any barrier
-  const int t_lo = split * SP, t_hi = min(t_lo + SP, e_tile);
+  // The tile's history [0, e_tile) is divided evenly (in 32-token blocks)
+  // over its n_act splits, so no split is a sliver; each is at most SP long
+  // and none is empty ((n_act - 1) * part <= (n_act - 1) * SP < e_tile).
+  const int part = ((e_tile + n_act - 1) / n_act + kChunk - 1) / kChunk * kChunk;
+  const int t_lo = split * part, t_hi = min(t_lo + part, e_tile);
   const int n_blocks = (t_hi - t_lo + kChunk - 1) / kChunk;
   const DevTables *T = KF == 1 ? p.tables[kv] : nullptr;
   float *books = reinterpret_cast<float *>(smem + Sl::RING * Sl::BYTES);
@@ -565,9 +575,9 @@ hipError_t launch_ncb(const PrefillParams &p, const FastLayout &fl, hipStream_t 
     return allowed;
   }
   const unsigned units = (unsigned)(p.batch * p.kv_heads);
-  hipLaunchKernelGGL((prefill_kernel<D, KF, NN, SG, NCB>), dim3((unsigned)p.splits, (unsigned)p.tiles, units),
+  hipLaunchKernelGGL((prefill_kernel<D, KF, NN, SG, NCB>), dim3((unsigned)p.tiles, units, (unsigned)p.splits),
                      dim3(kThreads), lds, stream, p, fl);
-  hipError_t e = hipGetLastError();
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int nq = p.rows * p.G;
   hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((nq + kWaves - 1) / kWaves), units), dim3(kThreads),
