@@ -81,6 +81,15 @@ class PrefillDesc(ctypes.Structure):
                 ("max_length", ctypes.c_uint32), ("split_tokens", ctypes.c_int32),
                 ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
 
+class Binding(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("bytes", ctypes.c_size_t), ("tables", ctypes.c_void_p)]
+
+
+class ModelDispatch(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("params", ctypes.c_uint32 * 8), ("bindings", ctypes.POINTER(Binding)),
+                ("n_bindings", ctypes.c_size_t), ("x", ctypes.c_uint32), ("y", ctypes.c_uint32)]
+
+
 _VP, _SZ, _I32, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32
 _PP = ctypes.POINTER(ctypes.c_void_p)
 
@@ -128,6 +137,7 @@ SIGNATURES = {
     "bgtq_decode_append": (_I32, [_VP, ctypes.POINTER(DecodeDesc), ctypes.POINTER(AppendDesc)]),
     "bgtq_prefill_workspace_size": (_I32, [ctypes.POINTER(PrefillDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_prefill": (_I32, [_VP, ctypes.POINTER(PrefillDesc)]),
+    "bgtq_model_submit": (_I32, [_VP, ctypes.POINTER(ModelDispatch), _SZ]),
 }
 
 _lib = None

@@ -92,6 +92,16 @@ class CalibrationHead:
     row_bytes: int
     norm_stride: int
 
+    # The head's config and table bindings of the model dispatches
+    # (src/model/decoder.ts:52, :55): both are its device tables.
+    @property
+    def config(self):
+        return self.tables
+
+    @property
+    def table(self):
+        return self.tables
+
 
 class Calibration:
     """Device-resident tables of every (layer, KV head), index layer * kv_heads + head."""

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -195,7 +196,7 @@ struct bgtq_attention {
 extern "C" {
 
 const char *bgtq_last_error(void) { return g_error.c_str(); }
-int32_t bgtq_abi_version(void) { return 2; }
+int32_t bgtq_abi_version(void) { return 3; }
 
 // ---------------------------------------------------------------- context
 bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
@@ -1288,6 +1289,294 @@ void bgtq_attention_destroy(bgtq_attention *a) {
   (void)a->keys->ctx->use();
   (void)hipStreamSynchronize(a->keys->ctx->stream);
   delete a;
+}
+
+/* ---- device buffers ------------------------------------------------------ */
+
+struct bgtq_buffer {
+  bgtq_context *ctx = nullptr;
+  DeviceBuffer mem;
+};
+
+bgtq_status bgtq_buffer_create(bgtq_context *ctx, size_t bytes, bgtq_buffer **out) {
+  if (!ctx || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  const size_t size = (bytes + 3) / 4 * 4;
+  if (size < 4) return fail(BGTQ_ERR_RANGE, "unsupported buffer size %zu", size);
+  if (bgtq_status s = ctx->use()) return s;
+  std::unique_ptr<bgtq_buffer> b(new bgtq_buffer());
+  b->ctx = ctx;
+  if (bgtq_status s = b->mem.alloc(size, "buffer")) return s;  // zero-filled
+  *out = b.release();
+  return BGTQ_OK;
+}
+void *bgtq_buffer_device_ptr(const bgtq_buffer *b) { return b ? b->mem.ptr : nullptr; }
+size_t bgtq_buffer_size(const bgtq_buffer *b) { return b ? b->mem.bytes : 0; }
+bgtq_status bgtq_buffer_write(bgtq_buffer *b, size_t offset, const void *src, size_t bytes) {
+  if (!b || (bytes && !src)) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (offset > b->mem.bytes || bytes > b->mem.bytes - offset)
+    return fail(BGTQ_ERR_RANGE, "Unaligned/out-of-range buffer upload");
+  if (!bytes) return BGTQ_OK;
+  if (bgtq_status s = b->ctx->use()) return s;
+  HIP_TRY(hipMemcpyAsync(static_cast<uint8_t *>(b->mem.ptr) + offset, src, bytes, hipMemcpyHostToDevice,
+                         b->ctx->stream), "buffer upload");
+  HIP_TRY(hipStreamSynchronize(b->ctx->stream), "hipStreamSynchronize");
+  return BGTQ_OK;
+}
+bgtq_status bgtq_buffer_read(const bgtq_buffer *b, size_t offset, void *dst, size_t bytes) {
+  if (!b || (bytes && !dst)) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (offset > b->mem.bytes || bytes > b->mem.bytes - offset) return fail(BGTQ_ERR_RANGE, "Invalid readback length");
+  if (!bytes) return BGTQ_OK;
+  if (bgtq_status s = b->ctx->use()) return s;
+  HIP_TRY(hipStreamSynchronize(b->ctx->stream), "hipStreamSynchronize");
+  HIP_TRY(hipMemcpy(dst, static_cast<const uint8_t *>(b->mem.ptr) + offset, bytes, hipMemcpyDeviceToHost),
+          "buffer readback");
+  return BGTQ_OK;
+}
+void bgtq_buffer_destroy(bgtq_buffer *b) {
+  if (!b) return;
+  (void)b->ctx->use();
+  (void)hipStreamSynchronize(b->ctx->stream);
+  delete b;
+}
+
+/* ---- the model step's kernel protocol ----------------------------------- */
+
+}  // extern "C"
+
+namespace {
+
+enum class ModelOp { Append, Encode, Scores, Softmax, Weighted };
+
+struct ModelStep {
+  ModelOp op;
+  ModelAppendParams append{};
+  bgtq_encode_job encode{};
+  ModelScoresParams scores{};
+  int kv_count = 0, lds = 0;
+  ModelAttnParams attn{};
+  int64_t score_rows = 0;
+};
+
+bool aligned(const void *p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+// Checks one dispatch and turns it into a queued step; nothing is queued here.
+bgtq_status plan_model_dispatch(const bgtq_model_dispatch &D, size_t idx, ModelStep *st) {
+  if (!D.name) return fail(BGTQ_ERR_RANGE, "dispatch %zu: null name", idx);
+  const std::string name(D.name);
+  const uint32_t *P = D.params;
+  auto count = [&](size_t want) -> bgtq_status {
+    if (D.n_bindings != want || (want && !D.bindings))
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): %zu bindings, %zu expected", idx, D.name, D.n_bindings, want);
+    return BGTQ_OK;
+  };
+  auto need = [&](int b, uint64_t bytes, size_t align) -> bgtq_status {
+    const bgtq_binding &B = D.bindings[b];
+    if (!bytes) return BGTQ_OK;
+    if (!B.ptr) return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): binding %d is null", idx, D.name, b);
+    if (B.bytes < bytes)
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): binding %d holds %zu bytes, %llu needed", idx, D.name, b,
+                  B.bytes, (unsigned long long)bytes);
+    if (!aligned(B.ptr, align))
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): binding %d is not %zu-byte aligned", idx, D.name, b, align);
+    return BGTQ_OK;
+  };
+  auto tables_of = [&](const bgtq_tables **t) -> bgtq_status {
+    *t = D.bindings[0].tables;
+    if (!*t || (D.bindings[1].tables && D.bindings[1].tables != *t))
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): config and table bindings must name one calibration table set",
+                  idx, D.name);
+    return BGTQ_OK;
+  };
+  const uint64_t x = D.x, y = D.y;
+  if (name == "append") {
+    if (bgtq_status s = count(2)) return s;
+    const uint64_t rows = P[0], start = P[1], capacity = P[2], heads = P[3];
+    if (rows && (!heads || start + rows > capacity))
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (append): rows %llu from %llu exceed capacity %llu", idx,
+                  (unsigned long long)rows, (unsigned long long)start, (unsigned long long)capacity);
+    const uint64_t pairs = std::min<uint64_t>(x * 128, rows * heads * 32);
+    if (bgtq_status s = need(0, pairs * 8, 8)) return s;
+    if (bgtq_status s = need(1, pairs ? heads * capacity * 64 * 2 : 0, 4)) return s;
+    st->op = ModelOp::Append;
+    st->append.input = static_cast<const float *>(D.bindings[0].ptr);
+    st->append.cache = static_cast<uint32_t *>(D.bindings[1].ptr);
+    st->append.pairs = (int64_t)pairs;
+    st->append.start = (int32_t)start;
+    st->append.capacity = (int32_t)capacity;
+    st->append.heads = (int32_t)heads;
+    return BGTQ_OK;
+  }
+  if (name == "encode_k") {
+    if (bgtq_status s = count(5)) return s;
+    const bgtq_tables *t = nullptr;
+    if (bgtq_status s = tables_of(&t)) return s;
+    const uint64_t rows = std::min<uint64_t>(P[0], x), start = P[1], head = P[2], kvh = P[3];
+    const uint64_t d = (uint64_t)t->info.dim, rb = (uint64_t)t->info.row_bytes, ns = (uint64_t)t->info.norm_stride;
+    if (rows && head >= kvh)
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (encode_k): head %llu of %llu", idx, (unsigned long long)head,
+                  (unsigned long long)kvh);
+    if (bgtq_status s = need(2, rows ? ((rows - 1) * kvh + head + 1) * d * 4 : 0, 4)) return s;
+    if (bgtq_status s = need(3, rows ? (start + rows) * rb : 0, 4)) return s;
+    if (bgtq_status s = need(4, rows ? (start + rows) * ns * 2 : 0, 2)) return s;
+    if (kvh * d > INT32_MAX) return fail(BGTQ_ERR_RANGE, "dispatch %zu (encode_k): row stride above 2^31 - 1", idx);
+    st->op = ModelOp::Encode;
+    st->encode.tables = t;
+    st->encode.src = static_cast<const float *>(D.bindings[2].ptr) + head * d;
+    st->encode.src_row_stride = (int64_t)(kvh * d);
+    st->encode.rows = (int64_t)rows;
+    st->encode.packed = static_cast<uint8_t *>(D.bindings[3].ptr);
+    st->encode.norms = static_cast<uint16_t *>(D.bindings[4].ptr);
+    st->encode.dst_row0 = (int64_t)start;
+    return BGTQ_OK;
+  }
+  const bool compressed = name == "compressed_dot";
+  if (compressed || name == "dot" || name == "softmax" || name == "weighted") {
+    if (bgtq_status s = count(compressed ? 7 : 6)) return s;
+    // compressed_dot [rows,start,head,tokens,qHeads,gqa,headDim];
+    // the others [rows,tokens,capacity,start,qHeads,kvHeads,gqa,headDim].
+    const uint64_t rows = P[0];
+    const uint64_t start = compressed ? P[1] : P[3], tokens = compressed ? P[3] : P[1];
+    const uint64_t qh = P[4], gqa = compressed ? P[5] : P[6], d = compressed ? P[6] : P[7];
+    const uint64_t capacity = compressed ? 0 : P[2], kvh = compressed ? 0 : P[5];
+    if (d != 64 && d != 128)
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): head_dim %llu (64 or 128)", idx, D.name, (unsigned long long)d);
+    if (gqa < 1 || gqa > 16)
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): gqa %llu (1 to 16)", idx, D.name, (unsigned long long)gqa);
+    if (!compressed && qh != kvh * gqa)
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): q_heads must be kv_heads * gqa", idx, D.name);
+    if (rows > 65535 || kvh > 65535 || tokens > INT32_MAX || start + rows > INT32_MAX)
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (%s): sizes beyond the launch limits", idx, D.name);
+    // Tokens a query row can read: up to its causal end start + row.
+    const uint64_t span = std::min<uint64_t>(tokens, start + rows);
+    if (name == "dot" || compressed) {
+      const uint64_t n_tok = std::min<uint64_t>(tokens, x);
+      const uint64_t read = std::min<uint64_t>(n_tok, start + rows);
+      ModelScoresParams &sp = st->scores;
+      st->op = ModelOp::Scores;
+      sp.rows = (int32_t)rows;
+      sp.start = (int32_t)start;
+      sp.q_heads = (int32_t)qh;
+      sp.gqa = (int32_t)gqa;
+      sp.dim = (int32_t)d;
+      sp.tokens = (int32_t)tokens;
+      sp.n_tok = (int32_t)n_tok;
+      sp.y_limit = (int32_t)std::min<uint64_t>(y, INT32_MAX);
+      sp.scale = (float)(1.0 / std::sqrt((double)d));
+      const int sb = compressed ? 6 : 3, qb = 2 - (compressed ? 0 : 2);
+      uint64_t q_heads_used = qh;
+      if (compressed) {
+        const bgtq_tables *t = nullptr;
+        if (bgtq_status s = tables_of(&t)) return s;
+        const uint64_t head = P[2];
+        if ((head + 1) * gqa > qh)
+          return fail(BGTQ_ERR_RANGE, "dispatch %zu (compressed_dot): query heads beyond q_heads", idx);
+        if ((uint64_t)t->info.dim != d)
+          return fail(BGTQ_ERR_RANGE, "dispatch %zu (compressed_dot): tables of dim %d for head_dim %llu", idx,
+                      t->info.dim, (unsigned long long)d);
+        q_heads_used = (head + 1) * gqa;
+        if (bgtq_status s = need(3, read * (uint64_t)t->info.row_bytes, 1)) return s;
+        if (bgtq_status s = need(4, read * (uint64_t)t->info.norm_stride * 2, 2)) return s;
+        sp.tables = t->dev();
+        sp.packed = static_cast<const uint8_t *>(D.bindings[3].ptr);
+        sp.norms = static_cast<const uint16_t *>(D.bindings[4].ptr);
+        sp.head0 = (int32_t)head;
+        st->kv_count = 1;
+        st->lds = model_scores_lds_bytes((int)d, t->info.n_books * t->info.max_centroids);
+        if (st->lds > 64 * 1024)
+          return fail(BGTQ_ERR_UNSUPPORTED, "dispatch %zu (compressed_dot): centroid books too large", idx);
+      } else {
+        if (read > capacity)
+          return fail(BGTQ_ERR_RANGE, "dispatch %zu (dot): tokens beyond capacity %llu", idx,
+                      (unsigned long long)capacity);
+        if (bgtq_status s = need(1, (n_tok && rows) ? kvh * capacity * d * 2 : 0, 2)) return s;
+        sp.k = static_cast<const uint16_t *>(D.bindings[1].ptr);
+        sp.capacity = (int32_t)capacity;
+        sp.head0 = 0;
+        st->kv_count = (int)kvh;
+        st->lds = model_scores_lds_bytes((int)d, 0);
+      }
+      if (rows && n_tok) {
+        if (bgtq_status s = need(qb, ((rows - 1) * qh + q_heads_used) * d * 4, 4)) return s;
+        if (bgtq_status s = need(sb, (((rows - 1) * qh + q_heads_used - 1) * tokens + n_tok) * 4, 4)) return s;
+      }
+      sp.q = static_cast<const float *>(D.bindings[qb].ptr);
+      sp.scores = static_cast<float *>(D.bindings[sb].ptr);
+      return BGTQ_OK;
+    }
+    ModelAttnParams &ap = st->attn;
+    ap.tokens = (int32_t)tokens;
+    ap.start = (int32_t)start;
+    ap.q_heads = (int32_t)qh;
+    ap.gqa = (int32_t)gqa;
+    ap.dim = (int32_t)d;
+    ap.capacity = (int32_t)capacity;
+    ap.scores = static_cast<const float *>(D.bindings[3].ptr);
+    ap.probs = static_cast<float *>(D.bindings[4].ptr);
+    ap.v = static_cast<const uint16_t *>(D.bindings[2].ptr);
+    ap.out = static_cast<float *>(D.bindings[5].ptr);
+    if (name == "softmax") {
+      st->op = ModelOp::Softmax;
+      st->score_rows = (int64_t)std::min<uint64_t>(x, rows * qh);
+      if (bgtq_status s = need(3, (uint64_t)st->score_rows * tokens * 4, 4)) return s;
+      if (bgtq_status s = need(4, (uint64_t)st->score_rows * tokens * 4, 4)) return s;
+      return BGTQ_OK;
+    }
+    st->op = ModelOp::Weighted;
+    const uint64_t outs = std::min<uint64_t>(x, rows * qh * d);
+    ap.x_limit = (int64_t)outs;
+    st->score_rows = (int64_t)((outs + d - 1) / d);
+    if (outs && span > capacity)
+      return fail(BGTQ_ERR_RANGE, "dispatch %zu (weighted): tokens beyond capacity %llu", idx,
+                  (unsigned long long)capacity);
+    if (bgtq_status s = need(4, (uint64_t)st->score_rows * tokens * 4, 4)) return s;
+    if (bgtq_status s = need(2, outs ? kvh * capacity * d * 2 : 0, 2)) return s;
+    if (bgtq_status s = need(5, outs * 4, 4)) return s;
+    return BGTQ_OK;
+  }
+  static const char *const kOther[] = {"embedding", "matmul", "norm", "element", "rope"};
+  for (const char *o : kOther)
+    if (name == o)
+      return fail(BGTQ_ERR_UNSUPPORTED, "model kernel %s is outside the attention path this library serves", D.name);
+  return fail(BGTQ_ERR_RANGE, "dispatch %zu: unknown model kernel %s", idx, D.name);
+}
+
+}  // namespace
+
+extern "C" {
+
+bgtq_status bgtq_model_submit(bgtq_context *ctx, const bgtq_model_dispatch *dispatches, size_t n) {
+  if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
+  if (n && !dispatches) return fail(BGTQ_ERR_RANGE, "null dispatches");
+  std::vector<ModelStep> steps(n);
+  for (size_t i = 0; i < n; ++i)
+    if (bgtq_status s = plan_model_dispatch(dispatches[i], i, &steps[i])) return s;
+  if (bgtq_status s = ctx->use()) return s;
+  std::vector<bgtq_encode_job> jobs;
+  auto flush = [&]() -> bgtq_status {
+    if (jobs.empty()) return BGTQ_OK;
+    const bgtq_status s = bgtq_encode_batched(ctx, BGTQ_DTYPE_F32, jobs.data(), jobs.size());
+    jobs.clear();
+    return s;
+  };
+  for (const ModelStep &st : steps) {
+    if (st.op == ModelOp::Encode) {
+      jobs.push_back(st.encode);
+      continue;
+    }
+    if (bgtq_status s = flush()) return s;
+    switch (st.op) {
+      case ModelOp::Append: HIP_TRY(launch_model_append(st.append, ctx->stream), "model append"); break;
+      case ModelOp::Scores:
+        HIP_TRY(launch_model_scores(st.scores, st.kv_count, st.lds, ctx->stream), "model scores");
+        break;
+      case ModelOp::Softmax: HIP_TRY(launch_model_softmax(st.attn, st.score_rows, ctx->stream), "model softmax"); break;
+      case ModelOp::Weighted:
+        HIP_TRY(launch_model_weighted(st.attn, st.score_rows, ctx->stream), "model weighted");
+        break;
+      default: break;
+    }
+  }
+  return flush();
 }
 
 }  // extern "C"

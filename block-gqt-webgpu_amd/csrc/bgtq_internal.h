@@ -148,6 +148,38 @@ struct PrefillParams {
 __host__ __device__ constexpr int prefill_column_blocks(int dim) { return dim == 64 ? 4 : 2; }
 constexpr int kPrefillMaxSplits = 64;
 
+// The model step's separate attention passes (model_ops.hip), in the
+// reference's buffer layouts: q [rows][q_heads][dim] FP32, K/V caches
+// [kv_heads][capacity][dim] FP16, scores/probabilities [rows*q_heads][tokens].
+struct ModelAppendParams {
+  const float *input;  // [rows][heads][64]
+  uint32_t *cache;     // FP16 pairs, [heads][capacity][32]
+  int64_t pairs;       // pairs converted (rows*heads*32 or fewer)
+  int32_t start, capacity, heads;
+};
+struct ModelScoresParams {
+  const DevTables *tables;  // packed K (one KV head per dispatch), else null
+  const float *q;
+  const uint8_t *packed;    // [tokens][row_bytes] of the dispatch's head
+  const uint16_t *norms;    // [tokens][norm_stride]
+  const uint16_t *k;        // FP16 K cache
+  float *scores;
+  int32_t rows, start, q_heads, gqa, dim, capacity;
+  int32_t tokens;  // score row length
+  int32_t n_tok;   // tokens scored: min(tokens, the dispatch's x)
+  int32_t head0;   // first KV head of the launch (grid z adds to it)
+  int32_t y_limit; // the dispatch's y: workgroup rows of 128 query items
+  float scale;     // 1/sqrt(dim)
+};
+struct ModelAttnParams {
+  const float *scores;
+  float *probs;
+  const uint16_t *v;
+  float *out;
+  int32_t tokens, start, q_heads, gqa, dim, capacity;
+  int64_t x_limit;  // outputs written (weighted): min(x, rows*q_heads*dim)
+};
+
 // Structure of a layout the fused matrix-core decode handles: every 32-dim
 // K-step of the head-perm order lies in one group and one centroid book and is
 // either all nibble codes or all byte codes (nibble steps first); at most two
@@ -202,6 +234,11 @@ hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int n
 hipError_t launch_prefill(const PrefillParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
 hipError_t launch_reconstruct(const DevTables *t, const uint8_t *packed, const uint16_t *norms,
                               int64_t rows, float *out, hipStream_t stream);
+int model_scores_lds_bytes(int dim, int book_floats);
+hipError_t launch_model_append(const ModelAppendParams &p, hipStream_t stream);
+hipError_t launch_model_scores(const ModelScoresParams &p, int kv_count, int lds_bytes, hipStream_t stream);
+hipError_t launch_model_softmax(const ModelAttnParams &p, int64_t score_rows, hipStream_t stream);
+hipError_t launch_model_weighted(const ModelAttnParams &p, int64_t score_rows, hipStream_t stream);
 hipError_t launch_half_convert(const float *src, uint16_t *dst, int64_t n, hipStream_t stream);
 
 }  // namespace bgtq

@@ -23,6 +23,23 @@ export class DeviceView<T extends ArrayBufferView = ArrayBufferView> {
   read(): T;
 }
 export function readBuffer<T extends ArrayBufferView>(device: Device, view: DeviceView<T>): Promise<T>;
+/** src/webgpu/buffers.ts:3-25 over device memory of libbgtq (zero-filled, size rounded up to 4). */
+export class StorageBuffer { readonly device: Device; readonly size: number; readonly label: string; destroy(): void; }
+export function storage(device: Device, bytes: number, label: string): StorageBuffer;
+export function upload(device: Device, buffer: StorageBuffer, values: ArrayBufferView, offset?: number): void;
+export function readBuffer(device: Device, buffer: StorageBuffer, bytes?: number): Promise<ArrayBuffer>;
+/** src/model/ops.ts: the attention-path names append, encode_k, dot, compressed_dot, softmax, weighted. */
+export class ModelOps {
+  static create(device: Device): Promise<ModelOps>;
+  readonly device: Device;
+  commands(): Commands;
+}
+export class Commands {
+  uniformBytes: number;
+  dispatch(name: string, parameters: number[], buffers: (StorageBuffer | TablesBinding | null)[], x: number,
+           y?: number): void;
+  submit(): Promise<void>;
+}
 
 export function validateLayout(p: BlockGTQParameters): void;
 export function tables(p: BlockGTQParameters): { integer: Uint32Array; floating: Float32Array };
@@ -99,8 +116,13 @@ export class AttentionEngine {
 }
 
 /** src/model/calibration.ts: base is a directory with calibration.json and its payload. */
+/** A head's config/table: its device tables as a model dispatch binding (host copy in `host`). */
+export class TablesBinding<T extends ArrayBufferView = ArrayBufferView> {
+  readonly tables: unknown; readonly host: T; readonly size: number;
+}
 export type CalibrationHead = {
-  tables: unknown; config: Uint32Array; table: Float32Array; ranges: Uint32Array; rowBytes: number; normStride: number;
+  tables: unknown; config: TablesBinding<Uint32Array>; table: TablesBinding<Float32Array>;
+  ranges: TablesBinding<Uint32Array>; rowBytes: number; normStride: number;
 };
 export class Calibration {
   static load(device: Device, adapter?: { layers: number; kvHeads: number }, base?: string,

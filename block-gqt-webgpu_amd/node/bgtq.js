@@ -34,7 +34,79 @@ async function requestDevice(index) { return new Device(index); }
 class DeviceView {
   constructor(read) { this.read = read; }
 }
-async function readBuffer(device, view) { return view.read(); }
+
+// ---- device buffers (src/webgpu/buffers.ts:3-25) ---------------------------
+// A StorageBuffer stands for the reference's GPUBuffer of STORAGE usage:
+// zero-filled device memory of `size` bytes.
+class StorageBuffer {
+  constructor(device, size, label) {
+    this.device = device; this.size = size; this.label = label;
+    this.handle = native.bufferCreate(device.handle, size);
+  }
+  destroy() {
+    if (this.handle) native.bufferDestroy(this.handle);
+    this.handle = null;
+  }
+}
+const MAX_BUFFER_SIZE = 2 ** 40;
+function storage(device, bytes, label) {
+  const size = Math.ceil(bytes / 4) * 4;
+  if (!Number.isSafeInteger(size) || size < 4 || size > MAX_BUFFER_SIZE) {
+    throw new RangeError(`${label}: unsupported buffer size ${size}`);
+  }
+  return new StorageBuffer(device, size, label);
+}
+function upload(device, buffer, values, offset) {
+  offset = offset === undefined ? 0 : offset;
+  const data = new Uint8Array(Math.ceil(values.byteLength / 4) * 4);
+  data.set(new Uint8Array(values.buffer, values.byteOffset, values.byteLength));
+  if (offset % 4 || offset + data.byteLength > buffer.size) throw new RangeError('Unaligned/out-of-range buffer upload');
+  native.bufferWrite(buffer.handle, offset, data);
+}
+async function readBuffer(device, buffer, bytes) {
+  if (buffer instanceof DeviceView) return buffer.read();
+  bytes = bytes === undefined ? buffer.size : bytes;
+  if (bytes % 4 || bytes > buffer.size) throw new RangeError('Invalid readback length');
+  return native.bufferRead(buffer.handle, 0, bytes);
+}
+
+// ---- the model step's kernel protocol (src/model/ops.ts) -------------------
+// ModelOps.create(device).commands(): dispatch(name, parameters, buffers, x, y)
+// records, submit() queues every dispatch in order in libbgtq.so and waits.
+// The attention-path names are served (append, encode_k, dot,
+// compressed_dot, softmax, weighted); the model's other kernels are refused.
+// A buffer is a StorageBuffer, or a calibration head's config/table (its
+// device tables) or ranges (unused by the library's kernels).
+class TablesBinding {
+  constructor(tables, host) { this.tables = tables; this.host = host; this.size = host.byteLength; }
+}
+class ModelOps {
+  constructor(device) { this.device = device; }
+  static async create(device) { return new ModelOps(device); }
+  commands() { return new Commands(this); }
+}
+class Commands {
+  constructor(ops) { this.ops = ops; this.list = []; this.uniformBytes = 0; }
+  dispatch(name, parameters, buffers, x, y) {
+    y = y === undefined ? 1 : y;
+    const limit = this.ops.device.limits.maxComputeWorkgroupsPerDimension;
+    if (x > limit || y > limit) throw new RangeError('Model dispatch limit');
+    const params = Array.from({ length: 8 }, (_, i) => (parameters[i] === undefined ? 0 : parameters[i]) >>> 0);
+    const bindings = buffers.map((b) => {
+      if (b instanceof StorageBuffer) return [b.handle, null];
+      if (b instanceof TablesBinding) return [null, b.tables];
+      return null;
+    });
+    this.uniformBytes += 32;
+    this.list.push([name, params, bindings, x, y]);
+  }
+  async submit() {
+    const list = this.list;
+    this.list = [];
+    native.modelSubmit(this.ops.device.handle, list);
+    await this.ops.device.queue.onSubmittedWorkDone();
+  }
+}
 
 // ---- calibration tables (src/webgpu/layout.ts:8-31) ------------------------
 function isInt(x) { return Number.isInteger(x); }
@@ -254,7 +326,12 @@ class Calibration {
           }
         }
         const handle = native.tablesCreate(device.handle, config, table);
-        c.heads.push({ tables: handle, config, table, ranges, rowBytes: config[2], normStride: config[3] });
+        // config/table bind the head's device tables in the model dispatches
+        // (src/model/decoder.ts:52, :55), as the reference's GPU buffers do.
+        c.heads.push({
+          tables: handle, config: new TablesBinding(handle, config), table: new TablesBinding(handle, table),
+          ranges: new TablesBinding(null, ranges), rowBytes: config[2], normStride: config[3],
+        });
         c.allocations.push({ name: `head ${i} tables`, role: 'tables', bytes: native.tablesDeviceBytes(handle) });
       }
     } catch (e) {
@@ -270,6 +347,7 @@ class Calibration {
 }
 
 module.exports = {
-  native, Device, requestDevice, DeviceView, readBuffer, validateLayout, tables, appendCount,
+  native, Device, requestDevice, DeviceView, readBuffer, storage, upload, StorageBuffer, ModelOps, Commands,
+  validateLayout, tables, appendCount,
   FP16Keys, PackedKeys, CompressedKeys, Values, OptimizedAttention, AttentionEngine, AttentionSession, Calibration,
 };

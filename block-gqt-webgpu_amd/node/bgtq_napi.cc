@@ -377,6 +377,108 @@ napi_value AttentionDestroy(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---- device buffers (src/webgpu/buffers.ts storage/upload/readBuffer) ----
+napi_value BufferCreate(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  bgtq_buffer *b = nullptr;
+  BGTQ_TRY(env, bgtq_buffer_create(static_cast<bgtq_context *>(handle(env, a.v[0])), (size_t)to_i64(env, a.v[1]), &b));
+  return wrap(env, b);
+}
+napi_value BufferWrite(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  uint8_t *data;
+  size_t n;
+  if (!typed(env, a.v[2], napi_uint8_array, &data, &n)) return nullptr;
+  BGTQ_TRY(env, bgtq_buffer_write(static_cast<bgtq_buffer *>(handle(env, a.v[0])), (size_t)to_i64(env, a.v[1]), data, n));
+  return undefined(env);
+}
+napi_value BufferRead(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  const size_t n = (size_t)to_i64(env, a.v[2]);
+  napi_value ab;
+  void *raw = nullptr;
+  NAPI_TRY(env, napi_create_arraybuffer(env, n, &raw, &ab));
+  BGTQ_TRY(env, bgtq_buffer_read(static_cast<bgtq_buffer *>(handle(env, a.v[0])), (size_t)to_i64(env, a.v[1]), raw, n));
+  return ab;
+}
+napi_value BufferDestroy(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  bgtq_buffer_destroy(static_cast<bgtq_buffer *>(handle(env, a.v[0])));
+  return undefined(env);
+}
+
+// ---- the model step's kernel protocol (src/model/ops.ts:24-31) -------------
+// modelSubmit(ctx, [[name, params(8), bindings, x, y], ...]); a binding is
+// [buffer handle, null] (device memory), [null, tables handle] or null.
+napi_value ModelSubmit(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  uint32_t n = 0;
+  NAPI_TRY(env, napi_get_array_length(env, a.v[1], &n));
+  std::vector<std::string> names(n);
+  std::vector<std::vector<bgtq_binding>> binds(n);
+  std::vector<bgtq_model_dispatch> ds(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value item, v;
+    NAPI_TRY(env, napi_get_element(env, a.v[1], i, &item));
+    NAPI_TRY(env, napi_get_element(env, item, 0, &v));
+    size_t len = 0;
+    NAPI_TRY(env, napi_get_value_string_utf8(env, v, nullptr, 0, &len));
+    names[i].resize(len + 1);
+    NAPI_TRY(env, napi_get_value_string_utf8(env, v, &names[i][0], len + 1, &len));
+    names[i].resize(len);
+    bgtq_model_dispatch &d = ds[i];
+    d = bgtq_model_dispatch{};
+    NAPI_TRY(env, napi_get_element(env, item, 1, &v));
+    for (uint32_t k = 0; k < 8; ++k) {
+      napi_value e;
+      NAPI_TRY(env, napi_get_element(env, v, k, &e));
+      d.params[k] = (uint32_t)to_i64(env, e);
+    }
+    NAPI_TRY(env, napi_get_element(env, item, 2, &v));
+    uint32_t nb = 0;
+    NAPI_TRY(env, napi_get_array_length(env, v, &nb));
+    binds[i].resize(nb);
+    for (uint32_t k = 0; k < nb; ++k) {
+      napi_value e;
+      napi_valuetype t;
+      NAPI_TRY(env, napi_get_element(env, v, k, &e));
+      NAPI_TRY(env, napi_typeof(env, e, &t));
+      bgtq_binding b{};
+      if (t == napi_object) {
+        napi_value buf, tab;
+        napi_valuetype bt, tt;
+        NAPI_TRY(env, napi_get_element(env, e, 0, &buf));
+        NAPI_TRY(env, napi_get_element(env, e, 1, &tab));
+        NAPI_TRY(env, napi_typeof(env, buf, &bt));
+        NAPI_TRY(env, napi_typeof(env, tab, &tt));
+        if (bt == napi_external) {
+          const bgtq_buffer *bb = static_cast<const bgtq_buffer *>(handle(env, buf));
+          b.ptr = bgtq_buffer_device_ptr(bb);
+          b.bytes = bgtq_buffer_size(bb);
+        }
+        if (tt == napi_external) b.tables = static_cast<const bgtq_tables *>(handle(env, tab));
+      }
+      binds[i][k] = b;
+    }
+    NAPI_TRY(env, napi_get_element(env, item, 3, &v));
+    d.x = (uint32_t)to_i64(env, v);
+    NAPI_TRY(env, napi_get_element(env, item, 4, &v));
+    d.y = (uint32_t)to_i64(env, v);
+  }
+  for (uint32_t i = 0; i < n; ++i) {
+    ds[i].name = names[i].c_str();
+    ds[i].bindings = binds[i].data();
+    ds[i].n_bindings = binds[i].size();
+  }
+  BGTQ_TRY(env, bgtq_model_submit(static_cast<bgtq_context *>(handle(env, a.v[0])), ds.data(), ds.size()));
+  return undefined(env);
+}
+
 napi_value Init(napi_env env, napi_value exports) {
   struct Fn {
     const char *name;
@@ -396,7 +498,9 @@ napi_value Init(napi_env env, napi_value exports) {
       {"attentionCreate", AttentionCreate},   {"attentionSetQueries", AttentionSetQueries},
       {"attentionRecord", AttentionRecord},   {"attentionRead", AttentionRead},
       {"attentionQueries", AttentionQueries}, {"attentionAllocations", AttentionAllocations},
-      {"attentionDestroy", AttentionDestroy},
+      {"attentionDestroy", AttentionDestroy}, {"bufferCreate", BufferCreate},
+      {"bufferWrite", BufferWrite},           {"bufferRead", BufferRead},
+      {"bufferDestroy", BufferDestroy},       {"modelSubmit", ModelSubmit},
   };
   for (const Fn &f : fns) {
     napi_value fn;

@@ -96,6 +96,50 @@ async function main() {
   const cal = await bgtq.Calibration.load(device, undefined, path.join(FIXTURES, 'model'));
   check(cal.heads.length === 90 && cal.allocations.every((x) => x.bytes > 0), 'calibration: 90 heads on the device');
   check(cal.heads[1].rowBytes === 37 && cal.heads[1].normStride === 4, 'calibration: head 1 row geometry');
+  // The model codec flow of tests/webgpu/model-codec-test.ts:9-27 through the
+  // dispatch protocol: append rounds the post-RoPE rows to FP16, encode_k of
+  // every head writes what PackedKeys.append writes for those FP16 rows.
+  const ops = await bgtq.ModelOps.create(device);
+  const rope = readFixture(path.join(FIXTURES, 'model', 'rope.json')).arrays;
+  const data = rope.h3_p4095_y;
+  const x = bgtq.storage(device, data.byteLength, 'post-RoPE input');
+  const halves = bgtq.storage(device, 3 * 3 * 64 * 2, 'FP16 append reference');
+  bgtq.upload(device, x, data);
+  const cmd = ops.commands();
+  cmd.dispatch('append', [3, 0, 3, 3], [x, halves], 3);
+  await cmd.submit();
+  const half = new Uint16Array(await bgtq.readBuffer(device, halves));
+  let exactHeads = 0;
+  for (let h = 0; h < 90; h++) {
+    const c = cal.heads[h], cfg = c.config.host, t = c.table.host, maxc = cfg[5], off = 4096 + 64 * maxc, head = h % 3;
+    const p = {
+      dim: 64, groups: cfg[1], rowBytes: cfg[2], normStride: cfg[3], nibbleDims: cfg[4], maxCentroids: maxc,
+      permutation: cfg.slice(cfg[6], cfg[6] + 64), groupOf: cfg.slice(cfg[7], cfg[7] + 64),
+      positionToCodebook: cfg.slice(cfg[8], cfg[8] + 64), codeLut: Uint8Array.from(cfg.slice(cfg[9])),
+      rotation: t.slice(0, 4096), centroids: t.slice(4096, off), offsets: t.slice(off, off + 64),
+      inverseScales: t.slice(off + 64, off + 128),
+    };
+    const reference = await bgtq.PackedKeys.create(device, p, 3);
+    const packed = bgtq.storage(device, 3 * cfg[2], 'model codes'), norms = bgtq.storage(device, 3 * cfg[3] * 2, 'model norms');
+    await reference.append(half.subarray(head * 3 * 64, (head + 1) * 3 * 64));
+    const e = ops.commands();
+    e.dispatch('encode_k', [3, 0, head, 3], [c.config, c.table, x, packed, norms], 3);
+    await e.submit();
+    const got = new Uint8Array(await bgtq.readBuffer(device, packed));
+    const gotN = new Uint16Array(await bgtq.readBuffer(device, norms));
+    const ref = await bgtq.readBuffer(device, reference.packed), refN = await bgtq.readBuffer(device, reference.norms);
+    // storage() rounds sizes up to 4 bytes: the padding stays zero
+    const same = (a, b) => b.every((v, i) => v === a[i]) && a.every((v, i) => i < b.length || v === 0);
+    if (same(got, ref) && same(gotN, refN)) exactHeads += 1;
+    reference.destroy(); packed.destroy(); norms.destroy();
+  }
+  check(exactHeads === 90, `model codec: encode_k equals PackedKeys on ${exactHeads} of 90 heads`);
+  let limited = false;
+  try { cmd.dispatch('softmax', [], [], 2 ** 31); } catch (err) { limited = err instanceof RangeError && err.message === 'Model dispatch limit'; }
+  check(limited, 'model dispatch limit');
+  await rejects(() => { const r = ops.commands(); r.dispatch('rope', [3, 64, 0, 0, 0, 3, 100000], [x, x, x, x], 1); return r.submit(); },
+    Error, 'model kernel rope is outside the attention path this library serves', 'model: non-attention kernels refused');
+  x.destroy(); halves.destroy();
   cal.destroy();
   await rejects(() => bgtq.Calibration.load(device, { layers: 2, kvHeads: 3 }, path.join(FIXTURES, 'model')), Error,
     'Calibration mismatch', 'calibration: wrong model geometry');

@@ -50,7 +50,7 @@ typedef struct {
 
 /* Thread-local message of the last failing call on this thread. */
 const char *bgtq_last_error(void);
-/* 2: bgtq_tables_info gained device_bytes. */
+/* 2: bgtq_tables_info gained device_bytes. 3: bgtq_model_submit, bgtq_buffer_*. */
 int32_t bgtq_abi_version(void);
 
 /* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
@@ -268,6 +268,68 @@ typedef struct {
 } bgtq_prefill_desc;
 bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *bytes);
 bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d);
+
+/* ---- device buffers: storage / upload / readBuffer (src/webgpu/buffers.ts:3-25)
+ * For callers without their own device allocator (the Node mirror). A buffer
+ * holds `bytes` rounded up to a multiple of 4, zero-filled (WebGPU buffers
+ * start zeroed). Writes are ordered on the context stream and complete
+ * before returning; reads wait for the stream. */
+typedef struct bgtq_buffer bgtq_buffer;
+bgtq_status bgtq_buffer_create(bgtq_context *ctx, size_t bytes, bgtq_buffer **out);
+void *bgtq_buffer_device_ptr(const bgtq_buffer *b);
+size_t bgtq_buffer_size(const bgtq_buffer *b);
+bgtq_status bgtq_buffer_write(bgtq_buffer *b, size_t offset, const void *src, size_t bytes);
+bgtq_status bgtq_buffer_read(const bgtq_buffer *b, size_t offset, void *dst, size_t bytes);
+void bgtq_buffer_destroy(bgtq_buffer *b);
+
+/* ---- the model step's kernel protocol --------------------------------------
+ * Commands.dispatch(name, parameters, buffers, x, y) then submit()
+ * (src/model/ops.ts:24-30) for the attention-path names of ModelOps
+ * (src/model/ops.ts:6-12), as src/model/decoder.ts:46-56 dispatches them.
+ * One bgtq_model_dispatch per dispatch, with the reference's parameters
+ * (unused slots zero) and bindings in its binding order, the uniform slot
+ * left out. A binding is device memory (ptr, bytes); the config and table
+ * slots of encode_k and compressed_dot instead name the head's calibration
+ * tables (tables; both slots may carry the same handle). Layouts are the
+ * reference's: q and post-RoPE K/V rows [rows][heads][head_dim] FP32, caches
+ * [kv_heads][capacity][head_dim] FP16, packed K and scales per head
+ * [token][row_bytes] / [token][norm_stride], scores and probabilities
+ * [rows*q_heads][tokens], attention output [rows*q_heads][head_dim] FP32.
+ *   append         [rows,start,capacity,heads]   bindings input, cache
+ *                  (src/model/append.wgsl:6-10; 64 dims, FP32 -> FP16 RNE)
+ *   encode_k       [rows,start,head,kv_heads]    config, table, kr, codes, norms
+ *                  (src/model/codec.wgsl:11-33; = bgtq_encode_batched of the
+ *                  FP32 rows, which writes every byte of each row where the
+ *                  reference ORs codes into zeroed rows)
+ *   compressed_dot [rows,start,head,tokens,q_heads,gqa,head_dim]
+ *                  config, table, q, codes, norms, ranges (unused), scores
+ *                  (src/model/compressed-dot.wgsl:14-31)
+ *   dot, softmax, weighted [rows,tokens,capacity,start,q_heads,kv_heads,gqa,head_dim]
+ *                  q, k, v, scores, probabilities, attention
+ *                  (src/model/attention.wgsl:13-39)
+ * x and y are the dispatch's workgroup counts: each pass covers the work
+ * items those workgroups cover in the reference, clamped to the parameters'
+ * extents. head_dim is 64 or 128 (the reference's kernels fix 64), gqa at
+ * most 16, q_heads = kv_heads * gqa. Every dispatch is checked, bindings
+ * against the extents its pass reads and writes, before any work is queued;
+ * a failed check returns BGTQ_ERR_RANGE (BGTQ_ERR_UNSUPPORTED for the
+ * model's other kernels: embedding, matmul, norm, element, rope) and queues
+ * nothing. The work is queued on the context stream in order (consecutive
+ * encode_k dispatches share one launch); bgtq_context_synchronize waits for
+ * it, as the reference's submit() awaits the queue. */
+typedef struct {
+  void *ptr;
+  size_t bytes;
+  const bgtq_tables *tables;
+} bgtq_binding;
+typedef struct {
+  const char *name;
+  uint32_t params[8];
+  const bgtq_binding *bindings;
+  size_t n_bindings;
+  uint32_t x, y;
+} bgtq_model_dispatch;
+bgtq_status bgtq_model_submit(bgtq_context *ctx, const bgtq_model_dispatch *dispatches, size_t n);
 
 #ifdef __cplusplus
 }

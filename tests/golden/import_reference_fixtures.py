@@ -12,7 +12,8 @@ import shutil
 import sys
 from pathlib import Path
 
-WANTED = ["allocator.json", "mixed", "attention", "model/calibration.json", "model/calibration.bin"]
+WANTED = ["allocator.json", "mixed", "attention", "model/calibration.json", "model/calibration.bin", "model/rope.json",
+          "model/rope.bin"]
 
 
 def main(src):

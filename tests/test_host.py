@@ -18,7 +18,9 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(bgtq.LIB_PATH))
     missing = [name for name in sorted(declared) if not hasattr(lib, name)]
     assert not missing, missing
-    assert lib.bgtq_abi_version() == 2
+    assert lib.bgtq_abi_version() == 3
+    lib.bgtq_model_submit.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    assert lib.bgtq_model_submit(None, None, 0) == 1  # BGTQ_ERR_RANGE: null context, nothing touched
 
 
 def test_no_device_is_reported_cleanly():
@@ -152,16 +154,18 @@ def test_node_addon_loads_without_a_device():
         pytest.skip("node or the built addon is absent")
     script = ("const b=require(process.argv[1]);"
               "const want=['contextCreate','tablesCreate','packedKeysCreate','keysAppend','keysRead','valuesCreate',"
-              "'valuesAppend','attentionCreate','attentionSetQueries','attentionRecord','attentionRead','tablesDeviceBytes'];"
+              "'valuesAppend','attentionCreate','attentionSetQueries','attentionRecord','attentionRead','tablesDeviceBytes',"
+                  "'bufferCreate','bufferWrite','bufferRead','bufferDestroy','modelSubmit'];"
               "const miss=want.filter(k=>typeof b.native[k]!=='function');"
-              "const cls=['PackedKeys','CompressedKeys','FP16Keys','Values','OptimizedAttention','AttentionEngine','tables','Calibration'];"
+              "const cls=['PackedKeys','CompressedKeys','FP16Keys','Values','OptimizedAttention','AttentionEngine','tables','Calibration',"
+                  "'ModelOps','Commands','storage','upload','readBuffer'];"
               "const missc=cls.filter(k=>!b[k]);"
               "console.log(JSON.stringify({abi:b.native.abiVersion,miss,missc}));")
     r = subprocess.run([node, "-e", script, str(addon.parent / "bgtq.js")], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     import json
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert out == {"abi": 2, "miss": [], "missc": []}, out
+    assert out == {"abi": 3, "miss": [], "missc": []}, out
 
 
 def _tampered_calibration(tmp_path, edit_manifest=None, edit_payload=None):
