@@ -90,6 +90,10 @@ class ModelDispatch(ctypes.Structure):
                 ("n_bindings", ctypes.c_size_t), ("x", ctypes.c_uint32), ("y", ctypes.c_uint32)]
 
 
+class GroupTables(ctypes.Structure):
+    _fields_ = [("centroids", ctypes.c_void_p), ("rotation", ctypes.c_void_p)]
+
+
 _VP, _SZ, _I32, _U32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32
 _PP = ctypes.POINTER(ctypes.c_void_p)
 
@@ -138,6 +142,10 @@ SIGNATURES = {
     "bgtq_prefill_workspace_size": (_I32, [ctypes.POINTER(PrefillDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_prefill": (_I32, [_VP, ctypes.POINTER(PrefillDesc)]),
     "bgtq_model_submit": (_I32, [_VP, ctypes.POINTER(ModelDispatch), _SZ]),
+    "bgtq_allocate_bits": (_I32, [_VP, _SZ, ctypes.c_int64, _I32, _I32, _VP]),
+    "bgtq_layout_groups": (_I32, [_VP, _SZ, _VP, _VP, _VP]),
+    "bgtq_layout_build": (_I32, [_VP, _SZ, ctypes.POINTER(GroupTables), _SZ, _I32, _I32, _VP,
+                                 ctypes.POINTER(ctypes.c_size_t), _VP, ctypes.POINTER(ctypes.c_size_t)]),
 }
 
 _lib = None

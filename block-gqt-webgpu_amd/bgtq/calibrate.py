@@ -202,3 +202,51 @@ def layout_a(dim: int) -> BlockGTQParameters:
     """allocate_bits(0.9**i, 6*pairs, 4, 8): widths 4..8 at a 6.0 average."""
     n = dim // 2
     return make_parameters(allocate_bits(geometric_scores(n), 6 * n, 4, 8))
+
+
+# ---- the library's table pipeline (bgtq_allocate_bits / bgtq_layout_build) ----
+
+def native_allocate_bits(scores, budget: int, min_bits: int = 1, max_bits: int = 8) -> np.ndarray:
+    """allocate_bits in libbgtq (same results as allocate_bits above)."""
+    from ._lib import check, lib, ptr
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    w = np.zeros(len(s), np.int64)
+    check(lib().bgtq_allocate_bits(ptr(s) if len(s) else None, len(s), int(budget), int(min_bits), int(max_bits),
+                                   ptr(w) if len(s) else None))
+    return w
+
+
+def native_layout_groups(widths) -> list[tuple[int, int]]:
+    """(bits, dims) of each group of a width allocation, ascending widths."""
+    import ctypes
+    from ._lib import check, lib, ptr
+    w = np.ascontiguousarray(widths, dtype=np.int64)
+    n = ctypes.c_int32(0)
+    bits = np.zeros(8, np.int32)
+    dims = np.zeros(8, np.int32)
+    check(lib().bgtq_layout_groups(ptr(w), len(w), ctypes.byref(n), ptr(bits), ptr(dims)))
+    return [(int(bits[k]), int(dims[k])) for k in range(n.value)]
+
+
+def native_tables(widths, groups, row_bytes: int = 0, norm_stride: int = 0):
+    """tables(p) blobs (integer u32, floating f32) built by libbgtq from a width
+    allocation and, per group in ascending width, (centroids, rotation or None)."""
+    import ctypes
+    from . import _lib
+    from ._lib import check, lib, ptr
+    w = np.ascontiguousarray(widths, dtype=np.int64)
+    keep = []
+    arr = (_lib.GroupTables * max(1, len(groups)))()
+    for k, (c, r) in enumerate(groups):
+        c = np.ascontiguousarray(c, dtype=np.float32)
+        r = None if r is None else np.ascontiguousarray(r, dtype=np.float32)
+        keep += [c, r]
+        arr[k] = _lib.GroupTables(c.ctypes.data, None if r is None else r.ctypes.data)
+    ni, nf = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    check(lib().bgtq_layout_build(ptr(w), len(w), arr, len(groups), row_bytes, norm_stride, None, ctypes.byref(ni),
+                                  None, ctypes.byref(nf)))
+    integer = np.zeros(ni.value, np.uint32)
+    floating = np.zeros(nf.value, np.float32)
+    check(lib().bgtq_layout_build(ptr(w), len(w), arr, len(groups), row_bytes, norm_stride, ptr(integer),
+                                  ctypes.byref(ni), ptr(floating), ctypes.byref(nf)))
+    return integer, floating

@@ -34,6 +34,16 @@ bgtq_status fail(bgtq_status code, const char *fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+// The thread's last error, for the library's other host sources.
+bgtq_status bgtq::set_error(bgtq_status code, const char *msg) {
+  g_error = msg;
+  return code;
+}
+
+namespace {
+
 bgtq_status hip_fail(hipError_t e, const char *what) {
   return fail(BGTQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }

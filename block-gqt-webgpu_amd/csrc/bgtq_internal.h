@@ -198,6 +198,9 @@ struct FastLayout {
   const float *books[kMaxKvHeads];
 };
 
+// Sets the calling thread's bgtq_last_error() message; returns code.
+int32_t set_error(int32_t code, const char *msg);
+
 // Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).
 hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
                          hipStream_t stream);

@@ -44,6 +44,11 @@ export class Commands {
 export function validateLayout(p: BlockGTQParameters): void;
 export function tables(p: BlockGTQParameters): { integer: Uint32Array; floating: Float32Array };
 export function appendCount(values: Uint16Array, dim: number, length: number, capacity: number): number;
+/** The table pipeline of libbgtq (host only): allocator, grouping, code LUT. */
+export function allocateBits(scores: ArrayLike<number>, budget: number, minBits?: number, maxBits?: number): number[];
+export function layoutGroups(widths: ArrayLike<number>): [bits: number, dims: number][];
+export function buildTables(widths: ArrayLike<number>, groups: { centroids: ArrayLike<number>; rotation?: ArrayLike<number> | null }[],
+                            rowBytes?: number, normStride?: number): { integer: Uint32Array; floating: Float32Array };
 
 export type KeyView = { buffer: DeviceView<Uint16Array | Float32Array>; format: "f16" | "f32" };
 export interface KeyStore {

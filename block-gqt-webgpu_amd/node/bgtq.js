@@ -284,6 +284,21 @@ class AttentionEngine {
   }
 }
 
+// ---- calibration-table pipeline (libbgtq, host only) -----------------------
+// allocateBits: the greedy allocation of src/reference/allocator.py:4-17.
+// layoutGroups: [bits, dims] of each group of a width allocation (ascending
+// widths). buildTables: the tables(p) blobs of an allocation, given each
+// group's ascending centroids and its rotation (null = identity).
+function allocateBits(scores, budget, minBits, maxBits) {
+  return native.allocateBits(Float32Array.from(scores), budget, minBits === undefined ? 1 : minBits,
+    maxBits === undefined ? 8 : maxBits);
+}
+function layoutGroups(widths) { return native.layoutGroups(Array.from(widths)); }
+function buildTables(widths, groups, rowBytes, normStride) {
+  return native.layoutBuild(Array.from(widths), groups.map((g) => [Float32Array.from(g.centroids),
+    g.rotation ? Float32Array.from(g.rotation) : null]), rowBytes || 0, normStride || 0);
+}
+
 // ---- model calibration (src/model/calibration.ts:4-24) ---------------------
 // base is a directory holding calibration.json and its payload. Each head
 // keeps its host arrays and a device table set (tables) for the batched entry
@@ -348,6 +363,6 @@ class Calibration {
 
 module.exports = {
   native, Device, requestDevice, DeviceView, readBuffer, storage, upload, StorageBuffer, ModelOps, Commands,
-  validateLayout, tables, appendCount,
+  validateLayout, tables, appendCount, allocateBits, layoutGroups, buildTables,
   FP16Keys, PackedKeys, CompressedKeys, Values, OptimizedAttention, AttentionEngine, AttentionSession, Calibration,
 };

@@ -377,6 +377,90 @@ napi_value AttentionDestroy(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---- calibration-table pipeline (host only) --------------------------------
+std::vector<int64_t> int_list(napi_env env, napi_value arr, bool *ok) {
+  uint32_t n = 0;
+  std::vector<int64_t> out;
+  *ok = napi_get_array_length(env, arr, &n) == napi_ok;
+  for (uint32_t i = 0; *ok && i < n; ++i) {
+    napi_value e;
+    *ok = napi_get_element(env, arr, i, &e) == napi_ok;
+    if (*ok) out.push_back(to_i64(env, e));
+  }
+  if (!*ok) napi_throw_type_error(env, nullptr, "expected an array of integers");
+  return out;
+}
+napi_value AllocateBits(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  float *s;
+  size_t n;
+  if (!typed(env, a.v[0], napi_float32_array, &s, &n)) return nullptr;
+  std::vector<int64_t> w(n);
+  BGTQ_TRY(env, bgtq_allocate_bits(s, n, to_i64(env, a.v[1]), (int32_t)to_i64(env, a.v[2]), (int32_t)to_i64(env, a.v[3]),
+                                   w.data()));
+  napi_value arr;
+  NAPI_TRY(env, napi_create_array_with_length(env, n, &arr));
+  for (size_t i = 0; i < n; ++i) NAPI_TRY(env, napi_set_element(env, arr, (uint32_t)i, num(env, (double)w[i])));
+  return arr;
+}
+napi_value LayoutGroups(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  bool ok;
+  std::vector<int64_t> w = int_list(env, a.v[0], &ok);
+  if (!ok) return nullptr;
+  int32_t ng = 0, bits[8], dims[8];
+  BGTQ_TRY(env, bgtq_layout_groups(w.data(), w.size(), &ng, bits, dims));
+  napi_value arr;
+  NAPI_TRY(env, napi_create_array_with_length(env, ng, &arr));
+  for (int32_t k = 0; k < ng; ++k) {
+    napi_value pair;
+    NAPI_TRY(env, napi_create_array_with_length(env, 2, &pair));
+    NAPI_TRY(env, napi_set_element(env, pair, 0, num(env, bits[k])));
+    NAPI_TRY(env, napi_set_element(env, pair, 1, num(env, dims[k])));
+    NAPI_TRY(env, napi_set_element(env, arr, (uint32_t)k, pair));
+  }
+  return arr;
+}
+// layoutBuild(widths, [[Float32Array centroids, Float32Array|null rotation], ...], rowBytes, normStride)
+napi_value LayoutBuild(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  bool ok;
+  std::vector<int64_t> w = int_list(env, a.v[0], &ok);
+  if (!ok) return nullptr;
+  uint32_t ng = 0;
+  NAPI_TRY(env, napi_get_array_length(env, a.v[1], &ng));
+  std::vector<bgtq_group_tables> groups(ng);
+  for (uint32_t k = 0; k < ng; ++k) {
+    napi_value g, c, r;
+    napi_valuetype rt;
+    NAPI_TRY(env, napi_get_element(env, a.v[1], k, &g));
+    NAPI_TRY(env, napi_get_element(env, g, 0, &c));
+    NAPI_TRY(env, napi_get_element(env, g, 1, &r));
+    float *cd, *rd = nullptr;
+    size_t cn, rn;
+    if (!typed(env, c, napi_float32_array, &cd, &cn)) return nullptr;
+    NAPI_TRY(env, napi_typeof(env, r, &rt));
+    if (rt == napi_object && !typed(env, r, napi_float32_array, &rd, &rn)) return nullptr;
+    groups[k] = bgtq_group_tables{cd, rd};
+  }
+  const int32_t rb = (int32_t)to_i64(env, a.v[2]), ns = (int32_t)to_i64(env, a.v[3]);
+  size_t ni = 0, nf = 0;
+  BGTQ_TRY(env, bgtq_layout_build(w.data(), w.size(), groups.data(), groups.size(), rb, ns, nullptr, &ni, nullptr, &nf));
+  uint32_t *ints;
+  float *fl;
+  napi_value vi = new_typed(env, napi_uint32_array, ni, &ints), vf = new_typed(env, napi_float32_array, nf, &fl);
+  if (!vi || !vf) return nullptr;
+  BGTQ_TRY(env, bgtq_layout_build(w.data(), w.size(), groups.data(), groups.size(), rb, ns, ints, &ni, fl, &nf));
+  napi_value out;
+  NAPI_TRY(env, napi_create_object(env, &out));
+  NAPI_TRY(env, napi_set_named_property(env, out, "integer", vi));
+  NAPI_TRY(env, napi_set_named_property(env, out, "floating", vf));
+  return out;
+}
+
 // ---- device buffers (src/webgpu/buffers.ts storage/upload/readBuffer) ----
 napi_value BufferCreate(napi_env env, napi_callback_info info) {
   Args a;
@@ -501,6 +585,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"attentionDestroy", AttentionDestroy}, {"bufferCreate", BufferCreate},
       {"bufferWrite", BufferWrite},           {"bufferRead", BufferRead},
       {"bufferDestroy", BufferDestroy},       {"modelSubmit", ModelSubmit},
+      {"allocateBits", AllocateBits},         {"layoutGroups", LayoutGroups},
+      {"layoutBuild", LayoutBuild},
   };
   for (const Fn &f : fns) {
     napi_value fn;

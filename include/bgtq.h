@@ -50,7 +50,8 @@ typedef struct {
 
 /* Thread-local message of the last failing call on this thread. */
 const char *bgtq_last_error(void);
-/* 2: bgtq_tables_info gained device_bytes. 3: bgtq_model_submit, bgtq_buffer_*. */
+/* 2: bgtq_tables_info gained device_bytes. 3: bgtq_model_submit, bgtq_buffer_*, bgtq_allocate_bits,
+ * bgtq_layout_groups, bgtq_layout_build. */
 int32_t bgtq_abi_version(void);
 
 /* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
@@ -268,6 +269,36 @@ typedef struct {
 } bgtq_prefill_desc;
 bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *bytes);
 bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d);
+
+/* ---- calibration-table pipeline (host only, no device needed) ------------
+ * The setup that produces the tables(p) blobs bgtq_tables_create takes:
+ * bgtq_allocate_bits is the greedy per-pair allocation
+ * (src/reference/allocator.py:4-17: one more bit to the first argmax of
+ * s * 4^-w, FP32 scores, FP64 powers, until the budget is spent or every
+ * pair is at max_bits or no priority is positive). bgtq_layout_groups gives
+ * the groups of a width allocation (src/reference/mixed_layout.py:5-18:
+ * pairs stably sorted by width, one group per distinct width, ascending):
+ * their widths and dimensions, so that the caller can supply each group's
+ * codebook and rotation. bgtq_layout_build then forms the full table set:
+ * head_perm, group_of, the per-position code LUTs (one per distinct
+ * codebook), bin offsets and inverse widths
+ * (vendor/blockgtq/quant_kernels.py:276-364), the block-diagonal rotation and
+ * the centroid table, serialised as src/webgpu/layout.ts:24-31. groups[k]
+ * holds group k's 2^bits ascending centroids and its m x m rotation
+ * (row-major, y_j = sum_i x_i R[j*m+i]; NULL = identity, which the reference
+ * uses below 2 bits). row_bytes / norm_stride 0 take the natural values.
+ * Called with integer or floating NULL it only returns the element counts. */
+bgtq_status bgtq_allocate_bits(const float *scores, size_t n_pairs, int64_t budget, int32_t min_bits,
+                               int32_t max_bits, int64_t *widths);
+bgtq_status bgtq_layout_groups(const int64_t *widths, size_t n_pairs, int32_t *n_groups, int32_t *bits /*[8]*/,
+                               int32_t *group_dims /*[8]*/);
+typedef struct {
+  const float *centroids;
+  const float *rotation;
+} bgtq_group_tables;
+bgtq_status bgtq_layout_build(const int64_t *widths, size_t n_pairs, const bgtq_group_tables *groups, size_t n_groups,
+                              int32_t row_bytes, int32_t norm_stride, uint32_t *integer, size_t *n_integer,
+                              float *floating, size_t *n_floating);
 
 /* ---- device buffers: storage / upload / readBuffer (src/webgpu/buffers.ts:3-25)
  * For callers without their own device allocator (the Node mirror). A buffer

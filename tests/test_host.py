@@ -118,6 +118,129 @@ def test_calibration_tables_reproduce_reference(oracle):
         assert g["nopack_start"] == mm["nopack_start"]
 
 
+def _fixture_groups(calibrate, widths, integer, floating):
+    """Each group's (centroids, rotation block) as the committed table holds them."""
+    d, maxc = int(integer[0]), int(integer[5])
+    rot = np.asarray(floating[:d * d]).reshape(d, d)
+    cents = np.asarray(floating[d * d:d * d + d * maxc]).reshape(d, maxc)
+    groups, s = [], 0
+    for bits, dims in calibrate.native_layout_groups(widths):
+        groups.append((cents[s, :1 << bits], rot[s:s + dims, s:s + dims]))
+        s += dims
+    return groups
+
+
+def test_native_table_pipeline_reproduces_reference(oracle):
+    """libbgtq's allocator -> grouping -> code LUT pipeline (bgtq_layout_build), given each
+    group's codebook and rotation from the committed tables, rebuilds the whole table set
+    bit for bit: the 90 SmolLM2 heads and the mixed layouts (head_perm up to 32 pairs, as
+    for the Python generator)."""
+    import json
+    import bgtq
+    from bgtq import calibrate
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    for i in range(len(m["heads"])):
+        w = a[f"h{i}_widths"].astype(np.int64)
+        ints, fl = calibrate.native_tables(w, _fixture_groups(calibrate, w, a[f"h{i}_config"], a[f"h{i}_table"]))
+        np.testing.assert_array_equal(ints, a[f"h{i}_config"], err_msg=f"head {i}")
+        np.testing.assert_array_equal(fl.view(np.uint32), a[f"h{i}_table"].view(np.uint32), err_msg=f"head {i}")
+    for c in json.loads((REF / "mixed" / "index.json").read_text())["cases"]:
+        mm, aa = oracle.read_fixture(REF / "mixed" / f"{c['name']}.json")
+        w = aa["allocation"].astype(np.int64)
+        p = bgtq.BlockGTQParameters.from_mixed_fixture(mm, aa)
+        ints, fl = calibrate.native_tables(w, _fixture_groups(calibrate, w, *bgtq.tables(p)), mm["row_bytes"],
+                                           mm["norm_stride"])
+        q = bgtq.BlockGTQParameters.from_serialized(ints, fl)
+        for key, mine, ref in (("group_of", q.groupOf, aa["group_of"]), ("pos_to_cb", q.positionToCodebook, aa["pos_to_cb"]),
+                               ("code_lut", q.codeLut, aa["code_lut"]), ("rotation", q.rotation, aa["rotation"]),
+                               ("centroids", q.centroids, aa["centroids"]), ("offsets", q.offsets, aa["lut_offsets"]),
+                               ("inv", q.inverseScales, aa["lut_inv_scales"])):
+            np.testing.assert_array_equal(np.asarray(mine).reshape(-1), np.asarray(ref).reshape(-1),
+                                          err_msg=f"{c['name']} {key}")
+        assert (q.rowBytes, q.normStride, q.nibbleDims) == (mm["row_bytes"], mm["norm_stride"], mm["nopack_start"])
+        if mm["dim"] <= 64:
+            np.testing.assert_array_equal(q.permutation, aa["head_perm"], err_msg=c["name"])
+
+
+def test_native_table_pipeline_matches_python_generator(oracle):
+    """Same tables as calibrate.make_parameters for layouts A and B and random allocations,
+    with the generator's own codebooks and rotations as the groups' inputs; the allocator
+    equals the oracle's."""
+    import bgtq
+    from bgtq import calibrate
+    rng = np.random.default_rng(5)
+    cases = []
+    for d in (64, 128):
+        cases.append(4 * calibrate.allocate_bits(calibrate.geometric_scores(d // 2), (3 * d // 2) // 2, 1, 2))
+    for _ in range(6):
+        n = int(rng.choice([8, 16, 32, 64]))
+        cases.append(rng.integers(1, 9, n).astype(np.int64))
+    for w in cases:
+        p = calibrate.make_parameters(w)
+        ints, fl = calibrate.native_tables(w, _fixture_groups(calibrate, w, *bgtq.tables(p)))
+        ri, rf = bgtq.tables(p)
+        np.testing.assert_array_equal(ints, ri)
+        np.testing.assert_array_equal(fl.view(np.uint32), rf.view(np.uint32))
+    for _ in range(200):
+        n = int(rng.integers(1, 40))
+        s = rng.exponential(size=n).astype(np.float32) * (rng.random(n) > 0.2)
+        budget, lo = int(rng.integers(0, 8 * n + 4)), int(rng.integers(0, 3))
+        hi = int(rng.integers(lo, 9))
+        np.testing.assert_array_equal(calibrate.native_allocate_bits(s, budget, lo, hi),
+                                      oracle.allocate_bits(s, budget, lo, hi))
+    with pytest.raises(bgtq.RangeError, match="groups in this allocation"):
+        calibrate.native_tables(np.array([4, 8]), [(np.arange(16, dtype=np.float32), None)])
+    with pytest.raises(bgtq.RangeError, match="ascend"):
+        calibrate.native_tables(np.array([1, 1]), [(np.array([1.0, -1.0], np.float32), None)])
+    with pytest.raises(bgtq.RangeError, match="outside 1..8"):
+        calibrate.native_layout_groups(np.array([0, 3]))
+
+
+def test_node_table_pipeline(oracle):
+    """buildTables / layoutGroups / allocateBits of the Node module (no device needed) rebuild the
+    committed calibration tables of every head from their widths and group tables."""
+    import json
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    addon = ROOT / "block-gqt-webgpu_amd" / "node" / "bgtq_napi.node"
+    if node is None or not addon.exists():
+        pytest.skip("node or the built addon is absent")
+    script = r"""
+const b = require(process.argv[1]); const fs = require('fs'); const path = require('path');
+const dir = process.argv[2]; const m = JSON.parse(fs.readFileSync(path.join(dir, 'calibration.json')));
+const bin = fs.readFileSync(path.join(dir, m.binary));
+const arr = (name, T) => { const d = m.arrays[name]; const c = new Uint8Array(d.nbytes);
+  c.set(bin.subarray(d.offset, d.offset + d.nbytes)); return new T(c.buffer); };
+let exact = 0;
+for (let h = 0; h < m.heads.length; h++) {
+  const cfg = arr(`h${h}_config`, Uint32Array), tab = arr(`h${h}_table`, Float32Array);
+  const w = Array.from(arr(`h${h}_widths`, Uint32Array));
+  const d = cfg[0], maxc = cfg[5];
+  let s = 0; const groups = [];
+  for (const [bits, dims] of b.layoutGroups(w)) {
+    const rot = new Float32Array(dims * dims);
+    for (let i = 0; i < dims; i++) for (let j = 0; j < dims; j++) rot[i * dims + j] = tab[(s + i) * d + s + j];
+    groups.push({ centroids: tab.subarray(d * d + s * maxc, d * d + s * maxc + (1 << bits)), rotation: rot });
+    s += dims;
+  }
+  const t = b.buildTables(w, groups);
+  const same = (x, y) => x.length === y.length && x.every((v, i) => Object.is(v, y[i]) || v === y[i]);
+  if (same(t.integer, cfg) && same(new Uint32Array(t.floating.buffer), new Uint32Array(tab.buffer))) exact++;
+}
+const w = b.allocateBits(Array.from({ length: 32 }, (_, i) => 0.9 ** i), 48, 1, 2);
+let msg = ''; try { b.layoutGroups([0, 4]); } catch (e) { msg = e.constructor.name + ': ' + e.message; }
+console.log(JSON.stringify({ exact, heads: m.heads.length, ones: w.filter((x) => x === 1).length, msg }));
+"""
+    r = subprocess.run([node, "-e", script, str(addon.parent / "bgtq.js"), str(REF / "model")], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["exact"] == out["heads"] == 90, out
+    assert out["ones"] == 16, out  # layout B: half the pairs at one bit (x4 = 4 bits), half at two
+    assert out["msg"] == "RangeError: pair 0: width 0 outside 1..8", out
+
+
 def test_layout_b_and_a_shapes():
     from bgtq import calibrate
     for d, rb, groups in ((64, 48, 2), (128, 96, 2)):
