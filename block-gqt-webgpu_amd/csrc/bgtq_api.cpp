@@ -763,12 +763,13 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
   return BGTQ_OK;
 }
 
-// Token splits per (sequence, KV head): at least 256 tokens each, at most 256
-// splits (the fused kernel merges them through LDS). By default enough splits
-// for two resident workgroups per compute unit: more, shorter-lived
-// workgroups only add per-workgroup set-up and merge round trips.
+// Token splits per (sequence, KV head): at least 128 tokens each (one 32-token
+// chunk per wave of the fused kernel), at most 256 splits (the fused kernel
+// merges them through LDS). By default enough splits for two resident
+// workgroups per compute unit: more, shorter-lived workgroups only add
+// per-workgroup set-up and merge round trips.
 static int choose_splits(int64_t units, uint32_t max_length, int32_t requested) {
-  const int64_t max_splits = std::min<int64_t>(256, std::max<int64_t>(1, (max_length + 255) / 256));
+  const int64_t max_splits = std::min<int64_t>(256, std::max<int64_t>(1, (max_length + 127) / 128));
   if (requested > 0) return (int)std::min<int64_t>(requested, max_splits);
   const int64_t target = 2 * (int64_t)device_cus();
   const int64_t want = std::max<int64_t>(1, (target + units - 1) / units);
@@ -842,6 +843,7 @@ static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables,
     if (T->row_bytes % 8 || T->norm_stride != 2 || T->groups > 2 || T->nibble_dims % 32) return false;
     const int n = T->nibble_dims / 32;
     if (T->row_bytes != decode_fast_row_bytes(p.dim, n)) return false;
+    if (p.k_new && (int64_t)T->off_rot > decode_fast_enc_capacity(p.dim, n)) return false;
     int g0 = 0;
     for (int s = 0; s < ks; ++s) {
       const int g = T->group_of[32 * s], bk = T->pos_book[32 * s];
@@ -858,8 +860,7 @@ static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables,
     fl->mfma[h] = base + T->off_mfma;
     fl->rot_q[h] = base + T->off_rot_q;
     fl->rot_t[h] = reinterpret_cast<const float *>(base + T->off_rot_t);
-    fl->lut[h] = base + T->off_lut;
-    fl->books[h] = reinterpret_cast<const float *>(base + T->off_books);
+    fl->enc_bytes[h] = (int32_t)T->off_rot;  // header, LUT, books
     fl->cent_exp[h] = T->cent_exp;
     const int sgv = T->groups == 1 ? ks : g0;
     if (h == 0) {
@@ -949,7 +950,7 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
   p.ends = nullptr;
   p.splits = splits;
   p.split_tokens = (int)((d->max_length + splits - 1) / splits);
-  p.split_tokens = ((p.split_tokens + 255) / 256) * 256;
+  p.split_tokens = ((p.split_tokens + 127) / 128) * 128;
   p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
   p.out = d->out;
   p.logits = nullptr;
@@ -1254,7 +1255,7 @@ bgtq_status bgtq_attention_record(bgtq_attention *a) {
   p.ends = reinterpret_cast<const int32_t *>(static_cast<const uint32_t *>(a->small.ptr) + 1);
   p.splits = choose_splits(1, T, 0);
   p.splits = (int)std::min<uint32_t>((uint32_t)p.splits, a->max_splits);
-  p.split_tokens = (int)(((T + p.splits - 1) / p.splits + 255) / 256 * 256);
+  p.split_tokens = (int)(((T + p.splits - 1) / p.splits + 127) / 128 * 128);
   p.part = static_cast<float *>(a->part.ptr);
   p.stats = static_cast<float *>(a->stats.ptr);
   p.counters = static_cast<uint32_t *>(a->counters.ptr);

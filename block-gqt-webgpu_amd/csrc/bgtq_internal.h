@@ -192,10 +192,10 @@ struct FastLayout {
   const uint8_t *mfma[kMaxKvHeads];
   const uint8_t *rot_q[kMaxKvHeads];
   int32_t cent_exp[kMaxKvHeads];
-  // The decode-step append's encoder tables: transposed rotation, code LUT, books.
+  // The decode-step append's encoder: transposed rotation, and the bytes of
+  // the table set's header, code LUT and books (contiguous from its start).
   const float *rot_t[kMaxKvHeads];
-  const uint8_t *lut[kMaxKvHeads];
-  const float *books[kMaxKvHeads];
+  int32_t enc_bytes[kMaxKvHeads];
 };
 
 // Sets the calling thread's bgtq_last_error() message; returns code.
@@ -229,6 +229,9 @@ hipError_t launch_decode_tail(const DecodeParams &p, hipStream_t stream);
 hipError_t launch_decode_probs(const DecodeParams &p, hipStream_t stream);
 // Fused decode (decode_fast.hip): nn leading nibble K-steps, sg K-steps in group 0.
 bool decode_fast_supported(int dim, int key_format, int nn, int sg);
+// LDS bytes the fused kernel gives the append's copy of a table set's
+// header, code LUT and books.
+int decode_fast_enc_capacity(int dim, int nn);
 // Row bytes of the packed layout with nn leading nibble K-steps (no padding).
 int decode_fast_row_bytes(int dim, int nn);
 hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);

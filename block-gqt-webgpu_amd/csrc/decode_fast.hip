@@ -47,6 +47,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kChunk = 32;  // tokens per wave iteration: two 16-token MFMA tiles
 constexpr int kRing = 3;    // LDS chunk buffers per wave: compute one, the others in flight
 constexpr bool kInterleaved = true;
+constexpr int kMergeOneRound = 40;  // split counts merged with a single round of loads
 
 template <int D>
 struct Geo {
@@ -79,9 +80,54 @@ struct Slot {
   static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
   static constexpr int AHEAD = RING - 1;
   static constexpr int DYN = RING * kWaves * BYTES;  // dynamic LDS: the ring (the tables are static)
+  // Decode-step append: the new token's wave encodes it with its last ring
+  // slot as scratch (from offset 0) and a copy of its KV head's tables header,
+  // code LUT and centroid books (from ENC_OFF, ENC_DMAS 1 KB pieces).
+  static constexpr int ENC_OFF = KF == 1 ? (row_enc::scratch_bytes(D) + 1023) / 1024 * 1024 : 0;
+  static constexpr int ENC_DMAS = KF == 1 ? (BYTES - ENC_OFF) / 1024 : 0;
   static_assert(DYN + TABLES <= kLdsLimit, "LDS of one workgroup");
   static_assert(AHEAD >= 1 && AHEAD <= 3, "ring waits cover up to three chunks in flight");
 };
+
+// Split merge in one round trip: each output element of the KV head's G
+// query heads loads every split's (m, l, o) at once, S <= SMAX. Out of line,
+// and instantiated for a few SMAX, so the kernel's own code stays as small.
+template <int D, int SMAX>
+__device__ __noinline__ void merge_one_round(float *part, float *out, float *stats, int64_t head0, int G, int S,
+                                             int tid) {
+  for (int e = tid; e < G * D; e += kThreads) {
+    const int g = e / D, dm = e - g * D;
+    const int64_t head = head0 + g;
+    float *pp = part + head * S * (D + 2);
+    float m[SMAX], l[SMAX], o[SMAX];
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < S) {
+        m[s] = coherent_load(pp + s * (D + 2));
+        l[s] = coherent_load(pp + s * (D + 2) + 1);
+        o[s] = coherent_load(pp + s * (D + 2) + 2 + dm);
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s)
+      if (s < S) M = fmaxf(M, m[s]);
+    float Lsum = 0.0f, Ov = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < S) {
+        const float w = m[s] == -INFINITY ? 0.0f : exp2f(m[s] - M);
+        Lsum = __builtin_fmaf(l[s], w, Lsum);
+        Ov = __builtin_fmaf(o[s], w, Ov);
+      }
+    }
+    out[head * D + dm] = Ov / Lsum;
+    if (dm == 0 && stats) {
+      stats[head * 2] = M * kLn2;
+      stats[head * 2 + 1] = Lsum;
+    }
+  }
+}
 
 // KF: 1 = packed codes, 0 = FP16 K rows. NN: leading nibble K-steps.
 // SG: K-steps in group 0 (== KS: one scale per token).
@@ -93,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   constexpr int KS = Gm::KS, DT = Gm::DT, PR = Gm::PR, VI = Gm::VI;
   constexpr int RB = Sl::RB, KI = Sl::KI, L = Sl::L, AHEAD = Sl::AHEAD;
   static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
-  static_assert(kWaves * Sl::BYTES >= 16 * (D + 4) * 4, "q staging fits one ring slot of all waves");
+  static_assert(Sl::BYTES >= 16 * (D + 4) * 4, "q staging fits one ring slot");
   static_assert(KF == 0 || Gm::DT % kWaves == 0, "rotation tiles split evenly over the waves");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= kWaves * 16 * (D + 2) * 4, "wave merge fits the ring");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
@@ -183,6 +229,10 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
   const bool app = p.k_new != nullptr && t_new >= 0 && c_new % (p.splits * kWaves) == split * kWaves + wave;
   const int i_new = app ? c_new / (p.splits * kWaves) : -1;  // the wave's loop iteration of that chunk
+  // The q rotation stages through the last ring slot of a wave other than
+  // the new token's, whose slot receives the encoder's tables meanwhile.
+  const int own_w = p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
+  const int stage_w = own_w >= 0 && own_w < kWaves ? (own_w + 1) % kWaves : 0;
   uint32_t pk_new[JL] = {};                    // packed K bytes lane, lane + 64
   uint32_t h_new = 0;                          // FP16 scale bits (lanes below the norm stride)
   u32x4 v_new16{0u, 0u, 0u, 0u}, k_new16{0u, 0u, 0u, 0u};  // FP16 pieces of the V / K row (lanes below D / 8)
@@ -210,6 +260,15 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     return h;
   };
   if (app) {
+    if (KF == 1) {
+      // The tables' header, code LUT and books (contiguous from the start of
+      // the table set, fl.enc_bytes[kv] bytes) into this wave's last ring
+      // slot, first of this wave's loads: the prologue's wait covers them.
+      const __amdgpu_buffer_rsrc_t rt = rsrc(p.tables[kv], fl.enc_bytes[kv]);
+      uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
+#pragma unroll
+      for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
+    }
     if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
     if (KF == 1) {
 #pragma unroll
@@ -290,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     half8 bh[KS], bl[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) split_scaled(qv[s], __builtin_ldexpf(1.0f, e0), bh[s], bl[s]);
-    float *qs = reinterpret_cast<float *>(ring + (Sl::RING - 1) * kWaves * Sl::BYTES);  // [16][D + 4]
+    float *qs = reinterpret_cast<float *>(ring + ((Sl::RING - 1) * kWaves + stage_w) * Sl::BYTES);  // [16][D + 4]
     const float unscale = __builtin_ldexpf(1.0f, -e0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -304,7 +363,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       }
       *reinterpret_cast<f32x4 *>(qs + col * (D + 4) + 16 * (wave * NT + t) + 4 * gq) = acc * unscale;
     }
-    wait_vm<AHEAD * L>();  // wave 0's table DMAs, which precede the chunks
+    wait_vm<AHEAD * L>();  // the table DMAs, which precede the chunks
     lds_barrier();
 #pragma unroll
     for (int s = 0; s < KS; ++s)
@@ -351,8 +410,10 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
     if (KF == 1) {
       // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
-      const DevTables *T = p.tables[kv];
-      lc.init(T, lane);  // here, not with the prologue loads: its byte loads would be waited for there
+      // T: the LDS copy of the tables (header, LUT, books) loaded in the prologue.
+      const DevTables *T =
+          reinterpret_cast<const DevTables *>(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF);
+      lc.init(T, lane);
       float x[JL];
 #pragma unroll
       for (int jl = 0; jl < JL; ++jl) {
@@ -371,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       h_new = row_enc::encode_row<D>(
           T, lc, x,
           [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
-          fl.lut[kv], fl.books[kv], scr, lane);
+          tables_lut(T), tables_books(T), scr, lane);
       const int logical = T->nibble_dims / 2 + D - T->nibble_dims;
       uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * RB;
 #pragma unroll
@@ -619,9 +680,16 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
            (unsigned)(S - 1);
   __syncthreads();
   if (!last) return;
-  // Merge with every load of a stage in flight at once: (m, l) of all heads
-  // and splits, then per-head normalised weights, then the o rows in groups
-  // of eight splits.
+  if (S <= kMergeOneRound) {
+    if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
+    else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
+    else merge_one_round<D, kMergeOneRound>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
+    if (tid == 0) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  // More splits: every load of a stage in flight at once: (m, l) of all
+  // heads and splits, then per-head normalised weights, then the o rows in
+  // groups of eight splits.
   float *wgt = reinterpret_cast<float *>(smem);  // [16 heads][S] (reuses the ring)
   float *mrow = wgt + 16 * S;                     // [16 heads][S] split maxima
   for (int e = tid; e < G * S; e += kThreads) {
@@ -685,6 +753,17 @@ hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t s
 }  // namespace
 
 int decode_fast_row_bytes(int dim, int nn) { return nn * 16 + (dim / 32 - nn) * 32; }
+
+int decode_fast_enc_capacity(int dim, int nn) {
+  if (dim == 64) {
+    if (nn == 0) return Slot<64, 1, 0>::ENC_DMAS * 1024;
+    if (nn == 1) return Slot<64, 1, 1>::ENC_DMAS * 1024;
+    return Slot<64, 1, 2>::ENC_DMAS * 1024;
+  }
+  if (nn == 0) return Slot<128, 1, 0>::ENC_DMAS * 1024;
+  if (nn == 2) return Slot<128, 1, 2>::ENC_DMAS * 1024;
+  return Slot<128, 1, 4>::ENC_DMAS * 1024;
+}
 
 bool decode_fast_supported(int dim, int key_format, int nn, int sg) {
   if (dim != 64 && dim != 128) return false;
