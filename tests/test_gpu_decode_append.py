@@ -82,9 +82,16 @@ def test_append_packed_every_chunk_position(device, dim):
     _run(device, dim=dim, key_format="packed", lengths=[1, 32, 33, 64, 97, 1000, 4096])
 
 
-@pytest.mark.parametrize("splits", [1, 3, 16])
+@pytest.mark.parametrize("splits", [1, 3, 16, 32])
 def test_append_packed_forced_splits(device, splits):
     _run(device, dim=64, key_format="packed", lengths=[2000, 31, 4095], splits=splits, hkv=3, hq=9)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_append_smollm2_step_shape(device, dim):
+    """Batch 1 at 4096 + 1 tokens: the library's own split choice (one 32-token chunk per wave, the
+    new token alone in the last split) and the one-round merge."""
+    _run(device, dim=dim, key_format="packed", lengths=[4097], hkv=3, hq=9)
 
 
 def test_append_fp16_sources(device):

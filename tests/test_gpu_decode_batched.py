@@ -106,12 +106,21 @@ def test_fp16_keys_baseline(device, oracle, dim):
          key_format="fp16")
 
 
-@pytest.mark.parametrize("splits", [1, 3, 7])
+@pytest.mark.parametrize("splits", [1, 3, 7, 12])
 def test_forced_splits(device, oracle, splits):
     from bgtq import calibrate
     p = calibrate.layout_b(64)
     print("splits", splits, flush=True)
     _run(device, oracle, params=[p], batch=2, hq=3, hkv=1, dim=64, lengths=[2000, 1500], cap=2000, splits=splits)
+
+
+@pytest.mark.parametrize("splits", [30, 47])
+def test_forced_splits_long(device, oracle, splits):
+    """Split merges of every size class: one load round up to 40 splits, two phases beyond."""
+    from bgtq import calibrate
+    p = calibrate.layout_b(64)
+    print("splits", splits, flush=True)
+    _run(device, oracle, params=[p], batch=2, hq=7, hkv=1, dim=64, lengths=[6000, 5100], cap=6000, splits=splits)
 
 
 def test_non_fast_layouts_use_general_kernel(device, oracle):
