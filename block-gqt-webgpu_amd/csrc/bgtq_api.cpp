@@ -733,10 +733,12 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
         J.norms = j.norms;
         J.dst_row0 = j.dst_row0;
         J.dst_step = 1;
+        J.enc_bytes = (int32_t)j.tables->h()->off_rot;
+        J.off_rot_t = (int32_t)j.tables->h()->off_rot_t;
         max_rows = std::max(max_rows, j.rows);
         total_rows += j.rows;
         const bgtq_tables_info &ti = j.tables->info;
-        lds = std::max(lds, encode_wave_lds_bytes(dim, ti.n_codebooks * 256, ti.n_books * ti.max_centroids));
+        lds = std::max(lds, encode_wave_lds_bytes(dim, (int)j.tables->h()->off_rot));
         lut_max = std::max(lut_max, ti.n_codebooks * 256);
         books_max = std::max(books_max, ti.n_books * ti.max_centroids);
       }

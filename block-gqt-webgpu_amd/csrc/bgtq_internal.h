@@ -9,7 +9,7 @@ namespace bgtq {
 constexpr int kMaxDim = 128;
 constexpr int kMaxGroups = 8;
 constexpr int kMaxKvHeads = 16;
-constexpr int kEncodeJobsPerLaunch = 60;  // 56-byte jobs: the launch stays under 4 KB of kernel arguments
+constexpr int kEncodeJobsPerLaunch = 60;  // 64-byte jobs: the launch stays under 4 KB of kernel arguments
 
 // Device-resident calibration tables, built once on the host from the
 // reference's serialized tables (src/webgpu/layout.ts:24-31). Fixed header,
@@ -71,8 +71,10 @@ struct EncodeJobDev {
   int64_t dst_row0;
   int32_t src_stride;  // elements
   int32_t dst_step;    // destination row step per source row (>= 1)
+  int32_t enc_bytes;   // bytes of the table set's header, code LUT and books (off_rot)
+  int32_t off_rot_t;   // byte offset of the transposed rotation
 };
-static_assert(sizeof(EncodeJobDev) == 56, "encode job layout");
+static_assert(sizeof(EncodeJobDev) == 64, "encode job layout");
 
 struct EncodeLaunch {
   EncodeJobDev jobs[kEncodeJobsPerLaunch];
@@ -204,10 +206,10 @@ int32_t set_error(int32_t code, const char *msg);
 // Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).
 hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
                          hipStream_t stream);
-// Wave-per-row encode (encode_wave.hip): dynamic LDS for a job with the given
-// LUT bytes and centroid floats, and its launcher (wgs_per_job workgroups of
-// four waves per job, each wave striding over the job's rows).
-int encode_wave_lds_bytes(int dim, int lut_bytes, int book_floats);
+// Wave-per-row encode (encode_wave.hip): dynamic LDS for a job whose table
+// set's header, LUT and books take enc_bytes, and its launcher (wgs_per_job
+// workgroups of four waves per job, each wave striding over the job's rows).
+int encode_wave_lds_bytes(int dim, int enc_bytes);
 hipError_t launch_encode_wave(const EncodeLaunch &launch, int dim, int src_f32, int wgs_per_job, int lds_bytes,
                               hipStream_t stream);
 // Bulk thread-per-row encode (encode_bulk.hip) for layouts of two equal

@@ -6,6 +6,7 @@
 // one launch; throughput comes from many rows per wave with the next row's
 // inputs loaded while the current one is encoded.
 #include "encode_row.h"
+#include "gfx950_common.h"
 
 namespace bgtq {
 namespace {
@@ -14,17 +15,17 @@ using namespace row_enc;
 
 constexpr int kWaves = 4;
 
-// Shared tables of a job + per-wave scratch; byte offsets in dynamic LDS.
+// Dynamic LDS of a workgroup: the job's transposed rotation, a copy of its
+// table set's first enc_bytes (header, code LUT, books) in whole 1 KB DMA
+// pieces, then per-wave scratch.
 struct WaveLds {
-  int rot_t, lut, books, scratch, scratch_stride, total;
+  int rot_t, tab, scratch, scratch_stride, total;
 };
-__host__ __device__ inline WaveLds wave_lds(int D, int lut_bytes, int book_floats) {
-  auto a16 = [](int x) { return (x + 15) & ~15; };
+__host__ __device__ inline WaveLds wave_lds(int D, int enc_bytes) {
   WaveLds L;
   L.rot_t = 0;
-  L.lut = L.rot_t + D * D * 4;
-  L.books = L.lut + a16(lut_bytes);
-  L.scratch = L.books + a16(book_floats * 4);
+  L.tab = L.rot_t + D * D * 4;
+  L.scratch = L.tab + (enc_bytes + 1023) / 1024 * 1024;
   L.scratch_stride = scratch_bytes(D);
   L.total = L.scratch + kWaves * L.scratch_stride;
   return L;
@@ -35,50 +36,68 @@ __global__ __launch_bounds__(64 * kWaves) void encode_wave_kernel(EncodeLaunch l
   constexpr int JL = Lane<D>::JL;
   extern __shared__ __align__(16) uint8_t smem[];
   const EncodeJobDev job = launch.jobs[blockIdx.y];
-  const DevTables *__restrict__ T = job.t;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int mc = T->max_centroids;
-  const WaveLds L = wave_lds(D, T->n_codebooks * 256, T->n_books * mc);
+  const WaveLds L = wave_lds(D, job.enc_bytes);
   float *rot_t = reinterpret_cast<float *>(smem + L.rot_t);
-  uint8_t *lut = smem + L.lut;
-  float *books = reinterpret_cast<float *>(smem + L.books);
   const Scratch<D> scr(smem + L.scratch + wave * L.scratch_stride);
-
-  // Stage the job's transposed rotation, code LUT and centroid books.
-  {
-    const float *src = tables_rot_t(T);
-    for (int e = tid; e < D * D; e += 64 * kWaves) rot_t[e] = src[e];
-    const uint8_t *ls = tables_lut(T);
-    for (int e = tid; e < T->n_codebooks * 256; e += 64 * kWaves) lut[e] = ls[e];
-    const float *bs = tables_books(T);
-    for (int e = tid; e < T->n_books * mc; e += 64 * kWaves) books[e] = bs[e];
-  }
-  Lane<D> c;
-  c.init(T, lane);
-  __syncthreads();
-
-  const int RB = T->row_bytes, ns = T->nibble_dims, NS = T->norm_stride;
-  const int logical = ns / 2 + D - ns;
   const int64_t nwaves = (int64_t)gridDim.x * kWaves;
-  auto load_row = [&](int64_t r, float (&x)[JL]) {
+
+  // One round trip: the rotation (d*d*4 bytes, whole 1 KB pieces for d >= 16)
+  // and the tables' header, LUT and books go HBM -> LDS (1 KB pieces over the
+  // four waves; lanes past a region's size write zeros), the wave's first row
+  // is loaded in natural order.
+  static_assert(D * D * 4 % 1024 == 0, "rotation in whole DMA pieces");
+  {
+    const uint8_t *tb = reinterpret_cast<const uint8_t *>(job.t);
+    const __amdgpu_buffer_rsrc_t rr = gfx::rsrc(tb + job.off_rot_t, D * D * 4);
+    for (int k = wave; k < D * D * 4 / 1024; k += kWaves) gfx::dma16(rr, smem + L.rot_t + k * 1024, k * 1024 + lane * 16, 0);
+    const __amdgpu_buffer_rsrc_t rt = gfx::rsrc(tb, job.enc_bytes);
+    for (int k = wave; k < (job.enc_bytes + 1023) / 1024; k += kWaves)
+      gfx::dma16(rt, smem + L.tab + k * 1024, k * 1024 + lane * 16, 0);
+  }
+  // Natural-order row values: lane holds element lane + 64 jl (FP16-rounded).
+  auto load_row = [&](int64_t r, float (&v)[JL]) {
 #pragma unroll
     for (int jl = 0; jl < JL; ++jl) {
-      float v = 0.0f;
-      if (c.own[jl] && r < job.rows) {
-        const int64_t at = r * job.src_stride + c.perm[jl];
-        if (SRC_F32) v = f16_bits_to_f32(f32_to_f16_bits(static_cast<const float *>(job.src)[at]));
-        else v = f16_bits_to_f32(static_cast<const uint16_t *>(job.src)[at]);
+      float x = 0.0f;
+      const int e = lane + 64 * jl;
+      if (e < D && r < job.rows) {
+        const int64_t at = r * job.src_stride + e;
+        if (SRC_F32) x = f16_bits_to_f32(f32_to_f16_bits(static_cast<const float *>(job.src)[at]));
+        else x = f16_bits_to_f32(static_cast<const uint16_t *>(job.src)[at]);
       }
-      x[jl] = v;
+      v[jl] = x;
     }
   };
   int64_t row = (int64_t)blockIdx.x * kWaves + wave;
-  float x[JL];
-  load_row(row, x);
+  float xn[JL];
+  load_row(row, xn);
+  gfx::wait_vm<0>();
+  __syncthreads();
+
+  const DevTables *T = reinterpret_cast<const DevTables *>(smem + L.tab);
+  Lane<D> c;
+  c.init(T, lane);
+  const uint8_t *lut = tables_lut(T);
+  const float *books = tables_books(T);
+  const int RB = T->row_bytes, ns = T->nibble_dims, NS = T->norm_stride;
+  const int logical = ns / 2 + D - ns;
   for (; row < job.rows; row += nwaves) {
     float xnext[JL];
     load_row(row + nwaves, xnext);  // next row's inputs in flight meanwhile
+    // head-perm order: x[jl] = row[perm[lane + 64 jl]]
+    float x[JL];
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl) {
+      const int src = c.perm[jl];
+      float v = __shfl(xn[0], src & 63, 64);
+      if (JL > 1) {
+        const float hi = __shfl(xn[JL - 1], src & 63, 64);
+        v = src >= 64 ? hi : v;
+      }
+      x[jl] = c.own[jl] ? v : 0.0f;
+    }
     const uint16_t h = encode_row<D>(
         T, c, x, [&](int i, int jl) { return rot_t[i * D + (c.own[jl] ? lane + 64 * jl : 0)]; }, lut, books, scr, lane);
     const int64_t dst = job.dst_row0 + row * job.dst_step;
@@ -87,7 +106,7 @@ __global__ __launch_bounds__(64 * kWaves) void encode_wave_kernel(EncodeLaunch l
     if (lane < NS) job.norms[dst * NS + lane] = h;
     wave_sync();  // scratch is rewritten by the next row
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl) x[jl] = xnext[jl];
+    for (int jl = 0; jl < JL; ++jl) xn[jl] = xnext[jl];
   }
 }
 
@@ -110,7 +129,7 @@ hipError_t launch_wave_d(const EncodeLaunch &launch, int src_f32, int wgs_per_jo
 
 }  // namespace
 
-int encode_wave_lds_bytes(int dim, int lut_bytes, int book_floats) { return wave_lds(dim, lut_bytes, book_floats).total; }
+int encode_wave_lds_bytes(int dim, int enc_bytes) { return wave_lds(dim, enc_bytes).total; }
 
 hipError_t launch_encode_wave(const EncodeLaunch &launch, int dim, int src_f32, int wgs_per_job, int lds_bytes,
                               hipStream_t stream) {
