@@ -51,6 +51,9 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kChunk = 32;  // tokens per block: two 16-token MFMA tiles
 constexpr int kRing = 6;    // shared LDS buffers: compute one, four in flight, one draining
+// Merges of at most this many queries load all splits at once (one wave per
+// query, at most two per SIMD of a 256-CU device).
+constexpr int64_t kMergeOneRoundQueries = 2048;
 
 // One ring buffer: V block, K block, FP16 scales; every wave DMAs a quarter.
 // Packed-code kernels also hold the K-steps' centroid books (fp32) and two
@@ -514,10 +517,76 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   }
 }
 
-// LSE merge of the split partials of tiles with more than one active split:
-// one wave per query, lane s holding split s's (m, l), the o rows read
-// coalesced eight splits at a time.
+// One query's merge: every active split's o row is loaded in one round (split
+// k < SMAX reads split min(k, n_act - 1), whose weight is zero past n_act), then
+// combined with the log-sum-exp weights of the (m, l) pairs (lane s: split s).
+template <int D, int SMAX>
+__device__ __forceinline__ void merge_query(const float *part_o, float2 ml, int n_act, int lane, float *out) {
+  constexpr int DL = D / 64;  // output dims per lane
+  float o[SMAX][DL];
+#pragma unroll
+  for (int k = 0; k < SMAX; ++k)
+#pragma unroll
+    for (int e = 0; e < DL; ++e) o[k][e] = part_o[min(k, n_act - 1) * D + lane + 64 * e];
+  float M = ml.x;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) M = fmaxf(M, __shfl_xor(M, s, 64));
+  float w = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - M);
+  float L = w * ml.y;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) L += __shfl_xor(L, s, 64);
+  w = w / L;
+  float acc[DL];
+#pragma unroll
+  for (int e = 0; e < DL; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < SMAX; ++k) {
+    const float wk = __shfl(w, k, 64);
+#pragma unroll
+    for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[k][e], wk, acc[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < DL; ++e) out[lane + 64 * e] = acc[e];
+}
+
+// The same in rounds of eight splits: fewer registers, for launches with
+// enough queries that occupancy, not one query's latency, sets the time.
 template <int D>
+__device__ __forceinline__ void merge_query_rounds(const float *part_o, float2 ml, int n_act, int lane, float *out) {
+  constexpr int DL = D / 64;
+  float M = ml.x;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) M = fmaxf(M, __shfl_xor(M, s, 64));
+  float w = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - M);
+  float L = w * ml.y;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) L += __shfl_xor(L, s, 64);
+  w = w / L;
+  float acc[DL];
+#pragma unroll
+  for (int e = 0; e < DL; ++e) acc[e] = 0.0f;
+  for (int s0 = 0; s0 < n_act; s0 += 8) {
+    float o[8][DL];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int e = 0; e < DL; ++e) o[k][e] = s0 + k < n_act ? part_o[(s0 + k) * D + lane + 64 * e] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float wk = __shfl(w, min(s0 + k, 63), 64);
+#pragma unroll
+      for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[k][e], wk, acc[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < DL; ++e) out[lane + 64 * e] = acc[e];
+}
+
+// LSE merge of the split partials of tiles with more than one active split:
+// one wave per query, lane s holding split s's (m, l). ONE_ROUND: the o rows
+// of all active splits read at once (small launches, where each query's
+// latency is the time); else in rounds of eight.
+template <int D, bool ONE_ROUND>
 __global__ __launch_bounds__(kThreads) void prefill_merge_kernel(PrefillParams p, int tile_queries) {
   const int unit = blockIdx.y;
   const int b = unit / p.kv_heads, kv = unit - b * p.kv_heads;
@@ -536,33 +605,11 @@ __global__ __launch_bounds__(kThreads) void prefill_merge_kernel(PrefillParams p
   const float *part_o = p.part + (int64_t)p.batch * rows * Hq * S * 2 + g_row * S * D;
   const float2 ml = lane < n_act ? reinterpret_cast<const float2 *>(p.part)[g_row * S + lane]
                                  : float2{-INFINITY, 0.0f};
-  float M = ml.x;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-  float w = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - M);
-  float L = w * ml.y;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
-  w = w / L;
-  constexpr int DL = D / 64;  // output dims per lane
-  float acc[DL];
-#pragma unroll
-  for (int e = 0; e < DL; ++e) acc[e] = 0.0f;
-  for (int s0 = 0; s0 < n_act; s0 += 8) {
-    float o[8][DL];
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-#pragma unroll
-      for (int e = 0; e < DL; ++e) o[k][e] = s0 + k < n_act ? part_o[(s0 + k) * D + lane + 64 * e] : 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float wk = __shfl(w, min(s0 + k, 63), 64);
-#pragma unroll
-      for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[k][e], wk, acc[e]);
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < DL; ++e) p.out[g_row * D + lane + 64 * e] = acc[e];
+  if (!ONE_ROUND) merge_query_rounds<D>(part_o, ml, n_act, lane, p.out + g_row * D);
+  else if (n_act <= 8) merge_query<D, 8>(part_o, ml, n_act, lane, p.out + g_row * D);
+  else if (n_act <= 16) merge_query<D, 16>(part_o, ml, n_act, lane, p.out + g_row * D);
+  else if (n_act <= 32) merge_query<D, 32>(part_o, ml, n_act, lane, p.out + g_row * D);
+  else merge_query<D, kPrefillMaxSplits>(part_o, ml, n_act, lane, p.out + g_row * D);
 }
 
 template <int D, int KF, int NN, int SG, int NCB>
@@ -580,8 +627,11 @@ hipError_t launch_ncb(const PrefillParams &p, const FastLayout &fl, hipStream_t 
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int nq = p.rows * p.G;
-  hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((nq + kWaves - 1) / kWaves), units), dim3(kThreads),
-                     0, stream, p, kWaves * 16 * NCB);
+  const dim3 grid((unsigned)((nq + kWaves - 1) / kWaves), units);
+  if ((int64_t)nq * units <= kMergeOneRoundQueries)
+    hipLaunchKernelGGL((prefill_merge_kernel<D, true>), grid, dim3(kThreads), 0, stream, p, kWaves * 16 * NCB);
+  else
+    hipLaunchKernelGGL((prefill_merge_kernel<D, false>), grid, dim3(kThreads), 0, stream, p, kWaves * 16 * NCB);
   return hipGetLastError();
 }
 
