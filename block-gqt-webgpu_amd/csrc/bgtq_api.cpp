@@ -331,7 +331,8 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   const size_t off_rot_t = align(off_rot + sizeof(float) * d * d);
   const size_t off_mfma = align(off_rot_t + sizeof(float) * d * d);
   const size_t off_rot_q = align(off_mfma + (size_t)kMfmaTableBytes * nb);
-  const size_t total = off_rot_q + (d % 32 == 0 ? (size_t)rot_q_bytes((int)d) : 0);
+  const size_t off_gdesc = align(off_rot_q + (d % 32 == 0 ? (size_t)rot_q_bytes((int)d) : 0));
+  const size_t total = off_gdesc + sizeof(uint32_t) * d;
   auto *t = new bgtq_tables();
   t->ctx = ctx;
   t->host.assign(total, 0);
@@ -355,6 +356,7 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   T->off_rot_t = (uint32_t)off_rot_t;
   T->off_mfma = (uint32_t)off_mfma;
   T->off_rot_q = (uint32_t)off_rot_q;
+  T->off_gdesc = (uint32_t)off_gdesc;
   T->total_bytes = (uint32_t)total;
   float cmax = 0.0f;
   for (int64_t i = 0; i < d * mc; ++i) cmax = std::max(cmax, std::fabs(cent[i]));
@@ -368,6 +370,16 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
     T->lut_inv[j] = inv[j];
   }
   uint8_t *h = t->host.data();
+  {
+    // Per-position rebuild descriptors (src/reference/mixed_layout.py:21-27 row format).
+    uint32_t *gd = reinterpret_cast<uint32_t *>(h + off_gdesc);
+    for (int64_t j = 0; j < d; ++j) {
+      const bool nibble = j < nib;
+      const uint32_t off = (uint32_t)(nibble ? j / 2 : nib / 2 + (j - nib));
+      gd[j] = off | (uint32_t)(nibble ? 4 * (j & 1) : 0) << 8 | (uint32_t)nibble << 11 | (uint32_t)pos_book[j] << 12 |
+              (uint32_t)group_of[j] << 16;
+    }
+  }
   for (uint64_t i = 0; i < lut_len; ++i) h[off_lut + i] = (uint8_t)lut[i];
   for (int b = 0; b < nb; ++b)
     std::memcpy(h + off_books + sizeof(float) * b * mc, cent + book_rows[b] * mc, sizeof(float) * mc);
@@ -875,12 +887,55 @@ static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables,
   return decode_fast_supported(p.dim, 1, *nn, *sg);
 }
 
+// Whether the fused kernel's per-position code lookup serves a packed layout
+// the structured check (fast_layout) refused: FP16 V; 16-byte aligned packed
+// and scale bases and strides; per KV head up to decode_general_max_books
+// books of up to 256 centroids, norm stride up to 8, row bytes a multiple of
+// 4, nibble positions a multiple of 8 (a lane's 8 codes are all nibbles or
+// all bytes), groups in ascending position order with at most two in any 32
+// positions. Fills the per-head fields of fl.
+static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tables, FastLayout *fl) {
+  auto a16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  if (p.key_format != 1 || p.v_dtype != BGTQ_DTYPE_F16 || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
+  if (!a16(p.v) || (p.v_seq_stride * 2) % 16 || (p.v_head_stride * 2) % 16) return false;
+  if (!a16(p.packed) || p.packed_seq_stride % 16 || p.packed_head_stride % 16) return false;
+  if (!a16(p.norms) || (p.norms_seq_stride * 2) % 16 || (p.norms_head_stride * 2) % 16) return false;
+  for (int h = 0; h < p.kv_heads; ++h) {
+    const DevTables *T = tables[h]->h();
+    if (T->n_books > decode_general_max_books(p.dim) || T->max_centroids > 256 ||
+        T->norm_stride > kDecodeGeneralMaxNormStride || T->row_bytes > p.dim || T->row_bytes % 4 ||
+        T->nibble_dims % 8 || T->groups > 8)
+      return false;
+    for (int j = 1; j < p.dim; ++j)
+      if (T->group_of[j] < T->group_of[j - 1] || T->group_of[j] > T->group_of[j - 1] + 1) return false;
+    for (int s = 0; s < p.dim / 32; ++s)
+      if (T->group_of[32 * s + 31] > T->group_of[32 * s] + 1) return false;
+    if (p.k_new && (int64_t)T->off_rot > decode_fast_enc_capacity(p.dim, -1)) return false;
+    const uint8_t *base = reinterpret_cast<const uint8_t *>(tables[h]->dev());
+    fl->rot_q[h] = base + T->off_rot_q;
+    fl->rot_t[h] = reinterpret_cast<const float *>(base + T->off_rot_t);
+    fl->enc_bytes[h] = (int32_t)T->off_rot;
+    fl->cent_exp[h] = T->cent_exp;
+    fl->mfma[h] = base + T->off_mfma;
+    fl->gdesc[h] = reinterpret_cast<const uint32_t *>(base + T->off_gdesc);
+    fl->grb[h] = (int16_t)T->row_bytes;
+    fl->gns[h] = (int16_t)T->norm_stride;
+    fl->gnb[h] = (int16_t)T->n_books;
+  }
+  return true;
+}
+
 static bgtq_status launch_decode_common(bgtq_context *ctx, DecodeParams &p, const float *q,
                                         const bgtq_tables *const *tables) {
   p.q = q;
   FastLayout fl{};
   int nn = 0, sg = 0;
-  if (p.counters && fast_layout(p, tables, &fl, &nn, &sg)) {
+  bool fused = p.counters && fast_layout(p, tables, &fl, &nn, &sg);
+  if (p.counters && !fused && general_layout(p, tables, &fl)) {
+    nn = -1;
+    fused = true;
+  }
+  if (fused) {
     HIP_TRY(launch_decode_fast(p, fl, nn, sg, ctx->stream), "decode launch");
     if (p.probs) HIP_TRY(launch_decode_probs(p, ctx->stream), "probabilities launch");
     return BGTQ_OK;
@@ -970,7 +1025,12 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
     FastLayout fl{};
     int nn = 0, sg = 0;
     p.q = d->q;
-    if (!fast_layout(p, d->tables, &fl, &nn, &sg))
+    bool fused = fast_layout(p, d->tables, &fl, &nn, &sg);
+    if (!fused && general_layout(p, d->tables, &fl)) {
+      nn = -1;
+      fused = true;
+    }
+    if (!fused)
       return fail(BGTQ_ERR_UNSUPPORTED,
                   "decode_append needs the fused kernel's layouts; use bgtq_encode_batched and bgtq_decode");
     HIP_TRY(launch_decode_fast(p, fl, nn, sg, ctx->stream), "decode append launch");

@@ -17,7 +17,7 @@ constexpr int kEncodeJobsPerLaunch = 60;  // 64-byte jobs: the launch stays unde
 struct DevTables {
   int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids, n_books, n_codebooks;
   int32_t gstart[kMaxGroups], gend[kMaxGroups], gsize[kMaxGroups];  // group ranges (head-perm order)
-  uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, off_rot_q, total_bytes;
+  uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, off_rot_q, off_gdesc, total_bytes;
   int32_t cent_exp;  // 2^cent_exp * max|centroid| <= 2^14: fp16 hi/lo split range for MFMA operands
   uint8_t perm[kMaxDim];      // head_perm
   uint8_t group_of[kMaxDim];
@@ -39,6 +39,9 @@ struct DevTables {
   //             (hi, lo) MFMA A operands: for 16-row tile n, 32-column step
   //             s and lane l, 8 hi then 8 lo halves of
   //             Rq[16 n + l % 16][32 s + 8 (l / 16) + 0..7] (kRotQBytes).
+  // [off_gdesc] per head-perm position j, for the fused decode of any packed
+  //             layout: uint32 byte offset in the packed row | nibble shift << 8
+  //             | nibble flag << 11 | book << 12 | group << 16.
 };
 constexpr int kMfmaTableBytes = 3072;
 __host__ __device__ constexpr int rot_q_bytes(int dim) { return dim * dim * 4; }
@@ -198,6 +201,10 @@ struct FastLayout {
   // the table set's header, code LUT and books (contiguous from its start).
   const float *rot_t[kMaxKvHeads];
   int32_t enc_bytes[kMaxKvHeads];
+  // Packed layouts of any structure (the kernel's per-position code
+  // lookup): position descriptors, row bytes, norm stride, book count.
+  const uint32_t *gdesc[kMaxKvHeads];
+  int16_t grb[kMaxKvHeads], gns[kMaxKvHeads], gnb[kMaxKvHeads];
 };
 
 // Sets the calling thread's bgtq_last_error() message; returns code.
@@ -229,8 +236,13 @@ hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t strea
 hipError_t launch_decode_tail(const DecodeParams &p, hipStream_t stream);
 // Materialised probabilities exp(logit - m)/l from the final statistics.
 hipError_t launch_decode_probs(const DecodeParams &p, hipStream_t stream);
-// Fused decode (decode_fast.hip): nn leading nibble K-steps, sg K-steps in group 0.
+// Fused decode (decode_fast.hip): nn leading nibble K-steps, sg K-steps in group 0;
+// nn = -1: a packed layout of any structure (per-position code lookup).
 bool decode_fast_supported(int dim, int key_format, int nn, int sg);
+// Books (of up to 256 centroids) and the norm stride the per-position path
+// holds in LDS for head dim `dim`.
+int decode_general_max_books(int dim);
+constexpr int kDecodeGeneralMaxNormStride = 8;
 // LDS bytes the fused kernel gives the append's copy of a table set's
 // header, code LUT and books.
 int decode_fast_enc_capacity(int dim, int nn);

@@ -60,22 +60,25 @@ struct Geo {
 
 // One ring buffer: V chunk, FP16 scales (32 x 4 bytes), K chunk. Every DMA
 // instruction runs on all 64 lanes (lanes past the data read zeros into the
-// padding: scales to 256 bytes, K to whole 1 KB pieces), so the compiler's
+// padding: scales to 256 bytes per scale DMA, K to whole 1 KB pieces), so the compiler's
 // count of loads in flight matches the hardware's and its own waits for
 // register loads never wait for ring data. Two workgroups of the layout-B
 // d=64 kernel still fit one CU's 160 KB.
+// KF 2 (any packed layout): RB is the largest row a layout can have, NN the
+// scale DMAs (one for norm strides up to 4, two up to 8).
 template <int D, int KF, int NN>
 struct Slot {
   static constexpr int KS = D / 32;
-  static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : 2 * D;  // K row bytes
+  static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : KF == 2 ? D : 2 * D;  // K row bytes
   static constexpr int KBYTES = kChunk * RB;
   static constexpr int KI = (KBYTES + 1023) / 1024;  // 16-byte DMA instructions per K chunk
-  static constexpr int NBYTES = KF == 1 ? 64 * 4 : 0;
+  static constexpr int NSC = KF == 1 ? 1 : KF == 2 ? NN : 0;  // scale DMAs per chunk
+  static constexpr int NBYTES = NSC * 64 * 4;
   static constexpr int NOFF = Geo<D>::VBYTES;         // scales
   static constexpr int KOFF = NOFF + NBYTES;          // K
   static constexpr int BYTES = KOFF + KI * 1024;
-  static constexpr int L = Geo<D>::VI + KI + (KF == 1 ? 1 : 0);  // DMA instructions per chunk
-  static constexpr int TABLES = KF == 1 ? KS * 2048 : 0;
+  static constexpr int L = Geo<D>::VI + KI + NSC;  // DMA instructions per chunk
+  static constexpr int TABLES = KF >= 1 ? KS * 2048 : 0;
   // Three buffers per wave where they fit the CU, else two (FP16 K at d=128).
   static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
   static constexpr int AHEAD = RING - 1;
@@ -83,8 +86,8 @@ struct Slot {
   // Decode-step append: the new token's wave encodes it with its last ring
   // slot as scratch (from offset 0) and a copy of its KV head's tables header,
   // code LUT and centroid books (from ENC_OFF, ENC_DMAS 1 KB pieces).
-  static constexpr int ENC_OFF = KF == 1 ? (row_enc::scratch_bytes(D) + 1023) / 1024 * 1024 : 0;
-  static constexpr int ENC_DMAS = KF == 1 ? (BYTES - ENC_OFF) / 1024 : 0;
+  static constexpr int ENC_OFF = KF >= 1 ? (row_enc::scratch_bytes(D) + 1023) / 1024 * 1024 : 0;
+  static constexpr int ENC_DMAS = KF >= 1 ? (BYTES - ENC_OFF) / 1024 : 0;
   static_assert(DYN + TABLES <= kLdsLimit, "LDS of one workgroup");
   static_assert(AHEAD >= 1 && AHEAD <= 3, "ring waits cover up to three chunks in flight");
 };
@@ -129,8 +132,9 @@ __device__ __noinline__ void merge_one_round(float *part, float *out, float *sta
   }
 }
 
-// KF: 1 = packed codes, 0 = FP16 K rows. NN: leading nibble K-steps.
-// SG: K-steps in group 0 (== KS: one scale per token).
+// KF: 1 = packed codes of a structured layout, 2 = packed codes of any
+// layout, 0 = FP16 K rows. NN: leading nibble K-steps (KF 2: scale DMAs).
+// SG: K-steps in group 0 (== KS: one scale per token; unused by KF 2).
 template <int D, int KF, int NN, int SG>
 __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
@@ -141,6 +145,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
   static_assert(Sl::BYTES >= 16 * (D + 4) * 4, "q staging fits one ring slot");
   static_assert(KF == 0 || Gm::DT % kWaves == 0, "rotation tiles split evenly over the waves");
+  static_assert(KF != 2 || (NN >= 1 && NN <= 2), "one or two scale DMAs");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= kWaves * 16 * (D + 2) * 4, "wave merge fits the ring");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
   extern __shared__ __align__(16) uint8_t smem[];
@@ -159,7 +164,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // The K-steps' lookup tables are static LDS (an address fixed at compile
   // time, so a lookup's address is the code byte shifted: one instruction);
   // the ring is the dynamic LDS.
-  __shared__ __align__(16) uint8_t tabs[KF == 1 ? Sl::TABLES : 16];
+  // KF 2: the code tables of the KV head's books, 1 KB each.
+  __shared__ __align__(16) uint8_t tabs[KF >= 1 ? Sl::TABLES : 16];
   uint8_t *ring = smem;
   auto slot_base = [&](int s) { return ring + (s * kWaves + wave) * Sl::BYTES; };
 
@@ -168,10 +174,13 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // and sized to the chunk's tokens inside the sequence: the hardware range
   // check (which covers the per-lane offset) returns zeros past the length.
   const _Float16 *v_base = static_cast<const _Float16 *>(p.v) + b * p.v_seq_stride + kv * p.v_head_stride;
-  const uint8_t *k_base = KF == 1 ? p.packed + b * p.packed_seq_stride + kv * p.packed_head_stride
+  const uint8_t *k_base = KF >= 1 ? p.packed + b * p.packed_seq_stride + kv * p.packed_head_stride
                                   : reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(p.k) +
                                                                       b * p.k_seq_stride + kv * p.k_head_stride);
-  const uint16_t *n_base = KF == 1 ? p.norms + b * p.norms_seq_stride + kv * p.norms_head_stride : nullptr;
+  const uint16_t *n_base = KF >= 1 ? p.norms + b * p.norms_seq_stride + kv * p.norms_head_stride : nullptr;
+  // Packed row bytes and scales per row (runtime for KF 2).
+  const int rb = KF == 2 ? fl.grb[kv] : RB;
+  const int ns = KF == 2 ? fl.gns[kv] : 2;
   // Per-lane source offsets of the swizzled FP16 row pieces: DMA instruction k,
   // lane i fills LDS piece 64k + i = (row r, slot c) with global piece c ^ swz(r).
   uint32_t voff_rows[VI];
@@ -200,6 +209,19 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
       for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
       dma4<kStream>(rN, sb + Sl::NOFF, lane * 4, 0);
+    } else if (KF == 2) {
+      // Rows of rb bytes and ns scales, packed back to back: the chunk's rows
+      // fill the K area's front, its scale rows the scale area's. The range
+      // check zeroes a whole access that reaches past the range, so the ranges
+      // end on the access size (16 and 4 bytes): the last row's bytes arrive,
+      // and the few bytes past it lie in the same aligned 16 bytes as the row's
+      // end (both bases are 16-byte aligned, c0 a multiple of 32).
+      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * rb, (rest * rb + 15u) & ~15u);
+      const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * ns, (rest * ns * 2 + 3u) & ~3u);
+#pragma unroll
+      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+#pragma unroll
+      for (int k = 0; k < Sl::NSC; ++k) dma4<kStream>(rN, sb + Sl::NOFF + k * 256, k * 256 + lane * 4, 0);
     } else {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
 #pragma unroll
@@ -260,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     return h;
   };
   if (app) {
-    if (KF == 1) {
+    if (KF >= 1) {
       // The tables' header, code LUT and books (contiguous from the start of
       // the table set, fl.enc_bytes[kv] bytes) into this wave's last ring
       // slot, first of this wave's loads: the prologue's wait covers them.
@@ -270,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
     }
     if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
-    if (KF == 1) {
+    if (KF >= 1) {
 #pragma unroll
       for (int jl = 0; jl < JL; ++jl)
         k_nat[jl] = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new)[k_off + lane + 64 * jl]
@@ -299,6 +321,16 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       if (s < NN) dma16(rt, tabs + s * 2048 + 1024, 1024 + lane * 16, 0);
     }
   }
+  if (KF == 2 && wave == 0) {  // the code table ([code]: hi | lo << 16) of every book
+    const int nb = fl.gnb[kv];
+#pragma unroll
+    for (int bk = 0; bk < 2 * KS; ++bk) {
+      if (bk < nb) {
+        const __amdgpu_buffer_rsrc_t rt = rsrc(fl.mfma[kv] + bk * kMfmaTableBytes + 2048, 1024);
+        dma16(rt, tabs + bk * 1024, lane * 16, 0);
+      }
+    }
+  }
   f32x4 qload[KS][2];  // unconditional loads of a valid row; heads past G are zeroed after the chunk issue
   {
     const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + ((int64_t)b * Hq + hq0 + (head_ok ? col : 0)) * D);
@@ -307,9 +339,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) qload[s][hh] = src[8 * s + 2 * gq + hh];
   }
-  constexpr int NT = KF == 1 ? DT / kWaves : 1;  // 16-row tiles of the rotation per wave
+  constexpr int NT = KF >= 1 ? DT / kWaves : 1;  // 16-row tiles of the rotation per wave
   u32x4 rq[NT][KS][2];
-  if (KF == 1) {
+  if (KF >= 1) {
     const u32x4 *op = reinterpret_cast<const u32x4 *>(fl.rot_q[kv]);  // [tile][K-step][lane][hi, lo]
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -320,7 +352,19 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         rq[t][s][1] = op[at + 1];
       }
   }
-  const int ec = KF == 1 ? fl.cent_exp[kv] : 0;
+  const int ec = KF >= 1 ? fl.cent_exp[kv] : 0;
+  // KF 2: descriptors of this lane's positions 32 s + 8 gq + k (byte offset
+  // in the row | nibble shift << 8 | nibble flag << 11 | book << 12 | group << 16).
+  constexpr int KS2 = KF == 2 ? KS : 1;
+  u32x4 gdl[KS2][2];
+  if (KF == 2) {
+    const u32x4 *gd = reinterpret_cast<const u32x4 *>(fl.gdesc[kv]);
+#pragma unroll
+    for (int s = 0; s < KS2; ++s) {
+      gdl[s][0] = gd[8 * s + 2 * gq];
+      gdl[s][1] = gd[8 * s + 2 * gq + 1];
+    }
+  }
   // Unconditional, so every wave has exactly AHEAD * L chunk loads in flight
   // behind its prologue loads (chunks past the end are zero-sized). The
   // scheduling barriers keep the prologue's loads ahead of them, so waiting
@@ -334,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   for (int s = 0; s < KS; ++s)
 #pragma unroll
     for (int k = 0; k < 8; ++k) qv[s][k] = head_ok ? qload[s][k >> 2][k & 3] : 0.0f;
-  if (KF == 1) {
+  if (KF >= 1) {
     // qr^T = Rq q^T, Rq = R with the head permutation folded into its
     // columns, on the matrix cores (q and Rq split hi/lo, three MFMAs per
     // K-step, off-group entries exact zeros). Tile n leaves rows
@@ -401,14 +445,56 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       }
     kq = __builtin_ldexpf(kLog2e, -(eq + ec));
   }
-  if (KF == 1) lds_barrier();  // q staging (last ring slot) is dead
+  if (KF >= 1) lds_barrier();  // q staging (last ring slot) is dead
+
+  // KF 2: every K-step spans one group or two adjacent ones (glo[s], glo[s] + 1).
+  // The query's B operand is split by group (hi/lo pairs bh2/bl2[s][slot], the
+  // other group's positions zero), each slot accumulates on its own and the
+  // token's scale of that group weights it. Per lane and K-step: the row
+  // offset of its 8 codes (4 bytes of nibbles, or 8 bytes), the codes'
+  // shifts and width, and each code's table offset (book * 1 KB).
+  int glo[KS2], two[KS2], koff[KS2], kw[KS2];
+  uint32_t tbo[KS2][8];
+  half8 bh2[KS2][2], bl2[KS2][2];
+  constexpr int NSV = KF == 2 ? 2 * Sl::NSC : 1;  // scale entries a lane moves
+  int sc_src[NSV], sc_dst[NSV];
+  if (KF == 2) {
+#pragma unroll
+    for (int s = 0; s < KS2; ++s) {
+      const uint32_t first = __builtin_amdgcn_readfirstlane(gdl[s][0][0]);
+      const uint32_t last = __builtin_amdgcn_readfirstlane(__shfl(gdl[s][1][3], 48, 64));
+      glo[s] = (int)((first >> 16) & 15u);
+      two[s] = ((last >> 16) & 15u) != (first >> 16 & 15u);
+      koff[s] = (int)(gdl[s][0][0] & 255u);
+      kw[s] = (gdl[s][0][0] >> 11) & 1u ? 4 : 8;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t dsc = gdl[s][k >> 2][k & 3];
+        tbo[s][k] = ((dsc >> 12) & 15u) * 1024u;
+        const bool lo_grp = (int)((dsc >> 16) & 15u) == glo[s];
+        bh2[s][0][k] = lo_grp ? qhi[s][k] : (_Float16)0.0f;
+        bl2[s][0][k] = lo_grp ? qlo[s][k] : (_Float16)0.0f;
+        bh2[s][1][k] = lo_grp ? (_Float16)0.0f : qhi[s][k];
+        bl2[s][1][k] = lo_grp ? (_Float16)0.0f : qlo[s][k];
+      }
+    }
+    // The chunk's scale rows [token][ns] become [group][32 tokens] in place
+    // (lane moves entries lane + 64 k), so a lane's four tokens of one group
+    // are one 8-byte read.
+#pragma unroll
+    for (int k = 0; k < NSV; ++k) {
+      const int e = lane + 64 * k, t = e / ns;
+      sc_src[k] = e < 32 * ns ? 2 * e : -1;
+      sc_dst[k] = 2 * ((e - t * ns) * 32 + t);
+    }
+  }
 
   if (app) {  // the new token's rows: convert / encode, store to the caches
     if (lane < PR) {
       v_new16 = half_piece(p.v_new_f32, v_raw);
       *reinterpret_cast<u32x4 *>(const_cast<_Float16 *>(v_base) + (int64_t)t_new * D + 8 * lane) = v_new16;
     }
-    if (KF == 1) {
+    if (KF >= 1) {
       // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
       // T: the LDS copy of the tables (header, LUT, books) loaded in the prologue.
       const DevTables *T =
@@ -434,16 +520,16 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
           [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
           tables_lut(T), tables_books(T), scr, lane);
       const int logical = T->nibble_dims / 2 + D - T->nibble_dims;
-      uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * RB;
+      uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
 #pragma unroll
       for (int jl = 0; jl < JL; ++jl) {
         const int bb = lane + 64 * jl;
-        if (bb < RB) {
+        if (bb < rb) {
           pk_new[jl] = row_enc::packed_byte(scr.codes, bb, T->nibble_dims, logical);
           prow[bb] = (uint8_t)pk_new[jl];
         }
       }
-      if (lane < 2) const_cast<uint16_t *>(n_base)[(int64_t)t_new * 2 + lane] = (uint16_t)h_new;
+      if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
       row_enc::wave_sync();  // scratch reads done before the slot's first load
     } else if (lane < PR) {
       k_new16 = half_piece(p.k_new_f32, k_raw);
@@ -481,13 +567,66 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       const int r = t_new % kChunk;
       uint8_t *wsb = const_cast<uint8_t *>(sb);
       if (lane < PR) *reinterpret_cast<u32x4 *>(wsb + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = v_new16;
-      if (KF == 1) {
+      if (KF >= 1) {
 #pragma unroll
         for (int jl = 0; jl < JL; ++jl)
-          if (lane + 64 * jl < RB) wsb[Sl::KOFF + r * RB + lane + 64 * jl] = (uint8_t)pk_new[jl];
-        if (lane < 2) reinterpret_cast<uint16_t *>(wsb + Sl::NOFF)[2 * r + lane] = (uint16_t)h_new;
+          if (lane + 64 * jl < rb) wsb[Sl::KOFF + r * rb + lane + 64 * jl] = (uint8_t)pk_new[jl];
+        if (lane < ns) reinterpret_cast<uint16_t *>(wsb + Sl::NOFF)[ns * r + lane] = (uint16_t)h_new;
       } else if (lane < PR) {
         *reinterpret_cast<u32x4 *>(wsb + Sl::KOFF + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = k_new16;
+      }
+    }
+
+    // KF 2: transpose the scale rows (every read of the wave's slot precedes
+    // its writes: one wave's LDS operations complete in order).
+    if (KF == 2) {
+      uint8_t *ns_area = const_cast<uint8_t *>(sb) + Sl::NOFF;
+      uint32_t sv[NSV];
+#pragma unroll
+      for (int k = 0; k < NSV; ++k)
+        if (sc_src[k] >= 0) sv[k] = *reinterpret_cast<const uint16_t *>(ns_area + sc_src[k]);
+#pragma unroll
+      for (int k = 0; k < NSV; ++k)
+        if (sc_src[k] >= 0) *reinterpret_cast<uint16_t *>(ns_area + sc_dst[k]) = (uint16_t)sv[k];
+    }
+    // KF 2: acc2[u][s][slot], the K-step's codes against the slot's query part.
+    f32x4 acc2[KF == 2 ? 2 : 1][KS2][2];
+    if (KF == 2) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint8_t *row = kbuf + (16 * u + col) * rb;
+#pragma unroll
+        for (int s = 0; s < KS2; ++s) {
+          const uint32_t w0 = *reinterpret_cast<const uint32_t *>(row + koff[s]);
+          uint32_t w1 = *reinterpret_cast<const uint32_t *>(row + koff[s] + 4);
+          w1 = kw[s] == 4 ? w0 >> 16 : w1;  // nibbles 4..7 of the lane's 8
+          u32x4 hi, lo;
+#pragma unroll
+          for (int k2 = 0; k2 < 4; ++k2) {
+            uint32_t e[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int k = 2 * k2 + h;
+              const uint32_t code = __builtin_amdgcn_ubfe(k < 4 ? w0 : w1, (uint32_t)((k & 3) * kw[s]), (uint32_t)kw[s]);
+              e[h] = *reinterpret_cast<const uint32_t *>(tabs + tbo[s][k] + 4 * code);
+            }
+            hi[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
+            lo[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
+          }
+          const half8 ah = __builtin_bit_cast(half8, hi), al = __builtin_bit_cast(half8, lo);
+          f32x4 a0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          a0 = mfma(ah, bh2[s][0], a0);
+          a0 = mfma(al, bh2[s][0], a0);
+          a0 = mfma(ah, bl2[s][0], a0);
+          acc2[u][s][0] = a0;
+          f32x4 a1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          if (two[s]) {
+            a1 = mfma(ah, bh2[s][1], a1);
+            a1 = mfma(al, bh2[s][1], a1);
+            a1 = mfma(ah, bl2[s][1], a1);
+          }
+          acc2[u][s][1] = a1;
+        }
       }
     }
 
@@ -499,7 +638,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       const int t = 16 * u + col;  // A-operand row (token) of this lane
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
+      for (int s = 0; s < (KF == 2 ? 0 : KS); ++s) {
         const int g = s < SG ? 0 : 1;
         if (KF == 1) {
           u32x4 hi, lo;
@@ -538,7 +677,26 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     // logits of this lane: head col, tokens c0 + 16u + 4gq + r
     float x[8];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < 2 && KF == 2; ++u) {
+      float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < KS2; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (h == 1 && !two[s]) continue;
+          const u32x2 w =
+              *reinterpret_cast<const u32x2 *>(sb + Sl::NOFF + 2 * ((glo[s] + h) * 32 + 16 * u + 4 * gq));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float sc = __half2float(__ushort_as_half((uint16_t)(w[r >> 1] >> (16 * (r & 1)))));
+            xs[r] = __builtin_fmaf(sc, acc2[u][s][h][r], xs[r]);
+          }
+        }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[4 * u + r] = xs[r] * kq;
+    }
+#pragma unroll
+    for (int u = 0; u < (KF == 2 ? 0 : 2); ++u) {
       u32x4 nr{0u, 0u, 0u, 0u};
       if (KF == 1) nr = *reinterpret_cast<const u32x4 *>(sb + Sl::NOFF + (16 * u + 4 * gq) * 4);
 #pragma unroll
@@ -755,6 +913,7 @@ hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t s
 int decode_fast_row_bytes(int dim, int nn) { return nn * 16 + (dim / 32 - nn) * 32; }
 
 int decode_fast_enc_capacity(int dim, int nn) {
+  if (nn < 0) return dim == 64 ? Slot<64, 2, 1>::ENC_DMAS * 1024 : Slot<128, 2, 1>::ENC_DMAS * 1024;
   if (dim == 64) {
     if (nn == 0) return Slot<64, 1, 0>::ENC_DMAS * 1024;
     if (nn == 1) return Slot<64, 1, 1>::ENC_DMAS * 1024;
@@ -773,8 +932,16 @@ bool decode_fast_supported(int dim, int key_format, int nn, int sg) {
          (nn == 0 && sg == h);
 }
 
+int decode_general_max_books(int dim) { return dim / 16; }
+
 hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
   const int D = p.dim;
+  if (nn < 0) {  // any packed layout: one or two scale DMAs per chunk
+    int ns = 0;
+    for (int h = 0; h < p.kv_heads; ++h) ns = fl.gns[h] > ns ? fl.gns[h] : ns;
+    if (D == 64) return ns <= 4 ? launch_one<64, 2, 1, 1>(p, fl, stream) : launch_one<64, 2, 2, 1>(p, fl, stream);
+    return ns <= 4 ? launch_one<128, 2, 1, 1>(p, fl, stream) : launch_one<128, 2, 2, 1>(p, fl, stream);
+  }
   if (p.key_format == 0) return D == 64 ? launch_one<64, 0, 0, 2>(p, fl, stream) : launch_one<128, 0, 0, 4>(p, fl, stream);
 #define BGTQ_FAST(DD, N, S) \
   if (D == DD && nn == N && sg == S) return launch_one<DD, 1, N, S>(p, fl, stream);

@@ -10,11 +10,12 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="f32", hkv=2, hq=14, seed=0):
+def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="f32", hkv=2, hq=14, seed=0,
+         layout="B"):
     import torch
     import bgtq
     from bgtq import batched, calibrate
-    print("append", dim, key_format, lengths, splits, k_dtype, v_dtype, flush=True)
+    print("append", dim, key_format, layout, lengths, splits, k_dtype, v_dtype, flush=True)
     B, cap = len(lengths), max(lengths)
     g = torch.Generator().manual_seed(seed)
     hist = torch.randn((B, hkv, cap, dim), generator=g).half().cuda()
@@ -26,10 +27,10 @@ def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="
     lens = torch.tensor(lengths, dtype=torch.int32, device="cuda")
     outs, caches, tabs = [], [], []
     if key_format == "packed":
-        p = calibrate.layout_b(dim)
+        p = calibrate.layout_b(dim) if layout == "B" else calibrate.layout_a(dim)
         tabs = [bgtq.Tables(device, p) for _ in range(hkv)]
         rb, ns = p.rowBytes, p.normStride
-        packed0 = torch.zeros((B, hkv, cap * rb + 64), dtype=torch.uint8, device="cuda")
+        packed0 = torch.zeros((B, hkv, (cap * rb + 64 + 15) // 16 * 16), dtype=torch.uint8, device="cuda")
         # scale rows padded to 16 bytes: the fused kernel loads four tokens' scales at once
         norms0 = torch.zeros((B, hkv, (cap * ns + 32 + 7) // 8 * 8), dtype=torch.int16, device="cuda")
         batched.encode(device, [dict(tables=tabs[h], src=hist[b, h], src_row_stride=dim, rows=lengths[b] - 1,
@@ -92,6 +93,13 @@ def test_append_smollm2_step_shape(device, dim):
     """Batch 1 at 4096 + 1 tokens: the library's own split choice (one 32-token chunk per wave, the
     new token alone in the last split) and the one-round merge."""
     _run(device, dim=dim, key_format="packed", lengths=[4097], hkv=3, hq=9)
+
+
+@pytest.mark.parametrize("lengths,splits", [([1, 32, 33, 97, 1000, 4096], 0), ([2000, 31, 4095], 3)])
+def test_append_layout_a(device, lengths, splits):
+    """Layout A at d=64 (groups straddling K-steps, norm stride 3) through the fused kernel's
+    per-position code lookup: decode_append accepts only fused layouts."""
+    _run(device, dim=64, key_format="packed", layout="A", lengths=lengths, splits=splits, hkv=3, hq=9)
 
 
 def test_append_fp16_sources(device):

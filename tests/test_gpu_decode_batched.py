@@ -29,7 +29,7 @@ def _check(out, ref, what):
 
 
 def _run(device, oracle, *, params, batch, hq, hkv, dim, lengths, cap, key_format="packed", splits=0, seed=0,
-         zero_q=False):
+         zero_q=False, pad16=False):
     import torch
     import bgtq
     from bgtq import batched
@@ -47,8 +47,11 @@ def _run(device, oracle, *, params, batch, hq, hkv, dim, lengths, cap, key_forma
     if key_format == "packed":
         tabs = [bgtq.Tables(device, p) for p in params]
         rb, ns = params[0].rowBytes, params[0].normStride
-        packed = torch.zeros((batch, hkv, cap * rb + 64), dtype=torch.uint8, device="cuda")
-        norms = torch.zeros((batch, hkv, cap * ns + 32), dtype=torch.int16, device="cuda")
+        pk_len, nm_len = cap * rb + 64, cap * ns + 32
+        if pad16:  # 16-byte aligned head and sequence strides
+            pk_len, nm_len = (pk_len + 15) // 16 * 16, (nm_len + 7) // 8 * 8
+        packed = torch.zeros((batch, hkv, pk_len), dtype=torch.uint8, device="cuda")
+        norms = torch.zeros((batch, hkv, nm_len), dtype=torch.int16, device="cuda")
         kd = k.cuda()
         jobs = [dict(tables=tabs[h], src=kd[b, h], src_row_stride=dim, rows=cap, packed=packed[b, h],
                      norms=norms[b, h]) for b in range(batch) for h in range(hkv)]
@@ -137,6 +140,18 @@ def test_non_fast_layouts_use_general_kernel(device, oracle):
     pa = calibrate.layout_a(64)
     print("layout A", flush=True)
     _run(device, oracle, params=[pa, pa], batch=1, hq=14, hkv=2, dim=64, lengths=[700], cap=700)
+
+
+@pytest.mark.parametrize("dim,splits", [(64, 0), (128, 0), (64, 5), (128, 3)])
+def test_layout_a_fused(device, oracle, dim, splits):
+    """Layout A (widths 4..8: K-steps spanning two groups; at d=128 nibble and byte codes in one
+    K-step and a norm stride of 5) with 16-byte aligned caches: the fused kernel's per-position
+    code lookup, ragged GQA batch."""
+    from bgtq import calibrate
+    p = calibrate.layout_a(dim)
+    print("layout A fused", dim, splits, flush=True)
+    _run(device, oracle, params=[p, p], batch=3, hq=14, hkv=2, dim=dim, lengths=[1, 77, 2049], cap=2049,
+         splits=splits, pad16=True)
 
 
 def test_full_context_closed_form(device, oracle):
