@@ -889,11 +889,11 @@ static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables,
 
 // Whether the fused kernel's per-position code lookup serves a packed layout
 // the structured check (fast_layout) refused: FP16 V; 16-byte aligned packed
-// and scale bases and strides; per KV head up to decode_general_max_books
-// books of up to 256 centroids, norm stride up to 8, row bytes a multiple of
-// 4, nibble positions a multiple of 8 (a lane's 8 codes are all nibbles or
-// all bytes), groups in ascending position order with at most two in any 32
-// positions. Fills the per-head fields of fl.
+// and scale bases and strides; per KV head up to 8 books of up to 256
+// centroids whose code tables fit the kernel's LDS, each book's positions
+// all nibble or all byte codes, norm stride up to 8, groups in ascending
+// position order with at most four in any 32 positions. Fills the per-head
+// fields of fl.
 static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tables, FastLayout *fl) {
   auto a16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   if (p.key_format != 1 || p.v_dtype != BGTQ_DTYPE_F16 || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
@@ -902,14 +902,17 @@ static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tabl
   if (!a16(p.norms) || (p.norms_seq_stride * 2) % 16 || (p.norms_head_stride * 2) % 16) return false;
   for (int h = 0; h < p.kv_heads; ++h) {
     const DevTables *T = tables[h]->h();
-    if (T->n_books > decode_general_max_books(p.dim) || T->max_centroids > 256 ||
-        T->norm_stride > kDecodeGeneralMaxNormStride || T->row_bytes > p.dim || T->row_bytes % 4 ||
-        T->nibble_dims % 8 || T->groups > 8)
+    const int bstride = std::max(256, (T->max_centroids * 4 + 255) / 256 * 256);
+    if (T->n_books > 8 || T->max_centroids > 256 || T->n_books * (bstride + 32) > decode_general_table_bytes(p.dim) ||
+        T->norm_stride > kDecodeGeneralMaxNormStride || T->row_bytes > p.dim || T->groups > 8)
       return false;
     for (int j = 1; j < p.dim; ++j)
       if (T->group_of[j] < T->group_of[j - 1] || T->group_of[j] > T->group_of[j - 1] + 1) return false;
     for (int s = 0; s < p.dim / 32; ++s)
-      if (T->group_of[32 * s + 31] > T->group_of[32 * s] + 1) return false;
+      if (T->group_of[32 * s + 31] >= T->group_of[32 * s] + kDecodeGeneralMaxGroupsPerStep) return false;
+    uint32_t nib_books = 0, byte_books = 0;
+    for (int j = 0; j < p.dim; ++j) (j < T->nibble_dims ? nib_books : byte_books) |= 1u << T->pos_book[j];
+    if (nib_books & byte_books) return false;
     if (p.k_new && (int64_t)T->off_rot > decode_fast_enc_capacity(p.dim, -1)) return false;
     const uint8_t *base = reinterpret_cast<const uint8_t *>(tables[h]->dev());
     fl->rot_q[h] = base + T->off_rot_q;
@@ -921,6 +924,9 @@ static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tabl
     fl->grb[h] = (int16_t)T->row_bytes;
     fl->gns[h] = (int16_t)T->norm_stride;
     fl->gnb[h] = (int16_t)T->n_books;
+    fl->gbstride[h] = (int16_t)bstride;
+    fl->gbnib[h] = (uint8_t)nib_books;
+    fl->galign[h] = T->row_bytes % 4 == 0 && T->nibble_dims % 8 == 0;
   }
   return true;
 }

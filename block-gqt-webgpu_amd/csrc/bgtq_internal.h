@@ -202,9 +202,13 @@ struct FastLayout {
   const float *rot_t[kMaxKvHeads];
   int32_t enc_bytes[kMaxKvHeads];
   // Packed layouts of any structure (the kernel's per-position code
-  // lookup): position descriptors, row bytes, norm stride, book count.
+  // lookup): position descriptors, row bytes, norm stride, book count, bytes
+  // of each book's code table in LDS (whole 256-byte pieces), books of
+  // nibble codes (bit mask), and whether every lane's row bytes start on a
+  // word (row bytes a multiple of 4 and nibble positions a multiple of 8).
   const uint32_t *gdesc[kMaxKvHeads];
-  int16_t grb[kMaxKvHeads], gns[kMaxKvHeads], gnb[kMaxKvHeads];
+  int16_t grb[kMaxKvHeads], gns[kMaxKvHeads], gnb[kMaxKvHeads], gbstride[kMaxKvHeads];
+  uint8_t gbnib[kMaxKvHeads], galign[kMaxKvHeads];
 };
 
 // Sets the calling thread's bgtq_last_error() message; returns code.
@@ -239,10 +243,12 @@ hipError_t launch_decode_probs(const DecodeParams &p, hipStream_t stream);
 // Fused decode (decode_fast.hip): nn leading nibble K-steps, sg K-steps in group 0;
 // nn = -1: a packed layout of any structure (per-position code lookup).
 bool decode_fast_supported(int dim, int key_format, int nn, int sg);
-// Books (of up to 256 centroids) and the norm stride the per-position path
-// holds in LDS for head dim `dim`.
-int decode_general_max_books(int dim);
+// LDS bytes the per-position path holds for the books' code tables
+// (n_books * (table bytes + 32) must fit) at head dim `dim`, and its largest
+// norm stride and groups per 32 positions.
+int decode_general_table_bytes(int dim);
 constexpr int kDecodeGeneralMaxNormStride = 8;
+constexpr int kDecodeGeneralMaxGroupsPerStep = 4;
 // LDS bytes the fused kernel gives the append's copy of a table set's
 // header, code LUT and books.
 int decode_fast_enc_capacity(int dim, int nn);

@@ -321,13 +321,20 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       if (s < NN) dma16(rt, tabs + s * 2048 + 1024, 1024 + lane * 16, 0);
     }
   }
-  if (KF == 2 && wave == 0) {  // the code table ([code]: hi | lo << 16) of every book
-    const int nb = fl.gnb[kv];
+  if (KF == 2 && wave == 0) {
+    // The code table ([code]: hi | lo << 16) of every book: the first
+    // gbstride bytes (max_centroids entries, whole 256-byte pieces) at
+    // book * (gbstride + 32) + field width.
+    const int nb = fl.gnb[kv], pieces = fl.gbstride[kv] / 256, span = fl.gbstride[kv] + 32;
+    const uint32_t nibble_books = (uint32_t)fl.gbnib[kv];
 #pragma unroll
-    for (int bk = 0; bk < 2 * KS; ++bk) {
-      if (bk < nb) {
-        const __amdgpu_buffer_rsrc_t rt = rsrc(fl.mfma[kv] + bk * kMfmaTableBytes + 2048, 1024);
-        dma16(rt, tabs + bk * 1024, lane * 16, 0);
+    for (int bk = 0; bk < 8; ++bk) {
+#pragma unroll
+      for (int pc = 0; pc < 4; ++pc) {
+        if (bk < nb && pc < pieces) {
+          const __amdgpu_buffer_rsrc_t rt = rsrc(fl.mfma[kv] + bk * kMfmaTableBytes + 2048 + pc * 256, 256);
+          dma4(rt, tabs + bk * span + ((nibble_books >> bk) & 1u ? 4 : 8) + pc * 256, lane * 4, 0);
+        }
       }
     }
   }
@@ -447,36 +454,48 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   }
   if (KF >= 1) lds_barrier();  // q staging (last ring slot) is dead
 
-  // KF 2: every K-step spans one group or two adjacent ones (glo[s], glo[s] + 1).
-  // The query's B operand is split by group (hi/lo pairs bh2/bl2[s][slot], the
-  // other group's positions zero), each slot accumulates on its own and the
-  // token's scale of that group weights it. Per lane and K-step: the row
-  // offset of its 8 codes (4 bytes of nibbles, or 8 bytes), the codes'
-  // shifts and width, and each code's table offset (book * 1 KB).
-  int glo[KS2], two[KS2], koff[KS2], kw[KS2];
-  uint32_t tbo[KS2][8];
-  half8 bh2[KS2][2], bl2[KS2][2];
+  // KF 2: a K-step spans up to kSlots adjacent groups glo[s] .. glo[s] +
+  // nsl[s] - 1. Each group's part of the K-step runs its own MFMAs against
+  // the query with the other groups' positions masked to zero (gmask), and
+  // the token's scale of that group weights the result. A lane's 8 codes of
+  // a K-step are nibbles, then bytes (the head-perm order puts every nibble
+  // position first): they lie in the 8 row bytes from koff, read as two
+  // words; codes 0..3 come from the first word, codes 4..7 from the word
+  // starting at byte hib[s]. ext[s][k]: the code's bit offset in its word;
+  // tbo[s][k]: its book's LDS table offset plus the field width (4 or 8),
+  // whose low 5 bits are the width operand of the bit-field extract.
+  constexpr int kSlots = 4;
+  int glo[KS2], nsl[KS2], koff[KS2], hib[KS2];
+  uint32_t ext[KS2][8], tbo[KS2][8];
+  u32x4 gmask[KS2][kSlots];
   constexpr int NSV = KF == 2 ? 2 * Sl::NSC : 1;  // scale entries a lane moves
   int sc_src[NSV], sc_dst[NSV];
+  const bool rows_aligned = KF == 2 && fl.galign[kv] != 0;  // every lane's 8 bytes start on a word
   if (KF == 2) {
+    const int bspan = fl.gbstride[kv] + 32;  // LDS bytes per book table
 #pragma unroll
     for (int s = 0; s < KS2; ++s) {
       const uint32_t first = __builtin_amdgcn_readfirstlane(gdl[s][0][0]);
       const uint32_t last = __builtin_amdgcn_readfirstlane(__shfl(gdl[s][1][3], 48, 64));
       glo[s] = (int)((first >> 16) & 15u);
-      two[s] = ((last >> 16) & 15u) != (first >> 16 & 15u);
+      nsl[s] = (int)((last >> 16) & 15u) - glo[s] + 1;
       koff[s] = (int)(gdl[s][0][0] & 255u);
-      kw[s] = (gdl[s][0][0] >> 11) & 1u ? 4 : 8;
+      int bo[8], grp[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t dsc = gdl[s][k >> 2][k & 3];
-        tbo[s][k] = ((dsc >> 12) & 15u) * 1024u;
-        const bool lo_grp = (int)((dsc >> 16) & 15u) == glo[s];
-        bh2[s][0][k] = lo_grp ? qhi[s][k] : (_Float16)0.0f;
-        bl2[s][0][k] = lo_grp ? qlo[s][k] : (_Float16)0.0f;
-        bh2[s][1][k] = lo_grp ? (_Float16)0.0f : qhi[s][k];
-        bl2[s][1][k] = lo_grp ? (_Float16)0.0f : qlo[s][k];
+        bo[k] = 8 * ((int)(dsc & 255u) - koff[s]) + (int)((dsc >> 8) & 7u);
+        tbo[s][k] = ((dsc >> 12) & 15u) * (uint32_t)bspan + ((dsc >> 11) & 1u ? 4u : 8u);
+        grp[k] = (int)((dsc >> 16) & 15u) - glo[s];
       }
+      hib[s] = bo[4] >> 3;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ext[s][k] = (uint32_t)(k < 4 ? bo[k] : bo[k] - 8 * hib[s]);
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i)
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2)
+          gmask[s][i][k2] = (grp[2 * k2] == i ? 0x0000ffffu : 0u) | (grp[2 * k2 + 1] == i ? 0xffff0000u : 0u);
     }
     // The chunk's scale rows [token][ns] become [group][32 tokens] in place
     // (lane moves entries lane + 64 k), so a lane's four tokens of one group
@@ -589,17 +608,32 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       for (int k = 0; k < NSV; ++k)
         if (sc_src[k] >= 0) *reinterpret_cast<uint16_t *>(ns_area + sc_dst[k]) = (uint16_t)sv[k];
     }
-    // KF 2: acc2[u][s][slot], the K-step's codes against the slot's query part.
-    f32x4 acc2[KF == 2 ? 2 : 1][KS2][2];
+    // KF 2: logits x2[u][r] = sum over K-steps s and their groups of the
+    // token's group scale times that group's part of the K-step.
+    float x2[2][4];
     if (KF == 2) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const uint8_t *row = kbuf + (16 * u + col) * rb;
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int s = 0; s < KS2; ++s) {
-          const uint32_t w0 = *reinterpret_cast<const uint32_t *>(row + koff[s]);
-          uint32_t w1 = *reinterpret_cast<const uint32_t *>(row + koff[s] + 4);
-          w1 = kw[s] == 4 ? w0 >> 16 : w1;  // nibbles 4..7 of the lane's 8
+        for (int r = 0; r < 4; ++r) x2[u][r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS2; ++s) {
+        half8 ah[2], al[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int rofs = (16 * u + col) * rb + koff[s];
+          uint32_t w0, w1;
+          if (rows_aligned) {
+            w0 = *reinterpret_cast<const uint32_t *>(kbuf + rofs);
+            w1 = *reinterpret_cast<const uint32_t *>(kbuf + rofs + 4);
+          } else {  // kbuf is 256-byte aligned: the row offset's low bits are the address's
+            const int sh = rofs & 3;
+            const uint32_t *wp = reinterpret_cast<const uint32_t *>(kbuf + (rofs - sh));
+            const uint32_t d0 = wp[0], d1 = wp[1], d2 = wp[2];
+            w0 = __builtin_amdgcn_alignbyte(d1, d0, (uint32_t)sh);
+            w1 = __builtin_amdgcn_alignbyte(d2, d1, (uint32_t)sh);
+          }
+          const uint32_t wh = hib[s] == 4 ? w1 : __builtin_amdgcn_alignbyte(w1, w0, (uint32_t)hib[s]);
           u32x4 hi, lo;
 #pragma unroll
           for (int k2 = 0; k2 < 4; ++k2) {
@@ -607,25 +641,36 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
               const int k = 2 * k2 + h;
-              const uint32_t code = __builtin_amdgcn_ubfe(k < 4 ? w0 : w1, (uint32_t)((k & 3) * kw[s]), (uint32_t)kw[s]);
+              const uint32_t code = __builtin_amdgcn_ubfe(k < 4 ? w0 : wh, ext[s][k], tbo[s][k]);
               e[h] = *reinterpret_cast<const uint32_t *>(tabs + tbo[s][k] + 4 * code);
             }
             hi[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
             lo[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
           }
-          const half8 ah = __builtin_bit_cast(half8, hi), al = __builtin_bit_cast(half8, lo);
-          f32x4 a0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-          a0 = mfma(ah, bh2[s][0], a0);
-          a0 = mfma(al, bh2[s][0], a0);
-          a0 = mfma(ah, bl2[s][0], a0);
-          acc2[u][s][0] = a0;
-          f32x4 a1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-          if (two[s]) {
-            a1 = mfma(ah, bh2[s][1], a1);
-            a1 = mfma(al, bh2[s][1], a1);
-            a1 = mfma(ah, bl2[s][1], a1);
+          ah[u] = __builtin_bit_cast(half8, hi);
+          al[u] = __builtin_bit_cast(half8, lo);
+        }
+#pragma unroll
+        for (int i = 0; i < kSlots; ++i) {
+          if (i >= nsl[s]) continue;
+          half8 bh = qhi[s], bl = qlo[s];
+          if (nsl[s] > 1) {
+            bh = __builtin_bit_cast(half8, __builtin_bit_cast(u32x4, bh) & gmask[s][i]);
+            bl = __builtin_bit_cast(half8, __builtin_bit_cast(u32x4, bl) & gmask[s][i]);
           }
-          acc2[u][s][1] = a1;
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            f32x4 a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            a = mfma(ah[u], bh, a);
+            a = mfma(al[u], bh, a);
+            a = mfma(ah[u], bl, a);
+            const u32x2 w = *reinterpret_cast<const u32x2 *>(sb + Sl::NOFF + 2 * ((glo[s] + i) * 32 + 16 * u + 4 * gq));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float sc = __half2float(__ushort_as_half((uint16_t)(w[r >> 1] >> (16 * (r & 1)))));
+              x2[u][r] = __builtin_fmaf(sc, a[r], x2[u][r]);
+            }
+          }
         }
       }
     }
@@ -678,22 +723,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     float x[8];
 #pragma unroll
     for (int u = 0; u < 2 && KF == 2; ++u) {
-      float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int s = 0; s < KS2; ++s)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          if (h == 1 && !two[s]) continue;
-          const u32x2 w =
-              *reinterpret_cast<const u32x2 *>(sb + Sl::NOFF + 2 * ((glo[s] + h) * 32 + 16 * u + 4 * gq));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float sc = __half2float(__ushort_as_half((uint16_t)(w[r >> 1] >> (16 * (r & 1)))));
-            xs[r] = __builtin_fmaf(sc, acc2[u][s][h][r], xs[r]);
-          }
-        }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[4 * u + r] = xs[r] * kq;
+      for (int r = 0; r < 4; ++r) x[4 * u + r] = x2[u][r] * kq;
     }
 #pragma unroll
     for (int u = 0; u < (KF == 2 ? 0 : 2); ++u) {
@@ -932,7 +963,7 @@ bool decode_fast_supported(int dim, int key_format, int nn, int sg) {
          (nn == 0 && sg == h);
 }
 
-int decode_general_max_books(int dim) { return dim / 16; }
+int decode_general_table_bytes(int dim) { return dim == 64 ? Slot<64, 2, 1>::TABLES : Slot<128, 2, 1>::TABLES; }
 
 hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
   const int D = p.dim;

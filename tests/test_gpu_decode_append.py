@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="f32", hkv=2, hq=14, seed=0,
-         layout="B"):
+         layout="B", params=None):
     import torch
     import bgtq
     from bgtq import batched, calibrate
@@ -28,7 +28,9 @@ def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="
     outs, caches, tabs = [], [], []
     if key_format == "packed":
         p = calibrate.layout_b(dim) if layout == "B" else calibrate.layout_a(dim)
-        tabs = [bgtq.Tables(device, p) for _ in range(hkv)]
+        if params is not None:  # one parameter set per KV head, common row and norm strides
+            p = params[0]
+        tabs = [bgtq.Tables(device, params[h] if params is not None else p) for h in range(hkv)]
         rb, ns = p.rowBytes, p.normStride
         packed0 = torch.zeros((B, hkv, (cap * rb + 64 + 15) // 16 * 16), dtype=torch.uint8, device="cuda")
         # scale rows padded to 16 bytes: the fused kernel loads four tokens' scales at once
@@ -102,6 +104,20 @@ def test_append_layout_a(device, lengths, splits):
     _run(device, dim=64, key_format="packed", layout="A", lengths=lengths, splits=splits, hkv=3, hq=9)
 
 
+def test_append_smollm2_heads(device, oracle):
+    """Real SmolLM2 calibration heads (odd 37-byte rows, mixed nibble/byte lanes, K-steps spanning
+    three groups) with 16-byte aligned caches through the fused kernel's per-position lookup."""
+    from bgtq import BlockGTQParameters
+    from conftest import REF
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    heads = [BlockGTQParameters.from_serialized(a[f"{n}_config"], a[f"{n}_table"]) for n in ("h0", "h1", "h22")]
+    rb, ns = max(h.rowBytes for h in heads), max(h.normStride for h in heads)
+    for h in heads:
+        h.rowBytes, h.normStride = rb, ns
+    _run(device, dim=64, key_format="packed", layout="smollm2", lengths=[1, 33, 97, 4096], hkv=3, hq=9,
+         params=heads)
+
+
 def test_append_fp16_sources(device):
     _run(device, dim=64, key_format="packed", lengths=[513, 130], k_dtype="f16", v_dtype="f16")
 
@@ -112,8 +128,9 @@ def test_append_fp16_keys(device, dim):
 
 
 def test_append_unsupported_layout_is_rejected(device, oracle):
-    """A layout outside the fused kernel (a real SmolLM2 head: K-steps mixing groups) is refused and
-    nothing is written; the two-call path serves it."""
+    """Caches outside the fused kernel (a real SmolLM2 head's rows, 35 bytes, at a head stride of
+    T * 35 + 64 bytes: not 16-byte aligned) are refused and nothing is written; the two-call path
+    serves them."""
     import torch
     import bgtq
     from bgtq import batched

@@ -154,6 +154,31 @@ def test_layout_a_fused(device, oracle, dim, splits):
          splits=splits, pad16=True)
 
 
+def _smollm2_heads(oracle, names):
+    """Reference calibration heads of one layer: one cache row stride and norm stride for all
+    (src/model/decoder.ts:21 keeps one per head)."""
+    from bgtq import BlockGTQParameters
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    heads = [BlockGTQParameters.from_serialized(a[f"{n}_config"], a[f"{n}_table"]) for n in names]
+    rb = max(h.rowBytes for h in heads)
+    ns = max(h.normStride for h in heads)
+    for h in heads:
+        h.rowBytes, h.normStride = rb, ns
+    return heads
+
+
+@pytest.mark.parametrize("names,splits", [(("h3", "h56", "h26"), 0), (("h0", "h1", "h22"), 0),
+                                          (("h0", "h1", "h22"), 4)])
+def test_smollm2_heads_fused(device, oracle, names, splits):
+    """Real SmolLM2 calibration heads (K-steps spanning up to four groups, nibble and byte codes in
+    one lane's eight positions, 3-6 books, rows of 44 or of an odd 37 bytes, norm strides 4 and 6)
+    with 16-byte aligned caches: the fused kernel's per-position code lookup."""
+    heads = _smollm2_heads(oracle, names)
+    print("smollm2 heads fused", names, splits, flush=True)
+    _run(device, oracle, params=heads, batch=2, hq=9, hkv=3, dim=64, lengths=[1000, 77], cap=1000, splits=splits,
+         pad16=True)
+
+
 def test_full_context_closed_form(device, oracle):
     """32768-token context: zero q gives the mean of V exactly enough (uniform softmax)."""
     from bgtq import calibrate
