@@ -16,7 +16,11 @@ FP16-K kernel at the headline shape, and the Qwen2.5-0.5B 4096-token prompt
 prefill (24 layers x encode + causal attention on the matrix cores, as one
 chunk and in chunks of 32 rows).
 
-    python bench.py [--steps K] [--warmup W] [--layout B|A] [--no-cpu] [--no-extra] [--prefill-only]
+    python bench.py [--steps K] [--warmup W] [--layout B|A|S] [--no-cpu] [--no-extra] [--prefill-only]
+
+--layout A: widths 4..8 at a 6.0 average (groups straddling the 32-dim
+K-steps); --layout S: the reference's SmolLM2 calibration heads (first two KV
+heads of each layer, rows of 34-44 bytes, 3-6 groups), for the decode step.
 
 Prints one JSON line (value = algorithmic HBM GB/s of the decode step).
 """
@@ -46,7 +50,26 @@ def log(*a):
 
 def layout_params(name, dim):
     from bgtq import calibrate
+    if name == "S":
+        return smollm2_heads(0, 1)[0]
     return calibrate.layout_b(dim) if name == "B" else calibrate.layout_a(dim)
+
+
+_SMOLLM2 = []
+
+
+def smollm2_heads(layer, kv_heads):
+    """Layout S: the reference's SmolLM2 calibration (30 layers x 3 KV heads, d=64), the first
+    kv_heads heads of layer `layer` mod 30, with one row and norm stride for the layer's heads."""
+    from bgtq import BlockGTQParameters, calibration
+    if not _SMOLLM2:
+        _SMOLLM2.extend(calibration.read(ROOT / "tests" / "golden" / "reference" / "model")[2])
+    blobs = [_SMOLLM2[(layer % 30) * 3 + h] for h in range(kv_heads)]
+    heads = [BlockGTQParameters.from_serialized(b.config, b.table) for b in blobs]
+    rb, ns = max(h.rowBytes for h in heads), max(h.normStride for h in heads)
+    for h in heads:
+        h.rowBytes, h.normStride = rb, ns
+    return heads
 
 
 class DecodeWorkload:
@@ -65,6 +88,7 @@ class DecodeWorkload:
         p = layout_params(layout, dim) if key_format == "packed" else None
         self.row_bytes = p.rowBytes if p else 2 * dim
         self.norm_stride = p.normStride if p else 0
+        per_token = []  # K row, scales and V row bytes of each layer
         self.lengths = torch.full((batch,), ctx, dtype=torch.int32, device="cuda")
         self.out = torch.empty((batch, hq, dim), dtype=torch.float32, device="cuda")
         ws = None
@@ -73,10 +97,14 @@ class DecodeWorkload:
             v = torch.randn((batch, hkv, ctx, dim), generator=g, device="cuda", dtype=torch.float32).half()
             k = torch.randn((batch, hkv, ctx, dim), generator=g, device="cuda", dtype=torch.float32).half()
             if key_format == "packed":
-                tabs = [bgtq.Tables(dev, p) for _ in range(hkv)]  # one table set per (layer, KV head)
+                hp = smollm2_heads(layer, hkv) if layout == "S" else [p] * hkv
+                tabs = [bgtq.Tables(dev, x) for x in hp]  # one table set per (layer, KV head)
                 self.tables += tabs
-                packed = torch.empty((batch, hkv, ctx * p.rowBytes + 64), dtype=torch.uint8, device="cuda")
-                norms = torch.empty((batch, hkv, ctx * p.normStride + 32), dtype=torch.int16, device="cuda")
+                rb, ns = hp[0].rowBytes, hp[0].normStride
+                per_token.append(rb + 2 * ns + 2 * dim)
+                # head strides rounded to 16 bytes (the fused kernel's loads)
+                packed = torch.empty((batch, hkv, (ctx * rb + 64 + 15) // 16 * 16), dtype=torch.uint8, device="cuda")
+                norms = torch.empty((batch, hkv, (ctx * ns + 32 + 7) // 8 * 8), dtype=torch.int16, device="cuda")
                 jobs = [dict(tables=tabs[h], src=k[b, h], src_row_stride=dim, rows=ctx, packed=packed[b, h],
                              norms=norms[b, h], dst_row0=0) for b in range(batch) for h in range(hkv)]
                 batched.encode(dev, jobs, "f16")
@@ -86,6 +114,7 @@ class DecodeWorkload:
                           norms_head_stride=norms.stride(1))
                 self.keep += [packed, norms, v, q]
             else:
+                per_token.append(4 * dim)
                 kw = dict(k_f16=k, k_seq_stride=k.stride(0), k_head_stride=k.stride(1))
                 self.keep += [k, v, q]
             args = dict(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=q, out=self.out, lengths=self.lengths,
@@ -96,11 +125,12 @@ class DecodeWorkload:
                                  device="cuda")
             self.descs.append(batched.decode_desc(workspace=ws, **args))
         self.ws = ws
+        self.per_token = per_token
         torch.cuda.synchronize()
 
     def bytes_per_layer(self):
-        per_token = self.row_bytes + 2 * self.norm_stride + 2 * self.dim
-        return self.batch * self.hkv * self.ctx * per_token
+        """Algorithmic bytes of one layer (the mean over layers where row strides differ)."""
+        return self.batch * self.hkv * self.ctx * sum(self.per_token) / len(self.per_token)
 
     def set_splits(self, splits):
         from bgtq import batched
@@ -410,7 +440,7 @@ def main():
     # take that long to reach their sustained state; with 3 the timed steps
     # run about 5% slower.
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--layout", default="B", choices=["A", "B"])
+    ap.add_argument("--layout", default="B", choices=["A", "B", "S"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the side measurements")
     ap.add_argument("--eager", action="store_true", help="issue the per-layer launches directly, no HIP graph")
