@@ -1160,9 +1160,18 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   dp.v_head_stride = d->v_head_stride;
   FastLayout fl{};
   int nn = 0, sg = 0;
-  if (!fast_layout(dp, d->tables, &fl, &nn, &sg))
-    return fail(BGTQ_ERR_UNSUPPORTED, "prefill needs 16-byte aligned FP16 V/K/scales and a layout whose 32-dim "
-                                      "K-steps each lie in one group and book (at most two groups)");
+  bool fused = fast_layout(dp, d->tables, &fl, &nn, &sg);
+  if (!fused && general_layout(dp, d->tables, &fl)) {  // any packed layout: per-position K build
+    fused = true;
+    nn = -1;
+    for (int h = 0; h < d->kv_heads; ++h) {
+      const DevTables *T = d->tables[h]->h();
+      if (T->n_books * T->max_centroids * 4 > prefill_general_book_bytes(d->dim)) fused = false;
+    }
+  }
+  if (!fused)
+    return fail(BGTQ_ERR_UNSUPPORTED, "prefill needs 16-byte aligned FP16 V/K/scales and a packed layout the "
+                                      "fused kernels hold (books, groups per 32 dims and norm stride within their limits)");
   if (reinterpret_cast<uintptr_t>(d->q) & 15) return fail(BGTQ_ERR_RANGE, "q must be 16-byte aligned");
   if (bgtq_status s = ctx->use()) return s;
   PrefillParams p{};

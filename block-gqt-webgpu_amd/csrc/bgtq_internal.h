@@ -247,6 +247,9 @@ bool decode_fast_supported(int dim, int key_format, int nn, int sg);
 // (n_books * (table bytes + 32) must fit) at head dim `dim`, and its largest
 // norm stride and groups per 32 positions.
 int decode_general_table_bytes(int dim);
+// LDS bytes of centroid books (n_books * max_centroids floats) the prefill
+// kernel's per-position build holds at head dim `dim`.
+int prefill_general_book_bytes(int dim);
 constexpr int kDecodeGeneralMaxNormStride = 8;
 constexpr int kDecodeGeneralMaxGroupsPerStep = 4;
 // LDS bytes the fused kernel gives the append's copy of a table set's

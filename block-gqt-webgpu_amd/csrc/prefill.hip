@@ -58,23 +58,24 @@ constexpr int64_t kMergeOneRoundQueries = 2048;
 // One ring buffer: V block, K block, FP16 scales; every wave DMAs a quarter.
 // Packed-code kernels also hold the K-steps' centroid books (fp32) and two
 // buffers of built K operands. The ring is as deep as lets two workgroups
-// share a compute unit.
+// share a compute unit. KF 2 (any packed layout): K rows of up to D bytes,
+// up to 8 scales per token, every book (n_books x max_centroids floats).
 template <int D, int KF, int NN>
 struct PSlot {
   static constexpr int KS = D / 32, DT = D / 16, PR = D / 8;
   static constexpr int VBYTES = kChunk * D * 2;
   static constexpr int VI = VBYTES / 1024;  // 16-byte DMA instructions per V block
   static constexpr int VW = VI / kWaves;    // ... per wave
-  static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : 2 * D;  // K row bytes
+  static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : KF == 2 ? D : 2 * D;  // K row bytes
   static constexpr int KBYTES = kChunk * RB;
   static constexpr int KQ = KBYTES / kWaves;  // K bytes per wave
-  static constexpr int KW = KF == 1 ? (KQ + 1023) / 1024 : VW;
-  static constexpr int KLAST = KF == 1 ? (KQ - (KW - 1) * 1024) / 16 : 64;  // lanes of the last K instruction
-  static constexpr int NBYTES = KF == 1 ? kChunk * 4 : 0;
+  static constexpr int KW = KF >= 1 ? (KQ + 1023) / 1024 : VW;
+  static constexpr int KLAST = KF >= 1 ? (KQ - (KW - 1) * 1024) / 16 : 64;  // lanes of the last K instruction
+  static constexpr int NBYTES = KF == 1 ? kChunk * 4 : KF == 2 ? kChunk * 16 : 0;
   static constexpr int BYTES = VBYTES + KBYTES + NBYTES;
-  static constexpr int LW = VW + KW + (KF == 1 ? 1 : 0);  // DMA instructions per wave per block
-  static constexpr int BOOKS = KF == 1 ? KS * 1024 : 0;    // 256 fp32 centroids per K-step
-  static constexpr int KOP = KF == 1 ? 2 * 2 * KS * 2048 : 0;  // [buffer][u][s]: hi 1 KB, lo 1 KB
+  static constexpr int LW = VW + KW + (KF >= 1 ? 1 : 0);  // DMA instructions per wave per block
+  static constexpr int BOOKS = KF >= 1 ? KS * 1024 * KF : 0;  // KF 1: 256 fp32 centroids per K-step
+  static constexpr int KOP = KF >= 1 ? 2 * 2 * KS * 2048 : 0;  // [buffer][u][s]: hi 1 KB, lo 1 KB
   static constexpr int FIXED = BOOKS + KOP;
   static constexpr int RING = 6 * BYTES + FIXED <= kLdsLimit / 2 ? 6 : 4 * BYTES + FIXED <= kLdsLimit / 2 ? 4 : 3;
   static constexpr int AHEAD = RING - 2;
@@ -114,8 +115,8 @@ __device__ __forceinline__ int64_t query_row(int b, int rows, int Hq, int kv, in
   return ((int64_t)b * rows + row) * Hq + kv * G + h;
 }
 
-// KF: 1 = packed codes, 0 = FP16 K rows. NN: leading nibble K-steps. SG:
-// K-steps in group 0. NCB: 16-query column blocks per wave. At least two
+// KF: 1 = packed codes of a structured layout, 2 = packed codes of any
+// layout, 0 = FP16 K rows. NN: leading nibble K-steps. SG: K-steps in group 0. NCB: 16-query column blocks per wave. At least two
 // waves per SIMD (at most 256 registers each), so that one wave's softmax
 // overlaps another's matrix-core work; up to four for single-block tiles.
 //
@@ -162,17 +163,20 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   const int part = ((e_tile + n_act - 1) / n_act + kChunk - 1) / kChunk * kChunk;
   const int t_lo = split * part, t_hi = min(t_lo + part, e_tile);
   const int n_blocks = (t_hi - t_lo + kChunk - 1) / kChunk;
-  const DevTables *T = KF == 1 ? p.tables[kv] : nullptr;
+  const DevTables *T = KF >= 1 ? p.tables[kv] : nullptr;
+  // Row bytes and scales per token (runtime for KF 2).
+  const int rb = KF == 2 ? T->row_bytes : RB;
+  const int ns = KF == 2 ? T->norm_stride : 2;
   float *books = reinterpret_cast<float *>(smem + Sl::RING * Sl::BYTES);
   uint8_t *kop = smem + Sl::RING * Sl::BYTES + Sl::BOOKS;
   auto slot = [&](int i) { return smem + (i % Sl::RING) * Sl::BYTES; };
 
   // ---------------- streams of this unit ----------------
   const _Float16 *v_base = static_cast<const _Float16 *>(p.v) + b * p.v_seq_stride + kv * p.v_head_stride;
-  const uint8_t *k_base = KF == 1 ? p.packed + b * p.packed_seq_stride + kv * p.packed_head_stride
+  const uint8_t *k_base = KF >= 1 ? p.packed + b * p.packed_seq_stride + kv * p.packed_head_stride
                                   : reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(p.k) +
                                                                       b * p.k_seq_stride + kv * p.k_head_stride);
-  const uint16_t *n_base = KF == 1 ? p.norms + b * p.norms_seq_stride + kv * p.norms_head_stride : nullptr;
+  const uint16_t *n_base = KF >= 1 ? p.norms + b * p.norms_seq_stride + kv * p.norms_head_stride : nullptr;
   // Swizzled FP16 row pieces of this wave's V (and FP16 K) instructions:
   // instruction k, lane i fills LDS piece 64k + i = (row r, slot c) with
   // global piece c ^ swz(r).
@@ -201,6 +205,19 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         if (kk + 1 < Sl::KW || Sl::KLAST == 64 || lane < Sl::KLAST) dma16(rK, kb + off, off + lane * 16, 0);
       }
       if (lane < kChunk / kWaves) dma4(rN, kb + Sl::KBYTES + wave * 32, wave * 32 + lane * 4, 0);
+    } else if (KF == 2) {
+      // Ranges end on the access size: the range check zeroes a whole access
+      // reaching past the range; the bytes past the last row lie in the same
+      // aligned 16 bytes as its end (16-byte aligned bases, c0 a multiple of 32).
+      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * rb, (rest * rb + 15u) & ~15u);
+      const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * ns, (rest * ns * 2 + 3u) & ~3u);
+#pragma unroll
+      for (int kk = 0; kk < Sl::KW; ++kk) {
+        const int off = wave * Sl::KQ + kk * 1024;
+        if (kk + 1 < Sl::KW || Sl::KLAST == 64 || lane < Sl::KLAST) dma16(rK, kb + off, off + lane * 16, 0);
+      }
+      if (lane < Sl::NBYTES / kWaves / 4)
+        dma4(rN, kb + Sl::KBYTES + wave * (Sl::NBYTES / kWaves), wave * (Sl::NBYTES / kWaves) + lane * 4, 0);
     } else {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
 #pragma unroll
@@ -216,7 +233,27 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   // this wave's queries rotated, scaled by log2(e) / sqrt(d) and split into QK
   // operands. B operand of QK step s for column block cb: lane holds query
   // col's dims 32 s + 4 gq + 0..3 and 32 s + 16 + 4 gq + 0..3.
-  const int ec = KF == 1 ? T->cent_exp : 0;
+  const int ec = KF >= 1 ? T->cent_exp : 0;
+  if (KF == 2 && wave == 0) {  // every book's centroids, [n_books][max_centroids] floats
+    const uint32_t nbytes = (uint32_t)(T->n_books * T->max_centroids * 4);
+    const __amdgpu_buffer_rsrc_t rb_ = rsrc(tables_books(T), nbytes);
+#pragma unroll
+    for (int k = 0; k < Sl::BOOKS / 256; ++k)
+      if ((uint32_t)k * 256 < nbytes) dma4(rb_, reinterpret_cast<uint8_t *>(books) + 256 * k, 256 * k + lane * 4, 0);
+  }
+  // KF 2: descriptors of the build's positions 32 s + 4 gq + 0..3 and
+  // 32 s + 16 + 4 gq + 0..3 (byte offset | nibble shift << 8 | nibble flag
+  // << 11 | book << 12 | group << 16).
+  constexpr int KS2 = KF == 2 ? KS : 1;
+  u32x4 gdl[KS2][2];
+  if (KF == 2) {
+    const u32x4 *gd = reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint8_t *>(T) + T->off_gdesc);
+#pragma unroll
+    for (int s = 0; s < KS2; ++s) {
+      gdl[s][0] = gd[8 * s + gq];
+      gdl[s][1] = gd[8 * s + 4 + gq];
+    }
+  }
   if (KF == 1 && wave == 0) {
     const int mc = T->max_centroids;
 #pragma unroll
@@ -245,7 +282,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
       for (int hh = 0; hh < 2; ++hh) {
         // KF 1: natural order 32 s + 8 gq + 4 hh + 0..3 (the rotation's k order);
         // KF 0: QK order 32 s + 16 hh + 4 gq + 0..3.
-        const f32x4 v = valid[cb] ? src[KF == 1 ? 8 * s + 2 * gq + hh : 8 * s + 4 * hh + gq]
+        const f32x4 v = valid[cb] ? src[KF >= 1 ? 8 * s + 2 * gq + hh : 8 * s + 4 * hh + gq]
                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -254,7 +291,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         }
       }
     int eq = split_exp(col_max(qmax));
-    if (KF == 1) {
+    if (KF >= 1) {
       // qr^T = Rq q^T on the matrix cores (q and Rq split hi/lo, three MFMAs
       // per step): D layout, lane holds rows j = 16 n + 4 gq + r of query col.
       half8 bh[KS], bl[KS];
@@ -348,6 +385,45 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         *reinterpret_cast<half8 *>(dst + 1024) = lo;
       }
       return E;
+    } else if constexpr (KF == 2) {
+      // Any layout: each element's code through its descriptor, times its
+      // book's centroid and its group's scale of the token, 2^(ec - E).
+      const uint8_t *kraw = slot(i) + Sl::VBYTES;
+      const uint16_t *nrm = reinterpret_cast<const uint16_t *>(kraw + Sl::KBYTES);
+      float smax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < Sl::NBYTES / 2 / 64; ++k) {
+        const int e = lane + 64 * k;
+        if (e < kChunk * ns) smax = fmaxf(smax, fabsf(h2f(nrm[e])));
+      }
+      smax = wave_max(smax);
+      const int E = smax > 0.0f ? (int)ceilf(__builtin_log2f(smax)) : 0;
+      const int mc = T->max_centroids;
+      uint8_t *kb = kop + (i & 1) * (2 * KS * 2048);
+#pragma unroll
+      for (int k = 0; k < 2 * KS / kWaves; ++k) {
+        const int combo = wave + kWaves * k, u = combo / KS, s = combo - u * KS;
+        const int t = 16 * u + col;
+        float v[8];
+#pragma unroll
+        for (int k2 = 0; k2 < 8; ++k2) {
+          uint32_t dsc = 0;
+#pragma unroll
+          for (int ss = 0; ss < KS2; ++ss)  // static register indices
+            if (ss == s) dsc = gdl[ss][k2 >> 2][k2 & 3];
+          const uint32_t byte = kraw[t * rb + (int)(dsc & 255u)];
+          const uint32_t code = (dsc >> 11) & 1u ? (byte >> ((dsc >> 8) & 7u)) & 15u : byte;
+          const float c = books[(int)((dsc >> 12) & 15u) * mc + (int)code];
+          const float sc = h2f(nrm[t * ns + (int)((dsc >> 16) & 15u)]);
+          v[k2] = c * __builtin_ldexpf(sc, ec - E);
+        }
+        half8 hi, lo;
+        split_scaled(v, 1.0f, hi, lo);
+        uint8_t *dst = kb + (u * KS + s) * 2048 + lane * 16;
+        *reinterpret_cast<half8 *>(dst) = hi;
+        *reinterpret_cast<half8 *>(dst + 1024) = lo;
+      }
+      return E;
     } else {
       return 0;
     }
@@ -378,7 +454,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        if constexpr (KF == 1) {
+        if constexpr (KF >= 1) {
           const uint8_t *src = kop + (i & 1) * (2 * KS * 2048) + (u * KS + s) * 2048 + lane * 16;
           const half8 ah = *reinterpret_cast<const half8 *>(src), al = *reinterpret_cast<const half8 *>(src + 1024);
 #pragma unroll
@@ -645,8 +721,11 @@ hipError_t launch_one(const PrefillParams &p, const FastLayout &fl, hipStream_t 
 
 }  // namespace
 
+int prefill_general_book_bytes(int dim) { return dim == 64 ? PSlot<64, 2, 0>::BOOKS : PSlot<128, 2, 0>::BOOKS; }
+
 hipError_t launch_prefill(const PrefillParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
   const int D = p.dim;
+  if (nn < 0) return D == 64 ? launch_one<64, 2, 0, 1>(p, fl, stream) : launch_one<128, 2, 0, 1>(p, fl, stream);
   if (p.key_format == 0) return D == 64 ? launch_one<64, 0, 0, 2>(p, fl, stream) : launch_one<128, 0, 0, 4>(p, fl, stream);
 #define BGTQ_PREFILL(DD, N, S) \
   if (D == DD && nn == N && sg == S) return launch_one<DD, 1, N, S>(p, fl, stream);

@@ -29,7 +29,8 @@ def _check(out, ref, what):
 class Cache:
     """K (packed or FP16) and FP16 V for batch x KV heads x cap tokens on the device."""
 
-    def __init__(self, device, *, params, batch, hkv, dim, cap, key_format="packed", seed=0, zero_k=False):
+    def __init__(self, device, *, params, batch, hkv, dim, cap, key_format="packed", seed=0, zero_k=False,
+                 pad16=False):
         import torch
         import bgtq
         from bgtq import batched
@@ -45,8 +46,11 @@ class Cache:
         if key_format == "packed":
             self.tabs = [bgtq.Tables(device, p) for p in params]
             rb, ns = params[0].rowBytes, params[0].normStride
-            self.packed = torch.zeros((batch, hkv, cap * rb), dtype=torch.uint8, device="cuda")
-            self.norms = torch.zeros((batch, hkv, cap * ns), dtype=torch.int16, device="cuda")
+            pk_len, nm_len = cap * rb, cap * ns
+            if pad16:  # 16-byte aligned head and sequence strides
+                pk_len, nm_len = (pk_len + 15) // 16 * 16, (nm_len + 7) // 8 * 8
+            self.packed = torch.zeros((batch, hkv, pk_len), dtype=torch.uint8, device="cuda")
+            self.norms = torch.zeros((batch, hkv, nm_len), dtype=torch.int16, device="cuda")
             jobs = [dict(tables=self.tabs[h], src=kd[b, h], src_row_stride=dim, rows=cap, packed=self.packed[b, h],
                          norms=self.norms[b, h]) for b in range(batch) for h in range(hkv)]
             batched.encode(device, jobs, "f16")
@@ -100,9 +104,10 @@ def _reference(oracle, cache, q, starts, b, h, G, rows_sel=None):
 
 
 def _run(device, oracle, *, params, batch, rows, hq, hkv, dim, starts, cap, key_format="packed", split_tokens=0,
-         seed=0):
+         seed=0, pad16=False):
     import torch
-    cache = Cache(device, params=params, batch=batch, hkv=hkv, dim=dim, cap=cap, key_format=key_format, seed=seed)
+    cache = Cache(device, params=params, batch=batch, hkv=hkv, dim=dim, cap=cap, key_format=key_format, seed=seed,
+                  pad16=pad16)
     try:
         g = torch.Generator().manual_seed(seed + 1)
         q = torch.randn((batch, rows, hq, dim), generator=g)
@@ -123,6 +128,31 @@ def test_layout_b_ragged_starts(device, oracle, dim):
     p = calibrate.layout_b(dim)
     print("prefill layout B", dim, flush=True)
     _run(device, oracle, params=[p, p], batch=3, rows=37, hq=14, hkv=2, dim=dim, starts=[0, 5, 463], cap=500)
+
+
+@pytest.mark.parametrize("dim,split_tokens", [(64, 0), (128, 0), (64, 96)])
+def test_layout_a_any_layout_build(device, oracle, dim, split_tokens):
+    """Layout A (groups straddling the 32-dim K-steps, norm stride 3 or 5) with 16-byte aligned
+    caches: the prefill kernel's per-position K build."""
+    from bgtq import calibrate
+    p = calibrate.layout_a(dim)
+    print("prefill layout A", dim, split_tokens, flush=True)
+    _run(device, oracle, params=[p, p], batch=3, rows=37, hq=14, hkv=2, dim=dim, starts=[0, 5, 463], cap=500,
+         split_tokens=split_tokens, pad16=True)
+
+
+def test_smollm2_heads_any_layout_build(device, oracle):
+    """The reference's SmolLM2 calibration heads (odd 37-byte rows, nibble and byte codes mixed,
+    up to six groups and books): the prefill kernel's per-position K build, 32-row chunk."""
+    from bgtq import BlockGTQParameters
+    from conftest import REF
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    heads = [BlockGTQParameters.from_serialized(a[f"{n}_config"], a[f"{n}_table"]) for n in ("h0", "h56", "h22")]
+    rb, ns = max(h.rowBytes for h in heads), max(h.normStride for h in heads)
+    for h in heads:
+        h.rowBytes, h.normStride = rb, ns
+    print("prefill smollm2 heads", flush=True)
+    _run(device, oracle, params=heads, batch=2, rows=32, hq=9, hkv=3, dim=64, starts=[0, 700], cap=732, pad16=True)
 
 
 def test_fp16_keys(device, oracle):
@@ -210,7 +240,8 @@ def test_rejections(device):
     import torch
     import bgtq
     from bgtq import batched, calibrate
-    p = calibrate.layout_a(64)  # K-steps mix groups: not handled by the prefill kernel
+    # norm stride 9: beyond what the prefill kernel holds (8)
+    p = calibrate.make_parameters(calibrate.allocate_bits(calibrate.geometric_scores(32), 6 * 32, 4, 8), norm_stride=9)
     t = bgtq.Tables(device, p)
     try:
         z = torch.zeros(16, device="cuda")
