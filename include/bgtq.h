@@ -217,9 +217,12 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d);
  * converted into k_f16), its V (v_new) converted into the FP16 V rows, and
  * the attention covers lengths[b] tokens including it. Same results as
  * bgtq_encode_batched of those rows, the V rows written, then bgtq_decode.
- * Needs the fused kernel's layouts (FP16 V, d 64 or 128, 32-dim K-steps within
- * one group and book, norm_stride 2); other layouts return
- * BGTQ_ERR_UNSUPPORTED (use the two calls). The workspace is the decode's. */
+ * Needs the fused kernel: FP16 V, d 64 or 128, 16-byte aligned caches and
+ * strides, and a packed layout within its limits (at most four groups in any
+ * 32 head-perm positions, 8 books whose code tables fit its LDS, norm_stride
+ * up to 8; the reference's layouts and SmolLM2 calibration heads qualify);
+ * others return BGTQ_ERR_UNSUPPORTED and write nothing (use the two calls).
+ * The workspace is the decode's. */
 typedef struct {
   const void *k_new;
   int32_t k_new_dtype; /* BGTQ_DTYPE_F32 or BGTQ_DTYPE_F16 */
@@ -244,9 +247,9 @@ bgtq_status bgtq_decode_append(bgtq_context *ctx, const bgtq_decode_desc *d, con
  *   workspace: device memory of at least bgtq_prefill_workspace_size() bytes
  *   for the token splits' partial results (no initial contents needed);
  *   calls sharing a workspace must be ordered on one stream.
- * Layouts: d 64 or 128, every 32-dim K-step of the head-perm order in one
- * group and one centroid book, at most two groups (layout B and FP16 K);
- * others return BGTQ_ERR_UNSUPPORTED. */
+ * Layouts: FP16 K, or packed layouts the fused decode takes (see
+ * bgtq_decode_append) whose centroid books (n_books * max_centroids floats)
+ * fit 4 KB at d=64, 8 KB at d=128; others return BGTQ_ERR_UNSUPPORTED. */
 typedef struct {
   int32_t batch, rows, q_heads, kv_heads, dim;
   int32_t key_format;
