@@ -913,11 +913,12 @@ static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tabl
     uint32_t nib_books = 0, byte_books = 0;
     for (int j = 0; j < p.dim; ++j) (j < T->nibble_dims ? nib_books : byte_books) |= 1u << T->pos_book[j];
     if (nib_books & byte_books) return false;
-    if (p.k_new && (int64_t)T->off_rot > decode_fast_enc_capacity(p.dim, -1)) return false;
     const uint8_t *base = reinterpret_cast<const uint8_t *>(tables[h]->dev());
     fl->rot_q[h] = base + T->off_rot_q;
     fl->rot_t[h] = reinterpret_cast<const float *>(base + T->off_rot_t);
-    fl->enc_bytes[h] = (int32_t)T->off_rot;
+    // The append's encoder reads an LDS copy of the header, LUT and books
+    // when they fit a ring slot, else (0) the tables in device memory.
+    fl->enc_bytes[h] = (int64_t)T->off_rot <= decode_fast_enc_capacity(p.dim, -1) ? (int32_t)T->off_rot : 0;
     fl->cent_exp[h] = T->cent_exp;
     fl->mfma[h] = base + T->off_mfma;
     fl->gdesc[h] = reinterpret_cast<const uint32_t *>(base + T->off_gdesc);

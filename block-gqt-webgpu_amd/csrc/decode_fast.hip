@@ -515,40 +515,46 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
     if (KF >= 1) {
       // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
-      // T: the LDS copy of the tables (header, LUT, books) loaded in the prologue.
-      const DevTables *T =
+      // T: the LDS copy of the tables (header, LUT, books) loaded in the prologue,
+      // or (KF 2, enc_bytes 0: tables larger than the slot holds) the tables in
+      // device memory.
+      auto encode_new = [&](const DevTables *T) {
+        lc.init(T, lane);
+        float x[JL];
+#pragma unroll
+        for (int jl = 0; jl < JL; ++jl) {
+          const int src = lc.perm[jl];
+          uint32_t raw = __shfl(k_nat[0], src & 63, 64);
+          if (JL > 1) {
+            const uint32_t hi = __shfl(k_nat[JL - 1], src & 63, 64);
+            raw = src >= 64 ? hi : raw;
+          }
+          const uint16_t h16 = p.k_new_f32 ? row_enc::f32_to_f16_bits(__uint_as_float(raw)) : (uint16_t)raw;
+          x[jl] = lc.own[jl] ? row_enc::f16_bits_to_f32(h16) : 0.0f;
+        }
+        // Scratch: this wave's last ring slot, loaded into only from the loop on.
+        const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
+        const float *rt = fl.rot_t[kv];
+        h_new = row_enc::encode_row<D>(
+            T, lc, x,
+            [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
+            tables_lut(T), tables_books(T), scr, lane);
+        const int logical = T->nibble_dims / 2 + D - T->nibble_dims;
+        uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
+#pragma unroll
+        for (int jl = 0; jl < JL; ++jl) {
+          const int bb = lane + 64 * jl;
+          if (bb < rb) {
+            pk_new[jl] = row_enc::packed_byte(scr.codes, bb, T->nibble_dims, logical);
+            prow[bb] = (uint8_t)pk_new[jl];
+          }
+        }
+        if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
+      };
+      const DevTables *T_lds =
           reinterpret_cast<const DevTables *>(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF);
-      lc.init(T, lane);
-      float x[JL];
-#pragma unroll
-      for (int jl = 0; jl < JL; ++jl) {
-        const int src = lc.perm[jl];
-        uint32_t raw = __shfl(k_nat[0], src & 63, 64);
-        if (JL > 1) {
-          const uint32_t hi = __shfl(k_nat[JL - 1], src & 63, 64);
-          raw = src >= 64 ? hi : raw;
-        }
-        const uint16_t h16 = p.k_new_f32 ? row_enc::f32_to_f16_bits(__uint_as_float(raw)) : (uint16_t)raw;
-        x[jl] = lc.own[jl] ? row_enc::f16_bits_to_f32(h16) : 0.0f;
-      }
-      // Scratch: this wave's last ring slot, loaded into only from the loop on.
-      const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
-      const float *rt = fl.rot_t[kv];
-      h_new = row_enc::encode_row<D>(
-          T, lc, x,
-          [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
-          tables_lut(T), tables_books(T), scr, lane);
-      const int logical = T->nibble_dims / 2 + D - T->nibble_dims;
-      uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
-#pragma unroll
-      for (int jl = 0; jl < JL; ++jl) {
-        const int bb = lane + 64 * jl;
-        if (bb < rb) {
-          pk_new[jl] = row_enc::packed_byte(scr.codes, bb, T->nibble_dims, logical);
-          prow[bb] = (uint8_t)pk_new[jl];
-        }
-      }
-      if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
+      if (KF == 2 && fl.enc_bytes[kv] == 0) encode_new(reinterpret_cast<const DevTables *>(p.tables[kv]));
+      else encode_new(T_lds);
       row_enc::wave_sync();  // scratch reads done before the slot's first load
     } else if (lane < PR) {
       k_new16 = half_piece(p.k_new_f32, k_raw);

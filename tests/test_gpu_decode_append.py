@@ -118,6 +118,22 @@ def test_append_smollm2_heads(device, oracle):
          params=heads)
 
 
+def test_append_smollm2_every_layer(device, oracle):
+    """decode_append accepts all 90 SmolLM2 calibration heads (it refuses layouts outside the fused
+    kernel) and matches the two-call path on each layer's three heads."""
+    from bgtq import BlockGTQParameters
+    from conftest import REF
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    for layer in range(30):
+        heads = [BlockGTQParameters.from_serialized(a[f"h{3 * layer + h}_config"], a[f"h{3 * layer + h}_table"])
+                 for h in range(3)]
+        rb, ns = max(h.rowBytes for h in heads), max(h.normStride for h in heads)
+        for h in heads:
+            h.rowBytes, h.normStride = rb, ns
+        _run(device, dim=64, key_format="packed", layout=f"smollm2 layer {layer}", lengths=[1, 40, 130], hkv=3, hq=9,
+             params=heads, seed=layer)
+
+
 def test_append_fp16_sources(device):
     _run(device, dim=64, key_format="packed", lengths=[513, 130], k_dtype="f16", v_dtype="f16")
 

@@ -179,6 +179,15 @@ def test_smollm2_heads_fused(device, oracle, names, splits):
          pad16=True)
 
 
+def test_smollm2_every_layer_fused(device, oracle):
+    """All 90 SmolLM2 calibration heads (30 layers x 3 KV heads) through the fused decode."""
+    for layer in range(30):
+        heads = _smollm2_heads(oracle, [f"h{3 * layer + h}" for h in range(3)])
+        print("smollm2 layer", layer, flush=True)
+        _run(device, oracle, params=heads, batch=1, hq=9, hkv=3, dim=64, lengths=[150], cap=150, pad16=True,
+             seed=layer)
+
+
 def test_full_context_closed_form(device, oracle):
     """32768-token context: zero q gives the mean of V exactly enough (uniform softmax)."""
     from bgtq import calibrate
