@@ -904,7 +904,7 @@ static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tabl
     const DevTables *T = tables[h]->h();
     const int bstride = std::max(256, (T->max_centroids * 4 + 255) / 256 * 256);
     if (T->n_books > 8 || T->max_centroids > 256 || T->n_books * (bstride + 32) > decode_general_table_bytes(p.dim) ||
-        T->norm_stride > kDecodeGeneralMaxNormStride || T->row_bytes > p.dim || T->groups > 8)
+        T->norm_stride > decode_general_max_norm_stride(p.dim) || T->row_bytes > p.dim || T->groups > 8)
       return false;
     for (int j = 1; j < p.dim; ++j)
       if (T->group_of[j] < T->group_of[j - 1] || T->group_of[j] > T->group_of[j - 1] + 1) return false;

@@ -244,14 +244,14 @@ hipError_t launch_decode_probs(const DecodeParams &p, hipStream_t stream);
 // nn = -1: a packed layout of any structure (per-position code lookup).
 bool decode_fast_supported(int dim, int key_format, int nn, int sg);
 // LDS bytes the per-position path holds for the books' code tables
-// (n_books * (table bytes + 32) must fit) at head dim `dim`, and its largest
-// norm stride and groups per 32 positions.
+// (n_books * (table bytes + 32) must fit) at head dim `dim`, its largest norm
+// stride there (6 at d=64, 8 at d=128) and its groups per 32 positions.
 int decode_general_table_bytes(int dim);
+int decode_general_max_norm_stride(int dim);
+constexpr int kDecodeGeneralMaxGroupsPerStep = 4;
 // LDS bytes of centroid books (n_books * max_centroids floats) the prefill
 // kernel's per-position build holds at head dim `dim`.
 int prefill_general_book_bytes(int dim);
-constexpr int kDecodeGeneralMaxNormStride = 8;
-constexpr int kDecodeGeneralMaxGroupsPerStep = 4;
 // LDS bytes the fused kernel gives the append's copy of a table set's
 // header, code LUT and books.
 int decode_fast_enc_capacity(int dim, int nn);

@@ -65,7 +65,9 @@ struct Geo {
 // register loads never wait for ring data. Two workgroups of the layout-B
 // d=64 kernel still fit one CU's 160 KB.
 // KF 2 (any packed layout): RB is the largest row a layout can have, NN the
-// scale DMAs (one for norm strides up to 4, two up to 8).
+// scale DMAs (one for norm strides up to 4, two up to 8; at d=64 the second
+// covers 128 bytes, norm strides up to 6, and the book tables get 3.5 KB, so
+// that two workgroups still share a CU).
 template <int D, int KF, int NN>
 struct Slot {
   static constexpr int KS = D / 32;
@@ -73,12 +75,13 @@ struct Slot {
   static constexpr int KBYTES = kChunk * RB;
   static constexpr int KI = (KBYTES + 1023) / 1024;  // 16-byte DMA instructions per K chunk
   static constexpr int NSC = KF == 1 ? 1 : KF == 2 ? NN : 0;  // scale DMAs per chunk
-  static constexpr int NBYTES = NSC * 64 * 4;
+  static constexpr bool SMALL2 = KF == 2 && NN == 2 && D == 64;
+  static constexpr int NBYTES = SMALL2 ? 384 : NSC * 64 * 4;
   static constexpr int NOFF = Geo<D>::VBYTES;         // scales
   static constexpr int KOFF = NOFF + NBYTES;          // K
   static constexpr int BYTES = KOFF + KI * 1024;
   static constexpr int L = Geo<D>::VI + KI + NSC;  // DMA instructions per chunk
-  static constexpr int TABLES = KF >= 1 ? KS * 2048 : 0;
+  static constexpr int TABLES = KF == 2 && D == 64 ? 3584 : KF >= 1 ? KS * 2048 : 0;
   // Three buffers per wave where they fit the CU, else two (FP16 K at d=128).
   static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
   static constexpr int AHEAD = RING - 1;
@@ -89,6 +92,7 @@ struct Slot {
   static constexpr int ENC_OFF = KF >= 1 ? (row_enc::scratch_bytes(D) + 1023) / 1024 * 1024 : 0;
   static constexpr int ENC_DMAS = KF >= 1 ? (BYTES - ENC_OFF) / 1024 : 0;
   static_assert(DYN + TABLES <= kLdsLimit, "LDS of one workgroup");
+  static_assert(!SMALL2 || 2 * (DYN + TABLES) <= kLdsLimit, "two workgroups per CU");
   static_assert(AHEAD >= 1 && AHEAD <= 3, "ring waits cover up to three chunks in flight");
 };
 
@@ -221,7 +225,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
       for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
 #pragma unroll
-      for (int k = 0; k < Sl::NSC; ++k) dma4<kStream>(rN, sb + Sl::NOFF + k * 256, k * 256 + lane * 4, 0);
+      for (int k = 0; k < Sl::NSC; ++k)
+        if (k * 256 + lane * 4 < Sl::NBYTES) dma4<kStream>(rN, sb + Sl::NOFF + k * 256, k * 256 + lane * 4, 0);
     } else {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
 #pragma unroll
@@ -632,7 +637,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
           if (rows_aligned) {
             w0 = *reinterpret_cast<const uint32_t *>(kbuf + rofs);
             w1 = *reinterpret_cast<const uint32_t *>(kbuf + rofs + 4);
-          } else {  // kbuf is 256-byte aligned: the row offset's low bits are the address's
+          } else {  // kbuf is 16-byte aligned: the row offset's low bits are the address's
             const int sh = rofs & 3;
             const uint32_t *wp = reinterpret_cast<const uint32_t *>(kbuf + (rofs - sh));
             const uint32_t d0 = wp[0], d1 = wp[1], d2 = wp[2];
@@ -867,14 +872,17 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // Last workgroup of this (sequence, KV head) to finish merges the splits.
   // Every thread waits for its partial stores to complete before the arrival
   // is counted, so no cache write-back is needed.
-  __shared__ int last;
+  // The flag lives in the lookup tables' LDS (dead since the loop): a
+  // separate variable would add 16 bytes, and the two-scale-DMA d=64 layout
+  // uses exactly half of the CU's LDS.
+  int *last = reinterpret_cast<int *>(tabs);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0)
-    last = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           (unsigned)(S - 1);
+    *last = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (unsigned)(S - 1);
   __syncthreads();
-  if (!last) return;
+  if (!*last) return;
   if (S <= kMergeOneRound) {
     if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
     else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
@@ -970,6 +978,10 @@ bool decode_fast_supported(int dim, int key_format, int nn, int sg) {
 }
 
 int decode_general_table_bytes(int dim) { return dim == 64 ? Slot<64, 2, 1>::TABLES : Slot<128, 2, 1>::TABLES; }
+
+int decode_general_max_norm_stride(int dim) {
+  return dim == 64 ? Slot<64, 2, 2>::NBYTES / 64 : Slot<128, 2, 2>::NBYTES / 64;
+}
 
 hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
   const int D = p.dim;
