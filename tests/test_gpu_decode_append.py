@@ -134,6 +134,15 @@ def test_append_smollm2_every_layer(device, oracle):
              params=heads, seed=layer)
 
 
+def test_append_widths_1_to_6_d128(device):
+    """d=128, widths 1..6 (79-byte rows, mixed nibble/byte lanes, norm stride 6): the append's
+    encoder reads the tables from device memory when they exceed the ring slot."""
+    from bgtq import calibrate
+    p = calibrate.make_parameters(calibrate.allocate_bits(calibrate.geometric_scores(64), 206, 1, 8))
+    _run(device, dim=128, key_format="packed", layout="widths 1..6", lengths=[1, 33, 500], hkv=2, hq=14,
+         params=[p, p])
+
+
 def test_append_fp16_sources(device):
     _run(device, dim=64, key_format="packed", lengths=[513, 130], k_dtype="f16", v_dtype="f16")
 

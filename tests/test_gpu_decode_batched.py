@@ -188,6 +188,20 @@ def test_smollm2_every_layer_fused(device, oracle):
              seed=layer)
 
 
+def _widths_1_to_6_d128():
+    """d=128, widths 1..6 in six groups: 98 nibble positions (a lane's 8 codes mix nibbles and
+    bytes), 79-byte rows (not word aligned), norm stride 6, up to three groups per 32 positions."""
+    from bgtq import calibrate
+    return calibrate.make_parameters(calibrate.allocate_bits(calibrate.geometric_scores(64), 206, 1, 8))
+
+
+def test_widths_1_to_6_d128_fused(device, oracle):
+    p = _widths_1_to_6_d128()
+    assert (p.dim, p.nibbleDims, p.rowBytes, p.normStride) == (128, 98, 79, 6)
+    print("widths 1..6 d=128", flush=True)
+    _run(device, oracle, params=[p, p], batch=2, hq=14, hkv=2, dim=128, lengths=[77, 1000], cap=1000, pad16=True)
+
+
 def test_full_context_closed_form(device, oracle):
     """32768-token context: zero q gives the mean of V exactly enough (uniform softmax)."""
     from bgtq import calibrate

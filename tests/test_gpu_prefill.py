@@ -155,6 +155,15 @@ def test_smollm2_heads_any_layout_build(device, oracle):
     _run(device, oracle, params=heads, batch=2, rows=32, hq=9, hkv=3, dim=64, starts=[0, 700], cap=732, pad16=True)
 
 
+def test_widths_1_to_6_d128_any_layout_build(device, oracle):
+    """d=128, widths 1..6: 79-byte rows, 98 nibble positions, norm stride 6."""
+    from bgtq import calibrate
+    p = calibrate.make_parameters(calibrate.allocate_bits(calibrate.geometric_scores(64), 206, 1, 8))
+    print("prefill widths 1..6 d=128", flush=True)
+    _run(device, oracle, params=[p, p], batch=2, rows=37, hq=14, hkv=2, dim=128, starts=[0, 463], cap=500,
+         pad16=True)
+
+
 def test_fp16_keys(device, oracle):
     print("prefill fp16 K", flush=True)
     _run(device, oracle, params=None, batch=2, rows=45, hq=14, hkv=2, dim=64, starts=[100, 0], cap=300,
