@@ -219,11 +219,13 @@ def smollm2_decode_step(dev, steps, layout="B", splits=0):
     import bgtq
     from bgtq import batched
     L, HKV2, HQ2, T = 30, 3, 9, 4096
-    p = layout_params(layout, 64)
-    tabs = [bgtq.Tables(dev, p) for _ in range(L * HKV2)]
-    packed = torch.empty((L, 1, HKV2, (T + 1) * p.rowBytes + 64), dtype=torch.uint8, device="cuda")
-    # per-head scale rows padded to 16 bytes (the fused kernel reads four tokens' scales at once)
-    norms = torch.empty((L, 1, HKV2, ((T + 1) * p.normStride + 32 + 7) // 8 * 8), dtype=torch.int16, device="cuda")
+    # layout S: each layer's own three calibration heads (the reference model's decode step)
+    heads = [smollm2_heads(l, HKV2) if layout == "S" else [layout_params(layout, 64)] * HKV2 for l in range(L)]
+    tabs = [bgtq.Tables(dev, heads[l][h]) for l in range(L) for h in range(HKV2)]
+    rb_max, ns_max = max(h[0].rowBytes for h in heads), max(h[0].normStride for h in heads)
+    # per-head strides rounded to 16 bytes (the fused kernel's loads)
+    packed = torch.empty((L, 1, HKV2, ((T + 1) * rb_max + 64 + 15) // 16 * 16), dtype=torch.uint8, device="cuda")
+    norms = torch.empty((L, 1, HKV2, ((T + 1) * ns_max + 32 + 7) // 8 * 8), dtype=torch.int16, device="cuda")
     hist = torch.randn((L, HKV2, T, 64), device="cuda").half()
     for l in range(L):
         batched.encode(dev, [dict(tables=tabs[l * HKV2 + h], src=hist[l, h], src_row_stride=64, rows=T,
@@ -261,14 +263,13 @@ def smollm2_decode_step(dev, steps, layout="B", splits=0):
 
     ms = time_graph(torch, graph_of(torch, dev, step), steps, 3)
     ms2 = time_graph(torch, graph_of(torch, dev, step_two_calls), steps, 3)
-    per_token = p.rowBytes + 2 * p.normStride + 128
-    bytes_step = L * HKV2 * (T + 1) * per_token
+    bytes_step = sum(HKV2 * (T + 1) * (h[0].rowBytes + 2 * h[0].normStride + 128) for h in heads)
     for t in tabs:
         t.destroy()
     return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(bytes_step / (ms / 1e3) / 1e9, 1),
             "two_launches_per_layer_us_per_step": round(ms2 * 1e3, 2),
             "workload": "30 layers x (encode 1 token x 3 KV heads, append its V, attend 9 q heads over 4097 "
-                        "tokens), d=64, batch 1, layout B, FP16 V; one bgtq_decode_append launch per layer"}
+                        f"tokens), d=64, batch 1, layout {layout}, FP16 V; one bgtq_decode_append launch per layer"}
 
 
 def prefill_flops(prompt, hq, dim, layers):
@@ -524,7 +525,8 @@ def main():
         log("SmolLM2 decode step ...")
         extra["smollm2_decode_step_b1"] = smollm2_decode_step(dev, a.steps, a.layout)
         log("single head ...")
-        extra["single_head_t4096_d128"] = single_head(dev, a.steps, a.layout)
+        # layout S exists at d=64 only (the SmolLM2 calibration)
+        extra["single_head_t4096_d128"] = single_head(dev, a.steps, a.layout) if a.layout != "S" else None
         log("Qwen prefill, one chunk ...")
         extra["qwen_prefill_4096"] = qwen_prefill(dev, max(2, a.steps // 2), a.layout)
         log("Qwen prefill, chunks of 32 ...")
