@@ -332,7 +332,8 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   const size_t off_mfma = align(off_rot_t + sizeof(float) * d * d);
   const size_t off_rot_q = align(off_mfma + (size_t)kMfmaTableBytes * nb);
   const size_t off_gdesc = align(off_rot_q + (d % 32 == 0 ? (size_t)rot_q_bytes((int)d) : 0));
-  const size_t total = off_gdesc + sizeof(uint32_t) * d;
+  const size_t off_glane = align(off_gdesc + sizeof(uint32_t) * d);
+  const size_t total = off_glane + (d % 32 == 0 ? sizeof(uint32_t) * 36 * 4 * (d / 32) : 0);
   auto *t = new bgtq_tables();
   t->ctx = ctx;
   t->host.assign(total, 0);
@@ -357,6 +358,7 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   T->off_mfma = (uint32_t)off_mfma;
   T->off_rot_q = (uint32_t)off_rot_q;
   T->off_gdesc = (uint32_t)off_gdesc;
+  T->off_glane = (uint32_t)off_glane;
   T->total_bytes = (uint32_t)total;
   float cmax = 0.0f;
   for (int64_t i = 0; i < d * mc; ++i) cmax = std::max(cmax, std::fabs(cent[i]));
@@ -379,6 +381,33 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
       gd[j] = off | (uint32_t)(nibble ? 4 * (j & 1) : 0) << 8 | (uint32_t)nibble << 11 | (uint32_t)pos_book[j] << 12 |
               (uint32_t)group_of[j] << 16;
     }
+  }
+  if (d % 32 == 0) {
+    // The fused decode's per-lane code-lookup records (layout in DevTables).
+    const int bspan = std::max(256, (int)(mc * 4 + 255) / 256 * 256) + 32;
+    uint32_t *rec = reinterpret_cast<uint32_t *>(h + off_glane);
+    auto off_of = [&](int64_t j) { return j < nib ? j / 2 : nib / 2 + (j - nib); };
+    for (int64_t s = 0; s < d / 32; ++s)
+      for (int gq = 0; gq < 4; ++gq, rec += 36) {
+        const int64_t j0 = 32 * s + 8 * gq;
+        const int glo = (int)group_of[32 * s];
+        int bo[8], grp[8];
+        for (int k = 0; k < 8; ++k) {
+          const int64_t j = j0 + k;
+          bo[k] = (int)(8 * (off_of(j) - off_of(j0)) + (j < nib ? 4 * (j & 1) : 0));
+          grp[k] = (int)group_of[j] - glo;
+          rec[12 + k] = (uint32_t)(pos_book[j] * bspan + (j < nib ? 4 : 8));
+        }
+        const int hib = bo[4] >> 3;
+        rec[0] = (uint32_t)off_of(j0);
+        rec[1] = (uint32_t)hib;
+        rec[2] = (uint32_t)glo;
+        rec[3] = (uint32_t)((int)group_of[32 * s + 31] - glo + 1);
+        for (int k = 0; k < 8; ++k) rec[4 + k] = (uint32_t)(k < 4 ? bo[k] : bo[k] - 8 * hib);
+        for (int i = 0; i < 4; ++i)
+          for (int k2 = 0; k2 < 4; ++k2)
+            rec[20 + 4 * i + k2] = (grp[2 * k2] == i ? 0x0000ffffu : 0u) | (grp[2 * k2 + 1] == i ? 0xffff0000u : 0u);
+      }
   }
   for (uint64_t i = 0; i < lut_len; ++i) h[off_lut + i] = (uint8_t)lut[i];
   for (int b = 0; b < nb; ++b)
@@ -917,11 +946,21 @@ static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tabl
     fl->rot_q[h] = base + T->off_rot_q;
     fl->rot_t[h] = reinterpret_cast<const float *>(base + T->off_rot_t);
     // The append's encoder reads an LDS copy of the header, LUT and books
-    // when they fit a ring slot, else (0) the tables in device memory.
-    fl->enc_bytes[h] = (int64_t)T->off_rot <= decode_fast_enc_capacity(p.dim, -1) ? (int32_t)T->off_rot : 0;
+    // when they fit a ring slot, else of the LUT and books (the header in
+    // device memory), else (0) the tables in device memory.
+    const int64_t cap = decode_fast_enc_capacity(p.dim, -1);
+    fl->enc_from[h] = 0;
+    fl->enc_bytes[h] = 0;
+    if ((int64_t)T->off_rot <= cap) {
+      fl->enc_bytes[h] = (int32_t)T->off_rot;
+    } else if ((int64_t)(T->off_rot - T->off_lut) <= cap) {
+      fl->enc_from[h] = (int32_t)T->off_lut;
+      fl->enc_bytes[h] = (int32_t)(T->off_rot - T->off_lut);
+    }
     fl->cent_exp[h] = T->cent_exp;
     fl->mfma[h] = base + T->off_mfma;
     fl->gdesc[h] = reinterpret_cast<const uint32_t *>(base + T->off_gdesc);
+    fl->glane[h] = reinterpret_cast<const uint32_t *>(base + T->off_glane);
     fl->grb[h] = (int16_t)T->row_bytes;
     fl->gns[h] = (int16_t)T->norm_stride;
     fl->gnb[h] = (int16_t)T->n_books;

@@ -17,7 +17,7 @@ constexpr int kEncodeJobsPerLaunch = 60;  // 64-byte jobs: the launch stays unde
 struct DevTables {
   int32_t dim, groups, row_bytes, norm_stride, nibble_dims, max_centroids, n_books, n_codebooks;
   int32_t gstart[kMaxGroups], gend[kMaxGroups], gsize[kMaxGroups];  // group ranges (head-perm order)
-  uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, off_rot_q, off_gdesc, total_bytes;
+  uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, off_rot_q, off_gdesc, off_glane, total_bytes;
   int32_t cent_exp;  // 2^cent_exp * max|centroid| <= 2^14: fp16 hi/lo split range for MFMA operands
   uint8_t perm[kMaxDim];      // head_perm
   uint8_t group_of[kMaxDim];
@@ -42,6 +42,14 @@ struct DevTables {
   // [off_gdesc] per head-perm position j, for the fused decode of any packed
   //             layout: uint32 byte offset in the packed row | nibble shift << 8
   //             | nibble flag << 11 | book << 12 | group << 16.
+  // [off_glane]  (d % 32 == 0) the fused decode's per-lane code-lookup
+  //             records, [K-step s][lane group gq][36] uint32 for positions
+  //             j = 32 s + 8 gq + k: koff (row byte of code 0), hib (byte
+  //             where the word of codes 4..7 starts), glo (group of position
+  //             32 s), nsl (groups in the K-step), ext[8] (bit offset of each
+  //             code in its word), tbo[8] (LDS offset of its book's code table
+  //             plus its field width), gmask[4][4] (per slot i, the fp16
+  //             halves of the 8 positions in group glo + i).
 };
 constexpr int kMfmaTableBytes = 3072;
 __host__ __device__ constexpr int rot_q_bytes(int dim) { return dim * dim * 4; }
@@ -201,12 +209,17 @@ struct FastLayout {
   // the table set's header, code LUT and books (contiguous from its start).
   const float *rot_t[kMaxKvHeads];
   int32_t enc_bytes[kMaxKvHeads];
+  // Where that copy starts in the table set: 0 (header, LUT, books), or
+  // off_lut (LUT and books only; the encoder reads the header in device
+  // memory). enc_bytes 0: no copy, the encoder reads the tables in place.
+  int32_t enc_from[kMaxKvHeads];
   // Packed layouts of any structure (the kernel's per-position code
   // lookup): position descriptors, row bytes, norm stride, book count, bytes
   // of each book's code table in LDS (whole 256-byte pieces), books of
   // nibble codes (bit mask), and whether every lane's row bytes start on a
   // word (row bytes a multiple of 4 and nibble positions a multiple of 8).
   const uint32_t *gdesc[kMaxKvHeads];
+  const uint32_t *glane[kMaxKvHeads];
   int16_t grb[kMaxKvHeads], gns[kMaxKvHeads], gnb[kMaxKvHeads], gbstride[kMaxKvHeads];
   uint8_t gbnib[kMaxKvHeads], galign[kMaxKvHeads];
 };

@@ -291,7 +291,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       // The tables' header, code LUT and books (contiguous from the start of
       // the table set, fl.enc_bytes[kv] bytes) into this wave's last ring
       // slot, first of this wave's loads: the prologue's wait covers them.
-      const __amdgpu_buffer_rsrc_t rt = rsrc(p.tables[kv], fl.enc_bytes[kv]);
+      const __amdgpu_buffer_rsrc_t rt =
+          rsrc(reinterpret_cast<const uint8_t *>(p.tables[kv]) + fl.enc_from[kv], fl.enc_bytes[kv]);
       uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
 #pragma unroll
       for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
@@ -365,17 +366,17 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       }
   }
   const int ec = KF >= 1 ? fl.cent_exp[kv] : 0;
-  // KF 2: descriptors of this lane's positions 32 s + 8 gq + k (byte offset
-  // in the row | nibble shift << 8 | nibble flag << 11 | book << 12 | group << 16).
+  // KF 2: this lane's code-lookup record of each K-step (built with the
+  // tables, one per K-step and lane group gq): koff, hib, glo, nsl, ext[8],
+  // tbo[8], gmask[4][4] (36 words, described where they are used).
   constexpr int KS2 = KF == 2 ? KS : 1;
-  u32x4 gdl[KS2][2];
+  u32x4 grec[KS2][9];
   if (KF == 2) {
-    const u32x4 *gd = reinterpret_cast<const u32x4 *>(fl.gdesc[kv]);
+    const u32x4 *gr = reinterpret_cast<const u32x4 *>(fl.glane[kv]);
 #pragma unroll
-    for (int s = 0; s < KS2; ++s) {
-      gdl[s][0] = gd[8 * s + 2 * gq];
-      gdl[s][1] = gd[8 * s + 2 * gq + 1];
-    }
+    for (int s = 0; s < KS2; ++s)
+#pragma unroll
+      for (int m = 0; m < 9; ++m) grec[s][m] = gr[(s * 4 + gq) * 9 + m];
   }
   // Unconditional, so every wave has exactly AHEAD * L chunk loads in flight
   // behind its prologue loads (chunks past the end are zero-sized). The
@@ -477,30 +478,19 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   int sc_src[NSV], sc_dst[NSV];
   const bool rows_aligned = KF == 2 && fl.galign[kv] != 0;  // every lane's 8 bytes start on a word
   if (KF == 2) {
-    const int bspan = fl.gbstride[kv] + 32;  // LDS bytes per book table
 #pragma unroll
     for (int s = 0; s < KS2; ++s) {
-      const uint32_t first = __builtin_amdgcn_readfirstlane(gdl[s][0][0]);
-      const uint32_t last = __builtin_amdgcn_readfirstlane(__shfl(gdl[s][1][3], 48, 64));
-      glo[s] = (int)((first >> 16) & 15u);
-      nsl[s] = (int)((last >> 16) & 15u) - glo[s] + 1;
-      koff[s] = (int)(gdl[s][0][0] & 255u);
-      int bo[8], grp[8];
+      koff[s] = (int)grec[s][0][0];
+      hib[s] = (int)grec[s][0][1];
+      glo[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][2]);
+      nsl[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][3]);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const uint32_t dsc = gdl[s][k >> 2][k & 3];
-        bo[k] = 8 * ((int)(dsc & 255u) - koff[s]) + (int)((dsc >> 8) & 7u);
-        tbo[s][k] = ((dsc >> 12) & 15u) * (uint32_t)bspan + ((dsc >> 11) & 1u ? 4u : 8u);
-        grp[k] = (int)((dsc >> 16) & 15u) - glo[s];
+        ext[s][k] = grec[s][1 + (k >> 2)][k & 3];
+        tbo[s][k] = grec[s][3 + (k >> 2)][k & 3];
       }
-      hib[s] = bo[4] >> 3;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) ext[s][k] = (uint32_t)(k < 4 ? bo[k] : bo[k] - 8 * hib[s]);
-#pragma unroll
-      for (int i = 0; i < kSlots; ++i)
-#pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2)
-          gmask[s][i][k2] = (grp[2 * k2] == i ? 0x0000ffffu : 0u) | (grp[2 * k2 + 1] == i ? 0xffff0000u : 0u);
+      for (int i = 0; i < kSlots; ++i) gmask[s][i] = grec[s][5 + i];
     }
     // The chunk's scale rows [token][ns] become [group][32 tokens] in place
     // (lane moves entries lane + 64 k), so a lane's four tokens of one group
@@ -520,10 +510,11 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
     if (KF >= 1) {
       // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
-      // T: the LDS copy of the tables (header, LUT, books) loaded in the prologue,
-      // or (KF 2, enc_bytes 0: tables larger than the slot holds) the tables in
-      // device memory.
-      auto encode_new = [&](const DevTables *T) {
+      // T, lut, books: the LDS copy of the tables (header, LUT, books) loaded in
+      // the prologue; for KF 2 tables larger than the slot holds, the header in
+      // device memory with an LDS copy of the LUT and books, or (larger still)
+      // all three in device memory.
+      auto encode_new = [&](const DevTables *T, const uint8_t *lut, const float *books) {
         lc.init(T, lane);
         float x[JL];
 #pragma unroll
@@ -543,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         h_new = row_enc::encode_row<D>(
             T, lc, x,
             [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
-            tables_lut(T), tables_books(T), scr, lane);
+            lut, books, scr, lane);
         const int logical = T->nibble_dims / 2 + D - T->nibble_dims;
         uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
 #pragma unroll
@@ -556,10 +547,21 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         }
         if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
       };
-      const DevTables *T_lds =
-          reinterpret_cast<const DevTables *>(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF);
-      if (KF == 2 && fl.enc_bytes[kv] == 0) encode_new(reinterpret_cast<const DevTables *>(p.tables[kv]));
-      else encode_new(T_lds);
+      const uint8_t *enc_lds = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
+      const DevTables *T_dev = reinterpret_cast<const DevTables *>(p.tables[kv]);
+      const DevTables *T_use = reinterpret_cast<const DevTables *>(enc_lds);
+      const uint8_t *lut_use = tables_lut(T_use);
+      const float *books_use = tables_books(T_use);
+      if (KF == 2 && fl.enc_bytes[kv] == 0) {
+        T_use = T_dev;
+        lut_use = tables_lut(T_dev);
+        books_use = tables_books(T_dev);
+      } else if (KF == 2 && fl.enc_from[kv] != 0) {
+        T_use = T_dev;
+        lut_use = enc_lds;
+        books_use = reinterpret_cast<const float *>(enc_lds + (T_dev->off_books - T_dev->off_lut));
+      }
+      encode_new(T_use, lut_use, books_use);
       row_enc::wave_sync();  // scratch reads done before the slot's first load
     } else if (lane < PR) {
       k_new16 = half_piece(p.k_new_f32, k_raw);
