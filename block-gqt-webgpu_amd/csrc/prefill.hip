@@ -167,6 +167,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   // Row bytes and scales per token (runtime for KF 2).
   const int rb = KF == 2 ? T->row_bytes : RB;
   const int ns = KF == 2 ? T->norm_stride : 2;
+  const int mc = KF == 2 ? T->max_centroids : 0;  // read once, not per block
   float *books = reinterpret_cast<float *>(smem + Sl::RING * Sl::BYTES);
   uint8_t *kop = smem + Sl::RING * Sl::BYTES + Sl::BOOKS;
   auto slot = [&](int i) { return smem + (i % Sl::RING) * Sl::BYTES; };
@@ -398,7 +399,6 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
       }
       smax = wave_max(smax);
       const int E = smax > 0.0f ? (int)ceilf(__builtin_log2f(smax)) : 0;
-      const int mc = T->max_centroids;
       uint8_t *kb = kop + (i & 1) * (2 * KS * 2048);
 #pragma unroll
       for (int k = 0; k < 2 * KS / kWaves; ++k) {
