@@ -391,11 +391,15 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
       // book's centroid and its group's scale of the token, 2^(ec - E).
       const uint8_t *kraw = slot(i) + Sl::VBYTES;
       const uint16_t *nrm = reinterpret_cast<const uint16_t *>(kraw + Sl::KBYTES);
+      // E bounds the scales of the block's tokens inside the history only: the
+      // scale DMA's range is rounded up to 4 bytes, so with rest * ns odd the
+      // slot also holds the first scale of the token after the history.
+      const int n_in = min(T_b - (t_lo + i * kChunk), kChunk) * ns;
       float smax = 0.0f;
 #pragma unroll
       for (int k = 0; k < Sl::NBYTES / 2 / 64; ++k) {
         const int e = lane + 64 * k;
-        if (e < kChunk * ns) smax = fmaxf(smax, fabsf(h2f(nrm[e])));
+        if (e < n_in) smax = fmaxf(smax, fabsf(h2f(nrm[e])));
       }
       smax = wave_max(smax);
       const int E = smax > 0.0f ? (int)ceilf(__builtin_log2f(smax)) : 0;

@@ -155,6 +155,43 @@ def test_smollm2_heads_any_layout_build(device, oracle):
     _run(device, oracle, params=heads, batch=2, rows=32, hq=9, hkv=3, dim=64, starts=[0, 700], cap=732, pad16=True)
 
 
+@pytest.mark.parametrize("heads,split_tokens", [(("h0", "h2", "h7"), 0), (("h3", "h6", "h3"), 0),
+                                                (("h0", "h2", "h7"), 96)])
+def test_scales_past_the_history_are_ignored(device, oracle, heads, split_tokens):
+    """Heads of odd norm stride (3, 5) with chunks ending at an odd token count of their last block:
+    the scale DMA of that block is rounded up to 4 bytes and also brings in the first scale of the
+    token after the history. Filling every scale slot past the history with 65504 (0x7bff) and
+    with +inf (0x7c00) must leave the output bit-identical and finite."""
+    import torch
+    from bgtq import BlockGTQParameters
+    from conftest import REF
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    params = [BlockGTQParameters.from_serialized(a[f"{n}_config"], a[f"{n}_table"]) for n in heads]
+    rb, ns = max(h.rowBytes for h in params), max(h.normStride for h in params)
+    assert ns % 2 == 1
+    for h in params:
+        h.rowBytes, h.normStride = rb, ns
+    starts, rows, cap = [0, 700], 33, 800  # histories of 33 and 733 tokens: 1 and 29 in the last block
+    print("prefill scales past the history", heads, split_tokens, flush=True)
+    cache = Cache(device, params=params, batch=2, hkv=3, dim=64, cap=cap, seed=4, pad16=True)
+    try:
+        q = torch.randn((2, rows, 9, 64), generator=torch.Generator().manual_seed(12))
+        clean = cache.prefill(device, q, starts, cap, split_tokens)
+        G = 3
+        for b in range(2):
+            for h in range(3):
+                ref = _reference(oracle, cache, q, starts, b, h, G)
+                _check(clean[b, :, h * G:(h + 1) * G], ref.astype(np.float64), f"b{b} kv{h}")
+        for fill in (0x7bff, 0x7c00):
+            for b in range(2):
+                cache.norms[b, :, (starts[b] + rows) * ns:] = fill
+            got = cache.prefill(device, q, starts, cap, split_tokens)
+            assert np.isfinite(got).all(), f"non-finite output with scales {fill:#x} past the history"
+            assert np.array_equal(got, clean), f"output changed with scales {fill:#x} past the history"
+    finally:
+        cache.destroy()
+
+
 def test_widths_1_to_6_d128_any_layout_build(device, oracle):
     """d=128, widths 1..6: 79-byte rows, 98 nibble positions, norm stride 6."""
     from bgtq import calibrate
