@@ -33,15 +33,131 @@ def allocate_bits(scores, budget: int, min_bits: int = 1, max_bits: int = 8) -> 
     return w
 
 
-def grouping(widths) -> dict:
-    """Pairs sorted by width, (p, p + L) interleaved.
+def tie_order(widths) -> np.ndarray:
+    """torch.argsort(widths) (not stable) as it ordered the reference's committed tables.
 
-    Upstream sorts with torch's default argsort; the tables the reference
-    committed (10 mixed layouts, 90 SmolLM2 heads, written with torch 2.12)
-    all have ties in ascending pair order, i.e. a stable sort. A stable sort
-    reproduces them on any torch version.
+    src/reference/mixed_layout.py:7-8 keeps torch's non-stable argsort; the
+    goldens were written on Windows, where ATen sorts (key, index) pairs with
+    the Microsoft STL's std::sort comparing keys only. That introsort
+    insertion-sorts ranges of at most 32 elements (equal widths stay in pair
+    order, as a stable sort) and splits larger ones around a median guess
+    (median of three; Tukey's ninther above 40 elements) with a three-way
+    partition whose swaps set the order of equal widths: at 33..64 pairs the
+    order differs from a stable sort (fixtures mixed_d128, low_d128). Restated
+    from that published algorithm; libbgtq's grouping (csrc/calibrate.cpp,
+    TieOrderSort) is the same code.
     """
-    order = np.argsort(np.asarray(widths, dtype=np.int64), kind="stable")
+    key = [int(x) for x in np.asarray(widths, dtype=np.int64)]
+    idx = list(range(len(key)))
+
+    def lt(i, j):
+        return key[i] < key[j]
+
+    def swap(i, j):
+        key[i], key[j] = key[j], key[i]
+        idx[i], idx[j] = idx[j], idx[i]
+
+    def med3(f, m, l):
+        if lt(m, f):
+            swap(m, f)
+        if lt(l, m):
+            swap(l, m)
+            if lt(m, f):
+                swap(m, f)
+
+    def partition(first, last):
+        mid = first + ((last - first) >> 1)
+        f, l = first, last - 1
+        if l - f > 40:  # Tukey's ninther
+            step = (l - f + 1) >> 3
+            two = step << 1
+            med3(f, f + step, f + two)
+            med3(mid - step, mid, mid + step)
+            med3(l - two, l - step, l)
+            med3(f + step, mid, l - step)
+        else:
+            med3(f, mid, l)
+        pf, pl = mid, mid + 1
+        while first < pf and not lt(pf - 1, pf) and not lt(pf, pf - 1):
+            pf -= 1
+        while pl < last and not lt(pl, pf) and not lt(pf, pl):
+            pl += 1
+        gf, gl = pl, pf
+        while True:
+            while gf < last:
+                if lt(pf, gf):
+                    pass
+                elif lt(gf, pf):
+                    break
+                else:
+                    if pl != gf:
+                        swap(pl, gf)
+                    pl += 1
+                gf += 1
+            while first < gl:
+                gp = gl - 1
+                if lt(gp, pf):
+                    pass
+                elif lt(pf, gp):
+                    break
+                else:
+                    pf -= 1
+                    if pf != gp:
+                        swap(pf, gp)
+                gl -= 1
+            if gl == first and gf == last:
+                return pf, pl
+            if gl == first:  # no room below: rotate the pivot run upward
+                if pl != gf:
+                    swap(pf, pl)
+                pl += 1
+                swap(pf, gf)
+                pf += 1
+                gf += 1
+            elif gf == last:  # no room above: rotate it downward
+                gl -= 1
+                pf -= 1
+                if gl != pf:
+                    swap(gl, pf)
+                pl -= 1
+                swap(pf, pl)
+            else:
+                gl -= 1
+                swap(gf, gl)
+                gf += 1
+
+    def insertion(first, last):
+        for mid in range(first + 1, last):
+            k, ix, hole = key[mid], idx[mid], mid
+            while hole > first and k < key[hole - 1]:
+                key[hole], idx[hole] = key[hole - 1], idx[hole - 1]
+                hole -= 1
+            key[hole], idx[hole] = k, ix
+
+    def sort(first, last, ideal):
+        while True:
+            # ideal <= 0 (the heap-sort fallback) cannot happen for widths 1..8:
+            # each split removes every element equal to its pivot.
+            if last - first <= 32 or ideal <= 0:
+                insertion(first, last)
+                return
+            m0, m1 = partition(first, last)
+            ideal = (ideal >> 1) + (ideal >> 2)
+            if m0 - first < last - m1:
+                sort(first, m0, ideal)
+                first = m1
+            else:
+                sort(m1, last, ideal)
+                last = m0
+
+    sort(0, len(key), len(key))
+    return np.asarray(idx, dtype=np.int64)
+
+
+def grouping(widths) -> dict:
+    """Pairs sorted by width in the committed tables' tie order (tie_order), (p, p + L) interleaved
+    (src/reference/mixed_layout.py:5-18)."""
+    order = tie_order(widths)
     L = len(order)
     head_perm = np.empty(2 * L, np.int64)
     head_perm[0::2], head_perm[1::2] = order, order + L

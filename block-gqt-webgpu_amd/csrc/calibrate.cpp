@@ -8,7 +8,8 @@
 // inputs: they come from the committed calibration blobs or from the
 // caller's own generator. Same arithmetic as the reference's tables:
 //  * priorities s * 4^-w in FP64 from FP32 scores, first index on ties;
-//  * a stable sort of the pairs by width (the committed tables' tie order);
+//  * the pairs sorted by width in the tie order of the committed tables
+//    (torch's non-stable argsort as the Windows build evaluates it, below);
 //  * bin offsets and inverse widths in FP64, stored as FP32;
 //  * bin centres from an FP32 linspace (halves from each end, as torch
 //    evaluates it) and the code of a centre = the first boundary >= it
@@ -42,8 +43,143 @@ bgtq_status err(bgtq_status code, const char *fmt, ...) {
 
 constexpr int kBins = 256;
 
+// The order torch.argsort(widths) (not stable) gave the reference's
+// committed tables (src/reference/mixed_layout.py:7-8; the goldens were
+// written on Windows). ATen's CPU sort fills indices 0..n-1 beside the keys
+// and sorts the (key, index) pairs with std::sort comparing keys only; the
+// Microsoft STL's std::sort (<algorithm>, _Sort_unchecked) insertion-sorts a
+// range of at most 32 elements, which keeps equal widths in pair order, and
+// splits a larger one around a median guess (median of three, Tukey's
+// ninther above 40 elements) with a three-way partition whose swaps decide
+// the order of equal widths. Restated from that published algorithm; with
+// 33..64 pairs the result differs from a stable sort (fixtures mixed_d128,
+// low_d128). Widths take at most 8 distinct values and every partition
+// removes all elements equal to its pivot, so no range is split more than 8
+// times and the library's heap-sort fallback (after about 1.5 log2 n splits)
+// is never reached.
+class TieOrderSort {
+ public:
+  TieOrderSort(const int64_t *widths, size_t n) : key_(n), idx_(n) {
+    for (size_t i = 0; i < n; ++i) {
+      key_[i] = widths[i];
+      idx_[i] = (int64_t)i;
+    }
+  }
+  std::vector<int64_t> run() {
+    const int64_t n = (int64_t)key_.size();
+    sort(0, n, n);
+    return idx_;
+  }
+
+ private:
+  std::vector<int64_t> key_, idx_;
+  static constexpr int64_t kInsertionMax = 32;
+
+  bool lt(int64_t i, int64_t j) const { return key_[i] < key_[j]; }
+  void swap(int64_t i, int64_t j) {
+    std::swap(key_[i], key_[j]);
+    std::swap(idx_[i], idx_[j]);
+  }
+  void med3(int64_t f, int64_t m, int64_t l) {
+    if (lt(m, f)) swap(m, f);
+    if (lt(l, m)) {
+      swap(l, m);
+      if (lt(m, f)) swap(m, f);
+    }
+  }
+  // Moves a median guess of [f, l] (inclusive) to m.
+  void guess_median(int64_t f, int64_t m, int64_t l) {
+    const int64_t count = l - f;
+    if (count > 40) {
+      const int64_t step = (count + 1) >> 3, two = step << 1;
+      med3(f, f + step, f + two);
+      med3(m - step, m, m + step);
+      med3(l - two, l - step, l);
+      med3(f + step, m, l - step);
+    } else {
+      med3(f, m, l);
+    }
+  }
+  // Three-way partition of [first, last): returns the range of elements equal
+  // to the pivot; smaller ones lie before it, larger ones after.
+  std::pair<int64_t, int64_t> partition(int64_t first, int64_t last) {
+    const int64_t mid = first + ((last - first) >> 1);
+    guess_median(first, mid, last - 1);
+    int64_t pf = mid, pl = mid + 1;
+    while (first < pf && !lt(pf - 1, pf) && !lt(pf, pf - 1)) --pf;
+    while (pl < last && !lt(pl, pf) && !lt(pf, pl)) ++pl;
+    int64_t gf = pl, gl = pf;
+    for (;;) {
+      for (; gf < last; ++gf) {
+        if (lt(pf, gf)) continue;
+        if (lt(gf, pf)) break;
+        if (pl != gf) swap(pl, gf);
+        ++pl;
+      }
+      for (; first < gl; --gl) {
+        const int64_t gp = gl - 1;
+        if (lt(gp, pf)) continue;
+        if (lt(pf, gp)) break;
+        if (--pf != gp) swap(pf, gp);
+      }
+      if (gl == first && gf == last) return {pf, pl};
+      if (gl == first) {  // no room below: rotate the pivot run upward
+        if (pl != gf) swap(pf, pl);
+        ++pl;
+        swap(pf, gf);
+        ++pf;
+        ++gf;
+      } else if (gf == last) {  // no room above: rotate it downward
+        if (--gl != --pf) swap(gl, pf);
+        swap(pf, --pl);
+      } else {
+        swap(gf, --gl);
+        ++gf;
+      }
+    }
+  }
+  void insertion(int64_t first, int64_t last) {
+    for (int64_t mid = first + 1; mid < last; ++mid) {
+      const int64_t k = key_[mid], ix = idx_[mid];
+      int64_t hole = mid;
+      if (k < key_[first]) {
+        for (; hole > first; --hole) {
+          key_[hole] = key_[hole - 1];
+          idx_[hole] = idx_[hole - 1];
+        }
+      } else {
+        for (; k < key_[hole - 1]; --hole) {
+          key_[hole] = key_[hole - 1];
+          idx_[hole] = idx_[hole - 1];
+        }
+      }
+      key_[hole] = k;
+      idx_[hole] = ix;
+    }
+  }
+  void sort(int64_t first, int64_t last, int64_t ideal) {
+    for (;;) {
+      // ideal <= 0 (the library's heap-sort fallback) cannot happen for widths
+      // 1..8; an insertion sort keeps the result a correct sort regardless.
+      if (last - first <= kInsertionMax || ideal <= 0) {
+        insertion(first, last);
+        return;
+      }
+      const std::pair<int64_t, int64_t> m = partition(first, last);
+      ideal = (ideal >> 1) + (ideal >> 2);
+      if (m.first - first < last - m.second) {
+        sort(first, m.first, ideal);
+        first = m.second;
+      } else {
+        sort(m.second, last, ideal);
+        last = m.first;
+      }
+    }
+  }
+};
+
 struct Grouping {
-  std::vector<int64_t> order;       // pairs sorted by width (stable)
+  std::vector<int64_t> order;       // pairs sorted by width (tie order above)
   std::vector<int32_t> bits;        // width of each group, ascending
   std::vector<int32_t> offsets;     // group position ranges, size groups + 1
   std::vector<uint32_t> head_perm;  // [2L]: (p, p + L) interleaved in sorted order
@@ -53,9 +189,7 @@ struct Grouping {
 
 Grouping group_pairs(const int64_t *widths, size_t L) {
   Grouping g;
-  g.order.resize(L);
-  for (size_t i = 0; i < L; ++i) g.order[i] = (int64_t)i;
-  std::stable_sort(g.order.begin(), g.order.end(), [&](int64_t a, int64_t b) { return widths[a] < widths[b]; });
+  g.order = TieOrderSort(widths, L).run();
   g.head_perm.resize(2 * L);
   g.group_of.resize(2 * L);
   g.offsets.push_back(0);

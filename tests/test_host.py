@@ -90,9 +90,8 @@ def test_append_count_messages():
 
 def test_calibration_tables_reproduce_reference(oracle):
     """The table generator rebuilds every committed reference table set bit for bit: the 90 real
-    SmolLM2 heads and the mixed layouts up to 32 pairs (d <= 64). For 64 pairs the reference's
-    tie order among equal widths came from torch 2.12's unstable sort and is not reproduced;
-    every other table (rotations, codebooks, LUTs, offsets) still matches."""
+    SmolLM2 heads and the 10 mixed layouts, the 64-pair layouts' head_perm included (the tie
+    order of calibrate.tie_order)."""
     import json
     import bgtq
     from bgtq import calibrate
@@ -110,10 +109,9 @@ def test_calibration_tables_reproduce_reference(oracle):
                           ("rotation", p.rotation), ("centroids", p.centroids), ("lut_offsets", p.offsets),
                           ("lut_inv_scales", p.inverseScales)):
             np.testing.assert_array_equal(np.asarray(mine).reshape(-1), aa[key].reshape(-1), err_msg=f"{c['name']} {key}")
-        if mm["dim"] <= 64:
-            np.testing.assert_array_equal(p.permutation, aa["head_perm"], err_msg=c["name"])
+        np.testing.assert_array_equal(p.permutation, aa["head_perm"], err_msg=c["name"])
         g = calibrate.grouping(aa["allocation"].astype(np.int64))
-        for key in ("group_bits", "group_offsets", "group_of"):
+        for key in ("pair_order", "head_perm", "group_bits", "group_offsets", "group_of"):
             np.testing.assert_array_equal(g[key], aa[key], err_msg=f"{c['name']} {key}")
         assert g["nopack_start"] == mm["nopack_start"]
 
@@ -133,8 +131,7 @@ def _fixture_groups(calibrate, widths, integer, floating):
 def test_native_table_pipeline_reproduces_reference(oracle):
     """libbgtq's allocator -> grouping -> code LUT pipeline (bgtq_layout_build), given each
     group's codebook and rotation from the committed tables, rebuilds the whole table set
-    bit for bit: the 90 SmolLM2 heads and the mixed layouts (head_perm up to 32 pairs, as
-    for the Python generator)."""
+    bit for bit: the 90 SmolLM2 heads and the 10 mixed layouts, head_perm included."""
     import json
     import bgtq
     from bgtq import calibrate
@@ -158,8 +155,40 @@ def test_native_table_pipeline_reproduces_reference(oracle):
             np.testing.assert_array_equal(np.asarray(mine).reshape(-1), np.asarray(ref).reshape(-1),
                                           err_msg=f"{c['name']} {key}")
         assert (q.rowBytes, q.normStride, q.nibbleDims) == (mm["row_bytes"], mm["norm_stride"], mm["nopack_start"])
-        if mm["dim"] <= 64:
-            np.testing.assert_array_equal(q.permutation, aa["head_perm"], err_msg=c["name"])
+        np.testing.assert_array_equal(q.permutation, aa["head_perm"], err_msg=c["name"])
+
+
+def test_tie_order_of_equal_widths(oracle):
+    """The pair order of the grouping (torch's non-stable argsort as the reference's goldens were
+    written): the committed pair orders of all 10 mixed layouts, among them the two 64-pair
+    layouts whose ties a stable sort does not reproduce; on random allocations a sort (widths
+    ascending, a permutation), equal to a stable sort up to 32 pairs, and the same in libbgtq."""
+    import json
+    import bgtq
+    from bgtq import calibrate
+    unstable = 0
+    for c in json.loads((REF / "mixed" / "index.json").read_text())["cases"]:
+        mm, aa = oracle.read_fixture(REF / "mixed" / f"{c['name']}.json")
+        w = aa["allocation"].astype(np.int64)
+        np.testing.assert_array_equal(calibrate.tie_order(w), aa["pair_order"], err_msg=c["name"])
+        unstable += not np.array_equal(np.argsort(w, kind="stable"), aa["pair_order"])
+    assert unstable == 2  # mixed_d128 and low_d128: the fixtures pin the partition's swaps
+    rng = np.random.default_rng(11)
+    for _ in range(300):
+        n = int(rng.integers(1, 65))
+        w = rng.integers(1, int(rng.integers(2, 10)), n).astype(np.int64)
+        o = calibrate.tie_order(w)
+        assert sorted(o.tolist()) == list(range(n))
+        assert np.all(np.diff(w[o]) >= 0)
+        if n <= 32:
+            np.testing.assert_array_equal(o, np.argsort(w, kind="stable"))
+    for _ in range(20):  # libbgtq's grouping: the same head_perm through bgtq_layout_build
+        w = rng.integers(1, 9, int(rng.choice([33, 48, 64]))).astype(np.int64)
+        p = calibrate.make_parameters(w)
+        ints, _ = calibrate.native_tables(w, _fixture_groups(calibrate, w, *bgtq.tables(p)))
+        q = bgtq.BlockGTQParameters.from_serialized(ints, bgtq.tables(p)[1])
+        o = calibrate.tie_order(w)
+        np.testing.assert_array_equal(q.permutation, np.stack([o, o + len(w)], 1).reshape(-1))
 
 
 def test_native_table_pipeline_matches_python_generator(oracle):
