@@ -84,7 +84,7 @@ class DecodeWorkload:
         self.layers, self.batch, self.ctx, self.hq, self.hkv, self.dim = layers, batch, ctx, hq, hkv, dim
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
-        self.tables, self.descs, self.keep = [], [], []
+        self.tables, self.descs, self.keep, self.layer_tensors = [], [], [], []
         p = layout_params(layout, dim) if key_format == "packed" else None
         self.row_bytes = p.rowBytes if p else 2 * dim
         self.norm_stride = p.normStride if p else 0
@@ -113,10 +113,12 @@ class DecodeWorkload:
                           packed_head_stride=packed.stride(1), norms=norms, norms_seq_stride=norms.stride(0),
                           norms_head_stride=norms.stride(1))
                 self.keep += [packed, norms, v, q]
+                self.layer_tensors.append(dict(packed=packed, norms=norms, v=v, q=q, params=hp))
             else:
                 per_token.append(4 * dim)
                 kw = dict(k_f16=k, k_seq_stride=k.stride(0), k_head_stride=k.stride(1))
                 self.keep += [k, v, q]
+                self.layer_tensors.append(dict(k=k, v=v, q=q))
             args = dict(batch=batch, q_heads=hq, kv_heads=hkv, dim=dim, q=q, out=self.out, lengths=self.lengths,
                         max_length=ctx, v=v, v_dtype="f16", v_seq_stride=v.stride(0), v_head_stride=v.stride(1),
                         splits=splits, **kw)
@@ -212,60 +214,89 @@ def encode_throughput(dev, layout="B", reps=10):
             "gbs_algorithmic": round(rows * (128 + p.rowBytes + 2 * p.normStride) / (ms / 1e3) / 1e9, 1)}
 
 
+class SmolLM2Step:
+    """SmolLM2-135M geometry decode step at batch 1: per layer, encode the new token's K for
+    3 KV heads, then attend 9 query heads over the 4096 + 1 cached tokens. Layout S gives each
+    layer its own three calibration heads (the reference model's decode step)."""
+
+    L, HKV, HQ, T = 30, 3, 9, 4096
+
+    def __init__(self, dev, layout="B", splits=0, seed=0):
+        import torch
+        import bgtq
+        from bgtq import batched
+        L, HKV2, HQ2, T = self.L, self.HKV, self.HQ, self.T
+        self.dev, self.layout = dev, layout
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.heads = [smollm2_heads(l, HKV2) if layout == "S" else [layout_params(layout, 64)] * HKV2
+                      for l in range(L)]
+        self.tabs = [bgtq.Tables(dev, self.heads[l][h]) for l in range(L) for h in range(HKV2)]
+        rb_max = max(h[0].rowBytes for h in self.heads)
+        ns_max = max(h[0].normStride for h in self.heads)
+        # per-head strides rounded to 16 bytes (the fused kernel's loads)
+        self.packed = torch.empty((L, 1, HKV2, ((T + 1) * rb_max + 64 + 15) // 16 * 16), dtype=torch.uint8,
+                                  device="cuda")
+        self.norms = torch.empty((L, 1, HKV2, ((T + 1) * ns_max + 32 + 7) // 8 * 8), dtype=torch.int16,
+                                 device="cuda")
+        hist = torch.randn((L, HKV2, T, 64), generator=g, device="cuda").half()
+        for l in range(L):
+            batched.encode(dev, [dict(tables=self.tabs[l * HKV2 + h], src=hist[l, h], src_row_stride=64, rows=T,
+                                      packed=self.packed[l, 0, h], norms=self.norms[l, 0, h], dst_row0=0)
+                                 for h in range(HKV2)], "f16")
+        del hist
+        self.knew = torch.randn((L, 1, HKV2, 64), generator=g, device="cuda")  # post-RoPE FP32 K of the new token
+        self.vnew = torch.randn((L, 1, HKV2, 64), generator=g, device="cuda")  # its FP32 V
+        self.v = torch.randn((L, 1, HKV2, T + 1, 64), generator=g, device="cuda").half()
+        self.q = torch.randn((L, 1, HQ2, 64), generator=g, device="cuda")
+        self.out = torch.empty((L, 1, HQ2, 64), device="cuda")
+        self.lengths = torch.full((1,), T + 1, dtype=torch.int32, device="cuda")
+        self.jobs, self.descs, ws = [], [], None
+        for l in range(L):
+            self.jobs.append([dict(tables=self.tabs[l * HKV2 + h], src=self.knew[l, 0, h], src_row_stride=64, rows=1,
+                                   packed=self.packed[l, 0, h], norms=self.norms[l, 0, h], dst_row0=T)
+                              for h in range(HKV2)])
+            args = dict(batch=1, q_heads=HQ2, kv_heads=HKV2, dim=64, q=self.q[l], out=self.out[l],
+                        lengths=self.lengths, max_length=T + 1, v=self.v[l], v_seq_stride=self.v.stride(1),
+                        v_head_stride=self.v.stride(2), tables=self.tabs[l * HKV2:(l + 1) * HKV2],
+                        packed=self.packed[l], packed_seq_stride=self.packed.stride(1),
+                        packed_head_stride=self.packed.stride(2), norms=self.norms[l],
+                        norms_seq_stride=self.norms.stride(1), norms_head_stride=self.norms.stride(2), splits=splits)
+            if ws is None:
+                ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8,
+                                 device="cuda")
+            self.descs.append(batched.decode_desc(workspace=ws, **args))
+        self.ws = ws
+        self.appends = [batched.append_desc(k_new=self.knew[l], v_new=self.vnew[l]) for l in range(L)]
+
+    def step(self):
+        """One launch per layer: the new K's encode and its V append inside the attention launch."""
+        from bgtq import batched
+        for l in range(self.L):
+            batched.decode_append(self.dev, self.descs[l], self.appends[l])
+
+    def step_two_calls(self):
+        """The same step as two launches per layer (the V row is not written here)."""
+        from bgtq import batched
+        for l in range(self.L):
+            batched.encode(self.dev, self.jobs[l], "f32")
+            batched.decode(self.dev, self.descs[l])
+
+    def bytes_per_step(self):
+        return sum(self.HKV * (self.T + 1) * (h[0].rowBytes + 2 * h[0].normStride + 128) for h in self.heads)
+
+    def destroy(self):
+        for t in self.tabs:
+            t.destroy()
+
+
 def smollm2_decode_step(dev, steps, layout="B", splits=0):
-    """SmolLM2-135M geometry at batch 1: per layer, encode the new token's K for
-    3 KV heads, then attend 9 query heads over the 4096 + 1 cached tokens."""
     import torch
-    import bgtq
-    from bgtq import batched
-    L, HKV2, HQ2, T = 30, 3, 9, 4096
-    # layout S: each layer's own three calibration heads (the reference model's decode step)
-    heads = [smollm2_heads(l, HKV2) if layout == "S" else [layout_params(layout, 64)] * HKV2 for l in range(L)]
-    tabs = [bgtq.Tables(dev, heads[l][h]) for l in range(L) for h in range(HKV2)]
-    rb_max, ns_max = max(h[0].rowBytes for h in heads), max(h[0].normStride for h in heads)
-    # per-head strides rounded to 16 bytes (the fused kernel's loads)
-    packed = torch.empty((L, 1, HKV2, ((T + 1) * rb_max + 64 + 15) // 16 * 16), dtype=torch.uint8, device="cuda")
-    norms = torch.empty((L, 1, HKV2, ((T + 1) * ns_max + 32 + 7) // 8 * 8), dtype=torch.int16, device="cuda")
-    hist = torch.randn((L, HKV2, T, 64), device="cuda").half()
-    for l in range(L):
-        batched.encode(dev, [dict(tables=tabs[l * HKV2 + h], src=hist[l, h], src_row_stride=64, rows=T,
-                                  packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=0) for h in range(HKV2)], "f16")
-    del hist
-    knew = torch.randn((L, 1, HKV2, 64), device="cuda")  # post-RoPE FP32 K of the new token
-    vnew = torch.randn((L, 1, HKV2, 64), device="cuda")  # its FP32 V
-    v = torch.randn((L, 1, HKV2, T + 1, 64), device="cuda").half()
-    q = torch.randn((L, 1, HQ2, 64), device="cuda")
-    out = torch.empty((L, 1, HQ2, 64), device="cuda")
-    lengths = torch.full((1,), T + 1, dtype=torch.int32, device="cuda")
-    jobs, descs, ws = [], [], None
-    for l in range(L):
-        jobs.append([dict(tables=tabs[l * HKV2 + h], src=knew[l, 0, h], src_row_stride=64, rows=1,
-                          packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=T) for h in range(HKV2)])
-        args = dict(batch=1, q_heads=HQ2, kv_heads=HKV2, dim=64, q=q[l], out=out[l], lengths=lengths,
-                    max_length=T + 1, v=v[l], v_seq_stride=v.stride(1), v_head_stride=v.stride(2),
-                    tables=tabs[l * HKV2:(l + 1) * HKV2], packed=packed[l], packed_seq_stride=packed.stride(1),
-                    packed_head_stride=packed.stride(2), norms=norms[l], norms_seq_stride=norms.stride(1),
-                    norms_head_stride=norms.stride(2), splits=splits)
-        if ws is None:
-            ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8, device="cuda")
-        descs.append(batched.decode_desc(workspace=ws, **args))
-
-    appends = [batched.append_desc(k_new=knew[l], v_new=vnew[l]) for l in range(L)]
-
-    def step():  # one launch per layer: encode the new K and append its V inside the attention launch
-        for l in range(L):
-            batched.decode_append(dev, descs[l], appends[l])
-
-    def step_two_calls():  # the same step as two launches per layer (the V row is not written here)
-        for l in range(L):
-            batched.encode(dev, jobs[l], "f32")
-            batched.decode(dev, descs[l])
-
-    ms = time_graph(torch, graph_of(torch, dev, step), steps, 3)
-    ms2 = time_graph(torch, graph_of(torch, dev, step_two_calls), steps, 3)
-    bytes_step = sum(HKV2 * (T + 1) * (h[0].rowBytes + 2 * h[0].normStride + 128) for h in heads)
-    for t in tabs:
-        t.destroy()
+    w = SmolLM2Step(dev, layout, splits)
+    ms = time_graph(torch, graph_of(torch, dev, w.step), steps, 3)
+    ms2 = time_graph(torch, graph_of(torch, dev, w.step_two_calls), steps, 3)
+    bytes_step = w.bytes_per_step()
+    w.destroy()
     return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(bytes_step / (ms / 1e3) / 1e9, 1),
             "two_launches_per_layer_us_per_step": round(ms2 * 1e3, 2),
             "workload": "30 layers x (encode 1 token x 3 KV heads, append its V, attend 9 q heads over 4097 "
@@ -302,57 +333,75 @@ def device_ceilings():
                       "8 chains of v_mfma_f32_16x16x32_f16 per wave, 8 waves per CU"}
 
 
-def qwen_prefill(dev, steps, layout="B", chunk=0, prompt=4096, layers=LAYERS):
+class PrefillWorkload:
     """Qwen2.5-0.5B-geometry prompt prefill: per layer, encode the chunk's post-RoPE K for 2 KV heads,
     then causal attention of its rows x 14 query heads over the history so far (d=64, FP16 V).
-    chunk=0: the whole prompt as one chunk; else chunks of that many rows, chunk by chunk through all layers."""
+    chunk=0: the whole prompt as one chunk; else chunks of that many rows, chunk by chunk through all
+    layers."""
+
+    def __init__(self, dev, layout="B", chunk=0, prompt=4096, layers=LAYERS, seed=7):
+        import torch
+        import bgtq
+        from bgtq import batched
+        self.dev, self.layout, self.prompt, self.layers = dev, layout, prompt, layers
+        p = self.params = layout_params(layout, DIM)
+        self.chunk = chunk = chunk or prompt
+        starts = list(range(0, prompt, chunk))
+        self.tabs = [bgtq.Tables(dev, p) for _ in range(layers * HKV)]
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.k = torch.randn((layers, HKV, prompt, DIM), generator=g, device="cuda").half()
+        self.v = torch.randn((layers, 1, HKV, prompt, DIM), generator=g, device="cuda").half()
+        self.q = torch.randn((layers, prompt, HQ, DIM), generator=g, device="cuda")
+        self.out = torch.empty((layers, prompt, HQ, DIM), device="cuda")
+        self.packed = torch.empty((layers, 1, HKV, prompt * p.rowBytes), dtype=torch.uint8, device="cuda")
+        self.norms = torch.empty((layers, 1, HKV, prompt * p.normStride), dtype=torch.int16, device="cuda")
+        self.start_t = [torch.tensor([s], dtype=torch.int32, device="cuda") for s in starts]
+        self.enc, args_list = [], []
+        for c, s in enumerate(starts):
+            rows = min(chunk, prompt - s)
+            for l in range(layers):
+                self.enc.append([dict(tables=self.tabs[l * HKV + h], src=self.k[l, h, s:s + rows], src_row_stride=DIM,
+                                      rows=rows, packed=self.packed[l, 0, h], norms=self.norms[l, 0, h], dst_row0=s)
+                                 for h in range(HKV)])
+                args_list.append(dict(batch=1, rows=rows, q_heads=HQ, kv_heads=HKV, dim=DIM, q=self.q[l, s:s + rows],
+                                      out=self.out[l, s:s + rows], starts=self.start_t[c], max_length=prompt,
+                                      v=self.v[l], v_seq_stride=self.v.stride(1), v_head_stride=self.v.stride(2),
+                                      tables=self.tabs[l * HKV:(l + 1) * HKV], packed=self.packed[l],
+                                      packed_seq_stride=self.packed.stride(1),
+                                      packed_head_stride=self.packed.stride(2), norms=self.norms[l],
+                                      norms_seq_stride=self.norms.stride(1), norms_head_stride=self.norms.stride(2)))
+        # one workspace for every call: they are ordered on one stream
+        need = max(batched.prefill_workspace_bytes(batched.prefill_desc(**a)) for a in args_list)
+        self.ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+        self.descs = [batched.prefill_desc(workspace=self.ws, **a) for a in args_list]
+
+    def attend_only(self):
+        from bgtq import batched
+        for d in self.descs:
+            batched.prefill(self.dev, d)
+
+    def step(self):
+        from bgtq import batched
+        for e, d in zip(self.enc, self.descs):
+            batched.encode(self.dev, e, "f16")
+            batched.prefill(self.dev, d)
+
+    def flops(self):
+        return prefill_flops(self.prompt, HQ, DIM, self.layers)
+
+    def destroy(self):
+        for t in self.tabs:
+            t.destroy()
+
+
+def qwen_prefill(dev, steps, layout="B", chunk=0, prompt=4096, layers=LAYERS):
     import torch
-    import bgtq
-    from bgtq import batched
-    p = layout_params(layout, DIM)
-    chunk = chunk or prompt
-    starts = list(range(0, prompt, chunk))
-    tabs = [bgtq.Tables(dev, p) for _ in range(layers * HKV)]
-    g = torch.Generator(device="cuda")
-    g.manual_seed(7)
-    k = torch.randn((layers, HKV, prompt, DIM), generator=g, device="cuda").half()
-    v = torch.randn((layers, 1, HKV, prompt, DIM), generator=g, device="cuda").half()
-    q = torch.randn((layers, prompt, HQ, DIM), generator=g, device="cuda")
-    out = torch.empty((layers, prompt, HQ, DIM), device="cuda")
-    packed = torch.empty((layers, 1, HKV, prompt * p.rowBytes), dtype=torch.uint8, device="cuda")
-    norms = torch.empty((layers, 1, HKV, prompt * p.normStride), dtype=torch.int16, device="cuda")
-    start_t = [torch.tensor([s], dtype=torch.int32, device="cuda") for s in starts]
-    enc, args_list = [], []
-    for c, s in enumerate(starts):
-        rows = min(chunk, prompt - s)
-        for l in range(layers):
-            enc.append([dict(tables=tabs[l * HKV + h], src=k[l, h, s:s + rows], src_row_stride=DIM, rows=rows,
-                             packed=packed[l, 0, h], norms=norms[l, 0, h], dst_row0=s) for h in range(HKV)])
-            args_list.append(dict(batch=1, rows=rows, q_heads=HQ, kv_heads=HKV, dim=DIM, q=q[l, s:s + rows],
-                                  out=out[l, s:s + rows], starts=start_t[c], max_length=prompt, v=v[l],
-                                  v_seq_stride=v.stride(1), v_head_stride=v.stride(2),
-                                  tables=tabs[l * HKV:(l + 1) * HKV], packed=packed[l],
-                                  packed_seq_stride=packed.stride(1), packed_head_stride=packed.stride(2),
-                                  norms=norms[l], norms_seq_stride=norms.stride(1), norms_head_stride=norms.stride(2)))
-    # one workspace for every call: they are ordered on one stream
-    need = max(batched.prefill_workspace_bytes(batched.prefill_desc(**a)) for a in args_list)
-    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
-    descs = [batched.prefill_desc(workspace=ws, **a) for a in args_list]
-
-    def attend_only():
-        for d in descs:
-            batched.prefill(dev, d)
-
-    def step():
-        for e, d in zip(enc, descs):
-            batched.encode(dev, e, "f16")
-            batched.prefill(dev, d)
-
-    flops = prefill_flops(prompt, HQ, DIM, layers)
-    ms = time_graph(torch, graph_of(torch, dev, step), steps, 2)
-    ms_att = time_graph(torch, graph_of(torch, dev, attend_only), steps, 2)
-    for t in tabs:
-        t.destroy()
+    w = PrefillWorkload(dev, layout, chunk, prompt, layers)
+    flops = w.flops()
+    ms = time_graph(torch, graph_of(torch, dev, w.step), steps, 2)
+    ms_att = time_graph(torch, graph_of(torch, dev, w.attend_only), steps, 2)
+    w.destroy()
     return {"ms_per_prompt": round(ms, 4), "tokens_per_s": round(prompt / (ms / 1e3)),
             "attention_only_ms": round(ms_att, 4),
             "attention_tflops_algorithmic": round(flops / (ms_att / 1e3) / 1e12, 1),
@@ -360,7 +409,7 @@ def qwen_prefill(dev, steps, layout="B", chunk=0, prompt=4096, layers=LAYERS):
             "algorithmic_gflop": round(flops / 1e9, 1),
             "workload": f"{prompt}-token prompt, {layers} layers x (encode K of {HKV} KV heads + causal attention of "
                         f"{HQ} q heads), d={DIM}, layout {layout}, FP16 V, "
-                        + ("one chunk" if chunk == prompt else f"chunks of {chunk} rows")}
+                        + ("one chunk" if w.chunk == prompt else f"chunks of {w.chunk} rows")}
 
 
 def single_head(dev, steps, layout="B"):
