@@ -139,6 +139,7 @@ SIGNATURES = {
     "bgtq_decode_workspace_size": (_I32, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_decode": (_I32, [_VP, ctypes.POINTER(DecodeDesc)]),
     "bgtq_decode_append": (_I32, [_VP, ctypes.POINTER(DecodeDesc), ctypes.POINTER(AppendDesc)]),
+    "bgtq_decode_noalloc": (_I32, [_VP, ctypes.POINTER(DecodeDesc)]),
     "bgtq_prefill_workspace_size": (_I32, [ctypes.POINTER(PrefillDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_prefill": (_I32, [_VP, ctypes.POINTER(PrefillDesc)]),
     "bgtq_model_submit": (_I32, [_VP, ctypes.POINTER(ModelDispatch), _SZ]),

@@ -66,6 +66,12 @@ def decode(device, desc) -> None:
     check(lib().bgtq_decode(device.handle, ctypes.byref(desc)))
 
 
+def decode_noalloc(device, desc) -> None:
+    """bgtq_decode_noalloc: the decode with the library's own device scratch (the descriptor's
+    workspace is ignored); nothing is allocated."""
+    check(lib().bgtq_decode_noalloc(device.handle, ctypes.byref(desc)))
+
+
 def append_desc(*, k_new, v_new):
     """bgtq_append_desc over device tensors [B, Hkv, dim] (FP32 or FP16, any strides in elements)."""
     a = _lib.AppendDesc()

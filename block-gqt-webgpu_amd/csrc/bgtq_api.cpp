@@ -144,7 +144,8 @@ struct bgtq_context {
   int device = 0;
   hipStream_t own = nullptr;
   hipStream_t stream = nullptr;
-  DeviceBuffer staging;  // per-call upload area, never part of an object's ledger
+  DeviceBuffer staging;      // per-call upload area, never part of an object's ledger
+  uint8_t *scratch = nullptr;  // this device's bgtq_decode_noalloc workspace (library-owned array)
   bgtq_status use() {
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
     return BGTQ_OK;
@@ -206,7 +207,7 @@ struct bgtq_attention {
 extern "C" {
 
 const char *bgtq_last_error(void) { return g_error.c_str(); }
-int32_t bgtq_abi_version(void) { return 3; }
+int32_t bgtq_abi_version(void) { return 4; }
 
 // ---------------------------------------------------------------- context
 bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
@@ -222,6 +223,11 @@ bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
     return hip_fail(e, "context");
   }
   c->stream = c->own;
+  if ((e = decode_scratch_setup(device, c->own, &c->scratch)) != hipSuccess) {
+    (void)hipStreamDestroy(c->own);
+    delete c;
+    return hip_fail(e, "decode scratch");
+  }
   *out = c;
   return BGTQ_OK;
 }
@@ -1011,6 +1017,20 @@ bgtq_status bgtq_decode_append(bgtq_context *ctx, const bgtq_decode_desc *d, con
   if (d && (a->k_new_seq_stride < 0 || a->k_new_head_stride < 0 || a->v_new_seq_stride < 0 || a->v_new_head_stride < 0))
     return fail(BGTQ_ERR_RANGE, "negative new K/V stride");
   return decode_impl(ctx, d, a);
+}
+
+bgtq_status bgtq_decode_noalloc(bgtq_context *ctx, const bgtq_decode_desc *d) {
+  if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
+  int splits = 1;
+  if (bgtq_status s = validate_decode(d, &splits)) return s;
+  const size_t need = decode_ws((int64_t)d->batch * d->kv_heads, (int64_t)d->batch * d->q_heads, d->dim, splits).total;
+  if (need > BGTQ_DECODE_SCRATCH_BYTES)
+    return fail(BGTQ_ERR_RANGE, "decode needs %zu bytes of workspace, above the %u-byte scratch of bgtq_decode_noalloc",
+                need, (unsigned)BGTQ_DECODE_SCRATCH_BYTES);
+  bgtq_decode_desc own = *d;
+  own.workspace = ctx->scratch;
+  own.workspace_bytes = BGTQ_DECODE_SCRATCH_BYTES;
+  return decode_impl(ctx, &own, nullptr);
 }
 
 static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, const bgtq_append_desc *a) {

@@ -247,6 +247,8 @@ int encode_bulk_lds_bytes(int kind, int wg, int lut_bytes, int book_floats);
 hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int wg, int src_f32, int64_t max_rows,
                               int lut_bytes, int book_floats, hipStream_t stream);
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
+// Device address of this device's bgtq_decode_noalloc scratch (decode_scratch.hip).
+hipError_t decode_scratch_setup(int device, hipStream_t stream, uint8_t **out);
 int decode_lds_bytes(int G, int dim, int key_format, int books_bytes, int row_bytes, int norm_stride);
 hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t stream);
 // LSE merge of split partials and the optional probabilities pass.

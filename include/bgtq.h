@@ -233,6 +233,20 @@ typedef struct {
 } bgtq_append_desc;
 bgtq_status bgtq_decode_append(bgtq_context *ctx, const bgtq_decode_desc *d, const bgtq_append_desc *a);
 
+/* bgtq_decode without a caller workspace and without any allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc). d->workspace and d->workspace_bytes are ignored;
+ * the decode's workspace is a library-owned device array of
+ * BGTQ_DECODE_SCRATCH_BYTES per device, held until the process ends and
+ * resolved and cleared by bgtq_context_create (once per device). A launch
+ * whose bgtq_decode_workspace_size exceeds it fails with BGTQ_ERR_RANGE and
+ * queues nothing. Same kernels and results as bgtq_decode. Every call on one
+ * device shares that device's array: calls that may overlap on one device
+ * (several streams or contexts) race and must be ordered by the caller. */
+#define BGTQ_DECODE_SCRATCH_BYTES (4u << 20)
+bgtq_status bgtq_decode_noalloc(bgtq_context *ctx, const bgtq_decode_desc *d);
+
 /* Chunked-prefill attention for one layer: the model forward over a chunk of
  * prompt rows (src/model/decoder.ts:46-56 with rows > 1, called per chunk by
  * src/model/decoder.ts:82; the reference caps chunks at 32 rows,
