@@ -118,6 +118,30 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Two transposed FP16 reads (ds_read_b64_tr_b16: lane i of a 16-lane group
+// gets column i of the four rows the group addresses) issued from inline asm.
+// The builtin form makes the compiler wait for every vector-memory load in
+// flight first (it may alias an LDS DMA), which drains a DMA ring; the caller
+// has waited for the DMA that wrote these rows. The compiler's hazard
+// recognizer does not look into asm: the s_nop 7 covers the wait states a
+// matrix-core instruction that read the destination registers as its
+// accumulator input needs before they are written (8-pass XDL). The results
+// are not valid until a wait_lds_tied on them.
+__device__ __forceinline__ void ds_read_tr16_pair(const uint8_t *lds0, const uint8_t *lds1, u32x2 &a, u32x2 &b) {
+  asm volatile("s_nop 7\n\tds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3"
+               : "=&v"(a), "=&v"(b)
+               : "v"((uint32_t)(uintptr_t)(lds_void *)lds0), "v"((uint32_t)(uintptr_t)(lds_void *)lds1));
+}
+// Waits until at most N LDS operations of this wave are in flight; a and b
+// are tied to the wait so nothing that reads them is scheduled before it.
+// LDS operations complete in order, so with the reads of a and b issued
+// before the N newest, they have landed.
+template <int N>
+__device__ __forceinline__ void wait_lds_tied(u32x2 &a, u32x2 &b) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
+}
+
 // 16-byte piece swizzle of an FP16 row of D values in LDS: conflict-free
 // transposed (ds_read_b64_tr_b16) and row reads.
 template <int D>

@@ -107,6 +107,32 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Wait for transposed read pair dt of DT issued in order (2 (DT - 1 - dt)
+// newer reads may still be in flight); dt is a compile-time index after
+// unrolling.
+template <int DT>
+__device__ __forceinline__ void wait_dt(int dt, u32x2 &a, u32x2 &b) {
+  if constexpr (DT == 2) {
+    if (dt == 0) wait_lds_tied<2>(a, b);
+    else wait_lds_tied<0>(a, b);
+  } else if constexpr (DT == 4) {
+    if (dt == 0) wait_lds_tied<6>(a, b);
+    else if (dt == 1) wait_lds_tied<4>(a, b);
+    else if (dt == 2) wait_lds_tied<2>(a, b);
+    else wait_lds_tied<0>(a, b);
+  } else {
+    static_assert(DT == 8, "head dim 32, 64 or 128");
+    if (dt == 0) wait_lds_tied<14>(a, b);
+    else if (dt == 1) wait_lds_tied<12>(a, b);
+    else if (dt == 2) wait_lds_tied<10>(a, b);
+    else if (dt == 3) wait_lds_tied<8>(a, b);
+    else if (dt == 4) wait_lds_tied<6>(a, b);
+    else if (dt == 5) wait_lds_tied<4>(a, b);
+    else if (dt == 6) wait_lds_tied<2>(a, b);
+    else wait_lds_tied<0>(a, b);
+  }
+}
+
 __device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((uint16_t)bits)); }
 
 // The query's row of [B, rows, Hq] (outputs, partials).
@@ -483,6 +509,21 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         }
       }
     }
+    // V of this block, read transposed for the PV B operands (lane: V[tokens
+    // of its P slots][16 dt + col]). At d=64 issued before the softmax, so
+    // the LDS latency hides under it; at d=128 just before PV (the 32 more
+    // live registers across the softmax would spill).
+    u32x2 vt[DT][2];
+    auto read_v = [&]() {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int piece = 2 * dt + tpiece;
+        ds_read_tr16_pair(sb + trow * (2 * D) + ((piece ^ swz<D>(trow)) * 16) + thalf,
+                          sb + (16 + trow) * (2 * D) + ((piece ^ swz<D>(16 + trow)) * 16) + thalf, vt[dt][0],
+                          vt[dt][1]);
+      }
+    };
+    if constexpr (D == 64) read_v();
     half8 pha[NCB], pla[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
@@ -529,15 +570,13 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         }
       }
     }
-    // PV: B operand = V[tokens of this lane's P slots][16 dt + col], read transposed.
+    // PV: B operand = the transposed V reads; dt's pair has landed once at
+    // most the 2 (DT - 1 - dt) newer reads are in flight.
+    if constexpr (D != 64) read_v();
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const int piece = 2 * dt + tpiece;
-      const fp16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (lds_fp16x4 *)(sb + trow * (2 * D) + ((piece ^ swz<D>(trow)) * 16) + thalf));
-      const fp16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (lds_fp16x4 *)(sb + (16 + trow) * (2 * D) + ((piece ^ swz<D>(16 + trow)) * 16) + thalf));
-      const u32x2 a0 = __builtin_bit_cast(u32x2, v0), a1 = __builtin_bit_cast(u32x2, v1);
+      wait_dt<DT>(dt, vt[dt][0], vt[dt][1]);
+      const u32x2 a0 = vt[dt][0], a1 = vt[dt][1];
       const half8 vb = __builtin_bit_cast(half8, u32x4{a0[0], a0[1], a1[0], a1[1]});
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
@@ -555,7 +594,9 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     if (i + 1 < n_blocks) wait_blocks<Sl::LW, AHEAD - 1>(min(n_blocks - 2 - i, AHEAD - 1));
     // Block i + 1 visible to all waves; block i's K operand (built last
     // iteration) complete; every wave done with the operand buffer of i - 1.
-    __syncthreads();
+    // An LDS-only barrier: the wait above covers the DMAs of block i + 1, and
+    // __syncthreads() would also wait for those of the blocks still in flight.
+    lds_barrier();
     const int E_next = i + 1 < n_blocks ? build(i + 1) : 0;
     if (t_lo + i * kChunk + kChunk > lim_min) compute(i, std::true_type{});
     else compute(i, std::false_type{});
