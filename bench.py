@@ -134,6 +134,12 @@ class DecodeWorkload:
         """Algorithmic bytes of one layer (the mean over layers where row strides differ)."""
         return self.batch * self.hkv * self.ctx * sum(self.per_token) / len(self.per_token)
 
+    def set_q_rotated(self, flag):
+        """Queries given in the code domain (a projection baked with bgtq_bake_qproj): the kernels
+        skip their rotation. The synthetic queries are N(0, 1) either way."""
+        for d in self.descs:
+            d.q_rotated = int(bool(flag))
+
     def set_splits(self, splits):
         from bgtq import batched
         for d in self.descs:
@@ -221,7 +227,7 @@ class SmolLM2Step:
 
     L, HKV, HQ, T = 30, 3, 9, 4096
 
-    def __init__(self, dev, layout="B", splits=0, seed=0):
+    def __init__(self, dev, layout="B", splits=0, seed=0, q_rotated=False):
         import torch
         import bgtq
         from bgtq import batched
@@ -261,7 +267,8 @@ class SmolLM2Step:
                         v_head_stride=self.v.stride(2), tables=self.tabs[l * HKV2:(l + 1) * HKV2],
                         packed=self.packed[l], packed_seq_stride=self.packed.stride(1),
                         packed_head_stride=self.packed.stride(2), norms=self.norms[l],
-                        norms_seq_stride=self.norms.stride(1), norms_head_stride=self.norms.stride(2), splits=splits)
+                        norms_seq_stride=self.norms.stride(1), norms_head_stride=self.norms.stride(2), splits=splits,
+                        q_rotated=q_rotated)
             if ws is None:
                 ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(**args)), dtype=torch.uint8,
                                  device="cuda")
@@ -297,8 +304,12 @@ def smollm2_decode_step(dev, steps, layout="B", splits=0):
     ms2 = time_graph(torch, graph_of(torch, dev, w.step_two_calls), steps, 3)
     bytes_step = w.bytes_per_step()
     w.destroy()
+    wr = SmolLM2Step(dev, layout, splits, q_rotated=True)
+    ms_rot = time_graph(torch, graph_of(torch, dev, wr.step), steps, 3)
+    wr.destroy()
     return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(bytes_step / (ms / 1e3) / 1e9, 1),
             "two_launches_per_layer_us_per_step": round(ms2 * 1e3, 2),
+            "q_rotated_us_per_step": round(ms_rot * 1e3, 2),
             "workload": "30 layers x (encode 1 token x 3 KV heads, append its V, attend 9 q heads over 4097 "
                         f"tokens), d=64, batch 1, layout {layout}, FP16 V; one bgtq_decode_append launch per layer"}
 
@@ -418,7 +429,10 @@ def single_head(dev, steps, layout="B"):
     w = DecodeWorkload(dev, layout, layers=1, batch=1, ctx=4096, hq=1, hkv=1, dim=128)
     g = graph_of(torch, dev, w.step)
     ms = time_graph(torch, g, steps * 10, 5)
+    w.set_q_rotated(True)
+    ms_rot = time_graph(torch, graph_of(torch, dev, w.step), steps * 10, 5)
     return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(w.bytes_per_layer() / (ms / 1e3) / 1e9, 1),
+            "q_rotated_us_per_step": round(ms_rot * 1e3, 2),
             "workload": "1 query, T=4096, d=128, one head, layout B, FP16 V"}
 
 
@@ -551,11 +565,14 @@ def main():
     else:
         ms_step = time_graph(torch, graph_of(torch, dev, w.step), a.steps, a.warmup)
     ms_eager = time_eager(torch, w.step, max(2, a.steps // 2), 1)
+    w.set_q_rotated(True)  # the same step with queries from a baked projection
+    ms_rot = time_graph(torch, graph_of(torch, dev, w.step), a.steps, 5)
+    w.set_q_rotated(False)
     bytes_layer = w.bytes_per_layer()
     gbs = LAYERS * bytes_layer / (ms_step / 1e3) / 1e9
     ms_launch = ms_step / LAYERS  # one decode launch per layer, back to back in the graph
     achieved = bytes_layer / (ms_launch / 1e3) / 1e9
-    extra = {"eager_ms_per_step": round(ms_eager, 4)}
+    extra = {"eager_ms_per_step": round(ms_eager, 4), "q_rotated_ms_per_step": round(ms_rot, 4)}
     log("device ceilings ...")
     ceil = device_ceilings()
     extra["ceilings"] = ceil

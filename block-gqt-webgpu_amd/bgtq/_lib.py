@@ -59,7 +59,8 @@ class DecodeDesc(ctypes.Structure):
                 ("v", ctypes.c_void_p), ("v_dtype", ctypes.c_int32), ("v_seq_stride", ctypes.c_int64),
                 ("v_head_stride", ctypes.c_int64), ("q", ctypes.c_void_p), ("out", ctypes.c_void_p),
                 ("lengths", ctypes.c_void_p), ("max_length", ctypes.c_uint32), ("splits", ctypes.c_int32),
-                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+                ("q_rotated", ctypes.c_int32)]
 
 
 
@@ -79,7 +80,8 @@ class PrefillDesc(ctypes.Structure):
                 ("v", ctypes.c_void_p), ("v_seq_stride", ctypes.c_int64), ("v_head_stride", ctypes.c_int64),
                 ("q", ctypes.c_void_p), ("out", ctypes.c_void_p), ("starts", ctypes.c_void_p),
                 ("max_length", ctypes.c_uint32), ("split_tokens", ctypes.c_int32),
-                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+                ("q_rotated", ctypes.c_int32)]
 
 class Binding(ctypes.Structure):
     _fields_ = [("ptr", ctypes.c_void_p), ("bytes", ctypes.c_size_t), ("tables", ctypes.c_void_p)]
@@ -140,6 +142,8 @@ SIGNATURES = {
     "bgtq_decode": (_I32, [_VP, ctypes.POINTER(DecodeDesc)]),
     "bgtq_decode_append": (_I32, [_VP, ctypes.POINTER(DecodeDesc), ctypes.POINTER(AppendDesc)]),
     "bgtq_decode_noalloc": (_I32, [_VP, ctypes.POINTER(DecodeDesc)]),
+    "bgtq_bake_qproj": (_I32, [_VP, ctypes.c_size_t, _VP, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int64, _VP, _VP,
+                               _VP, _VP]),
     "bgtq_prefill_workspace_size": (_I32, [ctypes.POINTER(PrefillDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_prefill": (_I32, [_VP, ctypes.POINTER(PrefillDesc)]),
     "bgtq_model_submit": (_I32, [_VP, ctypes.POINTER(ModelDispatch), _SZ]),

@@ -38,8 +38,11 @@ def encode(device, jobs, src_dtype="f16"):
 def decode_desc(*, batch, q_heads, kv_heads, dim, q, out, lengths, max_length, v, v_dtype="f16",
                 v_seq_stride, v_head_stride, tables=None, packed=None, packed_seq_stride=0,
                 packed_head_stride=0, norms=None, norms_seq_stride=0, norms_head_stride=0, k_f16=None,
-                k_seq_stride=0, k_head_stride=0, splits=0, workspace=None):
+                k_seq_stride=0, k_head_stride=0, splits=0, workspace=None, q_rotated=False):
+    """bgtq_decode_desc over device tensors. q_rotated: q is already R q[perm] per its KV head's
+    tables (from a projection baked with calibrate.bake_qproj)."""
     d = _lib.DecodeDesc()
+    d.q_rotated = int(bool(q_rotated))
     d.batch, d.q_heads, d.kv_heads, d.dim = batch, q_heads, kv_heads, dim
     d.key_format = _lib.KEYS_PACKED if packed is not None else _lib.KEYS_FP16
     for i, t in enumerate(tables or []):
@@ -91,9 +94,11 @@ def decode_append(device, desc, append) -> None:
 def prefill_desc(*, batch, rows, q_heads, kv_heads, dim, q, out, starts, max_length, v, v_seq_stride,
                  v_head_stride, tables=None, packed=None, packed_seq_stride=0, packed_head_stride=0, norms=None,
                  norms_seq_stride=0, norms_head_stride=0, k_f16=None, k_seq_stride=0, k_head_stride=0,
-                 split_tokens=0, workspace=None):
-    """bgtq_prefill_desc over device tensors: q/out [B, rows, Hq, dim] FP32, v FP16, starts uint32 [B]."""
+                 split_tokens=0, workspace=None, q_rotated=False):
+    """bgtq_prefill_desc over device tensors: q/out [B, rows, Hq, dim] FP32, v FP16, starts uint32 [B];
+    q_rotated as for decode_desc."""
     d = _lib.PrefillDesc()
+    d.q_rotated = int(bool(q_rotated))
     d.batch, d.rows, d.q_heads, d.kv_heads, d.dim = batch, rows, q_heads, kv_heads, dim
     d.key_format = _lib.KEYS_PACKED if packed is not None else _lib.KEYS_FP16
     for i, t in enumerate(tables or []):

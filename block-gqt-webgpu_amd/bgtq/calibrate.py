@@ -366,3 +366,28 @@ def native_tables(widths, groups, row_bytes: int = 0, norm_stride: int = 0):
     check(lib().bgtq_layout_build(ptr(w), len(w), arr, len(groups), row_bytes, norm_stride, ptr(integer),
                                   ctypes.byref(ni), ptr(floating), ctypes.byref(nf)))
     return integer, floating
+
+
+def bake_qproj(params: BlockGTQParameters, weight, bias=None):
+    """The query-projection rows of the query heads that use one KV head, with that head's
+    permutation and rotation folded in (bgtq_bake_qproj; the optimisation of
+    vendor/blockgtq/quantizer.py:1190-1244): weight [heads * dim, in_features], bias [heads * dim]
+    or None, FP32. Returns (weight', bias'); queries from them go to the kernels with q_rotated."""
+    from . import layout
+    from ._lib import RangeError, check, lib, ptr
+    ints, fl = layout.tables(params)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    d = int(params.dim)
+    if w.ndim != 2 or w.shape[0] % d:
+        raise RangeError(f"weight rows must be a multiple of dim={d}")
+    heads = w.shape[0] // d
+    out_w = np.empty_like(w)
+    b = out_b = None
+    if bias is not None:
+        b = np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+        if b.shape[0] != w.shape[0]:
+            raise RangeError("bias length must equal the weight rows")
+        out_b = np.empty_like(b)
+    check(lib().bgtq_bake_qproj(ptr(ints), len(ints), ptr(fl), len(fl), heads, w.shape[1], ptr(w), ptr(b),
+                                ptr(out_w), ptr(out_b)))
+    return out_w, out_b

@@ -860,6 +860,8 @@ static bgtq_status validate_decode(const bgtq_decode_desc *d, int *splits) {
   }
   if (!d->v || (d->v_dtype != BGTQ_DTYPE_F16 && d->v_dtype != BGTQ_DTYPE_F32)) return fail(BGTQ_ERR_RANGE, "invalid V");
   if (!d->q || !d->out || !d->lengths) return fail(BGTQ_ERR_RANGE, "null q/out/lengths");
+  if (d->q_rotated != 0 && d->q_rotated != 1) return fail(BGTQ_ERR_RANGE, "q_rotated must be 0 or 1");
+  if (d->q_rotated && d->key_format != BGTQ_KEYS_PACKED) return fail(BGTQ_ERR_RANGE, "q_rotated needs packed K");
   *splits = choose_splits((int64_t)d->batch * d->kv_heads, d->max_length, d->splits);
   return BGTQ_OK;
 }
@@ -1069,6 +1071,7 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
   p.part = reinterpret_cast<float *>(ws + w.part);
   p.stats = reinterpret_cast<float *>(ws + w.stats);
   p.lengths = d->lengths;
+  p.q_rotated = d->q_rotated;
   p.max_length = (int32_t)d->max_length;
   p.ends = nullptr;
   p.splits = splits;
@@ -1137,6 +1140,8 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
     return fail(BGTQ_ERR_RANGE, "invalid key format");
   }
   if (!d->v || !d->q || !d->out || !d->starts) return fail(BGTQ_ERR_RANGE, "null v/q/out/starts");
+  if (d->q_rotated != 0 && d->q_rotated != 1) return fail(BGTQ_ERR_RANGE, "q_rotated must be 0 or 1");
+  if (d->q_rotated && d->key_format != BGTQ_KEYS_PACKED) return fail(BGTQ_ERR_RANGE, "q_rotated needs packed K");
   if (d->split_tokens < 0) return fail(BGTQ_ERR_RANGE, "negative split_tokens");
   if ((int64_t)d->batch * d->kv_heads > 65535) return fail(BGTQ_ERR_UNSUPPORTED, "prefill handles up to 65535 sequence x KV head units");
   const int64_t G = d->q_heads / d->kv_heads, nq = (int64_t)d->rows * G;
@@ -1256,6 +1261,7 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   p.v_seq_stride = d->v_seq_stride;
   p.v_head_stride = d->v_head_stride;
   p.q = d->q;
+  p.q_rotated = d->q_rotated;
   p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
   p.starts = d->starts;
   p.max_length = (int32_t)d->max_length;

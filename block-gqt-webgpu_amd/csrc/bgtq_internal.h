@@ -108,6 +108,7 @@ struct DecodeParams {
   int32_t v_dtype;  // 0 = FP32, 1 = FP16
   int64_t v_seq_stride, v_head_stride;  // elements
   const float *q;         // [B*Hq*dim] queries
+  int32_t q_rotated;      // 1: q is already R q[perm] (code domain); the kernels do not rotate it
   const float *qr;        // [B*Hq*dim] rotated, permuted, scaled by 1/sqrt(dim)
   const uint32_t *lengths;  // [B]; kernels clamp them to max_length
   int32_t max_length;       // tokens every K/V buffer holds per (sequence, KV head)
@@ -147,6 +148,7 @@ struct PrefillParams {
   const void *v;                        // FP16
   int64_t v_seq_stride, v_head_stride;  // elements
   const float *q;           // [B*rows*Hq*dim] queries
+  int32_t q_rotated;        // 1: q is already R q[perm] (code domain); the kernel does not rotate it
   float inv_sqrt_d;
   const uint32_t *starts;   // [B] position of each chunk's first row
   int32_t max_length;       // tokens every K/V buffer holds; kernels clamp starts to max_length - rows

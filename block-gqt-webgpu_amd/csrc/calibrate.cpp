@@ -364,3 +364,59 @@ bgtq_status bgtq_layout_build(const int64_t *widths, size_t n_pairs, const bgtq_
 }
 
 }  // extern "C"
+
+extern "C" {
+
+// The rotation R and head permutation of a tables(p) blob (src/webgpu/layout.ts:24-31)
+// folded into query-projection rows: out[h*d + j] = sum_i R[j][i] w[h*d + perm[i]].
+// Upstream's bake_permutation_into_qproj (vendor/blockgtq/quantizer.py:1190-1244)
+// does the same fold for its fused kernels; this one is written so that the
+// baked queries equal the in-kernel rotation of the decode and prefill
+// kernels, qr = R q[perm] (k = ((c s) R)[inv_perm], src/reference/production_math.py:27-31,
+// so q . k = qr . (c s)).
+bgtq_status bgtq_bake_qproj(const uint32_t *integer, size_t n_integer, const float *floating, size_t n_floating,
+                            int32_t heads, int64_t in_features, const float *weight, const float *bias,
+                            float *weight_out, float *bias_out) {
+  if (!integer || n_integer < 10) return err(BGTQ_ERR_RANGE, "Invalid Block-GTQ layout");
+  const int64_t d = integer[0], mc = integer[5];
+  if (d < 2 || d > 128 || d % 2 || mc < 2 || mc > 256) return err(BGTQ_ERR_RANGE, "Invalid Block-GTQ layout");
+  const uint64_t o_perm = integer[6];
+  if (o_perm > n_integer || (uint64_t)d > n_integer - o_perm) return err(BGTQ_ERR_RANGE, "Invalid calibration table shape");
+  const uint32_t *perm = integer + o_perm;
+  std::vector<int> seen(d, 0);
+  for (int64_t i = 0; i < d; ++i)
+    if (perm[i] >= (uint64_t)d || seen[perm[i]]++) return err(BGTQ_ERR_RANGE, "Invalid calibration table shape");
+  if (!floating || n_floating != (size_t)(d * d + d * mc + 2 * d)) return err(BGTQ_ERR_RANGE, "Invalid calibration table shape");
+  for (int64_t i = 0; i < d * d; ++i)
+    if (!std::isfinite(floating[i])) return err(BGTQ_ERR_RANGE, "Nonfinite calibration table");
+  if (heads < 1 || in_features < 1) return err(BGTQ_ERR_RANGE, "heads and in_features must be positive");
+  if (!weight || !weight_out) return err(BGTQ_ERR_RANGE, "null weight");
+  if ((bias == nullptr) != (bias_out == nullptr)) return err(BGTQ_ERR_RANGE, "bias and bias_out go together");
+  const float *R = floating;
+  const int64_t cols = in_features;
+  // Each head's rows are computed into a staging copy first, so weight_out
+  // (bias_out) may be weight (bias) itself: the bake in place, as upstream's.
+  std::vector<double> acc(cols);
+  std::vector<float> rows((size_t)(d * cols)), brow((size_t)d);
+  for (int32_t h = 0; h < heads; ++h) {
+    const float *w = weight + (int64_t)h * d * cols;
+    for (int64_t j = 0; j < d; ++j) {
+      std::fill(acc.begin(), acc.end(), 0.0);
+      double accb = 0.0;
+      for (int64_t i = 0; i < d; ++i) {
+        const double r = R[j * d + i];
+        if (r == 0.0) continue;  // off-group entries
+        const float *src = w + (int64_t)perm[i] * cols;
+        for (int64_t c = 0; c < cols; ++c) acc[c] += r * (double)src[c];
+        if (bias) accb += r * (double)bias[(int64_t)h * d + perm[i]];
+      }
+      for (int64_t c = 0; c < cols; ++c) rows[j * cols + c] = (float)acc[c];
+      brow[j] = (float)accb;
+    }
+    std::copy(rows.begin(), rows.end(), weight_out + (int64_t)h * d * cols);
+    if (bias) std::copy(brow.begin(), brow.end(), bias_out + (int64_t)h * d);
+  }
+  return BGTQ_OK;
+}
+
+}  // extern "C"

@@ -63,7 +63,7 @@ __global__ void rotate_q_kernel(DecodeParams p, const float *__restrict__ q, flo
   const int h = idx % p.q_heads;
   const float *qv = q + (int64_t)idx * d;
   float r;
-  if (p.key_format == 1) {
+  if (p.key_format == 1 && !p.q_rotated) {
     const DevTables *T = p.tables[h / p.G];
     const float *R = tables_rot(T);
     const int g = T->group_of[j];

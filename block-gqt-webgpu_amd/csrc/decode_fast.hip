@@ -354,7 +354,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   }
   constexpr int NT = KF >= 1 ? DT / kWaves : 1;  // 16-row tiles of the rotation per wave
   u32x4 rq[NT][KS][2];
-  if (KF >= 1) {
+  // A query already in the code domain (q_rotated) is the QK operand as loaded.
+  const bool rotate = KF >= 1 && !p.q_rotated;
+  if (rotate) {
     const u32x4 *op = reinterpret_cast<const u32x4 *>(fl.rot_q[kv]);  // [tile][K-step][lane][hi, lo]
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -391,7 +393,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   for (int s = 0; s < KS; ++s)
 #pragma unroll
     for (int k = 0; k < 8; ++k) qv[s][k] = head_ok ? qload[s][k >> 2][k & 3] : 0.0f;
-  if (KF >= 1) {
+  if (rotate) {
     // qr^T = Rq q^T, Rq = R with the head permutation folded into its
     // columns, on the matrix cores (q and Rq split hi/lo, three MFMAs per
     // K-step, off-group entries exact zeros). Tile n leaves rows
@@ -430,6 +432,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
         for (int k = 0; k < 4; ++k) qv[s][4 * hh + k] = v[k];
       }
+  } else if (KF >= 1) {
+    wait_vm<AHEAD * L>();  // the table DMAs, which precede the chunks
+    lds_barrier();
   }
   // B operand of QK: lane holds qr[head = col][32 s + 8 gq + 0..7], split hi/lo
   // after scaling the head's row so its largest entry is near 2^14.
@@ -458,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       }
     kq = __builtin_ldexpf(kLog2e, -(eq + ec));
   }
-  if (KF >= 1) lds_barrier();  // q staging (last ring slot) is dead
+  if (rotate) lds_barrier();  // q staging (last ring slot) is dead
 
   // KF 2: a K-step spans up to kSlots adjacent groups glo[s] .. glo[s] +
   // nsl[s] - 1. Each group's part of the K-step runs its own MFMAs against

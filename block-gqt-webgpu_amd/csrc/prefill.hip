@@ -291,6 +291,8 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     }
   }
   const float qscale = kLog2e * p.inv_sqrt_d;
+  // A query already in the code domain (q_rotated) loads in the QK order.
+  const bool rotate = KF >= 1 && !p.q_rotated;
   bool valid[NCB];
   half8 qhi[NCB][KS], qlo[NCB][KS];
   int eqs[NCB];   // logit = acc * 2^(E - ec - eqs)
@@ -307,9 +309,9 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        // KF 1: natural order 32 s + 8 gq + 4 hh + 0..3 (the rotation's k order);
-        // KF 0: QK order 32 s + 16 hh + 4 gq + 0..3.
-        const f32x4 v = valid[cb] ? src[KF >= 1 ? 8 * s + 2 * gq + hh : 8 * s + 4 * hh + gq]
+        // Rotated in the kernel: natural order 32 s + 8 gq + 4 hh + 0..3 (the
+        // rotation's k order); otherwise QK order 32 s + 16 hh + 4 gq + 0..3.
+        const f32x4 v = valid[cb] ? src[rotate ? 8 * s + 2 * gq + hh : 8 * s + 4 * hh + gq]
                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -318,7 +320,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         }
       }
     int eq = split_exp(col_max(qmax));
-    if (KF >= 1) {
+    if (rotate) {
       // qr^T = Rq q^T on the matrix cores (q and Rq split hi/lo, three MFMAs
       // per step): D layout, lane holds rows j = 16 n + 4 gq + r of query col.
       half8 bh[KS], bl[KS];

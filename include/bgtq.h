@@ -51,7 +51,8 @@ typedef struct {
 /* Thread-local message of the last failing call on this thread. */
 const char *bgtq_last_error(void);
 /* 2: bgtq_tables_info gained device_bytes. 3: bgtq_model_submit, bgtq_buffer_*, bgtq_allocate_bits,
- * bgtq_layout_groups, bgtq_layout_build. */
+ * bgtq_layout_groups, bgtq_layout_build. 4: bgtq_decode_noalloc; q_rotated closes the decode and
+ * prefill descriptors; bgtq_bake_qproj. */
 int32_t bgtq_abi_version(void);
 
 /* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
@@ -203,6 +204,12 @@ typedef struct {
   int32_t splits; /* token splits per (sequence, KV head); 0 = choose */
   void *workspace;
   size_t workspace_bytes;
+  /* 0: q as the model produces it. 1 (packed K only): q is already in the
+   * code domain of its KV head's tables, qr[j] = sum_i R[j][i] q[perm[i]]
+   * (the query of vendor/blockgtq/quantizer.py:1160-1188,
+   * rotate_q_for_packed_kernel, e.g. from a projection baked with
+   * bgtq_bake_qproj), and the kernels skip their own rotation. */
+  int32_t q_rotated;
 } bgtq_decode_desc;
 bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes);
 bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d);
@@ -283,6 +290,7 @@ typedef struct {
   int32_t split_tokens; /* tokens per split, rounded up to a multiple of 32; 0 = choose */
   void *workspace;
   size_t workspace_bytes;
+  int32_t q_rotated; /* as in bgtq_decode_desc */
 } bgtq_prefill_desc;
 bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *bytes);
 bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d);
@@ -316,6 +324,23 @@ typedef struct {
 bgtq_status bgtq_layout_build(const int64_t *widths, size_t n_pairs, const bgtq_group_tables *groups, size_t n_groups,
                               int32_t row_bytes, int32_t norm_stride, uint32_t *integer, size_t *n_integer,
                               float *floating, size_t *n_floating);
+
+/* Bakes a KV head's head permutation and rotation into the query projection
+ * of its query heads, so the queries it produces are already in the code
+ * domain and the attention kernels skip their rotation (the optimisation of
+ * vendor/blockgtq/quantizer.py:1190-1244, bake_permutation_into_qproj; the
+ * packing permutation is the identity in the reference,
+ * tests/oracles/calibrate_model.py:34). integer/floating: the KV head's
+ * tables(p) blobs (src/webgpu/layout.ts:24-31), checked as bgtq_tables_create
+ * checks them. weight: the projection rows of `heads` query heads,
+ * [heads * dim][in_features] row-major FP32; bias: [heads * dim] or NULL.
+ * Per head h: out[h*dim + j][c] = sum_i R[j][i] w[h*dim + perm[i]][c], and
+ * the same for the bias, accumulated in FP64 and rounded once. Queries from
+ * the baked projection go to bgtq_decode / bgtq_prefill with q_rotated = 1.
+ * Host only; no device is used. */
+bgtq_status bgtq_bake_qproj(const uint32_t *integer, size_t n_integer, const float *floating, size_t n_floating,
+                            int32_t heads, int64_t in_features, const float *weight, const float *bias,
+                            float *weight_out, float *bias_out);
 
 /* ---- device buffers: storage / upload / readBuffer (src/webgpu/buffers.ts:3-25)
  * For callers without their own device allocator (the Node mirror). A buffer

@@ -429,3 +429,62 @@ def test_node_calibration_checks(oracle, tmp_path):
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out == {m: m for m in cases}, out
+
+
+def test_bake_qproj_puts_queries_in_the_code_domain(oracle):
+    """bgtq_bake_qproj (vendor/blockgtq/quantizer.py:1190-1244): for any x, the baked projection's
+    query q' = W'x + b' satisfies q'.(c s) = q.k for every K row, where q = Wx + b and k is the
+    oracle's reconstruction of the row's codes c and scales s (src/reference/production_math.py:27-31).
+    Checked on oracle-encoded rows for layout B (d=64), layout A (d=128) and a SmolLM2 calibration
+    head; the transposed fold fails the same check; in-place baking equals out-of-place."""
+    import ctypes
+    import bgtq
+    from bgtq import _lib, calibrate
+    m, a = oracle.read_fixture(REF / "model" / "calibration.json")
+    heads = [calibrate.layout_b(64), calibrate.layout_a(128),
+             bgtq.BlockGTQParameters.from_serialized(a["h5_config"], a["h5_table"])]
+    rng = np.random.default_rng(3)
+    for p in heads:
+        d, G, F = p.dim, 3, 40
+        L = oracle.Layout(dim=p.dim, groups=p.groups, row_bytes=p.rowBytes, norm_stride=p.normStride,
+                          nibble_dims=p.nibbleDims, max_centroids=p.maxCentroids, perm=p.permutation,
+                          group_of=p.groupOf, pos_to_cb=p.positionToCodebook, code_lut=p.codeLut,
+                          rotation=p.rotation, centroids=p.centroids, offsets=p.offsets, inv_scales=p.inverseScales)
+        k16 = (rng.standard_normal((50, d)) * 0.9).astype(np.float16)
+        packed, norms = oracle.encode_pack(L, k16.view(np.uint16))
+        codes = oracle.unpack(packed, d, p.nibbleDims)
+        scales = norms.view(np.float16).astype(np.float32)
+        keff = oracle.reconstruct(L, codes, scales).astype(np.float64)
+        cent = np.asarray(p.centroids, np.float64).reshape(d, p.maxCentroids)
+        grp = np.asarray(p.groupOf)
+        y = cent[np.arange(d)[None, :], codes] * scales[:, grp]  # code-domain rows (c s), [rows, d]
+        W = rng.standard_normal((G * d, F)).astype(np.float32)
+        b = rng.standard_normal(G * d).astype(np.float32)
+        Wb, bb = calibrate.bake_qproj(p, W, b)
+        x = rng.standard_normal((F, 5))
+        q = (W.astype(np.float64) @ x + b[:, None]).reshape(G, d, 5)
+        qb = (Wb.astype(np.float64) @ x + bb[:, None]).reshape(G, d, 5)
+        ref = np.einsum("gdn,td->gtn", q, keff)
+        got = np.einsum("gdn,td->gtn", qb, y)
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+        # the fold with the rotation transposed (R^T W[perm]) is a different map unless R is symmetric
+        R = np.asarray(p.rotation, np.float64).reshape(d, d)
+        if not np.allclose(R, R.T):
+            perm = np.asarray(p.permutation)
+            qt = np.stack([R.T @ q[g][perm] for g in range(G)])
+            assert not np.allclose(np.einsum("gdn,td->gtn", qt, y), ref, rtol=1e-3, atol=1e-3)
+        # in place (weight_out = weight, bias_out = bias), as upstream bakes
+        ints, fl = bgtq.tables(p)
+        Wi, bi = W.copy(), b.copy()
+        _lib.check(_lib.lib().bgtq_bake_qproj(_lib.ptr(ints), len(ints), _lib.ptr(fl), len(fl), G, F, _lib.ptr(Wi),
+                                              _lib.ptr(bi), _lib.ptr(Wi), _lib.ptr(bi)))
+        np.testing.assert_array_equal(Wi, Wb)
+        np.testing.assert_array_equal(bi, bb)
+    with pytest.raises(bgtq.RangeError, match="multiple of dim"):
+        calibrate.bake_qproj(heads[0], np.zeros((65, 4), np.float32))
+    ints, fl = bgtq.tables(heads[0])
+    bad = ints.copy()
+    bad[int(bad[6])] = bad[int(bad[6]) + 1]  # perm no longer a permutation
+    z = np.zeros((64, 4), np.float32)
+    assert _lib.lib().bgtq_bake_qproj(_lib.ptr(bad), len(bad), _lib.ptr(fl), len(fl), 1, 4, _lib.ptr(z), None,
+                                      _lib.ptr(z), None) == _lib.ERR_RANGE
