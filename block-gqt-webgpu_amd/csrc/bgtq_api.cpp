@@ -6,12 +6,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -145,6 +147,7 @@ struct bgtq_context {
   hipStream_t own = nullptr;
   hipStream_t stream = nullptr;
   DeviceBuffer staging;      // per-call upload area, never part of an object's ledger
+  std::mutex staging_mutex;  // appends on several threads share the staging area
   uint8_t *scratch = nullptr;  // this device's bgtq_decode_noalloc workspace (library-owned array)
   bgtq_status use() {
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
@@ -175,8 +178,11 @@ struct bgtq_keys {
   int32_t kind = 0;
   bgtq_context *ctx = nullptr;
   bgtq_tables *tables = nullptr;
-  uint32_t dim = 0, capacity = 0, length = 0;
-  bool pending = false;
+  uint32_t dim = 0, capacity = 0;
+  // An append may run on another thread (the Node addon's asynchronous
+  // append) while this thread reads the length or checks readiness.
+  std::atomic<uint32_t> length{0};
+  std::atomic<bool> pending{false};
   DeviceBuffer packed, norms, fp16, decoded;
   Ledger ledger;
 };
@@ -257,6 +263,70 @@ bgtq_status bgtq_context_set_stream(bgtq_context *ctx, void *hip_stream) {
   if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
   ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
   return BGTQ_OK;
+}
+
+// ---------------------------------------------------------------- timestamps
+struct bgtq_timestamps {
+  bgtq_context *ctx = nullptr;
+  std::vector<hipEvent_t> events;
+  std::vector<uint8_t> written;
+};
+
+bgtq_status bgtq_timestamps_create(bgtq_context *ctx, uint32_t count, bgtq_timestamps **out) {
+  if (!ctx || !out) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (count < 1 || count > 4096) return fail(BGTQ_ERR_RANGE, "timestamp count must be 1..4096");
+  if (bgtq_status s = ctx->use()) return s;
+  auto *t = new bgtq_timestamps();
+  t->ctx = ctx;
+  t->written.assign(count, 0);
+  for (uint32_t i = 0; i < count; ++i) {
+    hipEvent_t e = nullptr;
+    hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) {
+      bgtq_timestamps_destroy(t);
+      return hip_fail(err, "timestamp event");
+    }
+    t->events.push_back(e);
+  }
+  *out = t;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_timestamps_write(bgtq_timestamps *t, uint32_t index) {
+  if (!t) return fail(BGTQ_ERR_RANGE, "null timestamps");
+  if (index >= t->events.size()) return fail(BGTQ_ERR_RANGE, "timestamp index %u out of range", index);
+  if (bgtq_status s = t->ctx->use()) return s;
+  HIP_TRY(hipEventRecord(t->events[index], t->ctx->stream), "timestamp write");
+  t->written[index] = 1;
+  return BGTQ_OK;
+}
+
+bgtq_status bgtq_timestamps_resolve(bgtq_timestamps *t, uint32_t first, uint32_t count, uint64_t *ns) {
+  if (!t || (count && !ns)) return fail(BGTQ_ERR_RANGE, "null argument");
+  if (first > t->events.size() || count > t->events.size() - first)
+    return fail(BGTQ_ERR_RANGE, "timestamp range out of range");
+  if (bgtq_status s = t->ctx->use()) return s;
+  // Time base: the first written index of the range, placed at 2^40 ns so
+  // writes before it stay positive.
+  int64_t ref = -1;
+  for (uint32_t i = first; i < first + count && ref < 0; ++i)
+    if (t->written[i]) ref = i;
+  for (uint32_t i = first; i < first + count; ++i) {
+    ns[i - first] = 0;
+    if (!t->written[i]) continue;
+    HIP_TRY(hipEventSynchronize(t->events[i]), "timestamp wait");
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, t->events[ref], t->events[i]), "timestamp resolve");
+    ns[i - first] = (uint64_t)((int64_t)1 << 40) + (uint64_t)std::llround((double)ms * 1e6);
+  }
+  return BGTQ_OK;
+}
+
+void bgtq_timestamps_destroy(bgtq_timestamps *t) {
+  if (!t) return;
+  (void)t->ctx->use();
+  for (hipEvent_t e : t->events) (void)hipEventDestroy(e);
+  delete t;
 }
 
 // ---------------------------------------------------------------- tables
@@ -579,7 +649,9 @@ bgtq_status bgtq_keys_append(bgtq_keys *k, const uint16_t *v, size_t n) {
     k->length += count;
     return BGTQ_OK;
   }
-  k->pending = true;
+  bool idle = false;
+  if (!k->pending.compare_exchange_strong(idle, true)) return fail(BGTQ_ERR_STATE, "Concurrent K appends unsupported");
+  std::lock_guard<std::mutex> lock(ctx->staging_mutex);
   bgtq_status s = ctx->ensure_staging(n * 2);
   if (!s) {
     hipError_t e = hipMemcpy(ctx->staging.ptr, v, n * 2, hipMemcpyHostToDevice);
@@ -606,7 +678,7 @@ bgtq_status bgtq_keys_ready(const bgtq_keys *k) {
   return BGTQ_OK;
 }
 int32_t bgtq_keys_kind(const bgtq_keys *k) { return k ? k->kind : -1; }
-uint32_t bgtq_keys_length(const bgtq_keys *k) { return k ? k->length : 0; }
+uint32_t bgtq_keys_length(const bgtq_keys *k) { return k ? k->length.load() : 0u; }
 uint32_t bgtq_keys_capacity(const bgtq_keys *k) { return k ? k->capacity : 0; }
 uint32_t bgtq_keys_dim(const bgtq_keys *k) { return k ? k->dim : 0; }
 

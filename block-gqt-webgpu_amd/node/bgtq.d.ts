@@ -1,7 +1,8 @@
 // Type declarations for bgtq.js: the reference's public runtime types
 // (src/webgpu/layout.ts:2-5, src/webgpu/buffers.ts:1, src/runtime/keys.ts:3-10,
 // src/attention/attention.ts, src/attention/optimized.ts) with GPUDevice and
-// GPUBuffer replaced by the HIP-backed Device and DeviceView.
+// GPUBuffer replaced by the HIP-backed Device and DeviceView, and the WebGPU
+// encoder / queue / timestamp objects those classes take.
 
 export type BlockGTQParameters = {
   dim: number; groups: number; rowBytes: number; normStride: number; nibbleDims: number; maxCentroids: number;
@@ -10,10 +11,51 @@ export type BlockGTQParameters = {
 };
 export type Allocation = { name: string; role: "persistent-k" | "persistent-v" | "shared" | "scratch"; bytes: number };
 
+export const GPUBufferUsage: {
+  readonly MAP_READ: number; readonly MAP_WRITE: number; readonly COPY_SRC: number; readonly COPY_DST: number;
+  readonly INDEX: number; readonly VERTEX: number; readonly UNIFORM: number; readonly STORAGE: number;
+  readonly INDIRECT: number; readonly QUERY_RESOLVE: number;
+};
+export const GPUMapMode: { readonly READ: number; readonly WRITE: number };
+
+/** GPUQuerySet of type "timestamp": HIP events on the context's stream. */
+export class QuerySet { readonly device: Device; readonly type: "timestamp"; readonly count: number; destroy(): void; }
+export type TimestampWrites = { querySet: QuerySet; beginningOfPassWriteIndex?: number; endOfPassWriteIndex?: number };
+/** A compute pass holds the library's work; WGSL pipeline calls throw. */
+export class ComputePass { end(): void; }
+export class CommandBuffer {}
+/** GPUCommandEncoder: recorded work runs on the device at queue.submit, in order. */
+export class CommandEncoder {
+  readonly device: Device;
+  beginComputePass(descriptor?: { timestampWrites?: TimestampWrites }): ComputePass;
+  resolveQuerySet(querySet: QuerySet, firstQuery: number, queryCount: number, destination: HostBuffer,
+                  destinationOffset?: number): void;
+  copyBufferToBuffer(source: StorageBuffer | HostBuffer | DeviceView, sourceOffset: number,
+                     destination: StorageBuffer | HostBuffer, destinationOffset: number, size: number): void;
+  finish(): CommandBuffer;
+}
+/** A mappable (MAP_READ / MAP_WRITE) or query-resolve buffer in host memory. */
+export class HostBuffer {
+  readonly device: Device; readonly size: number; readonly usage: number;
+  mapAsync(mode: number): Promise<void>;
+  getMappedRange(offset?: number, size?: number): ArrayBuffer;
+  unmap(): void;
+  destroy(): void;
+}
+export class Queue {
+  submit(commandBuffers: CommandBuffer[]): void;
+  /** Resolves off the JS thread once the device finished the submitted work. */
+  onSubmittedWorkDone(): Promise<void>;
+  writeBuffer(buffer: StorageBuffer | HostBuffer, offset: number, data: ArrayBufferView | ArrayBuffer,
+              dataOffset?: number, size?: number): void;
+}
 export class Device {
   readonly index: number;
-  readonly limits: { maxComputeWorkgroupsPerDimension: number };
-  readonly queue: { onSubmittedWorkDone(): Promise<void> };
+  readonly limits: { maxComputeWorkgroupsPerDimension: number; maxBufferSize: number; maxStorageBufferBindingSize: number };
+  readonly queue: Queue;
+  createCommandEncoder(): CommandEncoder;
+  createQuerySet(descriptor: { type: "timestamp"; count: number }): QuerySet;
+  createBuffer(descriptor: { size: number; usage: number; label?: string }): StorageBuffer | HostBuffer;
   destroy(): void;
 }
 export function requestDevice(index?: number): Promise<Device>;
@@ -27,7 +69,7 @@ export function readBuffer<T extends ArrayBufferView>(device: Device, view: Devi
 export class StorageBuffer { readonly device: Device; readonly size: number; readonly label: string; destroy(): void; }
 export function storage(device: Device, bytes: number, label: string): StorageBuffer;
 export function upload(device: Device, buffer: StorageBuffer, values: ArrayBufferView, offset?: number): void;
-export function readBuffer(device: Device, buffer: StorageBuffer, bytes?: number): Promise<ArrayBuffer>;
+export function readBuffer(device: Device, buffer: StorageBuffer | HostBuffer, bytes?: number): Promise<ArrayBuffer>;
 /** src/model/ops.ts: the attention-path names append, encode_k, dot, compressed_dot, softmax, weighted. */
 export class ModelOps {
   static create(device: Device): Promise<ModelOps>;
@@ -55,7 +97,7 @@ export interface KeyStore {
   readonly device: Device; readonly dim: number; readonly capacity: number; readonly length: number;
   readonly allocations: Allocation[]; readonly kind: "fp16" | "block-gtq";
   append(values: Uint16Array): Promise<void>;
-  prepare(): KeyView;
+  prepare(encoder?: CommandEncoder, start?: TimestampWrites): KeyView;
   destroy(): void;
 }
 
@@ -65,7 +107,7 @@ export class FP16Keys implements KeyStore {
   readonly allocations: Allocation[]; readonly kind: "fp16";
   readonly buffer: DeviceView<Uint16Array>;
   append(values: Uint16Array): Promise<void>;
-  prepare(): KeyView;
+  prepare(encoder?: CommandEncoder, start?: TimestampWrites): KeyView;
   destroy(): void;
 }
 
@@ -82,7 +124,8 @@ export class PackedKeys {
 }
 export class CompressedKeys extends PackedKeys implements KeyStore {
   static create(device: Device, p: BlockGTQParameters, capacity: number): Promise<CompressedKeys>;
-  prepare(): KeyView;
+  /** A pass materialising FP32 K (with the caller's start timestamp), recorded into encoder. */
+  prepare(encoder?: CommandEncoder, start?: TimestampWrites): KeyView;
 }
 
 export class Values {
@@ -101,7 +144,8 @@ declare class Session {
   readonly device: Device; readonly maxQueries: number; readonly allocations: Allocation[];
   readonly output: DeviceView<Float32Array>;
   setQueries(q: Float32Array, positions: Uint32Array, causal?: boolean): void;
-  record(): void;
+  /** One compute pass (timestamps index 0 at its start, 1 at its end); without an encoder, queued at once. */
+  record(encoder?: CommandEncoder, timestamps?: QuerySet): void;
   attend(q: Float32Array, positions: Uint32Array, causal?: boolean): Promise<DeviceView<Float32Array>>;
   inspect(): Inspection;
   destroy(): void;

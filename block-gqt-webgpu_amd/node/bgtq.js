@@ -15,14 +15,171 @@ const DTYPE_F32 = 0;
 const DTYPE_F16 = 1;
 
 // ---- GPUDevice facade ----------------------------------------------------
+// createCommandEncoder / queue.submit / queue.onSubmittedWorkDone /
+// createQuerySet / createBuffer keep the shapes of the WebGPU objects the
+// reference's runtime classes, tests and benchmarks use
+// (src/attention/attention.ts:44-58, benchmarks/timing.ts:7-31). Work a class
+// records into an encoder runs on the device when the command buffer is
+// submitted, in recording order; onSubmittedWorkDone resolves off the JS
+// thread once the device has finished it.
+const GPUBufferUsage = Object.freeze({ MAP_READ: 0x1, MAP_WRITE: 0x2, COPY_SRC: 0x4, COPY_DST: 0x8, INDEX: 0x10,
+  VERTEX: 0x20, UNIFORM: 0x40, STORAGE: 0x80, INDIRECT: 0x100, QUERY_RESOLVE: 0x200 });
+const GPUMapMode = Object.freeze({ READ: 0x1, WRITE: 0x2 });
+
+class Queue {
+  constructor(device) { this.device = device; }
+  submit(commandBuffers) {
+    for (const b of commandBuffers) {
+      if (!(b instanceof CommandBuffer) || !b._ops) throw new Error('Invalid or already submitted command buffer');
+      const ops = b._ops;
+      b._ops = null;
+      for (const op of ops) op();
+    }
+  }
+  onSubmittedWorkDone() { return native.contextSynchronizeAsync(this.device.handle); }
+  writeBuffer(buffer, offset, data, dataOffset, size) {
+    const bytes = new Uint8Array(data.buffer || data, (data.byteOffset || 0) + (dataOffset || 0),
+      size === undefined ? (data.byteLength - (dataOffset || 0)) : size);
+    if (buffer instanceof HostBuffer) { buffer._write(offset, bytes); return; }
+    if (offset % 4 || bytes.byteLength % 4 || offset + bytes.byteLength > buffer.size) {
+      throw new RangeError('Unaligned/out-of-range buffer upload');
+    }
+    native.bufferWrite(buffer.handle, offset, bytes);
+  }
+}
+
+// GPUQuerySet of type "timestamp" (HIP events on the context's stream).
+class QuerySet {
+  constructor(device, descriptor) {
+    if (!descriptor || descriptor.type !== 'timestamp') throw new TypeError('Only timestamp query sets are supported');
+    if (!Number.isInteger(descriptor.count) || descriptor.count < 1 || descriptor.count > 4096) {
+      throw new RangeError('Invalid query set count');
+    }
+    this.device = device; this.type = 'timestamp'; this.count = descriptor.count;
+    this.handle = native.timestampsCreate(device.handle, this.count);
+  }
+  destroy() { if (this.handle) native.timestampsDestroy(this.handle); this.handle = null; }
+}
+
+class CommandBuffer { constructor(ops) { this._ops = ops; } }
+
+// A compute pass: its timestampWrites and the library work queued in it
+// (_enqueue). WGSL pipelines do not exist on this device, so the raw
+// setPipeline / dispatchWorkgroups calls are refused.
+class ComputePass {
+  constructor(encoder, descriptor) {
+    this._encoder = encoder; this._ended = false;
+    const tw = descriptor.timestampWrites;
+    this._endWrite = tw && tw.endOfPassWriteIndex !== undefined ? [tw.querySet, tw.endOfPassWriteIndex] : null;
+    if (tw && tw.beginningOfPassWriteIndex !== undefined) encoder._timestamp(tw.querySet, tw.beginningOfPassWriteIndex);
+  }
+  _enqueue(fn) {
+    if (this._ended) throw new Error('Compute pass already ended');
+    this._encoder._ops.push(fn);
+  }
+  setPipeline() { throw new Error('WGSL pipelines do not run on this device; record through the library classes'); }
+  setBindGroup() { throw new Error('WGSL pipelines do not run on this device; record through the library classes'); }
+  dispatchWorkgroups() { throw new Error('WGSL pipelines do not run on this device; record through the library classes'); }
+  end() {
+    if (this._ended) throw new Error('Compute pass already ended');
+    this._ended = true;
+    if (this._endWrite) this._encoder._timestamp(this._endWrite[0], this._endWrite[1]);
+  }
+}
+
+class CommandEncoder {
+  constructor(device) { this.device = device; this._ops = []; }
+  _live() { if (!this._ops) throw new Error('Command encoder already finished'); }
+  _timestamp(querySet, index) {
+    this._live();
+    if (!(querySet instanceof QuerySet) || !Number.isInteger(index) || index < 0 || index >= querySet.count) {
+      throw new RangeError('Invalid timestamp write');
+    }
+    this._ops.push(() => native.timestampsWrite(querySet.handle, index));
+  }
+  beginComputePass(descriptor) { this._live(); return new ComputePass(this, descriptor || {}); }
+  resolveQuerySet(querySet, firstQuery, queryCount, destination, destinationOffset) {
+    this._live();
+    const off = destinationOffset || 0;
+    if (!(querySet instanceof QuerySet) || firstQuery + queryCount > querySet.count || !(destination instanceof HostBuffer) ||
+        off % 8 || off + 8 * queryCount > destination.size) {
+      throw new RangeError('Invalid query set resolve');
+    }
+    this._ops.push(() => destination._defer(() => destination._write(off,
+      native.timestampsResolve(querySet.handle, firstQuery, queryCount))));
+  }
+  copyBufferToBuffer(source, sourceOffset, destination, destinationOffset, size) {
+    this._live();
+    if (sourceOffset % 4 || destinationOffset % 4 || size % 4 || destinationOffset + size > destination.size ||
+        (source.size !== undefined && sourceOffset + size > source.size)) {
+      throw new RangeError('Invalid buffer copy');
+    }
+    const bytes = () => sourceBytes(source, sourceOffset, size);
+    if (destination instanceof HostBuffer) {
+      this._ops.push(() => destination._defer(() => destination._write(destinationOffset, bytes())));
+    } else {
+      this._ops.push(() => native.bufferWrite(destination.handle, destinationOffset, bytes()));
+    }
+  }
+  finish() { this._live(); const b = new CommandBuffer(this._ops); this._ops = null; return b; }
+}
+
+// A buffer the host maps (MAP_READ / MAP_WRITE) or that receives resolved
+// queries: host memory whose copies and resolves, recorded in order, are
+// carried out once the device has finished the work queued before them.
+class HostBuffer {
+  constructor(device, size, usage) {
+    this.device = device; this.size = size; this.usage = usage;
+    this._data = new ArrayBuffer(size); this._pending = []; this._mapped = false;
+  }
+  _defer(fn) { this._pending.push(fn); }
+  _flush() { const p = this._pending; this._pending = []; for (const fn of p) fn(); }
+  _write(offset, view) {
+    const src = new Uint8Array(view.buffer, view.byteOffset, view.byteLength);
+    new Uint8Array(this._data, offset, src.byteLength).set(src);
+  }
+  _bytes(offset, size) { this._flush(); return new Uint8Array(this._data.slice(offset, offset + size)); }
+  async mapAsync(mode) {
+    if (!(mode & (GPUMapMode.READ | GPUMapMode.WRITE))) throw new RangeError('Invalid map mode');
+    await this.device.queue.onSubmittedWorkDone();
+    this._flush();
+    this._mapped = true;
+  }
+  getMappedRange(offset, size) {
+    if (!this._mapped) throw new Error('Buffer is not mapped');
+    offset = offset || 0;
+    return this._data.slice(offset, size === undefined ? this.size : offset + size);
+  }
+  unmap() { this._mapped = false; }
+  destroy() { this._data = new ArrayBuffer(0); this._pending = []; }
+}
+
+function sourceBytes(source, offset, size) {
+  if (source instanceof HostBuffer) return source._bytes(offset, size);
+  if (source instanceof DeviceView) {
+    const a = source.read();
+    return new Uint8Array(a.buffer, a.byteOffset + offset, size).slice();
+  }
+  return native.bufferRead(source.handle, offset, size);
+}
+
 class Device {
   constructor(index) {
     this.index = index === undefined ? 0 : index;
     this.handle = native.contextCreate(this.index);
     // HBM bounds capacity here, not the WebGPU dispatch limit.
-    this.limits = { maxComputeWorkgroupsPerDimension: 0x7fffffff };
-    const self = this;
-    this.queue = { onSubmittedWorkDone: async function () { native.contextSynchronize(self.handle); } };
+    this.limits = { maxComputeWorkgroupsPerDimension: 0x7fffffff, maxBufferSize: MAX_BUFFER_SIZE,
+                    maxStorageBufferBindingSize: MAX_BUFFER_SIZE };
+    this.queue = new Queue(this);
+  }
+  createCommandEncoder() { return new CommandEncoder(this); }
+  createQuerySet(descriptor) { return new QuerySet(this, descriptor); }
+  createBuffer(descriptor) {
+    const usage = descriptor.usage || 0;
+    if (usage & (GPUBufferUsage.MAP_READ | GPUBufferUsage.MAP_WRITE | GPUBufferUsage.QUERY_RESOLVE)) {
+      return new HostBuffer(this, descriptor.size, usage);
+    }
+    return storage(this, descriptor.size, descriptor.label || 'buffer');
   }
   destroy() {
     if (this.handle) native.contextDestroy(this.handle);
@@ -65,6 +222,10 @@ function upload(device, buffer, values, offset) {
 }
 async function readBuffer(device, buffer, bytes) {
   if (buffer instanceof DeviceView) return buffer.read();
+  if (buffer instanceof HostBuffer) {
+    await device.queue.onSubmittedWorkDone();
+    return buffer._bytes(0, bytes === undefined ? buffer.size : bytes).buffer;
+  }
   bytes = bytes === undefined ? buffer.size : bytes;
   if (bytes % 4 || bytes > buffer.size) throw new RangeError('Invalid readback length');
   return native.bufferRead(buffer.handle, 0, bytes);
@@ -173,11 +334,31 @@ class FP16Keys {
   }
   get length() { return native.keysLength(this.handle); }
   async append(values) {
+    if (this._pending) throw new Error('Concurrent K appends unsupported');
     appendCount(values, this.dim, this.length, this.capacity);
-    native.keysAppend(this.handle, values);
+    await runAppend(this, values);
   }
   prepare() { return { buffer: this.buffer, format: 'f16' }; }
-  destroy() { if (this.handle) native.keysDestroy(this.handle); this.handle = null; }
+  destroy() { destroyAfterAppend(this); }
+}
+
+// The append runs off the JS thread and its Promise resolves once the rows
+// are on the device (src/runtime/packed-keys.ts:39-49); destroy() during an
+// append waits for it.
+async function runAppend(keys, values) {
+  keys._pending = true;
+  try {
+    await native.keysAppendAsync(keys.handle, values);
+  } finally {
+    keys._pending = false;
+    if (keys._destroyRequested) keys.destroy();
+  }
+}
+function destroyAfterAppend(keys) {
+  if (keys._pending) { keys._destroyRequested = true; return; }
+  if (keys.handle) native.keysDestroy(keys.handle);
+  if (keys.tablesHandle) native.tablesDestroy(keys.tablesHandle);
+  keys.handle = keys.tablesHandle = null;
 }
 
 class PackedKeys {
@@ -204,21 +385,27 @@ class PackedKeys {
   static async create(device, p, capacity) { return new PackedKeys(device, p, capacity, false); }
   get length() { return native.keysLength(this.handle); }
   async append(values) {
+    if (this._pending) throw new Error('Concurrent K appends unsupported');
     appendCount(values, this.dim, this.length, this.capacity);
-    native.keysAppend(this.handle, values);  // resolves after the encode has completed
+    await runAppend(this, values);
   }
   ready() { native.keysReady(this.handle); }
-  destroy() {
-    if (this.handle) native.keysDestroy(this.handle);
-    if (this.tablesHandle) native.tablesDestroy(this.tablesHandle);
-    this.handle = this.tablesHandle = null;
-  }
+  destroy() { destroyAfterAppend(this); }
 }
 
 class CompressedKeys extends PackedKeys {
   static async create(device, p, capacity) { return new CompressedKeys(device, p, capacity, true); }
-  prepare() {
+  // prepare(encoder, start?) (src/runtime/compressed-keys.ts:51-57): a pass
+  // that materialises FP32 K, with the caller's start timestamp; the view
+  // reads the materialised rows.
+  prepare(encoder, start) {
+    if (this._pending) throw new Error('K append is still pending');
     const self = this;
+    if (encoder) {
+      const pass = encoder.beginComputePass(start ? { timestampWrites: start } : {});
+      pass._enqueue(() => native.keysPrepareDevice(self.handle));
+      pass.end();
+    }
     return { buffer: new DeviceView(() => native.keysPrepare(self.handle, self.length * self.dim)), format: 'f32' };
   }
 }
@@ -254,10 +441,28 @@ class Session {
     this._probabilities = new DeviceView(() => native.attentionRead(self.handle, 1, q() * self.keys.length));
   }
   setQueries(q, positions, causal) { native.attentionSetQueries(this.handle, q, positions, !!causal); }
-  record() { native.attentionRecord(this.handle); }
+  // record(encoder, timestamps?) (src/attention/attention.ts:44-58): one
+  // compute pass (the fused kernel), timestamps index 0 at its start and 1 at
+  // its end. Readiness is checked now, as the reference's record does; the
+  // launch happens when the command buffer is submitted. Without an encoder
+  // the work is queued at once.
+  record(encoder, timestamps) {
+    if (encoder === undefined) { native.attentionRecord(this.handle); return; }
+    if (this._optimized) this.keys.ready();
+    if (!native.attentionQueries(this.handle) || this.keys.length !== this.values.length) {
+      throw new Error(this._optimized ? 'Attention not ready' : 'Queries/storage not ready');
+    }
+    const pass = encoder.beginComputePass(timestamps
+      ? { timestampWrites: { querySet: timestamps, beginningOfPassWriteIndex: 0, endOfPassWriteIndex: 1 } } : {});
+    const h = this.handle;
+    pass._enqueue(() => native.attentionRecord(h));
+    pass.end();
+  }
   async attend(q, positions, causal) {
     this.setQueries(q, positions, causal);
-    this.record();
+    const encoder = this.device.createCommandEncoder();
+    this.record(encoder);
+    this.device.queue.submit([encoder.finish()]);
     await this.device.queue.onSubmittedWorkDone();
     return this.output;
   }
@@ -272,6 +477,7 @@ class OptimizedAttention extends Session {
   static async create(device, keys, values, maxQueries, tailMode) {
     const s = new OptimizedAttention(device, keys, values, maxQueries === undefined ? 3 : maxQueries, true);
     s.tailMode = tailMode === undefined ? 'parallel' : tailMode;
+    s._optimized = true;
     return s;
   }
 }
@@ -363,6 +569,7 @@ class Calibration {
 
 module.exports = {
   native, Device, requestDevice, DeviceView, readBuffer, storage, upload, StorageBuffer, ModelOps, Commands,
+  GPUBufferUsage, GPUMapMode, CommandEncoder, ComputePass, CommandBuffer, Queue, QuerySet, HostBuffer,
   validateLayout, tables, appendCount, allocateBits, layoutGroups, buildTables,
   FP16Keys, PackedKeys, CompressedKeys, Values, OptimizedAttention, AttentionEngine, AttentionSession, Calibration,
 };

@@ -11,6 +11,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -563,6 +564,121 @@ napi_value ModelSubmit(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---- work off the JS thread -------------------------------------------------
+// A library call run by napi_async_work on a worker thread: the returned
+// Promise resolves once the call (and the device work it waits for) has
+// completed, or rejects with the call's RangeError / Error. The thread-local
+// error message is taken on the worker thread.
+struct AsyncCall {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  std::function<bgtq_status()> fn;
+  std::vector<uint16_t> data;  // a copy of the caller's typed array, owned by the call
+  bgtq_status status = BGTQ_OK;
+  std::string message;
+};
+
+void async_execute(napi_env, void *p) {
+  auto *c = static_cast<AsyncCall *>(p);
+  c->status = c->fn();
+  if (c->status != BGTQ_OK) c->message = bgtq_last_error();
+}
+
+void async_complete(napi_env env, napi_status, void *p) {
+  auto *c = static_cast<AsyncCall *>(p);
+  if (c->status == BGTQ_OK) {
+    napi_resolve_deferred(env, c->deferred, undefined(env));
+  } else {
+    napi_value msg, err;
+    napi_create_string_utf8(env, c->message.c_str(), NAPI_AUTO_LENGTH, &msg);
+    if (c->status == BGTQ_ERR_RANGE) napi_create_range_error(env, nullptr, msg, &err);
+    else napi_create_error(env, nullptr, msg, &err);
+    napi_reject_deferred(env, c->deferred, err);
+  }
+  napi_delete_async_work(env, c->work);
+  delete c;
+}
+
+napi_value start_async(napi_env env, AsyncCall *c, const char *name) {
+  napi_value promise, res;
+  if (napi_create_promise(env, &c->deferred, &promise) != napi_ok ||
+      napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &res) != napi_ok ||
+      napi_create_async_work(env, nullptr, res, async_execute, async_complete, c, &c->work) != napi_ok ||
+      napi_queue_async_work(env, c->work) != napi_ok) {
+    delete c;
+    napi_throw_error(env, nullptr, "could not queue asynchronous work");
+    return nullptr;
+  }
+  return promise;
+}
+
+// keysAppendAsync(keys, Uint16Array) -> Promise: PackedKeys/CompressedKeys/FP16Keys.append,
+// resolved after the encode has completed (src/runtime/packed-keys.ts:39-49).
+napi_value KeysAppendAsync(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  uint16_t *bits;
+  size_t n;
+  if (!typed(env, a.v[1], napi_uint16_array, &bits, &n)) return nullptr;
+  auto *c = new AsyncCall();
+  c->data.assign(bits, bits + n);
+  bgtq_keys *k = static_cast<bgtq_keys *>(handle(env, a.v[0]));
+  c->fn = [c, k]() { return bgtq_keys_append(k, c->data.data(), c->data.size()); };
+  return start_async(env, c, "bgtq.keysAppend");
+}
+
+// contextSynchronizeAsync(ctx) -> Promise: device.queue.onSubmittedWorkDone().
+napi_value ContextSynchronizeAsync(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  auto *c = new AsyncCall();
+  bgtq_context *ctx = static_cast<bgtq_context *>(handle(env, a.v[0]));
+  c->fn = [ctx]() { return bgtq_context_synchronize(ctx); };
+  return start_async(env, c, "bgtq.onSubmittedWorkDone");
+}
+
+// keysPrepareDevice(keys): CompressedKeys.prepare's materialisation, queued on the stream.
+napi_value KeysPrepareDevice(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  BGTQ_TRY(env, bgtq_keys_prepare(static_cast<bgtq_keys *>(handle(env, a.v[0])), nullptr, 0));
+  return undefined(env);
+}
+
+// ---- timestamps (GPUQuerySet of type "timestamp") ---------------------------
+napi_value TimestampsCreate(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  bgtq_timestamps *t = nullptr;
+  BGTQ_TRY(env, bgtq_timestamps_create(static_cast<bgtq_context *>(handle(env, a.v[0])),
+                                       (uint32_t)to_i64(env, a.v[1]), &t));
+  return wrap(env, t);
+}
+napi_value TimestampsWrite(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  BGTQ_TRY(env, bgtq_timestamps_write(static_cast<bgtq_timestamps *>(handle(env, a.v[0])),
+                                      (uint32_t)to_i64(env, a.v[1])));
+  return undefined(env);
+}
+napi_value TimestampsResolve(napi_env env, napi_callback_info info) {
+  // -> BigUint64Array of `count` nanosecond timestamps
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  const uint32_t first = (uint32_t)to_i64(env, a.v[1]), count = (uint32_t)to_i64(env, a.v[2]);
+  uint64_t *ns;
+  napi_value out = new_typed<uint64_t>(env, napi_biguint64_array, count, &ns);
+  if (!out) return nullptr;
+  BGTQ_TRY(env, bgtq_timestamps_resolve(static_cast<bgtq_timestamps *>(handle(env, a.v[0])), first, count, ns));
+  return out;
+}
+napi_value TimestampsDestroy(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  bgtq_timestamps_destroy(static_cast<bgtq_timestamps *>(handle(env, a.v[0])));
+  return undefined(env);
+}
+
 napi_value Init(napi_env env, napi_value exports) {
   struct Fn {
     const char *name;
@@ -587,6 +703,10 @@ napi_value Init(napi_env env, napi_value exports) {
       {"bufferDestroy", BufferDestroy},       {"modelSubmit", ModelSubmit},
       {"allocateBits", AllocateBits},         {"layoutGroups", LayoutGroups},
       {"layoutBuild", LayoutBuild},
+      {"keysAppendAsync", KeysAppendAsync},   {"contextSynchronizeAsync", ContextSynchronizeAsync},
+      {"keysPrepareDevice", KeysPrepareDevice}, {"timestampsCreate", TimestampsCreate},
+      {"timestampsWrite", TimestampsWrite},   {"timestampsResolve", TimestampsResolve},
+      {"timestampsDestroy", TimestampsDestroy},
   };
   for (const Fn &f : fns) {
     napi_value fn;

@@ -1,7 +1,9 @@
 'use strict';
 // Drop-in check through the Node classes (needs a GPU): the reference's
-// optimized-attention flow (tests/webgpu/optimized-test.ts:18-45) on a
-// committed golden workload. Packed K and FP16 scales must equal the
+// attention validation flow (tests/webgpu/attention-test.ts:21-60), its
+// optimized-attention flow (tests/webgpu/optimized-test.ts:18-45) and the
+// encoder timing proxy of benchmarks/timing.ts:7-31 on committed golden
+// workloads. Packed K and FP16 scales must equal the
 // reference encoder's bytes; outputs must match the golden within the
 // fixture's baseline tolerance; rejections keep the reference's messages.
 //     node block-gqt-webgpu_amd/node/test_napi.js [fixture dir]
@@ -45,8 +47,129 @@ async function rejects(fn, type, message, what) {
   }
 }
 
+// Element-wise |actual - expected| <= atol + rtol |expected| (both -Infinity counts as equal),
+// the rule of the reference's tests/webgpu/compare.ts.
+function within(actual, expected, tol) {
+  if (actual.length !== expected.length) return false;
+  for (let i = 0; i < actual.length; i++) {
+    if (actual[i] === -Infinity && expected[i] === -Infinity) continue;
+    if (!(Math.abs(actual[i] - expected[i]) <= tol[0] + tol[1] * Math.abs(expected[i]))) return false;
+  }
+  return true;
+}
+
+// The reference's attention validation flow (tests/webgpu/attention-test.ts:21-60) over this
+// device: FP16 and compressed key stores appended in two calls (an odd row boundary), an
+// incomplete session refused, the compressed store's prepare(encoder) recorded, submitted and read
+// back, rejections, then causal and non-causal attend() with every stage within the fixture's
+// tolerances, probabilities summing to one and the first causal query returning V0 exactly.
+async function attentionTestFlow(device, name) {
+  const { meta: m, arrays: f } = readFixture(path.join(FIXTURES, 'attention', name + '.json'));
+  const lay = readFixture(path.join(FIXTURES, 'mixed', m.layout + '.json'));
+  const parameters = parametersFromMixed(lay.meta, lay.arrays);
+  const engine = await bgtq.AttentionEngine.create(device);
+  const T = m.context_length, d = m.dim;
+  const values = new bgtq.Values(device, d, T);
+  const paths = [new bgtq.FP16Keys(device, d, T), await bgtq.CompressedKeys.create(device, parameters, T)];
+  try {
+    for (const keys of paths) {
+      await keys.append(f.k.subarray(0, 3 * d));
+      const incomplete = engine.session(keys, values, m.queries);
+      try {
+        await rejects(() => incomplete.setQueries(f.q, f.positions), RangeError, 'K/V lengths must match and be nonzero',
+          `${name} ${keys.kind}: mismatched K/V lengths`);
+      } finally { incomplete.destroy(); }
+      await keys.append(f.k.subarray(3 * d));
+    }
+    values.append(f.v.subarray(0, 3 * d));
+    values.append(f.v.subarray(3 * d));
+    for (const keys of paths) {
+      const label = keys.kind === 'fp16' ? 'baseline' : 'compressed';
+      const session = engine.session(keys, values, m.queries);
+      try {
+        if (keys.kind === 'block-gtq') {
+          const encoder = device.createCommandEncoder(), view = keys.prepare(encoder);
+          device.queue.submit([encoder.finish()]);
+          const decoded = new Float32Array((await bgtq.readBuffer(device, view.buffer, T * d * 4)).buffer);
+          check(within(decoded, f.reconstructed_k, [1e-4, 0]), `${name}: prepare(encoder) materialises the reconstructed K`);
+        }
+        await rejects(() => keys.append(new Uint16Array(d)), RangeError, 'K capacity exceeded', `${name} ${label}: capacity`);
+        await rejects(() => session.setQueries(new Float32Array(d - 1), new Uint32Array([0])), RangeError,
+          'Invalid query shape or causal positions', `${name} ${label}: query shape`);
+        await rejects(() => session.setQueries(f.q, new Uint32Array([0, 0, T])), RangeError,
+          'Invalid query shape or causal positions', `${name} ${label}: query position`);
+        for (const causal of [false, true]) {
+          await session.attend(f.q, f.positions, causal);
+          const ins = session.inspect(), prefix = causal ? 'causal_' : '';
+          const got = {
+            logits: await bgtq.readBuffer(device, ins.logits), probabilities: await bgtq.readBuffer(device, ins.probabilities),
+            output: await bgtq.readBuffer(device, ins.output),
+          };
+          for (const stage of ['logits', 'probabilities', 'output']) {
+            const tol = m.tolerances[label === 'baseline' ? 'baseline' : 'port'][stage];
+            check(within(got[stage], f[`${prefix}${label}_${stage}`], tol), `${name} ${label} causal=${causal}: ${stage}`);
+          }
+          let sums = true, zeros = true;
+          for (let r = 0; r < m.queries; r++) {
+            let sum = 0;
+            for (let t = 0; t < T; t++) {
+              const pr = got.probabilities[r * T + t];
+              sum += pr;
+              if (pr < 0 || (causal && t > f.positions[r] && pr !== 0)) zeros = false;
+            }
+            if (Math.abs(sum - 1) > 1e-4) sums = false;
+          }
+          check(sums && zeros, `${name} ${label} causal=${causal}: probabilities sum to one, causal zeros`);
+          if (causal) check(got.output.subarray(0, d).every((x, i) => x === f.v[i]), `${name} ${label}: first causal query = V0`);
+        }
+      } finally { session.destroy(); }
+    }
+  } finally { paths.forEach((k) => k.destroy()); values.destroy(); }
+}
+
+// The timing flow of benchmarks/timing.ts:7-31 as a caller writes it against WebGPU: a
+// timestamp query set, a resolve buffer, a mappable readback buffer, and an encoder proxy that
+// adds timestampWrites to every compute pass the recorded work begins; per-pass durations from
+// the resolved timestamps.
+async function timePasses(device, record, passes, warmups, repetitions) {
+  const query = device.createQuerySet({ type: 'timestamp', count: passes * 2 });
+  const resolved = device.createBuffer({ size: passes * 16, usage: bgtq.GPUBufferUsage.QUERY_RESOLVE | bgtq.GPUBufferUsage.COPY_SRC });
+  const mapped = device.createBuffer({ size: passes * 16, usage: bgtq.GPUBufferUsage.COPY_DST | bgtq.GPUBufferUsage.MAP_READ });
+  const samples = Array.from({ length: passes }, () => []);
+  try {
+    for (let r = -warmups; r < repetitions; r++) {
+      const encoder = device.createCommandEncoder();
+      let index = 0;
+      const proxy = new Proxy(encoder, {
+        get(target, key) {
+          if (key === 'beginComputePass') {
+            return (descriptor) => {
+              const i = index++;
+              return target.beginComputePass(Object.assign({}, descriptor || {}, {
+                timestampWrites: { querySet: query, beginningOfPassWriteIndex: i * 2, endOfPassWriteIndex: i * 2 + 1 } }));
+            };
+          }
+          const v = Reflect.get(target, key, target);
+          return typeof v === 'function' ? v.bind(target) : v;
+        },
+      });
+      record(proxy);
+      if (index !== passes) throw new Error(`Expected ${passes} passes, got ${index}`);
+      encoder.resolveQuerySet(query, 0, passes * 2, resolved, 0);
+      encoder.copyBufferToBuffer(resolved, 0, mapped, 0, passes * 16);
+      device.queue.submit([encoder.finish()]);
+      await mapped.mapAsync(bgtq.GPUMapMode.READ);
+      const t = new BigUint64Array(mapped.getMappedRange());
+      if (r >= 0) for (let i = 0; i < passes; i++) samples[i].push(Number(t[i * 2 + 1] - t[i * 2]) / 1000);
+      mapped.unmap();
+    }
+    return samples;
+  } finally { query.destroy(); resolved.destroy(); mapped.destroy(); }
+}
+
 async function main() {
   const device = await bgtq.requestDevice(0);
+  for (const name of ['t128_d64', 't512_d128']) await attentionTestFlow(device, name);
   for (const name of ['t128_d64', 't256_d128']) {
     const { meta, arrays: a } = readFixture(path.join(FIXTURES, 'attention', name + '.json'));
     const lay = readFixture(path.join(FIXTURES, 'mixed', meta.layout + '.json'));
@@ -80,6 +203,51 @@ async function main() {
     await rejects(() => att.attend(a.q, new Uint32Array([0, 1, T]), false), RangeError,
       'Invalid Q/K/V shape or positions', `${name}: position out of range`);
     att.destroy(); values.destroy(); keys.destroy();
+  }
+  {
+    // Encoder timing proxy over OptimizedAttention.record (one fused pass) and
+    // AttentionSession.record(encoder, timestamps) with its own query set.
+    const { meta, arrays: a } = readFixture(path.join(FIXTURES, 'attention', 't512_d128.json'));
+    const lay = readFixture(path.join(FIXTURES, 'mixed', meta.layout + '.json'));
+    const p = parametersFromMixed(lay.meta, lay.arrays);
+    const T = meta.context_length, d = meta.dim;
+    const keys = await bgtq.PackedKeys.create(device, p, T);
+    const values = new bgtq.Values(device, d, T);
+    const att = await bgtq.OptimizedAttention.create(device, keys, values, meta.queries);
+    // The append resolves off the JS thread: while it runs the store is pending.
+    const first = keys.append(a.k.subarray(0, 100 * d));
+    await rejects(() => keys.append(a.k.subarray(100 * d)), Error, 'Concurrent K appends unsupported',
+      'append: a second append while one is pending');
+    let pendingReady = false;
+    try { keys.ready(); } catch (e) { pendingReady = e.message === 'K storage not ready'; }
+    check(pendingReady, 'append: the store is not ready while its append runs');
+    await first;
+    await keys.append(a.k.subarray(100 * d));
+    check(keys.length === T, 'append: both appends committed');
+    values.append(a.v);
+    att.setQueries(a.q, a.positions, false);
+    const samples = await timePasses(device, (e) => att.record(e), 1, 2, 5);
+    check(samples[0].length === 5 && samples[0].every((x) => x > 0 && x < 1e6),
+      `timing proxy: 5 samples of the fused pass, median ${samples[0].slice().sort((x, y) => x - y)[2].toFixed(1)} us`);
+    const engine = await bgtq.AttentionEngine.create(device);
+    const fk = new bgtq.FP16Keys(device, d, T);
+    await fk.append(a.k);
+    const session = engine.session(fk, values, meta.queries);
+    session.setQueries(a.q, a.positions, true);
+    const qs = device.createQuerySet({ type: 'timestamp', count: 2 });
+    const res = device.createBuffer({ size: 16, usage: bgtq.GPUBufferUsage.QUERY_RESOLVE | bgtq.GPUBufferUsage.COPY_SRC });
+    const enc = device.createCommandEncoder();
+    session.record(enc, qs);
+    enc.resolveQuerySet(qs, 0, 2, res, 0);
+    device.queue.submit([enc.finish()]);
+    const stamps = new BigUint64Array(await bgtq.readBuffer(device, res));
+    check(stamps[1] > stamps[0], `record(encoder, timestamps): ${(Number(stamps[1] - stamps[0]) / 1000).toFixed(1)} us`);
+    const out = await bgtq.readBuffer(device, session.output);
+    check(within(out, a.causal_baseline_output, meta.tolerances.baseline.output), 'record(encoder, timestamps): output');
+    let refused = false;
+    try { device.createCommandEncoder().beginComputePass().setPipeline(null); } catch (e) { refused = true; }
+    check(refused, 'raw WGSL pipelines are refused');
+    qs.destroy(); session.destroy(); fk.destroy(); att.destroy(); values.destroy(); keys.destroy();
   }
   const lay = readFixture(path.join(FIXTURES, 'mixed', 'mixed_d64.json'));
   const keys = await bgtq.PackedKeys.create(device, parametersFromMixed(lay.meta, lay.arrays), 4);

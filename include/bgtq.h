@@ -52,7 +52,7 @@ typedef struct {
 const char *bgtq_last_error(void);
 /* 2: bgtq_tables_info gained device_bytes. 3: bgtq_model_submit, bgtq_buffer_*, bgtq_allocate_bits,
  * bgtq_layout_groups, bgtq_layout_build. 4: bgtq_decode_noalloc; q_rotated closes the decode and
- * prefill descriptors; bgtq_bake_qproj. */
+ * prefill descriptors; bgtq_bake_qproj; bgtq_timestamps_*. */
 int32_t bgtq_abi_version(void);
 
 /* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
@@ -66,6 +66,20 @@ bgtq_status bgtq_context_synchronize(bgtq_context *ctx);
  * context's own stream. */
 void *bgtq_context_stream(bgtq_context *ctx);
 bgtq_status bgtq_context_set_stream(bgtq_context *ctx, void *hip_stream);
+
+/* ---- GPU timestamps: replace a GPUQuerySet of type "timestamp" ----------- *
+ * device.createQuerySet({type:"timestamp",count}), the timestampWrites of a
+ * compute pass (src/attention/attention.ts:44-58, benchmarks/timing.ts:13-16)
+ * and encoder.resolveQuerySet (benchmarks/timing.ts:20). write() records
+ * index on the context's stream: the time all work queued before it on the
+ * stream completed. resolve() waits for the writes and gives nanoseconds on
+ * one time base per call (differences are durations); indices never written
+ * resolve to 0. */
+typedef struct bgtq_timestamps bgtq_timestamps;
+bgtq_status bgtq_timestamps_create(bgtq_context *ctx, uint32_t count, bgtq_timestamps **out);
+bgtq_status bgtq_timestamps_write(bgtq_timestamps *t, uint32_t index);
+bgtq_status bgtq_timestamps_resolve(bgtq_timestamps *t, uint32_t first, uint32_t count, uint64_t *ns);
+void bgtq_timestamps_destroy(bgtq_timestamps *t);
 
 /* ---- calibration tables: replaces tables(p)/validateLayout --------------- *
  * src/webgpu/layout.ts:8-31. integer = [dim, groups, rowBytes, normStride,
