@@ -436,40 +436,69 @@ def single_head(dev, steps, layout="B"):
             "workload": "1 query, T=4096, d=128, one head, layout B, FP16 V"}
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(layout="B", budget_s=10.0, threads=None):
-    """The oracle (scalar C) on whole (sequence, KV head) units of the same workload: one thread for
-    budget_s, then `threads` threads (the box's CPU share, at most 16) for budget_s, each running units
-    on its own buffers (the ctypes calls release the GIL). The all-threads rate is the value."""
+    """The oracle's CPU path built for this host (-O3 -march=native, no fast-math, no contraction):
+    unpack + reconstruct + FP32 attention on whole (sequence, KV head) units of the headline workload,
+    one thread for budget_s, then `threads` threads (the box's CPU share, at most 16; each on its own
+    buffers, the ctypes calls release the GIL) for budget_s. The all-threads rate is the value. Also
+    the single-head shape (T=4096, d=128, one query) on one thread, timed as the reference's
+    benchmarks time (5 warm-up and 20 timed calls, the median; benchmarks/timing.ts:7-31)."""
     import os
+    import statistics
+    import tempfile
     import threading
     import numpy as np
     from oracle import oracle as O
+    build_dir = tempfile.mkdtemp(prefix="bgtq_oracle_native_")
+    O.use_native_build(build_dir)
+
+    def olayout(p):
+        return O.Layout(dim=p.dim, groups=p.groups, row_bytes=p.rowBytes, norm_stride=p.normStride,
+                        nibble_dims=p.nibbleDims, max_centroids=p.maxCentroids, perm=p.permutation,
+                        group_of=p.groupOf, pos_to_cb=p.positionToCodebook, code_lut=p.codeLut,
+                        rotation=p.rotation, centroids=p.centroids, offsets=p.offsets, inv_scales=p.inverseScales)
+
+    def unit(p, T, dim, nq, causal, seed):
+        L = olayout(p)
+        rng = np.random.default_rng(seed)
+        k = rng.standard_normal((T, dim)).astype(np.float16).view(np.uint16)
+        packed, norms = O.encode_pack(L, k)
+        v = rng.standard_normal((T, dim)).astype(np.float16).astype(np.float32)
+        q = rng.standard_normal((nq, dim)).astype(np.float32)
+        pos = np.full(nq, T - 1, np.uint32)
+        scales = norms.view(np.float16).astype(np.float32)
+
+        def run():
+            codes = O.unpack(packed, dim, p.nibbleDims)
+            keff = O.reconstruct(L, codes, scales)
+            return O.attention(q, keff, v, pos, causal, fp32=True)
+        return run
+
     p = layout_params(layout, DIM)
-    L = O.Layout(dim=p.dim, groups=p.groups, row_bytes=p.rowBytes, norm_stride=p.normStride, nibble_dims=p.nibbleDims,
-                 max_centroids=p.maxCentroids, perm=p.permutation, group_of=p.groupOf, pos_to_cb=p.positionToCodebook,
-                 code_lut=p.codeLut, rotation=p.rotation, centroids=p.centroids, offsets=p.offsets,
-                 inv_scales=p.inverseScales)
-    rng = np.random.default_rng(0)
-    k = rng.standard_normal((CTX, DIM)).astype(np.float16).view(np.uint16)
-    packed, norms = O.encode_pack(L, k)
-    v = rng.standard_normal((CTX, DIM)).astype(np.float16).astype(np.float32)
-    q = rng.standard_normal((HQ // HKV, DIM)).astype(np.float32)
-    pos = np.full(HQ // HKV, CTX - 1, np.uint32)
     unit_bytes = CTX * (p.rowBytes + 2 * p.normStride + 2 * DIM)
 
-    def run(deadline, counts, slot):
+    def run_for(deadline, counts, slot):
+        fn = unit(p, CTX, DIM, HQ // HKV, False, slot)
         n = 0
         while time.perf_counter() < deadline or n == 0:
-            codes = O.unpack(packed, DIM, p.nibbleDims)
-            keff = O.reconstruct(L, codes, norms.view(np.float16).astype(np.float32))
-            O.attention(q, keff, v, pos, False)
+            fn()
             n += 1
         counts[slot] = n
 
     def timed(nthreads):
         counts = [0] * nthreads
         t0 = time.perf_counter()
-        ts = [threading.Thread(target=run, args=(t0 + budget_s, counts, i)) for i in range(nthreads)]
+        ts = [threading.Thread(target=run_for, args=(t0 + budget_s, counts, i)) for i in range(nthreads)]
         for t in ts:
             t.start()
         for t in ts:
@@ -477,13 +506,36 @@ def cpu_baseline(layout="B", budget_s=10.0, threads=None):
         return sum(counts), time.perf_counter() - t0
 
     n1, dt1 = timed(1)
-    threads = threads or min(16, os.cpu_count() or 1)
+    nproc = os.cpu_count() or 1
+    threads = threads or min(16, nproc)
     nn, dtn = timed(threads)
+    # the single-head shape, one thread
+    ph = calibrate_layout_b(128) if layout != "S" else None
+    c1 = None
+    if ph is not None:
+        fn = unit(ph, 4096, 128, 1, True, 99)
+        samples = []
+        for r in range(-5, 20):
+            t0 = time.perf_counter()
+            fn()
+            if r >= 0:
+                samples.append((time.perf_counter() - t0) * 1e6)
+        c1 = {"us_median": round(statistics.median(samples), 1), "threads": 1,
+              "workload": "1 query, T=4096, d=128, one head, layout B: unpack + reconstruct + FP32 attention; "
+                          "5 warm-up and 20 timed calls, the median"}
     return {"value": round(nn * unit_bytes / dtn / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "one_thread_value": round(n1 * unit_bytes / dt1 / 1e9, 4),
+            "one_thread_value": round(n1 * unit_bytes / dt1 / 1e9, 4), "nproc": nproc, "cpu_model": cpu_model(),
+            "build": "oracle/bgtq_oracle.c, gcc -O3 -march=native -ffp-contract=off -fno-fast-math, built on this host",
+            "arithmetic": "fp32 (attention), fp32 FMA chains (reconstruct)",
+            "single_head_t4096_d128": c1,
             "sample": f"(sequence, KV head) units of {CTX} tokens x {HQ // HKV} query heads, d={DIM}: oracle "
-                      f"unpack + reconstruct + attention; {nn} units on {threads} threads in {dtn:.1f} s "
+                      f"unpack + reconstruct + FP32 attention; {nn} units on {threads} threads in {dtn:.1f} s "
                       f"({n1} units on one thread in {dt1:.1f} s)"}
+
+
+def calibrate_layout_b(dim):
+    from bgtq import calibrate
+    return calibrate.layout_b(dim)
 
 
 def read_traffic():
@@ -604,7 +656,8 @@ def main():
     rec = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms_step, 4), "us_per_layer": round(ms_step * 1e3 / LAYERS, 2),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (u8 codes, fp16 scales and V; fp16 hi/lo split MFMA, fp32 accumulate)",
         "data": "synthetic N(0,1) K/V/Q, K encoded by the library",
         "config": {"workload": f"Qwen2.5-0.5B-geometry decode attention: batch {BATCH} x {CTX} ctx, {LAYERS} layers, "
                                f"{HQ} q / {HKV} kv heads, d={DIM}, layout {a.layout} (u8 codes, f16 scales), "
@@ -613,6 +666,9 @@ def main():
                    "launch": "eager" if a.eager else "hip graph of 24 per-layer launches"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "traffic_source": "profiles/decode_fast_qwen_b64_t32k_layoutB_pmc.txt (rocprofv3 --pmc "
+                                       "FETCH_SIZE / WRITE_SIZE of this launch, calibrated on a copy; committed, "
+                                       "not measured in this run)",
                      "frac_of_measured_read_ceiling": round(achieved / ceil["hbm_read_gbs"], 4),
                      "kernel": "decode_fast_kernel<64,1,1,1> (one launch per layer)", "bytes_per_launch": bytes_layer},
         "cpu_baseline": cpu,

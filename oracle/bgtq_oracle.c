@@ -254,15 +254,19 @@ void bgtq_oracle_reconstruct(const bgtq_oracle_layout *L, const uint8_t *codes,
                              const float *scales, int32_t scale_stride, int64_t rows,
                              float *k_out) {
   const int32_t d = L->dim, mc = L->max_centroids;
-  float yv[128];
+  float yv[128], acc[128];
   for (int64_t r = 0; r < rows; ++r) {
     for (int32_t j = 0; j < d; ++j)
       yv[j] = L->centroids[(size_t)j * mc + codes[r * d + j]] * scales[r * scale_stride + L->group_of[j]];
-    for (int32_t i = 0; i < d; ++i) {
-      float acc = 0.0f;
-      for (int32_t j = 0; j < d; ++j) acc = fmaf(yv[j], L->rotation[(size_t)j * d + i], acc);
-      k_out[r * d + L->perm[i]] = acc;
+    /* k[i] = fma chain over j ascending (the sgemm K-loop of y @ R); the
+     * loops run j outer so the d independent chains advance together. */
+    for (int32_t i = 0; i < d; ++i) acc[i] = 0.0f;
+    for (int32_t j = 0; j < d; ++j) {
+      const float y = yv[j];
+      const float *row = L->rotation + (size_t)j * d;
+      for (int32_t i = 0; i < d; ++i) acc[i] = fmaf(y, row[i], acc[i]);
     }
+    for (int32_t i = 0; i < d; ++i) k_out[r * d + L->perm[i]] = acc[i];
   }
 }
 
@@ -300,6 +304,63 @@ int32_t bgtq_oracle_attention(const float *q, int32_t nq, const float *k, const 
         for (int32_t i = 0; i < dim; ++i) acc[i] += p * (double)v[t * dim + i];
     }
     for (int32_t i = 0; i < dim; ++i) out[(int64_t)r * dim + i] = (float)acc[i];
+  }
+  free(l);
+  free(acc);
+  return 0;
+}
+
+/* src/reference/attention.py:17-21 in FP32 (q.float() @ k.float().T / sqrt(d),
+ * softmax, @ v.float()), with sums in ascending order: a float restatement of
+ * the reference's own arithmetic type, within the fixtures' tolerances of its
+ * results, for timing the CPU path. Logits of 16 tokens accumulate together
+ * (independent chains); validation as bgtq_oracle_attention. */
+int32_t bgtq_oracle_attention_f32(const float *q, int32_t nq, const float *k, const float *v,
+                                  int64_t T, int32_t dim, const uint32_t *positions, int32_t causal,
+                                  float *logits, float *probs, float *out) {
+  if (nq < 1 || T < 1 || dim < 1) return -1;
+  for (int32_t r = 0; r < nq; ++r)
+    if ((int64_t)positions[r] >= T) return -2;
+  for (int64_t i = 0; i < (int64_t)nq * dim; ++i) if (!isfinite(q[i])) return -3;
+  for (int64_t i = 0; i < T * dim; ++i) if (!isfinite(k[i]) || !isfinite(v[i])) return -3;
+  float *l = (float *)malloc(sizeof(float) * (size_t)T);
+  float *acc = (float *)malloc(sizeof(float) * (size_t)dim);
+  if (!l || !acc) { free(l); free(acc); return -4; }
+  const float scale = (float)sqrt((double)dim);
+  for (int32_t r = 0; r < nq; ++r) {
+    const float *qr = q + (int64_t)r * dim;
+    const int64_t end = causal ? (int64_t)positions[r] + 1 : T;
+    float mx = -INFINITY;
+    int64_t t = 0;
+    for (; t + 16 <= end; t += 16) {
+      float s[16] = {0.0f};
+      for (int32_t i = 0; i < dim; ++i)
+        for (int b = 0; b < 16; ++b) s[b] = fmaf(qr[i], k[(t + b) * dim + i], s[b]);
+      for (int b = 0; b < 16; ++b) {
+        l[t + b] = s[b] / scale;
+        if (l[t + b] > mx) mx = l[t + b];
+      }
+    }
+    for (; t < end; ++t) {
+      float s = 0.0f;
+      for (int32_t i = 0; i < dim; ++i) s = fmaf(qr[i], k[t * dim + i], s);
+      l[t] = s / scale;
+      if (l[t] > mx) mx = l[t];
+    }
+    for (; t < T; ++t) l[t] = -INFINITY;
+    float den = 0.0f;
+    for (t = 0; t < end; ++t) den += expf(l[t] - mx);
+    for (int32_t i = 0; i < dim; ++i) acc[i] = 0.0f;
+    for (t = 0; t < T; ++t) {
+      const float p = t < end ? expf(l[t] - mx) / den : 0.0f;
+      if (logits) logits[(int64_t)r * T + t] = l[t];
+      if (probs) probs[(int64_t)r * T + t] = p;
+      if (p != 0.0f) {
+        const float *vt = v + t * dim;
+        for (int32_t i = 0; i < dim; ++i) acc[i] = fmaf(p, vt[i], acc[i]);
+      }
+    }
+    for (int32_t i = 0; i < dim; ++i) out[(int64_t)r * dim + i] = acc[i];
   }
   free(l);
   free(acc);

@@ -1,7 +1,7 @@
 /* Block-GTQ CPU oracle: TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of the reference's Python path (encode, pack, unpack,
- * reconstruct, attention, allocator, grouping). Only tests/, the smoke check
+ * reconstruct, attention, allocator). Only tests/, the smoke check
  * and bench.py's CPU-baseline leg may load it, and only as the checker. The
  * product library (libbgtq.so) never links or calls anything declared here.
  */
@@ -69,6 +69,10 @@ void bgtq_oracle_reconstruct(const bgtq_oracle_layout *L, const uint8_t *codes,
 int32_t bgtq_oracle_attention(const float *q, int32_t nq, const float *k, const float *v,
                               int64_t T, int32_t dim, const uint32_t *positions, int32_t causal,
                               float *logits, float *probs, float *out);
+/* The same in FP32 (the reference's arithmetic type), for the CPU baseline. */
+int32_t bgtq_oracle_attention_f32(const float *q, int32_t nq, const float *k, const float *v,
+                                  int64_t T, int32_t dim, const uint32_t *positions, int32_t causal,
+                                  float *logits, float *probs, float *out);
 
 /* allocate_bits (src/reference/allocator.py:4-17). */
 void bgtq_oracle_allocate_bits(const float *scores, int32_t n, int64_t budget, int32_t min_bits,

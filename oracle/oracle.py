@@ -85,17 +85,29 @@ class _Profile(ctypes.Structure):
 _lib = None
 
 
-def lib():
+def use_native_build(out_dir):
+    """Build the oracle source for this host's CPU (-O3 -march=native, still no fast-math and no
+    contraction: the same results) into out_dir and route every call here through it. The
+    benchmark's CPU-baseline leg times it; tests use the portable build."""
+    global _lib
+    out = Path(out_dir) / "libbgtq_oracle_native.so"
+    subprocess.run(["make", "-s", "-C", str(HERE), "native", f"OUT={out}"], check=True)
+    _lib = None
+    return lib(out)
+
+
+def lib(path=None):
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
+        if path is None and not LIB_PATH.exists():
             build()
-        _lib = ctypes.CDLL(str(LIB_PATH))
+        _lib = ctypes.CDLL(str(path or LIB_PATH))
         _lib.bgtq_oracle_f32_to_f16.restype = ctypes.c_uint16
         _lib.bgtq_oracle_f32_to_f16.argtypes = [ctypes.c_float]
         _lib.bgtq_oracle_aten_sum.restype = ctypes.c_float
         _lib.bgtq_oracle_aten_sum.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32]
-        for name in ("bgtq_oracle_encode", "bgtq_oracle_encode_pack", "bgtq_oracle_attention"):
+        for name in ("bgtq_oracle_encode", "bgtq_oracle_encode_pack", "bgtq_oracle_attention",
+                     "bgtq_oracle_attention_f32"):
             getattr(_lib, name).restype = ctypes.c_int32
     return _lib
 
@@ -222,8 +234,9 @@ def reconstruct(layout: Layout, codes, scales):
     return out
 
 
-def attention(q, k, v, positions, causal=False):
-    """logits, probabilities, output (src/reference/attention.py:5-22), float64 accumulation."""
+def attention(q, k, v, positions, causal=False, fp32=False):
+    """logits, probabilities, output (src/reference/attention.py:5-22), float64 accumulation;
+    fp32=True: the FP32 restatement (the CPU baseline's arithmetic)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     k = np.ascontiguousarray(k, dtype=np.float32)
     v = np.ascontiguousarray(v, dtype=np.float32)
@@ -237,8 +250,8 @@ def attention(q, k, v, positions, causal=False):
     logits = np.zeros((nq, T), np.float32)
     probs = np.zeros((nq, T), np.float32)
     out = np.zeros((nq, d), np.float32)
-    rc = lib().bgtq_oracle_attention(_p(q), nq, _p(k), _p(v), ctypes.c_int64(T), d, _p(pos), int(bool(causal)),
-                                     _p(logits), _p(probs), _p(out))
+    fn = lib().bgtq_oracle_attention_f32 if fp32 else lib().bgtq_oracle_attention
+    rc = fn(_p(q), nq, _p(k), _p(v), ctypes.c_int64(T), d, _p(pos), int(bool(causal)), _p(logits), _p(probs), _p(out))
     if rc:
         raise ValueError(f"invalid attention inputs ({rc})")
     return logits, probs, out

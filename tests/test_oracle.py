@@ -99,15 +99,17 @@ def test_reconstruct(mixed_cases, attention_cases, oracle):
         np.testing.assert_allclose(r, a["reconstructed_k"], atol=2e-6, rtol=2e-6, err_msg=name)
 
 
-def test_attention_against_goldens_and_closed_forms(attention_cases, oracle):
-    """tests/test_attention.py:15-46: goldens within the fixture baseline tolerances."""
+@pytest.mark.parametrize("fp32", [False, True])
+def test_attention_against_goldens_and_closed_forms(attention_cases, oracle, fp32):
+    """tests/test_attention.py:15-46: goldens within the fixture baseline tolerances, for the
+    float64-accumulating oracle and its FP32 restatement (the CPU baseline's arithmetic)."""
     for name, m, a, lm, la in attention_cases:
         tol = m["tolerances"]["baseline"]
         for causal in (False, True):
             prefix = "causal_" if causal else ""
             for label, keys in (("baseline", a["k"].astype(np.float32)), ("compressed", a["reconstructed_k"]),
                                 ("fp32_source", a["k_source"])):
-                res = oracle.attention(a["q"], keys, a["v"], a["positions"], causal)
+                res = oracle.attention(a["q"], keys, a["v"], a["positions"], causal, fp32=fp32)
                 for kind, got in zip(("logits", "probabilities", "output"), res):
                     exp = a[prefix + label + "_" + kind]
                     fin = np.isfinite(exp)
