@@ -148,6 +148,13 @@ struct bgtq_context {
   hipStream_t stream = nullptr;
   DeviceBuffer staging;      // per-call upload area, never part of an object's ledger
   std::mutex staging_mutex;  // appends on several threads share the staging area
+  // Device job table of the thread-per-row encoders (kEncodeJobTable jobs),
+  // written on the stream by launch_encode_upload right before each encode
+  // launch; the mutex keeps another thread's upload from landing between the
+  // two on the stream.
+  DeviceBuffer encode_jobs;
+  std::mutex encode_mutex;
+  hipEvent_t switch_event = nullptr;  // orders a newly set stream after the previous one
   uint8_t *scratch = nullptr;  // this device's bgtq_decode_noalloc workspace (library-owned array)
   bgtq_status use() {
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
@@ -234,6 +241,16 @@ bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
     delete c;
     return hip_fail(e, "decode scratch");
   }
+  if (bgtq_status s = c->encode_jobs.alloc(sizeof(EncodeJobDev) * kEncodeJobTable, "encode job table")) {
+    (void)hipStreamDestroy(c->own);
+    delete c;
+    return s;
+  }
+  if ((e = hipEventCreateWithFlags(&c->switch_event, hipEventDisableTiming)) != hipSuccess) {
+    (void)hipStreamDestroy(c->own);
+    delete c;
+    return hip_fail(e, "context event");
+  }
   *out = c;
   return BGTQ_OK;
 }
@@ -246,6 +263,7 @@ void bgtq_context_destroy(bgtq_context *ctx) {
     (void)hipFree(ctx->staging.ptr);
     ctx->staging.ptr = nullptr;
   }
+  (void)hipEventDestroy(ctx->switch_event);
   (void)hipStreamDestroy(ctx->own);
   delete ctx;
 }
@@ -261,7 +279,22 @@ void *bgtq_context_stream(bgtq_context *ctx) { return ctx ? (void *)ctx->stream 
 
 bgtq_status bgtq_context_set_stream(bgtq_context *ctx, void *hip_stream) {
   if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
-  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+  hipStream_t next = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+  if (next == ctx->stream) return BGTQ_OK;
+  if (bgtq_status s = ctx->use()) return s;
+  // Every call reuses the context's device-side state (the encode job table,
+  // the staging area), so work queued on the new stream must not overtake
+  // work still queued on the previous one. Outside stream capture an event
+  // carries that order; a caller switching streams during capture orders the
+  // two captures itself.
+  hipStreamCaptureStatus prev_capture = hipStreamCaptureStatusNone, next_capture = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(ctx->stream, &prev_capture), "hipStreamIsCapturing");
+  HIP_TRY(hipStreamIsCapturing(next, &next_capture), "hipStreamIsCapturing");
+  if (prev_capture == hipStreamCaptureStatusNone && next_capture == hipStreamCaptureStatusNone) {
+    HIP_TRY(hipEventRecord(ctx->switch_event, ctx->stream), "hipEventRecord");
+    HIP_TRY(hipStreamWaitEvent(next, ctx->switch_event, 0), "hipStreamWaitEvent");
+  }
+  ctx->stream = next;
   return BGTQ_OK;
 }
 
@@ -826,58 +859,85 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
     if (j.src_row_stride > INT32_MAX) return fail(BGTQ_ERR_RANGE, "encode job %zu: row stride above 2^31 - 1", i);
   }
   if (bgtq_status s = ctx->use()) return s;
-  // Group jobs by dimension and bulk-encoder kind into launches of at most
-  // kEncodeJobsPerLaunch.
+  // Group jobs by dimension and bulk-encoder kind. Few rows in all (a decode
+  // step's appended tokens) go to the wave-per-row encoder, its jobs in kernel
+  // arguments (kEncodeJobsPerLaunch per launch); otherwise one thread-per-row
+  // launch covers up to kEncodeJobTable jobs through the context's job table,
+  // so every job's rows share one grid and one round of workgroups.
   std::map<std::pair<int, int>, std::vector<size_t>> by_kind;
   for (size_t i = 0; i < n_jobs; ++i)
     if (jobs[i].rows > 0) {
       const bgtq_tables *t = jobs[i].tables;
       by_kind[{t->info.dim, encode_bulk_kind(t->h())}].push_back(i);
     }
+  const bool src_f32 = src_dtype == BGTQ_DTYPE_F32;
+  auto job_dev = [&](const bgtq_encode_job &j) {
+    EncodeJobDev J{};
+    J.t = j.tables->dev();
+    J.src = j.src;
+    J.src_stride = (int32_t)j.src_row_stride;
+    J.rows = j.rows;
+    J.packed = j.packed;
+    J.norms = j.norms;
+    J.dst_row0 = j.dst_row0;
+    J.dst_step = 1;
+    J.enc_bytes = (int32_t)j.tables->h()->off_rot;
+    J.off_rot_t = (int32_t)j.tables->h()->off_rot_t;
+    return J;
+  };
   for (auto &kv : by_kind) {
     const int dim = kv.first.first, kind = kv.first.second;
     const std::vector<size_t> &idx = kv.second;
-    for (size_t b = 0; b < idx.size(); b += kEncodeJobsPerLaunch) {
-      EncodeLaunch L{};
-      int64_t max_rows = 0, total_rows = 0;
-      int lds = 0, lut_max = 0, books_max = 0;
-      for (size_t k = b; k < std::min(idx.size(), b + kEncodeJobsPerLaunch); ++k) {
-        const bgtq_encode_job &j = jobs[idx[k]];
-        EncodeJobDev &J = L.jobs[L.n_jobs++];
-        J.t = j.tables->dev();
-        J.src = j.src;
-        J.src_stride = (int32_t)j.src_row_stride;
-        J.rows = j.rows;
-        J.packed = j.packed;
-        J.norms = j.norms;
-        J.dst_row0 = j.dst_row0;
-        J.dst_step = 1;
-        J.enc_bytes = (int32_t)j.tables->h()->off_rot;
-        J.off_rot_t = (int32_t)j.tables->h()->off_rot_t;
-        max_rows = std::max(max_rows, j.rows);
-        total_rows += j.rows;
-        const bgtq_tables_info &ti = j.tables->info;
-        lds = std::max(lds, encode_wave_lds_bytes(dim, (int)j.tables->h()->off_rot));
-        lut_max = std::max(lut_max, ti.n_codebooks * 256);
-        books_max = std::max(books_max, ti.n_books * ti.max_centroids);
-      }
-      const bool src_f32 = src_dtype == BGTQ_DTYPE_F32;
-      const int wg = kind == 1 ? 256 : 128;
-      const bool bulk_ok = kind && encode_bulk_lds_bytes(kind, wg, lut_max, books_max) <= 64 * 1024;
-      if (lds <= 160 * 1024 && total_rows < kEncodeWaveMaxRows) {
-        // Few rows (a decode step's appended tokens): one wave per row, each
-        // wave striding over enough rows to keep about sixteen waves per
-        // compute unit busy.
+    int64_t total_rows = 0;
+    int wave_lds = 0;
+    for (size_t i : idx) {
+      total_rows += jobs[i].rows;
+      wave_lds = std::max(wave_lds, encode_wave_lds_bytes(dim, (int)jobs[i].tables->h()->off_rot));
+    }
+    if (wave_lds <= 160 * 1024 && total_rows < kEncodeWaveMaxRows) {
+      for (size_t b = 0; b < idx.size(); b += kEncodeJobsPerLaunch) {
+        EncodeLaunch L{};
+        int64_t max_rows = 0, rows = 0;
+        for (size_t k = b; k < std::min(idx.size(), b + kEncodeJobsPerLaunch); ++k) {
+          L.jobs[L.n_jobs++] = job_dev(jobs[idx[k]]);
+          max_rows = std::max(max_rows, jobs[idx[k]].rows);
+          rows += jobs[idx[k]].rows;
+        }
+        // One wave per row, each wave striding over enough rows to keep about
+        // sixteen waves per compute unit busy.
         const int64_t target_waves = 16 * (int64_t)device_cus();
-        const int64_t rows_per_wave = std::max<int64_t>(1, (total_rows + target_waves - 1) / target_waves);
+        const int64_t rows_per_wave = std::max<int64_t>(1, (rows + target_waves - 1) / target_waves);
         const int64_t wgs = std::max<int64_t>(1, (max_rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave));
-        HIP_TRY(launch_encode_wave(L, dim, src_f32, (int)std::min<int64_t>(wgs, 65535), lds, ctx->stream),
+        HIP_TRY(launch_encode_wave(L, dim, src_f32, (int)std::min<int64_t>(wgs, 65535), wave_lds, ctx->stream),
                 "encode launch");
-      } else if (bulk_ok) {
+      }
+      continue;
+    }
+    EncodeJobDev *table = static_cast<EncodeJobDev *>(ctx->encode_jobs.ptr);
+    std::lock_guard<std::mutex> lock(ctx->encode_mutex);
+    for (size_t b = 0; b < idx.size(); b += kEncodeJobTable) {
+      const size_t e = std::min(idx.size(), b + kEncodeJobTable);
+      int64_t max_rows = 0;
+      int lut_max = 0, books_max = 0;
+      for (size_t c = b; c < e; c += kEncodeJobsPerLaunch) {
+        EncodeLaunch L{};
+        for (size_t k = c; k < std::min(e, c + kEncodeJobsPerLaunch); ++k) {
+          const bgtq_encode_job &j = jobs[idx[k]];
+          L.jobs[L.n_jobs++] = job_dev(j);
+          max_rows = std::max(max_rows, j.rows);
+          lut_max = std::max(lut_max, j.tables->info.n_codebooks * 256);
+          books_max = std::max(books_max, j.tables->info.n_books * j.tables->info.max_centroids);
+        }
+        HIP_TRY(launch_encode_upload(L, table, (int)(c - b), ctx->stream), "encode job upload");
+      }
+      const int n = (int)(e - b);
+      const int wg = kind == 1 ? 256 : 128;
+      if (kind && encode_bulk_lds_bytes(kind, wg, lut_max, books_max) <= 64 * 1024) {
         // Bulk encodes of layout-B-shaped tables: thread per row, structure at compile time.
-        HIP_TRY(launch_encode_bulk(L, kind, wg, src_f32, max_rows, lut_max, books_max, ctx->stream), "encode launch");
+        HIP_TRY(launch_encode_bulk(table, n, kind, wg, src_f32, max_rows, lut_max, books_max, ctx->stream),
+                "encode launch");
       } else {
-        HIP_TRY(launch_encode(L, dim, src_f32, max_rows, ctx->stream), "encode launch");
+        HIP_TRY(launch_encode(table, n, dim, src_f32, max_rows, ctx->stream), "encode launch");
       }
     }
   }

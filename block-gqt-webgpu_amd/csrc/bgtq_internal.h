@@ -10,6 +10,7 @@ constexpr int kMaxDim = 128;
 constexpr int kMaxGroups = 8;
 constexpr int kMaxKvHeads = 16;
 constexpr int kEncodeJobsPerLaunch = 60;  // 64-byte jobs: the launch stays under 4 KB of kernel arguments
+constexpr int kEncodeJobTable = 4096;     // jobs in a context's device job table (thread-per-row encoders)
 
 // Device-resident calibration tables, built once on the host from the
 // reference's serialized tables (src/webgpu/layout.ts:24-31). Fixed header,
@@ -91,6 +92,35 @@ struct EncodeLaunch {
   EncodeJobDev jobs[kEncodeJobsPerLaunch];
   int32_t n_jobs;
 };
+
+// Pointers into global memory typed as such. The compiler knows the address
+// space of pointers it loads from kernel arguments, not of pointers it loads
+// from device memory (the encoders' job table): typed generic, wave-uniform
+// table reads become per-lane flat loads instead of scalar loads. (The host
+// pass of a HIP source parses kernels too; there the qualifier is empty.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define BGTQ_GLOBAL __attribute__((address_space(1)))
+#else
+#define BGTQ_GLOBAL
+#endif
+template <typename X>
+__host__ __device__ __forceinline__ BGTQ_GLOBAL X *to_global(X *p) {
+  return (BGTQ_GLOBAL X *)p;
+}
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ inline const BGTQ_GLOBAL uint8_t *tables_lut(const BGTQ_GLOBAL DevTables *t) {
+  return reinterpret_cast<const BGTQ_GLOBAL uint8_t *>(t) + t->off_lut;
+}
+__device__ inline const BGTQ_GLOBAL float *tables_books(const BGTQ_GLOBAL DevTables *t) {
+  return reinterpret_cast<const BGTQ_GLOBAL float *>(reinterpret_cast<const BGTQ_GLOBAL uint8_t *>(t) + t->off_books);
+}
+__device__ inline const BGTQ_GLOBAL float *tables_rot(const BGTQ_GLOBAL DevTables *t) {
+  return reinterpret_cast<const BGTQ_GLOBAL float *>(reinterpret_cast<const BGTQ_GLOBAL uint8_t *>(t) + t->off_rot);
+}
+__device__ inline const BGTQ_GLOBAL float *tables_rot_t(const BGTQ_GLOBAL DevTables *t) {
+  return reinterpret_cast<const BGTQ_GLOBAL float *>(reinterpret_cast<const BGTQ_GLOBAL uint8_t *>(t) + t->off_rot_t);
+}
+#endif
 
 // Decode attention of one layer. Units are (sequence, KV head); each unit
 // serves G query heads (GQA). Work per unit is split over token ranges.
@@ -230,7 +260,13 @@ struct FastLayout {
 int32_t set_error(int32_t code, const char *msg);
 
 // Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).
-hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
+// The thread-per-row encoders read their jobs from a device job table
+// (jobs[0 .. n_jobs), one grid row per job); launch_encode_upload writes up to
+// kEncodeJobsPerLaunch jobs of a chunk (kernel arguments) to table[base ..]
+// on the stream, so the table's contents are stream-ordered and a captured
+// graph re-writes them on every replay.
+hipError_t launch_encode_upload(const EncodeLaunch &chunk, EncodeJobDev *table, int base, hipStream_t stream);
+hipError_t launch_encode(const EncodeJobDev *jobs, int n_jobs, int dim, int src_f32, int64_t max_rows,
                          hipStream_t stream);
 // Wave-per-row encode (encode_wave.hip): dynamic LDS for a job whose table
 // set's header, LUT and books take enc_bytes, and its launcher (wgs_per_job
@@ -246,7 +282,7 @@ hipError_t launch_encode_wave(const EncodeLaunch &launch, int dim, int src_f32, 
 // set (floats) among its jobs.
 int encode_bulk_kind(const DevTables *T);
 int encode_bulk_lds_bytes(int kind, int wg, int lut_bytes, int book_floats);
-hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int wg, int src_f32, int64_t max_rows,
+hipError_t launch_encode_bulk(const EncodeJobDev *jobs, int n_jobs, int kind, int wg, int src_f32, int64_t max_rows,
                               int lut_bytes, int book_floats, hipStream_t stream);
 hipError_t launch_rotate_q(const DecodeParams &p, const float *q, float *qr, hipStream_t stream);
 // Device address of this device's bgtq_decode_noalloc scratch (decode_scratch.hip).

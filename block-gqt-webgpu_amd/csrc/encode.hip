@@ -58,18 +58,18 @@ __device__ __forceinline__ float aten_sum8(F leaf) {
 }
 
 template <int D, bool SRC_F32>
-__global__ __launch_bounds__(kRows) void encode_kernel(EncodeLaunch launch) {
+__global__ __launch_bounds__(kRows) void encode_kernel(const EncodeJobDev *__restrict__ jobs) {
   constexpr int SSTR = D + 2;  // staged halfs per row: odd dword stride, no bank conflicts
   constexpr int CSTR = D + 4;  // code bytes per row
   static_assert(kRows * CSTR <= kRows * SSTR * 2, "codes alias the staging buffer");
   __shared__ uint16_t stage[kRows * SSTR];
   __shared__ uint16_t scales[kRows * kMaxGroups];
 
-  const EncodeJobDev job = launch.jobs[blockIdx.y];
+  const EncodeJobDev job = jobs[blockIdx.y];
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
   if (row0 >= job.rows) return;  // uniform for the workgroup
   const int nr = (int)min((int64_t)kRows, job.rows - row0);
-  const DevTables *__restrict__ T = job.t;
+  const BGTQ_GLOBAL DevTables *__restrict__ T = to_global(job.t);
   const int tid = threadIdx.x;
 
   // Coalesced staging of the block's rows as FP16 bits. FP32 sources are
@@ -78,8 +78,8 @@ __global__ __launch_bounds__(kRows) void encode_kernel(EncodeLaunch launch) {
     const int r = e / D, c = e - r * D;
     const int64_t at = (row0 + r) * job.src_stride + c;
     uint16_t h;
-    if (SRC_F32) h = f32_to_f16_bits(static_cast<const float *>(job.src)[at]);
-    else h = static_cast<const uint16_t *>(job.src)[at];
+    if (SRC_F32) h = f32_to_f16_bits(to_global(static_cast<const float *>(job.src))[at]);
+    else h = to_global(static_cast<const uint16_t *>(job.src))[at];
     stage[r * SSTR + c] = h;
   }
   __syncthreads();
@@ -126,8 +126,8 @@ __global__ __launch_bounds__(kRows) void encode_kernel(EncodeLaunch launch) {
 
   // production_math.py:16-18: y_j = sum_i xn_i R[j,i] (FMA chain, ascending i),
   // bin = trunc(clamp((y - off)*inv, 0, 255)), code = LUT[posToCb[j]][bin].
-  const float *__restrict__ R = tables_rot(T);
-  const uint8_t *__restrict__ lut = tables_lut(T);
+  const BGTQ_GLOBAL float *__restrict__ R = tables_rot(T);
+  const BGTQ_GLOBAL uint8_t *__restrict__ lut = tables_lut(T);
   uint8_t *codes = reinterpret_cast<uint8_t *>(stage);
   for (int j = 0; j < D; ++j) {
     const int g = T->group_of[j];
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kRows) void encode_kernel(EncodeLaunch launch) {
   }
 
   // production_math.py:20-23: corrected_g = raw_g / max(sqrt(sum((c*c)*mask)), 1e-10)
-  const float *__restrict__ books = tables_books(T);
+  const BGTQ_GLOBAL float *__restrict__ books = tables_books(T);
   const int mc = T->max_centroids;
 #pragma unroll
   for (int i = 0; i < D; ++i) {
@@ -176,31 +176,44 @@ __global__ __launch_bounds__(kRows) void encode_kernel(EncodeLaunch launch) {
     uint8_t val = 0;
     if (b < ns / 2) val = (uint8_t)((cr[2 * b] & 15) | ((cr[2 * b + 1] & 15) << 4));
     else if (b < logical) val = cr[ns + b - ns / 2];
-    job.packed[(job.dst_row0 + (row0 + r) * step) * RB + b] = val;
+    to_global(job.packed)[(job.dst_row0 + (row0 + r) * step) * RB + b] = val;
   }
   for (int o = tid; o < nr * NS; o += kRows) {
     const int r = o / NS, g = o - r * NS;
-    job.norms[(job.dst_row0 + (row0 + r) * step) * NS + g] = g < ng ? scales[r * kMaxGroups + g] : (uint16_t)0;
+    to_global(job.norms)[(job.dst_row0 + (row0 + r) * step) * NS + g] = g < ng ? scales[r * kMaxGroups + g] : (uint16_t)0;
   }
 }
 
 template <int D>
-hipError_t launch_d(const EncodeLaunch &launch, int src_f32, int64_t max_rows, hipStream_t stream) {
-  dim3 grid((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)launch.n_jobs);
-  if (src_f32) hipLaunchKernelGGL((encode_kernel<D, true>), grid, dim3(kRows), 0, stream, launch);
-  else hipLaunchKernelGGL((encode_kernel<D, false>), grid, dim3(kRows), 0, stream, launch);
+hipError_t launch_d(const EncodeJobDev *jobs, int n_jobs, int src_f32, int64_t max_rows, hipStream_t stream) {
+  dim3 grid((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)n_jobs);
+  if (src_f32) hipLaunchKernelGGL((encode_kernel<D, true>), grid, dim3(kRows), 0, stream, jobs);
+  else hipLaunchKernelGGL((encode_kernel<D, false>), grid, dim3(kRows), 0, stream, jobs);
   return hipGetLastError();
+}
+
+// One wave per chunk: lane i copies job i (64 bytes) of the chunk's kernel
+// arguments into the table.
+__global__ __launch_bounds__(64) void encode_upload_kernel(EncodeLaunch chunk, EncodeJobDev *table, int base) {
+  const int i = threadIdx.x;
+  if (i < chunk.n_jobs) table[base + i] = chunk.jobs[i];
 }
 
 }  // namespace
 
-hipError_t launch_encode(const EncodeLaunch &launch, int dim, int src_f32, int64_t max_rows,
+hipError_t launch_encode_upload(const EncodeLaunch &chunk, EncodeJobDev *table, int base, hipStream_t stream) {
+  static_assert(kEncodeJobsPerLaunch <= 64, "one lane per job");
+  hipLaunchKernelGGL(encode_upload_kernel, dim3(1), dim3(64), 0, stream, chunk, table, base);
+  return hipGetLastError();
+}
+
+hipError_t launch_encode(const EncodeJobDev *jobs, int n_jobs, int dim, int src_f32, int64_t max_rows,
                          hipStream_t stream) {
   switch (dim) {
-    case 16: return launch_d<16>(launch, src_f32, max_rows, stream);
-    case 32: return launch_d<32>(launch, src_f32, max_rows, stream);
-    case 64: return launch_d<64>(launch, src_f32, max_rows, stream);
-    case 128: return launch_d<128>(launch, src_f32, max_rows, stream);
+    case 16: return launch_d<16>(jobs, n_jobs, src_f32, max_rows, stream);
+    case 32: return launch_d<32>(jobs, n_jobs, src_f32, max_rows, stream);
+    case 64: return launch_d<64>(jobs, n_jobs, src_f32, max_rows, stream);
+    case 128: return launch_d<128>(jobs, n_jobs, src_f32, max_rows, stream);
     default: return hipErrorInvalidValue;
   }
 }

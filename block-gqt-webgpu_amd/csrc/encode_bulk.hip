@@ -10,10 +10,13 @@
 //    each sum is a fixed sequence of adds over the group's positions;
 //  * y_j = sum_i xn_i R[j][i] (production_math.py:16) is one FMA chain over
 //    the group of j in ascending i from +0, the order of the CPU sgemm (the
-//    off-group rotation entries are exact zeros); the rotation rows are
-//    wave-uniform operands read through the scalar cache;
+//    off-group rotation entries are exact zeros); the group's chains advance
+//    together, column i of R (a row of the stored transpose) a wave-uniform
+//    operand read through the scalar cache;
 //  * division and square root are IEEE (built with -ffp-contract=off and
-//    correctly rounded fp32 division/sqrt).
+//    correctly rounded fp32 division/sqrt); a group's 32 divisions by its
+//    norm use its correctly rounded reciprocal and one FMA correction each,
+//    which gives the same quotients.
 // The code LUT and centroid books sit in LDS; codes are packed in registers
 // as they are produced (mixed_layout.py:21-27) and each thread writes its own
 // packed row and FP16 scales.
@@ -43,6 +46,10 @@ struct Bulk {
   static constexpr int ROWS = WG;     // rows (threads) per workgroup
   static constexpr int SSTR = D + 2;  // staged halfs per row: odd dword stride
   static constexpr int STAGE = ROWS * SSTR * 2;
+  // d <= 64: the two diagonal rotation blocks in LDS (8 KB); at d=128 (32 KB)
+  // the columns are read through the scalar cache instead.
+  static constexpr bool ROT_LDS = D <= 64;
+  static constexpr int ROT = ROT_LDS ? 2 * (D / 2) * (D / 2) * 4 : 0;
 };
 
 // ATen's 8-lane inner sum (vectorized_inner_sum: four interleaved
@@ -79,7 +86,8 @@ __device__ __forceinline__ float tree_sum(F &&leaf) {
 }
 
 template <int D, int NG, int NS, bool SRC_F32, int WG>
-__global__ __launch_bounds__(WG) void encode_bulk_kernel(EncodeLaunch launch, int lut_area) {
+__global__ __launch_bounds__(WG) void encode_bulk_kernel(const EncodeJobDev *__restrict__ jobs, int lut_area,
+                                                         int book_floats) {
   constexpr int ROWS = Bulk<D, WG>::ROWS, SSTR = Bulk<D, WG>::SSTR, GW = D / NG;
   constexpr int LOGICAL = NS / 2 + D - NS;  // packed bytes before padding
   static_assert(GW % 8 == 0 && NS % 8 == 0 && NS <= D && LOGICAL % 4 == 0, "layout");
@@ -87,12 +95,15 @@ __global__ __launch_bounds__(WG) void encode_bulk_kernel(EncodeLaunch launch, in
   uint16_t *stage = reinterpret_cast<uint16_t *>(smem);
   uint8_t *lut = smem + Bulk<D, WG>::STAGE;
   float *books = reinterpret_cast<float *>(lut + lut_area);
+  // The groups' diagonal rotation blocks, rot[g][i][j] = R[P0 + j][P0 + i]
+  // (column i of the block contiguous): read as wave-wide broadcasts.
+  float *rot = books + ((book_floats + 3) & ~3);
 
-  const EncodeJobDev job = launch.jobs[blockIdx.y];
+  const EncodeJobDev job = jobs[blockIdx.y];
   const int64_t row0 = (int64_t)blockIdx.x * ROWS;
   if (row0 >= job.rows) return;  // uniform for the workgroup
   const int nr = (int)min((int64_t)ROWS, job.rows - row0);
-  const DevTables *__restrict__ T = job.t;
+  const BGTQ_GLOBAL DevTables *__restrict__ T = to_global(job.t);
   const int tid = threadIdx.x;
   const int mc = T->max_centroids;
 
@@ -101,25 +112,28 @@ __global__ __launch_bounds__(WG) void encode_bulk_kernel(EncodeLaunch launch, in
   for (int e = tid; e < nr * D; e += ROWS) {
     const int r = e / D, c = e - r * D;
     const int64_t at = (row0 + r) * job.src_stride + c;
-    stage[r * SSTR + c] = SRC_F32 ? f32_to_f16_bits(static_cast<const float *>(job.src)[at])
-                                  : static_cast<const uint16_t *>(job.src)[at];
+    stage[r * SSTR + c] = SRC_F32 ? f32_to_f16_bits(to_global(static_cast<const float *>(job.src))[at])
+                                  : to_global(static_cast<const uint16_t *>(job.src))[at];
   }
   {
-    const uint8_t *lut_g = tables_lut(T);
+    const auto lut_g = tables_lut(T);
     const int lut_bytes = T->n_codebooks * 256;
     for (int e = tid; e < lut_bytes; e += ROWS) lut[e] = lut_g[e];
-    const float *books_g = tables_books(T);
+    const auto books_g = tables_books(T);
     const int nbf = T->n_books * mc;
     for (int e = tid; e < nbf; e += ROWS) books[e] = books_g[e];
+    if constexpr (Bulk<D, WG>::ROT_LDS) {
+      const BGTQ_GLOBAL float *__restrict__ Rt_g = tables_rot_t(T);  // Rt[i * D + j] = R[j][i]
+      for (int e = tid; e < NG * GW * GW; e += ROWS) {
+        const int g = e / (GW * GW), r = e - g * (GW * GW), i = r / GW, j = r - i * GW;
+        rot[e] = Rt_g[(g * GW + i) * D + g * GW + j];
+      }
+    }
   }
   __syncthreads();
   if (tid >= nr) return;  // no barrier below
 
-  float x[D];
-#pragma unroll
-  for (int i = 0; i < D; ++i) x[i] = f16_bits_to_f32(stage[tid * SSTR + T->perm[i]]);
-
-  const float *__restrict__ R = tables_rot(T);
+  const BGTQ_GLOBAL float *__restrict__ Rt = tables_rot_t(T);  // Rt[i * D + j] = R[j][i]
   uint32_t packed[LOGICAL / 4];
 #pragma unroll
   for (int w = 0; w < LOGICAL / 4; ++w) packed[w] = 0u;
@@ -127,58 +141,94 @@ __global__ __launch_bounds__(WG) void encode_bulk_kernel(EncodeLaunch launch, in
 
   static_for<0, NG>([&](auto gc) {
     constexpr int g = decltype(gc)::value, P0 = g * GW, P1 = P0 + GW;
+    // This group's inputs in head-perm order (the other groups' stay in LDS).
+    float x[GW];
+#pragma unroll
+    for (int i = 0; i < GW; ++i) x[i] = f16_bits_to_f32(stage[tid * SSTR + T->perm[P0 + i]]);
     // production_math.py:12-15: n_g, raw_g, x / where(n > 1e-10, n, 1)
-    const float n = __builtin_sqrtf(tree_sum<D, P0, P1>([&](int p) { return x[p] * x[p]; }) + 1e-30f);
+    const float n = __builtin_sqrtf(tree_sum<D, P0, P1>([&](int p) { return x[p - P0] * x[p - P0]; }) + 1e-30f);
     const float raw = NG > 1 ? tree_sum<D, P0, P1>([&](int) { return n; }) / (float)GW : n;
     const float den = n > 1e-10f ? n : 1.0f;
+    // The group's divisions share the divisor: with r = 1/den correctly
+    // rounded, q = x r is within an ulp of x/den and one FMA correction
+    // returns the correctly rounded quotient (Markstein's theorem; checked
+    // against IEEE division on every FP16 numerator, tests/host_division_check.c).
+    // A -0 numerator may come out +0, which the FMA chains below, starting
+    // from +0, cannot tell apart.
+    const float rden = 1.0f / den;
 #pragma unroll
-    for (int i = P0; i < P1; ++i) x[i] = x[i] / den;
-    // production_math.py:16-20 per output j of the group: FMA chain, bin,
-    // LUT code, centroid; codes packed as produced.
-    float c2[GW];
+    for (int i = 0; i < GW; ++i) {
+      const float q0 = x[i] * rden;
+      x[i] = __builtin_fmaf(__builtin_fmaf(-q0, den, x[i]), rden, q0);
+    }
+    // production_math.py:16: y_j = FMA chain over i ascending from +0 for
+    // every output j of the group, the chains advanced together (input i
+    // outer: column i of the group's block one broadcast LDS read, or one
+    // scalar read at d=128), each in its own order.
+    float y[GW];
 #pragma unroll
-    for (int j = P0; j < P1; ++j) {
-      const float *__restrict__ Rj = R + j * D;
-      float acc = 0.0f;
+    for (int j = 0; j < GW; ++j) y[j] = 0.0f;
 #pragma unroll
-      for (int i = P0; i < P1; ++i) acc = __builtin_fmaf(x[i], Rj[i], acc);
-      float t = (acc - T->lut_off[j]) * T->lut_inv[j];
+    for (int i = 0; i < GW; ++i) {
+      if constexpr (Bulk<D, WG>::ROT_LDS) {
+        const float4 *Ci = reinterpret_cast<const float4 *>(rot + (g * GW + i) * GW);
+#pragma unroll
+        for (int j4 = 0; j4 < GW / 4; ++j4) {
+          const float4 c = Ci[j4];
+          y[4 * j4 + 0] = __builtin_fmaf(x[i], c.x, y[4 * j4 + 0]);
+          y[4 * j4 + 1] = __builtin_fmaf(x[i], c.y, y[4 * j4 + 1]);
+          y[4 * j4 + 2] = __builtin_fmaf(x[i], c.z, y[4 * j4 + 2]);
+          y[4 * j4 + 3] = __builtin_fmaf(x[i], c.w, y[4 * j4 + 3]);
+        }
+      } else {
+        const BGTQ_GLOBAL float *__restrict__ Ci = Rt + (P0 + i) * D + P0;
+#pragma unroll
+        for (int j = 0; j < GW; ++j) y[j] = __builtin_fmaf(x[i], Ci[j], y[j]);
+      }
+    }
+    // production_math.py:17-23: output j's bin, LUT code and centroid are
+    // taken where the sum tree of c^2 takes its leaf j (the code packed as
+    // produced), so each c^2 is folded in at once; the tree visits every leaf
+    // once, in its own fixed order.
+    const float csum = tree_sum<D, P0, P1>([&](int j) {
+      float t = (y[j - P0] - T->lut_off[j]) * T->lut_inv[j];
       t = fminf(fmaxf(t, 0.0f), 255.0f);
       const uint32_t code = lut[(int)T->pos_cb[j] * 256 + (int)t];
       const float c = books[(int)T->pos_book[j] * mc + (int)code];
-      c2[j - P0] = c * c;
       const int byte = j < NS ? j / 2 : NS / 2 + (j - NS);
       const int shift = 8 * (byte % 4) + (j < NS ? 4 * (j % 2) : 0);
       packed[byte / 4] |= code << shift;
-    }
-    // production_math.py:21-23: corrected_g = raw_g / max(sqrt(sum c^2), 1e-10)
-    const float cn = fmaxf(__builtin_sqrtf(tree_sum<D, P0, P1>([&](int p) { return c2[p - P0]; })), 1e-10f);
-    scales[g] = f32_to_f16_bits(raw / cn);
+      return c * c;
+    });
+    // corrected_g = raw_g / max(sqrt(sum c^2), 1e-10)
+    scales[g] = f32_to_f16_bits(raw / fmaxf(__builtin_sqrtf(csum), 1e-10f));
   });
 
   // mixed_layout.py:21-27: every byte of the destination row written (zero
   // padding after the codes); FP16 scales zero-padded to norm_stride.
   const int64_t out_row = job.dst_row0 + (row0 + tid) * job.dst_step;
   const int RB = T->row_bytes, NSTR = T->norm_stride;
-  uint32_t *prow = reinterpret_cast<uint32_t *>(job.packed + out_row * RB);
+  BGTQ_GLOBAL uint32_t *prow = reinterpret_cast<BGTQ_GLOBAL uint32_t *>(to_global(job.packed) + out_row * RB);
 #pragma unroll
   for (int w = 0; w < LOGICAL / 4; ++w) prow[w] = packed[w];
   for (int w = LOGICAL / 4; w < RB / 4; ++w) prow[w] = 0u;
-  uint16_t *nrow = job.norms + out_row * NSTR;
+  BGTQ_GLOBAL uint16_t *nrow = to_global(job.norms) + out_row * NSTR;
 #pragma unroll
   for (int g = 0; g < NG; ++g) nrow[g] = scales[g];
   for (int g = NG; g < NSTR; ++g) nrow[g] = 0;
 }
 
 template <int D, int NG, int NS, int WG>
-hipError_t launch_kind(const EncodeLaunch &launch, int src_f32, int64_t max_rows, int lut_area, int book_floats,
-                       hipStream_t stream) {
-  const int lds = Bulk<D, WG>::STAGE + lut_area + book_floats * 4;
-  dim3 grid((unsigned)((max_rows + WG - 1) / WG), (unsigned)launch.n_jobs);
+hipError_t launch_kind(const EncodeJobDev *jobs, int n_jobs, int src_f32, int64_t max_rows, int lut_area,
+                       int book_floats, hipStream_t stream) {
+  const int lds = Bulk<D, WG>::STAGE + lut_area + ((book_floats + 3) & ~3) * 4 + Bulk<D, WG>::ROT;
+  dim3 grid((unsigned)((max_rows + WG - 1) / WG), (unsigned)n_jobs);
   if (src_f32)
-    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, true, WG>), grid, dim3(WG), lds, stream, launch, lut_area);
+    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, true, WG>), grid, dim3(WG), lds, stream, jobs, lut_area,
+                       book_floats);
   else
-    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, false, WG>), grid, dim3(WG), lds, stream, launch, lut_area);
+    hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, false, WG>), grid, dim3(WG), lds, stream, jobs, lut_area,
+                       book_floats);
   return hipGetLastError();
 }
 
@@ -194,14 +244,16 @@ int encode_bulk_kind(const DevTables *T) {
 
 int encode_bulk_lds_bytes(int kind, int wg, int lut_bytes, int book_floats) {
   const int d = kind == 1 ? 64 : 128;
-  return wg * (d + 2) * 2 + ((lut_bytes + 15) & ~15) + book_floats * 4;
+  return wg * (d + 2) * 2 + ((lut_bytes + 15) & ~15) + ((book_floats + 3) & ~3) * 4 +
+         (d <= 64 ? 2 * (d / 2) * (d / 2) * 4 : 0);
 }
 
-hipError_t launch_encode_bulk(const EncodeLaunch &launch, int kind, int wg, int src_f32, int64_t max_rows,
+hipError_t launch_encode_bulk(const EncodeJobDev *jobs, int n_jobs, int kind, int wg, int src_f32, int64_t max_rows,
                               int lut_bytes, int book_floats, hipStream_t stream) {
   const int lut_area = (lut_bytes + 15) & ~15;
-#define BGTQ_BULK(K, DD, NS, W) \
-  if (kind == K && wg == W) return launch_kind<DD, 2, NS, W>(launch, src_f32, max_rows, lut_area, book_floats, stream);
+#define BGTQ_BULK(K, DD, NS, W)                                                                           \
+  if (kind == K && wg == W)                                                                               \
+    return launch_kind<DD, 2, NS, W>(jobs, n_jobs, src_f32, max_rows, lut_area, book_floats, stream);
   BGTQ_BULK(1, 64, 32, 256)
   BGTQ_BULK(2, 128, 64, 128)
 #undef BGTQ_BULK

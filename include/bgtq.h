@@ -63,7 +63,10 @@ void bgtq_context_destroy(bgtq_context *ctx);
 bgtq_status bgtq_context_synchronize(bgtq_context *ctx);
 /* The hipStream_t all work of this context is ordered on. A caller may set a
  * stream it owns (for example PyTorch's current stream); NULL restores the
- * context's own stream. */
+ * context's own stream. Calls reuse context-owned device state (the encode
+ * job table, the staging area), so setting a different stream makes it wait
+ * for the work queued on the previous one (an event; not while either stream
+ * is capturing a graph, where the caller orders the two). */
 void *bgtq_context_stream(bgtq_context *ctx);
 bgtq_status bgtq_context_set_stream(bgtq_context *ctx, void *hip_stream);
 

@@ -283,3 +283,48 @@ def test_calibration_load_encodes_every_head(device, oracle):
             np.testing.assert_array_equal(norms.cpu().numpy().view(np.uint16), ref_n, err_msg=f"head {h}")
     finally:
         cal.destroy()
+
+
+def test_job_table_batches_and_stream_switch(device, oracle):
+    """More jobs in one call than the context's device job table holds (4100 jobs of 4 rows: two table
+    batches, each uploaded in chunks of 60), then, without waiting, a second call on another stream that
+    rewrites the table: both calls give the oracle's bytes."""
+    import torch
+    import bgtq
+    from bgtq import batched, calibrate
+    rng = np.random.default_rng(321)
+    p = calibrate.layout_b(64)
+    n_a, rows_a = 4100, 4
+    n_b, rows_b = 90, 200
+    ka = _random_half_rows(rng, n_a * rows_a, 64)
+    kb = _random_half_rows(rng, n_b * rows_b, 64)
+    tables = bgtq.Tables(device, p)
+    side_a, side_b = torch.cuda.Stream(), torch.cuda.Stream()
+    try:
+        bufs = []
+        for k in (ka, kb):
+            src = torch.from_numpy(k.view(np.int16)).cuda()
+            packed = torch.zeros((k.shape[0], p.rowBytes), dtype=torch.uint8, device="cuda")
+            norms = torch.zeros((k.shape[0], p.normStride), dtype=torch.int16, device="cuda")
+            bufs.append((src, packed, norms))
+        torch.cuda.synchronize()
+
+        def jobs(buf, n, rows):
+            src, packed, norms = buf
+            return [dict(tables=tables, src=src[i * rows:], src_row_stride=64, rows=rows,
+                         packed=packed[i * rows:], norms=norms[i * rows:]) for i in range(n)]
+
+        device.set_stream(side_a.cuda_stream)
+        batched.encode(device, jobs(bufs[0], n_a, rows_a), "f16")
+        device.set_stream(side_b.cuda_stream)
+        batched.encode(device, jobs(bufs[1], n_b, rows_b), "f16")
+        torch.cuda.synchronize()
+        for name, k, (_, packed, norms) in (("table batches", ka, bufs[0]), ("second stream", kb, bufs[1])):
+            ref_p, ref_n = oracle.encode_pack(_olayout(oracle, p), k)
+            got_p, got_n = packed.cpu().numpy(), norms.cpu().numpy().view(np.uint16)
+            bad = np.nonzero(np.any(got_p != ref_p, axis=1) | np.any(got_n != ref_n, axis=1))[0]
+            assert bad.size == 0, f"{name}: {bad.size} rows differ, first {bad[:5]}"
+    finally:
+        device.set_stream(None)
+        torch.cuda.synchronize()
+        tables.destroy()

@@ -488,3 +488,20 @@ def test_bake_qproj_puts_queries_in_the_code_domain(oracle):
     z = np.zeros((64, 4), np.float32)
     assert _lib.lib().bgtq_bake_qproj(_lib.ptr(bad), len(bad), _lib.ptr(fl), len(fl), 1, 4, _lib.ptr(z), None,
                                       _lib.ptr(z), None) == _lib.ERR_RANGE
+
+
+def test_encoder_division_by_reciprocal(tmp_path):
+    """The bulk encoder divides a group's 32 inputs by the group norm as x * r with one FMA
+    correction (r = 1/norm correctly rounded): equal to IEEE x / norm on every nonzero FP16
+    numerator for sampled divisors and group norms (the division check is plain C, built here)."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc is not installed")
+    exe = tmp_path / "host_division_check"
+    subprocess.run([gcc, "-O2", "-ffp-contract=off", "-fno-fast-math", "-o", str(exe),
+                    str(ROOT / "tests" / "host_division_check.c"), "-lm"], check=True)
+    r = subprocess.run([str(exe), "600"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout
+    assert r.stdout.strip().endswith("mismatches 0"), r.stdout
