@@ -1242,16 +1242,19 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
 
 // ---------------------------------------------------------------- chunked prefill
 struct PrefillPlan {
-  int tiles, tile_queries, split_tokens, splits;
-  size_t workspace;  // split partials: (m, l) then o per (query, split)
+  int tiles, tile_queries, ranges, range_blocks;
+  size_t records;    // bytes of the workgroups' partial records
+  size_t workspace;  // records, then the tile table (16 bytes per tile)
 };
 
 // Query tiles: four waves of one 16-query block each for small chunks (more
 // tiles to spread), of prefill_column_blocks(dim) blocks each for long ones
-// (the K operand rebuilt once per block serves more queries). Token splits:
-// enough (tile, split) workgroups for about two per compute unit over the
-// causal half of the history, at least 64 tokens each and at most
-// kPrefillMaxSplits splits.
+// (the K operand rebuilt once per block serves more queries). Workgroups:
+// the flattened work (every KV head, sequence and tile's causal history in
+// 32-token blocks) is cut into equal ranges, about two workgroups per
+// compute unit, sized here for the most work (every chunk at the end of the
+// cache: the starts are device values) and by the kernel for the actual one;
+// split_tokens > 0 fixes the range length instead.
 static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   if (!d) return fail(BGTQ_ERR_RANGE, "null descriptor");
   if (d->batch < 1 || d->rows < 1 || d->kv_heads < 1 || d->kv_heads > kMaxKvHeads || d->q_heads < d->kv_heads ||
@@ -1279,43 +1282,29 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   const int64_t G = d->q_heads / d->kv_heads, nq = (int64_t)d->rows * G;
   plan->tile_queries = nq >= 2048 ? 64 * prefill_column_blocks(d->dim) : 64;
   plan->tiles = (int)((nq + plan->tile_queries - 1) / plan->tile_queries);
-  const int64_t L = d->max_length;
-  const int64_t sp_min = std::max<int64_t>(32, ((L + kPrefillMaxSplits - 1) / kPrefillMaxSplits + 31) / 32 * 32);
-  const int64_t sp_max = (L + 31) / 32 * 32;
-  int64_t sp = d->split_tokens;
-  if (sp == 0) {
-    // The shortest split length whose workgroups fit one round of two per
-    // compute unit, for a chunk at the end of the cache (the most history:
-    // the start is a device value). A second, partly filled round would leave
-    // most of the GPU idle behind the first one's tail.
-    const int64_t units = (int64_t)d->batch * d->kv_heads, slots = 2 * (int64_t)device_cus();
-    const int64_t start = L - d->rows, tq = plan->tile_queries;
-    auto workgroups = [&](int64_t s) {
-      int64_t n = 0;
-      for (int64_t t = 0; t < plan->tiles; ++t) {
-        const int64_t e = start + (std::min(nq, (t + 1) * tq) - 1) / G + 1;
-        n += (e + s - 1) / s;
-      }
-      return n * units;
-    };
-    if (workgroups(sp_max) > slots) {
-      sp = std::max<int64_t>(64, units * plan->tiles * (L / 2 + 1) / slots);  // several rounds anyway
-    } else {
-      int64_t lo = sp_min / 32, hi = sp_max / 32;  // in blocks; workgroups() does not grow with the length
-      while (lo < hi) {
-        const int64_t mid = (lo + hi) / 2;
-        if (workgroups(mid * 32) <= slots) hi = mid;
-        else lo = mid + 1;
-      }
-      sp = lo * 32;
+  if ((int64_t)d->batch * plan->tiles > INT32_MAX / 2) return fail(BGTQ_ERR_UNSUPPORTED, "too many query tiles");
+  // The most work: 32-token blocks of every tile's history with each chunk at the end of the cache.
+  const int64_t start = (int64_t)d->max_length - d->rows, tq = plan->tile_queries;
+  int64_t w1 = 0;
+  for (int64_t t = 0; t < plan->tiles; ++t) w1 += (start + (std::min(nq, (t + 1) * tq) - 1) / G + 1 + 31) / 32;
+  const int64_t w_max = w1 * d->batch * d->kv_heads;
+  if (w_max > INT32_MAX / 2) return fail(BGTQ_ERR_UNSUPPORTED, "prefill work above 2^30 blocks of 32 tokens");
+  int64_t ranges, range_blocks = 0;
+  if (d->split_tokens > 0) {
+    range_blocks = (d->split_tokens + 31) / 32;
+    ranges = (w_max + range_blocks - 1) / range_blocks;
+    if (ranges > kPrefillMaxRanges) {
+      ranges = kPrefillMaxRanges;
+      range_blocks = (w_max + ranges - 1) / ranges;
     }
+  } else {
+    ranges = std::min<int64_t>(2 * (int64_t)device_cus(), (w_max + kPrefillMinRange - 1) / kPrefillMinRange);
   }
-  sp = std::max<int64_t>(sp, sp_min);
-  sp = std::min<int64_t>((sp + 31) / 32 * 32, sp_max);
-  plan->split_tokens = (int)sp;
-  plan->splits = (int)((L + sp - 1) / sp);
-  const int64_t queries = (int64_t)d->batch * d->rows * d->q_heads;
-  plan->workspace = plan->splits > 1 ? sizeof(float) * (size_t)(queries * plan->splits * (d->dim + 2)) : 0;
+  plan->ranges = (int)std::max<int64_t>(1, ranges);
+  plan->range_blocks = (int)range_blocks;
+  plan->records = plan->ranges > 1 ? sizeof(float) * (size_t)plan->ranges * 2 * tq * (d->dim + 2) : 0;
+  const size_t info = plan->ranges > 1 ? 16 * (size_t)d->batch * d->kv_heads * plan->tiles : 0;
+  plan->workspace = plan->records + info;
   return BGTQ_OK;
 }
 
@@ -1333,6 +1322,8 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   if (bgtq_status s = plan_prefill(d, &plan)) return s;
   if (plan.workspace && (!d->workspace || d->workspace_bytes < plan.workspace))
     return fail(BGTQ_ERR_RANGE, "workspace of %zu bytes required", plan.workspace);
+  if (plan.workspace && (reinterpret_cast<uintptr_t>(d->workspace) & 15))
+    return fail(BGTQ_ERR_RANGE, "workspace must be 16-byte aligned");
   // The layout check shares the fused decode's requirements.
   DecodeParams dp{};
   for (int h = 0; h < d->kv_heads; ++h) dp.tables[h] = d->key_format == BGTQ_KEYS_PACKED ? d->tables[h]->dev() : nullptr;
@@ -1397,11 +1388,12 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
   p.starts = d->starts;
   p.max_length = (int32_t)d->max_length;
-  p.split_tokens = plan.split_tokens;
-  p.splits = plan.splits;
   p.tiles = plan.tiles;
   p.tile_queries = plan.tile_queries;
+  p.ranges = plan.ranges;
+  p.range_blocks = plan.range_blocks;
   p.part = static_cast<float *>(d->workspace);
+  p.tile_info = plan.workspace ? reinterpret_cast<int32_t *>(static_cast<uint8_t *>(d->workspace) + plan.records) : nullptr;
   p.out = d->out;
   HIP_TRY(launch_prefill(p, fl, nn, sg, ctx->stream), "prefill launch");
   return BGTQ_OK;

@@ -194,16 +194,23 @@ hipError_t launch_d(const EncodeJobDev *jobs, int n_jobs, int src_f32, int64_t m
 
 // One wave per chunk: lane i copies job i (64 bytes) of the chunk's kernel
 // arguments into the table.
-__global__ __launch_bounds__(64) void encode_upload_kernel(EncodeLaunch chunk, EncodeJobDev *table, int base) {
+// One 16-byte piece of a descriptor per lane, so the chunk moves in a single
+// round of kernel-argument loads and stores.
+constexpr int kUploadPieces = sizeof(EncodeJobDev) / sizeof(uint4);
+
+__global__ __launch_bounds__(256) void encode_upload_kernel(EncodeLaunch chunk, EncodeJobDev *table, int base) {
   const int i = threadIdx.x;
-  if (i < chunk.n_jobs) table[base + i] = chunk.jobs[i];
+  if (i < chunk.n_jobs * kUploadPieces) {
+    const uint4 v = reinterpret_cast<const uint4 *>(chunk.jobs)[i];
+    reinterpret_cast<uint4 *>(table + base)[i] = v;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_encode_upload(const EncodeLaunch &chunk, EncodeJobDev *table, int base, hipStream_t stream) {
-  static_assert(kEncodeJobsPerLaunch <= 64, "one lane per job");
-  hipLaunchKernelGGL(encode_upload_kernel, dim3(1), dim3(64), 0, stream, chunk, table, base);
+  static_assert(kEncodeJobsPerLaunch * kUploadPieces <= 256, "one lane per 16-byte piece");
+  hipLaunchKernelGGL(encode_upload_kernel, dim3(1), dim3(256), 0, stream, chunk, table, base);
   return hipGetLastError();
 }
 

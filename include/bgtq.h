@@ -282,9 +282,14 @@ bgtq_status bgtq_decode_noalloc(bgtq_context *ctx, const bgtq_decode_desc *d);
  *   q, out: [B, rows, Hq, dim] FP32 contiguous; query head h uses KV head h / G.
  *   starts: device uint32 [B], starts[b] + rows <= max_length (kernels clamp).
  *   v: FP16. Key formats and strides are those of bgtq_decode.
- *   workspace: device memory of at least bgtq_prefill_workspace_size() bytes
- *   for the token splits' partial results (no initial contents needed);
+ *   workspace: 16-byte aligned device memory of at least
+ *   bgtq_prefill_workspace_size() bytes for the partial results of tiles
+ *   whose history several workgroups share (no initial contents needed);
  *   calls sharing a workspace must be ordered on one stream.
+ *   split_tokens: the work (every sequence, KV head and query tile's causal
+ *   history) is divided into equal ranges of this many history tokens, one
+ *   workgroup each (rounded up to 32); 0 = about two workgroups per compute
+ *   unit, sized on the device for the actual starts.
  * Layouts: FP16 K, or packed layouts the fused decode takes (see
  * bgtq_decode_append) whose centroid books (n_books * max_centroids floats)
  * fit 4 KB at d=64, 8 KB at d=128; others return BGTQ_ERR_UNSUPPORTED. */
@@ -304,7 +309,7 @@ typedef struct {
   float *out;
   const uint32_t *starts;
   uint32_t max_length;
-  int32_t split_tokens; /* tokens per split, rounded up to a multiple of 32; 0 = choose */
+  int32_t split_tokens; /* history tokens per workgroup range, rounded up to 32; 0 = choose */
   void *workspace;
   size_t workspace_bytes;
   int32_t q_rotated; /* as in bgtq_decode_desc */
