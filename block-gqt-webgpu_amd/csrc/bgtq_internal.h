@@ -184,15 +184,17 @@ struct PrefillParams {
   int32_t max_length;       // tokens every K/V buffer holds; kernels clamp starts to max_length - rows
   int32_t tiles;            // query tiles per (sequence, KV head)
   int32_t tile_queries;     // 64 or 64 * prefill_column_blocks(dim)
-  int32_t ranges;           // workgroups: each takes an equal range of the flattened 32-token blocks
-  int32_t range_blocks;     // blocks per range; 0 = ceil(work / ranges), at least kPrefillMinRange
+  int32_t ranges;           // workgroups: each takes an equal range of the flattened work
+  int32_t range_blocks;     // cost units per range; 0 = ceil(work / ranges), at least kPrefillMinRange
+  int32_t first_round;      // > 0: the first first_round ranges are 1.5 times the others
   float *part;              // two records per workgroup: (m, l, o[dim]) per query of a tile
   int32_t *tile_info;       // per (KV head, sequence, tile): first and last workgroup, first one's record
   float *out;               // [B*rows*Hq*dim]
 };
 // Most 16-query MFMA column blocks per wave of the prefill kernel (four waves per tile).
 __host__ __device__ constexpr int prefill_column_blocks(int dim) { return dim == 64 ? 4 : 2; }
-constexpr int kPrefillMinRange = 2;       // blocks per workgroup range the kernel picks at least
+constexpr int kPrefillMinRange = 2;       // cost units per workgroup range the kernel picks at least
+constexpr int kPrefillSegmentCost = 4;    // cost units of a tile's set-up (a 32-token block is one)
 constexpr int kPrefillMaxRanges = 2048;   // workgroups of one launch at most (bounds the records)
 
 // The model step's separate attention passes (model_ops.hip), in the

@@ -57,6 +57,7 @@ constexpr int kRing = 6;    // shared LDS buffers: compute one, four in flight, 
 // when a block's maximum exceeds it by more than kTau (log2 units), and
 // P = 2^(x - m + kPBias) stays within 2^15, so its fp16 lo part stays normal
 // for the largest terms. Partials carry o and l scaled by kPOut = 2^kPBias.
+constexpr int kSegmentCost = kPrefillSegmentCost;  // a segment's set-up, in 32-token blocks' worth of time
 constexpr int kTauLog2 = 8;
 constexpr float kTau = kTauLog2;
 constexpr float kPBias = 15 - kTauLog2;
@@ -207,42 +208,54 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
 
   // ---------------- this workgroup's range of the work ----------------
   // The work is every (KV head, sequence, query tile)'s causal history in
-  // 32-token blocks, flattened in that order (tiles in the order of tile_at;
-  // tile t of sequence b holds
-  // blocks(b, t) = ceil((start_b + e_off(t)) / 32)). Workgroup w takes blocks
-  // [w R, (w + 1) R): equal shares whatever the tiles' lengths, so the grid
-  // of about two workgroups per compute unit ends together. A share crosses
-  // tiles: each of its tiles is a segment (queries loaded, history streamed,
-  // output or partial written); only the first and the last segment can hold
-  // part of a tile, and their partials go to the workgroup's two records.
-  // The starts are device values, so the work is counted here, by all
-  // threads, before the LDS ring is in use.
+  // 32-token blocks, flattened in that order (tiles in the order of
+  // tile_at), each tile costing kSegmentCost blocks' worth of set-up (loading
+  // and rotating its queries, filling the ring, writing its result) before
+  // its blocks(b, t) = ceil((start_b + e_off(t)) / 32) blocks. Workgroup w
+  // takes cost units [w R, (w + 1) R): equal shares however long the tiles
+  // and however many of them a share touches, so the grid of about two
+  // workgroups per compute unit ends together. Each tile a share touches is
+  // a segment (queries loaded, history streamed, output or partial written);
+  // only the first and the last can hold part of a tile, and their partials
+  // go to the workgroup's two records. The starts are device values, so the
+  // work is counted here, by all threads, before the LDS ring is in use.
   int *red = reinterpret_cast<int *>(smem);
   const int pairs = B * n_tiles;
   auto pair_blocks = [&](int k) {
     const int b = k / n_tiles, t = tile_at(k - b * n_tiles, n_tiles);
     return (seq_start(p, b) + tile_end(nq, QT, G, t) + kChunk - 1) / kChunk;
   };
-  // Block counts fit 31 bits (the host refuses more work).
-  int w1 = 0;  // blocks of one KV head over every sequence and tile
+  // Costs fit 31 bits (the host refuses more work).
+  int w1 = 0;  // cost of one KV head over every sequence and tile
   for (int k0 = 0; k0 < pairs; k0 += kThreads) {
-    const int x = k0 + tid < pairs ? pair_blocks(k0 + tid) : 0;
+    const int x = k0 + tid < pairs ? kSegmentCost + pair_blocks(k0 + tid) : 0;
     int total;
     (void)block_incl_scan(x, red, lane, wave, total);
     w1 += total;
   }
   const int W = w1 * KV;
-  const int R = p.range_blocks > 0 ? p.range_blocks : max((W + (int)gridDim.x - 1) / (int)gridDim.x, kPrefillMinRange);
-  const int j0 = (int)blockIdx.x * R;
+  // Range lengths: R for every workgroup, or, with p.first_round set (two
+  // workgroups per compute unit), 3 R' for the first p.first_round workgroups
+  // and 2 R' for the rest: the first workgroup dispatched to a compute unit
+  // gets the larger share of its issue slots.
+  const int H = p.first_round, NW = (int)gridDim.x;
+  const int R = p.range_blocks > 0 ? p.range_blocks
+                : H > 0          ? max((W + 3 * H + 2 * (NW - H) - 1) / (3 * H + 2 * (NW - H)), 1)
+                                 : max((W + NW - 1) / NW, kPrefillMinRange);
+  const int w = (int)blockIdx.x;
+  const int j0 = H > 0 ? (w < H ? 3 * R * w : 3 * R * H + 2 * R * (w - H)) : w * R;
   if (j0 >= W) return;  // workgroup-uniform: before any barrier of the segments
-  const int j1 = min(j0 + R, W);
+  const int j1 = min(j0 + (H > 0 ? (w < H ? 3 * R : 2 * R) : R), W);
+  // The range holding cost unit c.
+  auto range_of = [&](int c) { return H > 0 ? (c < 3 * R * H ? c / (3 * R) : H + (c - 3 * R * H) / (2 * R)) : c / R; };
   int kv = j0 / w1;
   const int rem = j0 - kv * w1;
-  // The (sequence, tile) pair holding block rem of KV head kv.
-  int b = 0, t = 0, blk = 0;
+  // The (sequence, tile) pair holding cost unit rem of KV head kv, and the
+  // unit's offset in that tile's cost.
+  int b = 0, t = 0, off = 0;
   for (int k0 = 0, base = 0; k0 < pairs; k0 += kThreads) {
     const int k = k0 + tid;
-    const int x = k < pairs ? pair_blocks(k) : 0;
+    const int x = k < pairs ? kSegmentCost + pair_blocks(k) : 0;
     int total;
     const int excl = base + block_incl_scan(x, red, lane, wave, total) - x;
     if (x > 0 && excl <= rem && rem < excl + x) {
@@ -254,7 +267,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
       const int k_hit = __builtin_amdgcn_readfirstlane(red[kWaves]);
       b = k_hit / n_tiles;
       t = k_hit - b * n_tiles;  // position in the tile order
-      blk = __builtin_amdgcn_readfirstlane(red[kWaves + 1]);
+      off = __builtin_amdgcn_readfirstlane(red[kWaves + 1]);
       __syncthreads();  // every wave has read the cursor before the ring reuses the LDS
       break;
     }
@@ -354,6 +367,10 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         KF >= 1 ? reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(T) +
                                                   __builtin_amdgcn_readfirstlane((int)T->off_books))
                 : nullptr;
+    // Read with the other table fields, before the query loads, whose wait it
+    // would otherwise join.
+    const u32x4 *rq = reinterpret_cast<const u32x4 *>(
+        reinterpret_cast<const uint8_t *>(T) + (KF >= 1 ? __builtin_amdgcn_readfirstlane((int)T->off_rot_q) : 0));
     if (KF == 2 && wave == 0) {  // every book's centroids, [n_books][max_centroids] floats
       const uint32_t nbytes = (uint32_t)__builtin_amdgcn_readfirstlane(T->n_books * T->max_centroids * 4);
       const __amdgpu_buffer_rsrc_t rb_ = rsrc(tbooks, nbytes);
@@ -411,6 +428,19 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
       lim[cb] = valid[cb] ? min(start + qi / G + 1, t_hi) : t_hi;
       lim_min = min(lim_min, lim[cb]);
     }
+    // At d=64 the rotation operands (64 registers) load with the queries, so
+    // their round trips overlap; at d=128 they are too many to hold and load
+    // during the rotation. The ring starts after the rotation: its DMAs are
+    // lane-masked, and the compiler's waits for register loads issued before
+    // such branches would count the DMAs as well.
+    constexpr int RQ = D == 64 ? DT * KS * 2 : 1;
+    u32x4 rqo[RQ];
+    if constexpr (D == 64) {
+      if (rotate) {
+#pragma unroll
+        for (int i = 0; i < RQ; ++i) rqo[i] = rq[((i >> 1) * 64 + lane) * 2 + (i & 1)];
+      }
+    }
     // Scaled by log2(e) / sqrt(d) and split hi/lo with a per-query exponent:
     // the QK operands directly, or the rotation's B operands.
     int eq[NCB];
@@ -435,7 +465,6 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
       // qr^T = Rq q^T on the matrix cores (q and Rq split hi/lo, three MFMAs
       // per step), each operand pair of Rq loaded once for all column blocks:
       // D layout, lane holds rows j = 16 n + 4 gq + r of query col.
-      const u32x4 *rq = reinterpret_cast<const u32x4 *>(tables_rot_q(T));
       f32x4 qr[NCB][DT];
 #pragma unroll
       for (int n = 0; n < DT; ++n) {
@@ -443,8 +472,10 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         for (int cb = 0; cb < NCB; ++cb) qr[cb][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
+          const int io = (n * KS + s) * 2;
           const u32x4 *op = rq + ((n * KS + s) * 64 + lane) * 2;
-          const half8 ah = __builtin_bit_cast(half8, op[0]), al = __builtin_bit_cast(half8, op[1]);
+          const half8 ah = __builtin_bit_cast(half8, D == 64 ? rqo[min(io, RQ - 1)] : op[0]);
+          const half8 al = __builtin_bit_cast(half8, D == 64 ? rqo[min(io + 1, RQ - 1)] : op[1]);
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) {
             qr[cb][n] = mfma(ah, bh[cb][s], qr[cb][n]);
@@ -788,38 +819,45 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     cur[1] = b;
     cur[2] = t;
     cur[3] = kv;
-    cur[4] = blk;
+    cur[4] = off;
   }
-  for (bool first = true;; first = false) {
+  for (bool first = true;;) {
     const int j = __builtin_amdgcn_readfirstlane(cur[0]);
     if (j >= j1) break;  // workgroup-uniform
     const int sb = __builtin_amdgcn_readfirstlane(cur[1]), sk = __builtin_amdgcn_readfirstlane(cur[2]);
-    const int skv = __builtin_amdgcn_readfirstlane(cur[3]), sblk = __builtin_amdgcn_readfirstlane(cur[4]);
+    const int skv = __builtin_amdgcn_readfirstlane(cur[3]), soff = __builtin_amdgcn_readfirstlane(cur[4]);
     const int st = tile_at(sk, n_tiles);
     const int bt = (seq_start(p, sb) + tile_end(nq, QT, G, st) + kChunk - 1) / kChunk;
-    const int n = min(bt - sblk, j1 - j);
+    // This range's part of the tile's cost, [soff, cend), and its blocks.
+    const int cend = min(kSegmentCost + bt, soff + (j1 - j));
+    const int blk = max(soff - kSegmentCost, 0), n = max(cend - kSegmentCost, 0) - blk;
     const int slot = first ? 0 : 1;
-    if (sblk == 0 && tid == 0 && gridDim.x > 1) {
+    if (n > 0 && blk == 0 && tid == 0 && gridDim.x > 1) {
       // The merge finds a tile's partials from here: workgroups w_first ..
-      // w_last, the first one's in its record slot, the others' in slot 0.
+      // w_last (those holding the tile's first and last block), the first
+      // one's in its record slot, the others' in slot 0.
+      const int c_first = j - soff + kSegmentCost;  // cost unit of the tile's block 0
       int4 *info = reinterpret_cast<int4 *>(p.tile_info) + ((int64_t)skv * B + sb) * n_tiles + st;
-      *info = int4{(int)blockIdx.x, (j + bt - 1) / R, slot, 0};
+      *info = int4{(int)blockIdx.x, range_of(c_first + bt - 1), slot, 0};
     }
-    if (lane == 0) {  // the next segment: the following tile, from its first block
+    if (lane == 0) {  // the next segment: the following tile, from its start
       const bool wrap_t = sk + 1 == n_tiles, wrap_b = wrap_t && sb + 1 == B;
-      cur[0] = j + n;
+      cur[0] = j + (cend - soff);
       cur[1] = wrap_t ? (wrap_b ? 0 : sb + 1) : sb;
       cur[2] = wrap_t ? 0 : sk + 1;
       cur[3] = wrap_b ? skv + 1 : skv;
       cur[4] = 0;
     }
-    // Every wave is done with the previous segment's ring, books and operands.
-    if (!first) lds_barrier();
-    // The thread index goes in through an opaque copy, so per-lane offsets
-    // are recomputed per segment rather than held in registers across it.
-    int tid_s = tid;
-    asm volatile("" : "+v"(tid_s));
-    segment(p, tid_s, sb, skv, st, sblk, n, bt, slot);
+    if (n > 0) {  // a range can end inside a tile's set-up share, holding none of its blocks
+      // Every wave is done with the previous segment's ring, books and operands.
+      if (!first) lds_barrier();
+      // The thread index goes in through an opaque copy, so per-lane offsets
+      // are recomputed per segment rather than held in registers across it.
+      int tid_s = tid;
+      asm volatile("" : "+v"(tid_s));
+      segment(p, tid_s, sb, skv, st, blk, n, bt, slot);
+      first = false;
+    }
   }
 }
 
