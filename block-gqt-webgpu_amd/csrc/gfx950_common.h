@@ -87,6 +87,32 @@ __device__ __forceinline__ void split2(float x0, float x1, uint32_t &hi, uint32_
   lo = __builtin_bit_cast(uint32_t, l);
 }
 
+// The same split in four instructions instead of six: lo = fp16(x - hi)
+// through the mixed-precision FMA, which reads hi's fp16 halves directly.
+// `one` must be 1.0 from a register the compiler cannot see through (an
+// empty asm), or it folds the FMA into a subtraction and converts hi back.
+__device__ __forceinline__ void split2_mix(float x0, float x1, float one, uint32_t &hi, uint32_t &lo) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+  const float r0 = __builtin_fmaf(-(float)h[0], one, x0), r1 = __builtin_fmaf(-(float)h[1], one, x1);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, half2_t{(_Float16)r0, (_Float16)r1});
+}
+
+// Eight values split with split2_mix.
+__device__ __forceinline__ void split8_mix(const float *x, float one, half8 &hi, half8 &lo) {
+  u32x4 h4, l4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t h, l;
+    split2_mix(x[2 * k], x[2 * k + 1], one, h, l);
+    h4[k] = h;
+    l4[k] = l;
+  }
+  hi = __builtin_bit_cast(half8, h4);
+  lo = __builtin_bit_cast(half8, l4);
+}
+
 // Split of x * sc (sc a power of two) into fp16 hi (rounded toward zero) and lo halves.
 __device__ __forceinline__ void split_scaled(const float *x, float sc, half8 &hi, half8 &lo) {
   u32x4 h4, l4;

@@ -285,6 +285,8 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     const bool whole = blk_lo == 0 && n_blocks == bt;
     const int lane = tid & 63, gq = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float one = 1.0f;  // opaque 1.0 for the mixed-precision splits
+    asm volatile("" : "+s"(one));
     const int start = seq_start(p, b);  // the chunk's rows end inside the K/V buffers
     const int T_b = start + rows;
     const int q0 = tile * QT;
@@ -558,7 +560,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
 #pragma unroll
           for (int k2 = 0; k2 < 8; ++k2) v[k2] = books[s * 256 + e[k2]] * F;
           half8 hi, lo;
-          split_scaled(v, 1.0f, hi, lo);
+          split8_mix(v, one, hi, lo);
           uint8_t *dst = kb + (u * KS + s) * 2048 + lane * 16;
           *reinterpret_cast<half8 *>(dst) = hi;
           *reinterpret_cast<half8 *>(dst + 1024) = lo;
@@ -600,7 +602,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
             v[k2] = c * __builtin_ldexpf(sc, ec - E);
           }
           half8 hi, lo;
-          split_scaled(v, 1.0f, hi, lo);
+          split8_mix(v, one, hi, lo);
           uint8_t *dst = kb + (u * KS + s) * 2048 + lane * 16;
           *reinterpret_cast<half8 *>(dst) = hi;
           *reinterpret_cast<half8 *>(dst + 1024) = lo;
@@ -735,7 +737,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           uint32_t h, l;
-          split2(pr[2 * k], pr[2 * k + 1], h, l);
+          split2_mix(pr[2 * k], pr[2 * k + 1], one, h, l);
           ph[k] = h;
           pl[k] = l;
         }
