@@ -76,11 +76,16 @@ struct PSlot {
   static constexpr int VW = VI / kWaves;    // ... per wave
   static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : KF == 2 ? D : 2 * D;  // K row bytes
   static constexpr int KBYTES = kChunk * RB;
-  static constexpr int KQ = KBYTES / kWaves;  // K bytes per wave
-  static constexpr int KW = KF >= 1 ? (KQ + 1023) / 1024 : VW;
-  static constexpr int KLAST = KF >= 1 ? (KQ - (KW - 1) * 1024) / 16 : 64;  // lanes of the last K instruction
-  static constexpr int NBYTES = KF == 1 ? kChunk * 4 : KF == 2 ? kChunk * 16 : 0;
-  static constexpr int BYTES = VBYTES + KBYTES + NBYTES;
+  // Packed K and its scales move as 4-byte DMAs with every lane of every wave
+  // busy (no lane-masked instructions, so the compiler's waits for register
+  // loads issued before the ring stay exact): the K block padded to a
+  // multiple of 1 KB, the scales to 1 KB (past the block's tokens the range
+  // check reads zeros).
+  static constexpr int KPAD = KF >= 1 ? (KBYTES + 1023) / 1024 * 1024 : KBYTES;
+  static constexpr int KW = KF >= 1 ? KPAD / 1024 : VW;  // K DMA instructions per wave
+  static constexpr int NUSED = KF == 1 ? kChunk * 4 : KF == 2 ? kChunk * 16 : 0;  // scale bytes of a block
+  static constexpr int NBYTES = KF >= 1 ? 1024 : 0;
+  static constexpr int BYTES = VBYTES + KPAD + NBYTES;
   static constexpr int LW = VW + KW + (KF >= 1 ? 1 : 0);  // DMA instructions per wave per block
   static constexpr int BOOKS = KF >= 1 ? KS * 1024 * KF : 0;  // KF 1: 256 fp32 centroids per K-step
   static constexpr int KOP = KF >= 1 ? 2 * 2 * KS * 2048 : 0;  // [buffer][u][s]: hi 1 KB, lo 1 KB
@@ -89,7 +94,7 @@ struct PSlot {
   static constexpr int RING = 6 * BYTES + FIXED <= kLdsLimit / 2 ? 6 : 4 * BYTES + FIXED <= kLdsLimit / 2 ? 4 : 3;
   static constexpr int AHEAD = RING - 2;
   static constexpr int LDS = RING * BYTES + FIXED;
-  static_assert(VI % kWaves == 0 && KQ % 16 == 0 && KBYTES % 16 == 0, "DMA split over four waves");
+  static_assert(VI % kWaves == 0 && KBYTES % 16 == 0 && NUSED <= NBYTES, "DMA split over four waves");
   static_assert(LDS <= kLdsLimit, "LDS of one workgroup");
   static_assert(AHEAD * LW < 64, "vmcnt range");
 };
@@ -227,10 +232,13 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   };
   // Costs fit 31 bits (the host refuses more work).
   int w1 = 0;  // cost of one KV head over every sequence and tile
+  int x1 = 0, incl1 = 0;  // this thread's pair and prefix when one round holds every pair
   for (int k0 = 0; k0 < pairs; k0 += kThreads) {
     const int x = k0 + tid < pairs ? kSegmentCost + pair_blocks(k0 + tid) : 0;
     int total;
-    (void)block_incl_scan(x, red, lane, wave, total);
+    const int incl = block_incl_scan(x, red, lane, wave, total);
+    x1 = x;
+    incl1 = incl;
     w1 += total;
   }
   const int W = w1 * KV;
@@ -253,7 +261,20 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
   // The (sequence, tile) pair holding cost unit rem of KV head kv, and the
   // unit's offset in that tile's cost.
   int b = 0, t = 0, off = 0;
-  for (int k0 = 0, base = 0; k0 < pairs; k0 += kThreads) {
+  if (pairs <= kThreads) {  // the one round's prefixes are at hand
+    const int excl = incl1 - x1;
+    if (x1 > 0 && excl <= rem && rem < excl + x1) {
+      red[kWaves] = tid;
+      red[kWaves + 1] = rem - excl;
+    }
+    __syncthreads();
+    const int k_hit = __builtin_amdgcn_readfirstlane(red[kWaves]);
+    b = k_hit / n_tiles;
+    t = k_hit - b * n_tiles;
+    off = __builtin_amdgcn_readfirstlane(red[kWaves + 1]);
+    __syncthreads();  // every wave has read the cursor before the ring reuses the LDS
+  }
+  for (int k0 = 0, base = 0; pairs > kThreads && k0 < pairs; k0 += kThreads) {
     const int k = k0 + tid;
     const int x = k < pairs ? kSegmentCost + pair_blocks(k) : 0;
     int total;
@@ -330,28 +351,19 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
 #pragma unroll
       for (int kk = 0; kk < Sl::VW; ++kk) dma16(rV, sb + (wave * Sl::VW + kk) * 1024, voff_rows[kk], 0);
       uint8_t *kb = sb + Sl::VBYTES;
-      if (KF == 1) {
-        const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * RB, rest * RB);
-        const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * 2, rest * 4);
-#pragma unroll
-        for (int kk = 0; kk < Sl::KW; ++kk) {
-          const int off = wave * Sl::KQ + kk * 1024;
-          if (kk + 1 < Sl::KW || Sl::KLAST == 64 || ln < Sl::KLAST) dma16(rK, kb + off, off + ln * 16, 0);
-        }
-        if (ln < kChunk / kWaves) dma4(rN, kb + Sl::KBYTES + wave * 32, wave * 32 + ln * 4, 0);
-      } else if (KF == 2) {
+      if (KF >= 1) {
         // Ranges end on the access size: the range check zeroes a whole access
         // reaching past the range; the bytes past the last row lie in the same
-        // aligned 16 bytes as its end (16-byte aligned bases, c0 a multiple of 32).
-        const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * rb, (rest * rb + 15u) & ~15u);
-        const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * ns, (rest * ns * 2 + 3u) & ~3u);
+        // aligned 4 bytes as its end (16-byte aligned bases, c0 a multiple of 32).
+        const int rbk = KF == 1 ? RB : rb, nsk = KF == 1 ? 2 : ns;
+        const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * rbk, (rest * rbk + 3u) & ~3u);
+        const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * nsk, (rest * nsk * 2 + 3u) & ~3u);
 #pragma unroll
         for (int kk = 0; kk < Sl::KW; ++kk) {
-          const int off = wave * Sl::KQ + kk * 1024;
-          if (kk + 1 < Sl::KW || Sl::KLAST == 64 || ln < Sl::KLAST) dma16(rK, kb + off, off + ln * 16, 0);
+          const int off = (kk * kWaves + wave) * 256;
+          dma4(rK, kb + off, off + ln * 4, 0);
         }
-        if (ln < Sl::NBYTES / kWaves / 4)
-          dma4(rN, kb + Sl::KBYTES + wave * (Sl::NBYTES / kWaves), wave * (Sl::NBYTES / kWaves) + ln * 4, 0);
+        dma4(rN, kb + Sl::KPAD + wave * 256, wave * 256 + ln * 4, 0);
       } else {
         const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
 #pragma unroll
@@ -425,16 +437,21 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         for (int hh = 0; hh < 2; ++hh)
           // Rotated in the kernel: natural order 32 s + 8 gq + 4 hh + 0..3 (the
           // rotation's k order); otherwise QK order 32 s + 16 hh + 4 gq + 0..3.
-          qraw[cb][2 * s + hh] = valid[cb] ? src[rotate ? 8 * s + 2 * gq + hh : 8 * s + 4 * hh + gq]
-                                           : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        {
+          // Loaded unconditionally (an invalid query reads row 0) and then
+          // selected: no lane-masked load, so the waits stay exact.
+          const f32x4 v = src[rotate ? 8 * s + 2 * gq + hh : 8 * s + 4 * hh + gq];
+          qraw[cb][2 * s + hh] = valid[cb] ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
       lim[cb] = valid[cb] ? min(start + qi / G + 1, t_hi) : t_hi;
       lim_min = min(lim_min, lim[cb]);
     }
-    // At d=64 the rotation operands (64 registers) load with the queries, so
-    // their round trips overlap; at d=128 they are too many to hold and load
-    // during the rotation. The ring starts after the rotation: its DMAs are
-    // lane-masked, and the compiler's waits for register loads issued before
-    // such branches would count the DMAs as well.
+    // At d=64 the rotation operands (64 registers) load with the queries and
+    // the ring's first blocks follow at once, so all those round trips
+    // overlap (the DMAs are unmasked and straight-line, so the waits for the
+    // loads count exactly the DMAs after them). At d=128 the operands are too
+    // many to hold: they load during the rotation, and the ring starts after
+    // it (a wait for a load issued after the DMAs would wait for them too).
     constexpr int RQ = D == 64 ? DT * KS * 2 : 1;
     u32x4 rqo[RQ];
     if constexpr (D == 64) {
@@ -442,6 +459,9 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
 #pragma unroll
         for (int i = 0; i < RQ; ++i) rqo[i] = rq[((i >> 1) * 64 + lane) * 2 + (i & 1)];
       }
+#pragma unroll
+      for (int i = 0; i < AHEAD; ++i)
+        if (i < n_blocks) issue(i);
     }
     // Scaled by log2(e) / sqrt(d) and split hi/lo with a per-query exponent:
     // the QK operands directly, or the rotation's B operands.
@@ -509,9 +529,11 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
     }
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) eqs[cb] = eq[cb] + ec;
+    if constexpr (D != 64) {
 #pragma unroll
-    for (int i = 0; i < AHEAD; ++i)
-      if (i < n_blocks) issue(i);
+      for (int i = 0; i < AHEAD; ++i)
+        if (i < n_blocks) issue(i);
+    }
     // Wave-uniform: blocks reaching past lim_min need the per-query mask.
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o, 64));
@@ -529,7 +551,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         // the same step s = wave % KS).
         constexpr bool NIB = decltype(nib_c)::value;
         const uint8_t *kraw = slot(i) + Sl::VBYTES;
-        const uint32_t *nrm = reinterpret_cast<const uint32_t *>(kraw + Sl::KBYTES);
+        const uint32_t *nrm = reinterpret_cast<const uint32_t *>(kraw + Sl::KPAD);
         const uint32_t nw = nrm[lane & 31];
         const float smax = wave_max(SG < KS ? fmaxf(h2f(nw & 0xffffu), h2f(nw >> 16)) : h2f(nw & 0xffffu));
         const int E = smax > 0.0f ? (int)ceilf(__builtin_log2f(smax)) : 0;
@@ -570,14 +592,14 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         // Any layout: each element's code through its descriptor, times its
         // book's centroid and its group's scale of the token, 2^(ec - E).
         const uint8_t *kraw = slot(i) + Sl::VBYTES;
-        const uint16_t *nrm = reinterpret_cast<const uint16_t *>(kraw + Sl::KBYTES);
+        const uint16_t *nrm = reinterpret_cast<const uint16_t *>(kraw + Sl::KPAD);
         // E bounds the scales of the block's tokens inside the history only: the
         // scale DMA's range is rounded up to 4 bytes, so with rest * ns odd the
         // slot also holds the first scale of the token after the history.
         const int n_in = min(T_b - (t_lo + i * kChunk), kChunk) * ns;
         float smax = 0.0f;
 #pragma unroll
-        for (int k = 0; k < Sl::NBYTES / 2 / 64; ++k) {
+        for (int k = 0; k < Sl::NUSED / 2 / 64; ++k) {
           const int e = lane + 64 * k;
           if (e < n_in) smax = fmaxf(smax, fabsf(h2f(nrm[e])));
         }
@@ -929,6 +951,94 @@ __global__ __launch_bounds__(kThreads) void prefill_merge_kernel(PrefillParams p
   for (int e = 0; e < DL; ++e) *reinterpret_cast<f32x4 *>(out + 64 * e + 4 * c) = acc[e] * inv_l;
 }
 
+// The same merge for launches with few queries: one wave per query, every
+// record's (m, l) pair in one lane and every record's o row loaded in one
+// round (record k < SMAX reads record min(k, n - 1), whose weight is zero
+// past n); tiles with more than SMAX records take the rounds above instead.
+template <int D, int SMAX>
+__global__ __launch_bounds__(kThreads) void prefill_merge_one_round_kernel(PrefillParams p) {
+  constexpr int DL = D / 64;
+  const int unit = blockIdx.y;
+  const int b = unit / p.kv_heads, kv = unit - b * p.kv_heads;
+  const int G = p.G, rows = p.rows, nq = rows * G, QT = p.tile_queries;
+  const int lane = threadIdx.x & 63;
+  const int qi = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (qi >= nq) return;
+  const int tile = qi / QT, qt = qi - tile * QT;
+  const int4 info = reinterpret_cast<const int4 *>(p.tile_info)[((int64_t)kv * p.batch + b) * p.tiles + tile];
+  const int n = info.y - info.x + 1;
+  if (n == 1) return;
+  const int64_t rs = (int64_t)QT * (D + 2);  // floats per record
+  const float *first = p.part + ((int64_t)info.x * 2 + info.z) * rs + (int64_t)qt * (D + 2);
+  const float *rest = p.part + ((int64_t)info.x + 1) * 2 * rs + (int64_t)qt * (D + 2);
+  auto rec = [&](int k) { return k == 0 ? first : rest + (int64_t)(k - 1) * 2 * rs; };
+  float *out = p.out + query_row(b, rows, p.q_heads, kv, G, qi) * D;
+  if (n > SMAX) {  // wave-uniform: online rounds of eight records
+    float M = -INFINITY, L = 0.0f, acc[DL];
+#pragma unroll
+    for (int e = 0; e < DL; ++e) acc[e] = 0.0f;
+    for (int k0 = 0; k0 < n; k0 += 8) {
+      float m[8], l[8], o[8][DL];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const float *r = rec(min(k0 + kk, n - 1));
+        m[kk] = k0 + kk < n ? r[0] : -INFINITY;
+        l[kk] = r[1];
+#pragma unroll
+        for (int e = 0; e < DL; ++e) o[kk][e] = r[2 + lane + 64 * e];
+      }
+      float Mn = M;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) Mn = fmaxf(Mn, m[kk]);
+      const float sc = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+      L *= sc;
+#pragma unroll
+      for (int e = 0; e < DL; ++e) acc[e] *= sc;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const float w = m[kk] == -INFINITY ? 0.0f : exp2f(m[kk] - Mn);
+        L = __builtin_fmaf(w, l[kk], L);
+#pragma unroll
+        for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[kk][e], w, acc[e]);
+      }
+      M = Mn;
+    }
+#pragma unroll
+    for (int e = 0; e < DL; ++e) out[lane + 64 * e] = acc[e] / L;
+    return;
+  }
+  float o[SMAX][DL];
+#pragma unroll
+  for (int k = 0; k < SMAX; ++k)
+#pragma unroll
+    for (int e = 0; e < DL; ++e) o[k][e] = rec(min(k, n - 1))[2 + lane + 64 * e];
+  const float *rl = rec(min(lane, n - 1));
+  const float ml = lane < n ? rl[0] : -INFINITY, ll = rl[1];
+  float M = ml;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) M = fmaxf(M, __shfl_xor(M, s, 64));
+  float w = ml == -INFINITY ? 0.0f : exp2f(ml - M);
+  float L = w * ll;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) L += __shfl_xor(L, s, 64);
+  w = w / L;
+  float acc[DL];
+#pragma unroll
+  for (int e = 0; e < DL; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < SMAX; ++k) {
+    const float wk = __shfl(w, k, 64);
+#pragma unroll
+    for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[k][e], wk, acc[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < DL; ++e) out[lane + 64 * e] = acc[e];
+}
+
+// Launches with at most this many queries merge one query per wave in one
+// round of loads (latency bound: few queries, many records each).
+constexpr int64_t kMergeOneRoundQueries = 2048;
+
 template <int D, int KF, int NN, int SG, int NCB>
 hipError_t launch_ncb(const PrefillParams &p, const FastLayout &fl, hipStream_t stream) {
   constexpr int lds = PSlot<D, KF, NN>::LDS;
@@ -942,8 +1052,13 @@ hipError_t launch_ncb(const PrefillParams &p, const FastLayout &fl, hipStream_t 
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ranges == 1) return e;
   const unsigned units = (unsigned)(p.batch * p.kv_heads);
-  hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)(p.tiles * (p.tile_queries / (kThreads / 16))), units),
-                     dim3(kThreads), 0, stream, p);
+  const int nq = p.rows * p.G;
+  if ((int64_t)nq * units <= kMergeOneRoundQueries)
+    hipLaunchKernelGGL((prefill_merge_one_round_kernel<D, 64>), dim3((unsigned)((nq + kWaves - 1) / kWaves), units),
+                       dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)(p.tiles * (p.tile_queries / (kThreads / 16))), units),
+                       dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 
