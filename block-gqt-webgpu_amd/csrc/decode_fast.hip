@@ -9,10 +9,11 @@
 //             tables of fp16 (hi, lo) pairs: for nibble K-steps one entry per
 //             packed byte (two dims), for byte K-steps one entry per code.
 //   main loop each wave streams 32-token chunks of packed codes, FP16 scales
-//             and FP16 V straight from HBM into a three-deep ring of LDS
+//             and FP16 V straight from HBM into a two-slot ring of LDS
 //             buffers with buffer_load ... lds (no VGPR staging, non-temporal:
-//             every byte is read once), two chunks ahead of the one it
-//             computes on. Reads past the sequence's length return zeros, so
+//             every byte is read once): the chunk issued at the top of an
+//             iteration lands while the wave computes QK and the softmax of
+//             the previous one. Reads past the sequence's length return zeros, so
 //             the tail needs no clamping. From LDS it rebuilds the K
 //             operand through the tables, runs QK as 16x16x32
 //             f16 MFMAs (hi*hi + lo*hi + hi*lo, FP32-level logits), an online
@@ -45,7 +46,7 @@ using namespace gfx;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kChunk = 32;  // tokens per wave iteration: two 16-token MFMA tiles
-constexpr int kRing = 3;    // LDS chunk buffers per wave: compute one, the others in flight
+constexpr int kRing = 2;    // LDS chunk buffers per wave: compute one, the next in flight
 constexpr bool kInterleaved = true;
 constexpr int kMergeOneRound = 40;  // split counts merged with a single round of loads
 
@@ -82,7 +83,6 @@ struct Slot {
   static constexpr int BYTES = KOFF + KI * 1024;
   static constexpr int L = Geo<D>::VI + KI + NSC;  // DMA instructions per chunk
   static constexpr int TABLES = KF == 2 && D == 64 ? 3584 : KF >= 1 ? KS * 2048 : 0;
-  // Three buffers per wave where they fit the CU, else two (FP16 K at d=128).
   static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
   static constexpr int AHEAD = RING - 1;
   static constexpr int DYN = RING * kWaves * BYTES;  // dynamic LDS: the ring (the tables are static)
@@ -809,17 +809,29 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         for (int dt = 0; dt < DT; ++dt) O[dt][r] *= ar;
       }
     }
-    // PV: B operand = V[tokens of this lane's P slots][16 dt + col], read transposed.
-    const half8 pha = __builtin_bit_cast(half8, ph), pla = __builtin_bit_cast(half8, pl);
+    // PV: B operand = V[tokens of this lane's P slots][16 dt + col], read
+    // transposed (inline asm with explicit LDS waits; the appended row's LDS
+    // stores above are ordered before the reads by the memory clobber).
+    // Before them the wave waits for the chunk issued at the top of this
+    // iteration, so each wave has loads in flight only during the first half
+    // of an iteration. Measured at 64 x 32768 tokens (layout B), this is
+    // faster than keeping a ring full across iterations: 6264 GB/s against
+    // 5826 for these two slots waited for at the next iteration's top, 5780
+    // for three slots (two chunks ahead), 6170 for three slots waited for
+    // here.
+    wait_vm<0>();
+    u32x2 vt[DT][2];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const int piece = 2 * dt + tpiece;
-      const fp16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (lds_fp16x4 *)(sb + trow * (2 * D) + ((piece ^ swz<D>(trow)) * 16) + thalf));
-      const fp16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (lds_fp16x4 *)(sb + (16 + trow) * (2 * D) + ((piece ^ swz<D>(16 + trow)) * 16) + thalf));
-      const u32x2 a0 = __builtin_bit_cast(u32x2, v0), a1 = __builtin_bit_cast(u32x2, v1);
-      const half8 vb = __builtin_bit_cast(half8, u32x4{a0[0], a0[1], a1[0], a1[1]});
+      ds_read_tr16_pair(sb + trow * (2 * D) + ((piece ^ swz<D>(trow)) * 16) + thalf,
+                        sb + (16 + trow) * (2 * D) + ((piece ^ swz<D>(16 + trow)) * 16) + thalf, vt[dt][0], vt[dt][1]);
+    }
+    const half8 pha = __builtin_bit_cast(half8, ph), pla = __builtin_bit_cast(half8, pl);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      wait_dt<DT>(dt, vt[dt][0], vt[dt][1]);
+      const half8 vb = __builtin_bit_cast(half8, u32x4{vt[dt][0][0], vt[dt][0][1], vt[dt][1][0], vt[dt][1][1]});
       O[dt] = mfma(pha, vb, O[dt]);
       O[dt] = mfma(pla, vb, O[dt]);
     }

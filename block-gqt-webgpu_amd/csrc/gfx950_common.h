@@ -183,6 +183,32 @@ __device__ __forceinline__ void wait_lds_tied(u32x2 &a, u32x2 &b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
 }
 
+// Wait for transposed read pair dt of DT issued in order (2 (DT - 1 - dt)
+// newer reads may still be in flight); dt is a compile-time index after
+// unrolling.
+template <int DT>
+__device__ __forceinline__ void wait_dt(int dt, u32x2 &a, u32x2 &b) {
+  if constexpr (DT == 2) {
+    if (dt == 0) wait_lds_tied<2>(a, b);
+    else wait_lds_tied<0>(a, b);
+  } else if constexpr (DT == 4) {
+    if (dt == 0) wait_lds_tied<6>(a, b);
+    else if (dt == 1) wait_lds_tied<4>(a, b);
+    else if (dt == 2) wait_lds_tied<2>(a, b);
+    else wait_lds_tied<0>(a, b);
+  } else {
+    static_assert(DT == 8, "head dim 32, 64 or 128");
+    if (dt == 0) wait_lds_tied<14>(a, b);
+    else if (dt == 1) wait_lds_tied<12>(a, b);
+    else if (dt == 2) wait_lds_tied<10>(a, b);
+    else if (dt == 3) wait_lds_tied<8>(a, b);
+    else if (dt == 4) wait_lds_tied<6>(a, b);
+    else if (dt == 5) wait_lds_tied<4>(a, b);
+    else if (dt == 6) wait_lds_tied<2>(a, b);
+    else wait_lds_tied<0>(a, b);
+  }
+}
+
 // 16-byte piece swizzle of an FP16 row of D values in LDS: conflict-free
 // transposed (ds_read_b64_tr_b16) and row reads.
 template <int D>

@@ -332,7 +332,7 @@ class FP16Keys {
     const self = this;
     this.buffer = new DeviceView(() => native.keysReadFp16(self.handle, self.capacity * self.dim));
   }
-  get length() { return native.keysLength(this.handle); }
+  get length() { return keysLength(this); }
   async append(values) {
     if (this._pending) throw new Error('Concurrent K appends unsupported');
     appendCount(values, this.dim, this.length, this.capacity);
@@ -344,8 +344,16 @@ class FP16Keys {
 
 // The append runs off the JS thread and its Promise resolves once the rows
 // are on the device (src/runtime/packed-keys.ts:39-49); destroy() during an
-// append waits for it.
+// append waits for it. As in the reference, the store reports its earlier
+// length and is not ready until that Promise settles, even when the device
+// work finished before (src/runtime/packed-keys.ts:43,47,49).
+function keysLength(keys) { return keys._pending ? keys._lengthBefore : native.keysLength(keys.handle); }
+function keysReady(keys) {
+  if (keys._pending) throw new Error('K storage not ready');
+  native.keysReady(keys.handle);
+}
 async function runAppend(keys, values) {
+  keys._lengthBefore = native.keysLength(keys.handle);
   keys._pending = true;
   try {
     await native.keysAppendAsync(keys.handle, values);
@@ -383,13 +391,13 @@ class PackedKeys {
     this.norms = new DeviceView(() => both()[1]);
   }
   static async create(device, p, capacity) { return new PackedKeys(device, p, capacity, false); }
-  get length() { return native.keysLength(this.handle); }
+  get length() { return keysLength(this); }
   async append(values) {
     if (this._pending) throw new Error('Concurrent K appends unsupported');
     appendCount(values, this.dim, this.length, this.capacity);
     await runAppend(this, values);
   }
-  ready() { native.keysReady(this.handle); }
+  ready() { keysReady(this); }
   destroy() { destroyAfterAppend(this); }
 }
 
