@@ -466,19 +466,30 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   if (rotate) lds_barrier();  // q staging (last ring slot) is dead
 
   // KF 2: a K-step spans up to kSlots adjacent groups glo[s] .. glo[s] +
-  // nsl[s] - 1. Each group's part of the K-step runs its own MFMAs against
-  // the query with the other groups' positions masked to zero (gmask), and
-  // the token's scale of that group weights the result. A lane's 8 codes of
+  // nsl[s] - 1. Each group's part of the K-step runs MFMAs against the query
+  // with the other groups' positions masked to zero (the record's per-slot
+  // masks), and the token's scale of that group weights the result. A lane's 8 codes of
   // a K-step are nibbles, then bytes (the head-perm order puts every nibble
   // position first): they lie in the 8 row bytes from koff, read as two
   // words; codes 0..3 come from the first word, codes 4..7 from the word
   // starting at byte hib[s]. ext[s][k]: the code's bit offset in its word;
   // tbo[s][k]: its book's LDS table offset plus the field width (4 or 8),
   // whose low 5 bits are the width operand of the bit-field extract.
+  //
+  // Group packing: with at most 8 (4) query heads, one MFMA's 16 columns hold
+  // the query operands of two (four) groups side by side. Column c carries
+  // head hc = c % HW masked to group slot m * GP + c / HW of MFMA m, so a
+  // K-step of nsl groups takes ceil(nsl / GP) MFMA triples instead of nsl.
+  // Each lane weights its partial logits with its own group's scales, and
+  // row rotations by 8 (and 4) lanes then sum the slots of each head: every
+  // lane c ends with head hc's logit, and the real heads (c < G <= HW) are
+  // where the softmax expects them.
   constexpr int kSlots = 4;
-  int glo[KS2], nsl[KS2], koff[KS2], hib[KS2];
+  int glo[KS2], nsl[KS2], koff[KS2], hib[KS2], nmf[KS2];
   uint32_t ext[KS2][8], tbo[KS2][8];
-  u32x4 gmask[KS2][kSlots];
+  half8 qbh[KS2][kSlots], qbl[KS2][kSlots];  // masked (packed) query operands of MFMA m
+  const int GP = KF == 2 ? (G <= 4 ? 4 : G <= 8 ? 2 : 1) : 1;  // group slots per MFMA
+  const int HW = 16 / GP, cg = col / HW;
   constexpr int NSV = KF == 2 ? 2 * Sl::NSC : 1;  // scale entries a lane moves
   int sc_src[NSV], sc_dst[NSV];
   const bool rows_aligned = KF == 2 && fl.galign[kv] != 0;  // every lane's 8 bytes start on a word
@@ -494,8 +505,27 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         ext[s][k] = grec[s][1 + (k >> 2)][k & 3];
         tbo[s][k] = grec[s][3 + (k >> 2)][k & 3];
       }
+      nmf[s] = (nsl[s] + GP - 1) / GP;
+      // Head hc's operands come from lane (gq, hc); slot cg + m * GP's mask
+      // keeps that group's positions (slots past the K-step's groups: none).
+      const u32x4 h = __builtin_bit_cast(u32x4, qhi[s]), l = __builtin_bit_cast(u32x4, qlo[s]);
+      const int src = 16 * gq + (col & (HW - 1));
+      u32x4 hs, ls;
 #pragma unroll
-      for (int i = 0; i < kSlots; ++i) gmask[s][i] = grec[s][5 + i];
+      for (int k = 0; k < 4; ++k) {
+        hs[k] = (uint32_t)__shfl((int)h[k], src, 64);
+        ls[k] = (uint32_t)__shfl((int)l[k], src, 64);
+      }
+#pragma unroll
+      for (int m = 0; m < kSlots; ++m) {
+        const int slot = m * GP + cg;
+        u32x4 mk{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < kSlots; ++i)
+          if (slot == i) mk = grec[s][5 + i];
+        qbh[s][m] = __builtin_bit_cast(half8, hs & mk);
+        qbl[s][m] = __builtin_bit_cast(half8, ls & mk);
+      }
     }
     // The chunk's scale rows [token][ns] become [group][32 tokens] in place
     // (lane moves entries lane + 64 k), so a lane's four tokens of one group
@@ -669,20 +699,18 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
           al[u] = __builtin_bit_cast(half8, lo);
         }
 #pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-          if (i >= nsl[s]) continue;
-          half8 bh = qhi[s], bl = qlo[s];
-          if (nsl[s] > 1) {
-            bh = __builtin_bit_cast(half8, __builtin_bit_cast(u32x4, bh) & gmask[s][i]);
-            bl = __builtin_bit_cast(half8, __builtin_bit_cast(u32x4, bl) & gmask[s][i]);
-          }
+        for (int m = 0; m < kSlots; ++m) {
+          if (m >= nmf[s]) continue;
+          // This lane's group; a slot past the K-step's groups has a zero
+          // operand, and reads the last group's (finite) scales.
+          const int g = min(glo[s] + m * GP + cg, glo[s] + nsl[s] - 1);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             f32x4 a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            a = mfma(ah[u], bh, a);
-            a = mfma(al[u], bh, a);
-            a = mfma(ah[u], bl, a);
-            const u32x2 w = *reinterpret_cast<const u32x2 *>(sb + Sl::NOFF + 2 * ((glo[s] + i) * 32 + 16 * u + 4 * gq));
+            a = mfma(ah[u], qbh[s][m], a);
+            a = mfma(al[u], qbh[s][m], a);
+            a = mfma(ah[u], qbl[s][m], a);
+            const u32x2 w = *reinterpret_cast<const u32x2 *>(sb + Sl::NOFF + 2 * (g * 32 + 16 * u + 4 * gq));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float sc = __half2float(__ushort_as_half((uint16_t)(w[r >> 1] >> (16 * (r & 1)))));
@@ -690,6 +718,21 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
             }
           }
         }
+      }
+      // Sum the group slots of each head (lanes c, c + 8 (, c + 4, c + 12)).
+      if (GP >= 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            x2[u][r] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x2[u][r]), 0x128, 0xf, 0xf, false));
+      }
+      if (GP == 4) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            x2[u][r] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x2[u][r]), 0x124, 0xf, 0xf, false));
       }
     }
 

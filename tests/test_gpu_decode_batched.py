@@ -154,6 +154,23 @@ def test_layout_a_fused(device, oracle, dim, splits):
          splits=splits, pad16=True)
 
 
+@pytest.mark.parametrize("dim,G", [(64, 1), (64, 4), (64, 5), (64, 8), (64, 9), (64, 16), (128, 3), (128, 8),
+                                   (128, 12)])
+def test_any_layout_group_packing(device, oracle, dim, G):
+    """The fused per-position kernel packs four (G <= 4) or two (G <= 8) group slots into one
+    matrix-core product and sums them across lanes; G > 8 runs one slot per product. Every
+    packing width against the oracle, on layout A (two groups per K-step) and the real heads."""
+    from bgtq import calibrate
+    p = calibrate.layout_a(dim)
+    print("group packing", dim, G, flush=True)
+    _run(device, oracle, params=[p, p], batch=2, hq=2 * G, hkv=2, dim=dim, lengths=[300, 1031], cap=1031,
+         pad16=True, seed=G)
+    if dim == 64:
+        heads = _smollm2_heads(oracle, ["h0", "h1", "h22"])
+        _run(device, oracle, params=heads, batch=1, hq=3 * G, hkv=3, dim=dim, lengths=[517], cap=517, pad16=True,
+             seed=G + 1)
+
+
 def _smollm2_heads(oracle, names):
     """Reference calibration heads of one layer: one cache row stride and norm stride for all
     (src/model/decoder.ts:21 keeps one per head)."""
