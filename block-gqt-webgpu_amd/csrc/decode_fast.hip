@@ -82,7 +82,10 @@ struct Slot {
   static constexpr int KOFF = NOFF + NBYTES;          // K
   static constexpr int BYTES = KOFF + KI * 1024;
   static constexpr int L = Geo<D>::VI + KI + NSC;  // DMA instructions per chunk
-  static constexpr int TABLES = KF == 2 && D == 64 ? 3584 : KF >= 1 ? KS * 2048 : 0;
+  // Lookup tables (static LDS): KF 1, the K-steps' books; KF 2, the books'
+  // code tables (CTABLES bytes), then kPairSlots pair tables of 2 KB.
+  static constexpr int CTABLES = KF == 2 && D == 64 ? 3584 : KF >= 1 ? KS * 2048 : 0;
+  static constexpr int TABLES = CTABLES + (KF == 2 ? kPairSlots * 2048 : 0);
   static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
   static constexpr int AHEAD = RING - 1;
   static constexpr int DYN = RING * kWaves * BYTES;  // dynamic LDS: the ring (the tables are static)
@@ -343,6 +346,17 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         }
       }
     }
+    // The pair tables ([byte]: hi pair, lo pair) of the pair K-steps' books.
+    const uint32_t pair_books = fl.gpair[kv];
+#pragma unroll
+    for (int ps = 0; ps < kPairSlots; ++ps) {
+      const uint32_t bk = (pair_books >> (8 * ps)) & 0xffu;
+      if (bk != 0xffu) {
+        const __amdgpu_buffer_rsrc_t rt = rsrc(fl.mfma[kv] + bk * kMfmaTableBytes, 2048);
+        dma16(rt, tabs + Sl::CTABLES + ps * 2048, lane * 16, 0);
+        dma16(rt, tabs + Sl::CTABLES + ps * 2048 + 1024, 1024 + lane * 16, 0);
+      }
+    }
   }
   f32x4 qload[KS][2];  // unconditional loads of a valid row; heads past G are zeroed after the chunk issue
   {
@@ -485,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // lane c ends with head hc's logit, and the real heads (c < G <= HW) are
   // where the softmax expects them.
   constexpr int kSlots = 4;
-  int glo[KS2], nsl[KS2], koff[KS2], hib[KS2], nmf[KS2];
+  int glo[KS2], nsl[KS2], koff[KS2], hib[KS2], nmf[KS2], pair[KS2];
   uint32_t ext[KS2][8], tbo[KS2][8];
   half8 qbh[KS2][kSlots], qbl[KS2][kSlots];  // masked (packed) query operands of MFMA m
   const int GP = KF == 2 ? (G <= 4 ? 4 : G <= 8 ? 2 : 1) : 1;  // group slots per MFMA
@@ -499,7 +513,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       koff[s] = (int)grec[s][0][0];
       hib[s] = (int)grec[s][0][1];
       glo[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][2]);
-      nsl[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][3]);
+      nsl[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][3]) & 0xff;
+      pair[s] = ((int)__builtin_amdgcn_readfirstlane(grec[s][0][3]) >> 8) & 1;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         ext[s][k] = grec[s][1 + (k >> 2)][k & 3];
@@ -668,7 +683,31 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       for (int s = 0; s < KS2; ++s) {
         half8 ah[2], al[2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < 2 && pair[s]; ++u) {
+          // Pair K-step: the lane's 8 nibble codes are the 4 bytes from
+          // koff; each byte's pair table entry is an (hi, lo) operand pair.
+          const int rofs = (16 * u + col) * rb + koff[s];
+          uint32_t w0;
+          if (rows_aligned) {
+            w0 = *reinterpret_cast<const uint32_t *>(kbuf + rofs);
+          } else {
+            const int sh = rofs & 3;
+            const uint32_t *wp = reinterpret_cast<const uint32_t *>(kbuf + (rofs - sh));
+            w0 = __builtin_amdgcn_alignbyte(wp[1], wp[0], (uint32_t)sh);
+          }
+          u32x4 hi, lo;
+#pragma unroll
+          for (int k2 = 0; k2 < 4; ++k2) {
+            const uint32_t byte = __builtin_amdgcn_ubfe(w0, 8 * k2, 8);
+            const u32x2 e = *reinterpret_cast<const u32x2 *>(tabs + Sl::CTABLES + tbo[s][k2] + 8 * byte);
+            hi[k2] = e[0];
+            lo[k2] = e[1];
+          }
+          ah[u] = __builtin_bit_cast(half8, hi);
+          al[u] = __builtin_bit_cast(half8, lo);
+        }
+#pragma unroll
+        for (int u = 0; u < 2 && !pair[s]; ++u) {
           const int rofs = (16 * u + col) * rb + koff[s];
           uint32_t w0, w1;
           if (rows_aligned) {
@@ -1039,7 +1078,7 @@ bool decode_fast_supported(int dim, int key_format, int nn, int sg) {
          (nn == 0 && sg == h);
 }
 
-int decode_general_table_bytes(int dim) { return dim == 64 ? Slot<64, 2, 1>::TABLES : Slot<128, 2, 1>::TABLES; }
+int decode_general_table_bytes(int dim) { return dim == 64 ? Slot<64, 2, 1>::CTABLES : Slot<128, 2, 1>::CTABLES; }
 
 int decode_general_max_norm_stride(int dim) {
   return dim == 64 ? Slot<64, 2, 2>::NBYTES / 64 : Slot<128, 2, 2>::NBYTES / 64;
