@@ -442,7 +442,7 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
   const size_t off_rot_q = align(off_mfma + (size_t)kMfmaTableBytes * nb);
   const size_t off_gdesc = align(off_rot_q + (d % 32 == 0 ? (size_t)rot_q_bytes((int)d) : 0));
   const size_t off_glane = align(off_gdesc + sizeof(uint32_t) * d);
-  const size_t total = off_glane + (d % 32 == 0 ? sizeof(uint32_t) * 36 * 4 * (d / 32) : 0);
+  const size_t total = off_glane + (d % 32 == 0 ? sizeof(uint32_t) * kLaneRecordWords * 4 * (d / 32) : 0);
   auto *t = new bgtq_tables();
   t->ctx = ctx;
   t->host.assign(total, 0);
@@ -491,35 +491,33 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
               (uint32_t)group_of[j] << 16;
     }
   }
+  T->pair_lead = 0;
   T->pair_books = 0xffffffffu;
   if (d % 32 == 0) {
     // The fused decode's per-lane code-lookup records (layout in DevTables).
     const int bspan = std::max(256, (int)(mc * 4 + 255) / 256 * 256) + 32;
     uint32_t *rec = reinterpret_cast<uint32_t *>(h + off_glane);
     auto off_of = [&](int64_t j) { return j < nib ? j / 2 : nib / 2 + (j - nib); };
-    // Pair K-steps and the pair slots of their books, in K-step order while
-    // the slots last.
+    // Leading pair K-steps, while their books fit the pair slots.
     std::vector<int> pair_slot_of(nb, -1);
-    std::vector<bool> pair_step(d / 32, false);
     int n_pair = 0;
     for (int64_t s = 0; s < d / 32; ++s) {
       bool ok = 32 * s + 32 <= nib;
       for (int64_t j = 32 * s; ok && j < 32 * s + 32; j += 2) ok = pos_book[j] == pos_book[j + 1];
-      if (!ok) continue;
       std::vector<int> fresh;
-      for (int64_t j = 32 * s; j < 32 * s + 32; j += 2)
+      for (int64_t j = 32 * s; ok && j < 32 * s + 32; j += 2)
         if (pair_slot_of[pos_book[j]] < 0 && std::find(fresh.begin(), fresh.end(), pos_book[j]) == fresh.end())
           fresh.push_back(pos_book[j]);
-      if (n_pair + (int)fresh.size() > kPairSlots) continue;
+      if (!ok || n_pair + (int)fresh.size() > kPairSlots) break;
       for (int b : fresh) {
         pair_slot_of[b] = n_pair;
         T->pair_books = (T->pair_books & ~(0xffu << (8 * n_pair))) | (uint32_t)b << (8 * n_pair);
         ++n_pair;
       }
-      pair_step[s] = true;
+      T->pair_lead = (int32_t)(s + 1);
     }
     for (int64_t s = 0; s < d / 32; ++s)
-      for (int gq = 0; gq < 4; ++gq, rec += 36) {
+      for (int gq = 0; gq < 4; ++gq, rec += kLaneRecordWords) {
         const int64_t j0 = 32 * s + 8 * gq;
         const int glo = (int)group_of[32 * s];
         int bo[8], grp[8];
@@ -533,13 +531,16 @@ bgtq_status bgtq_tables_create(bgtq_context *ctx, const uint32_t *integer, size_
         rec[0] = (uint32_t)off_of(j0);
         rec[1] = (uint32_t)hib;
         rec[2] = (uint32_t)glo;
-        rec[3] = (uint32_t)((int)group_of[32 * s + 31] - glo + 1) | (uint32_t)pair_step[s] << 8;
-        if (pair_step[s])
-          for (int k2 = 0; k2 < 4; ++k2) rec[12 + k2] = (uint32_t)(pair_slot_of[pos_book[j0 + 2 * k2]] * 2048);
+        rec[3] = (uint32_t)((int)group_of[32 * s + 31] - glo + 1);
         for (int k = 0; k < 8; ++k) rec[4 + k] = (uint32_t)(k < 4 ? bo[k] : bo[k] - 8 * hib);
         for (int i = 0; i < 4; ++i)
           for (int k2 = 0; k2 < 4; ++k2)
             rec[20 + 4 * i + k2] = (grp[2 * k2] == i ? 0x0000ffffu : 0u) | (grp[2 * k2 + 1] == i ? 0xffff0000u : 0u);
+        for (int k2 = 0; k2 < 4; ++k2) {
+          const int slot = s < T->pair_lead ? pair_slot_of[pos_book[j0 + 2 * k2]] : 0;
+          rec[36 + k2] = (uint32_t)(slot * 2048);
+          rec[40 + k2] = (uint32_t)(slot * 2048 + 1024);
+        }
       }
   }
   for (uint64_t i = 0; i < lut_len; ++i) h[off_lut + i] = (uint8_t)lut[i];
@@ -1132,6 +1133,7 @@ static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tabl
     fl->gbnib[h] = (uint8_t)nib_books;
     fl->galign[h] = T->row_bytes % 4 == 0 && T->nibble_dims % 8 == 0;
     fl->gpair[h] = T->pair_books;
+    fl->gpair_lead = h == 0 ? T->pair_lead : std::min(fl->gpair_lead, T->pair_lead);
   }
   return true;
 }

@@ -20,9 +20,10 @@ struct DevTables {
   int32_t gstart[kMaxGroups], gend[kMaxGroups], gsize[kMaxGroups];  // group ranges (head-perm order)
   uint32_t off_lut, off_books, off_rot, off_rot_t, off_mfma, off_rot_q, off_gdesc, off_glane, total_bytes;
   int32_t cent_exp;  // 2^cent_exp * max|centroid| <= 2^14: fp16 hi/lo split range for MFMA operands
-  // Books whose pair tables the fused decode of any packed layout keeps in
-  // LDS for its pair K-steps (see off_glane): byte i = book of pair slot i,
-  // 0xff = unused.
+  // The fused decode of any packed layout: its leading pair K-steps (see
+  // off_glane) and the books whose pair tables it keeps in LDS for them
+  // (byte i = book of pair slot i, 0xff = unused).
+  int32_t pair_lead;
   uint32_t pair_books;
   uint8_t perm[kMaxDim];      // head_perm
   uint8_t group_of[kMaxDim];
@@ -48,21 +49,23 @@ struct DevTables {
   //             layout: uint32 byte offset in the packed row | nibble shift << 8
   //             | nibble flag << 11 | book << 12 | group << 16.
   // [off_glane]  (d % 32 == 0) the fused decode's per-lane code-lookup
-  //             records, [K-step s][lane group gq][36] uint32 for positions
-  //             j = 32 s + 8 gq + k: koff (row byte of code 0), hib (byte
-  //             where the word of codes 4..7 starts), glo (group of position
-  //             32 s), nsl (groups in the K-step) | pair flag << 8, ext[8]
-  //             (bit offset of each code in its word), tbo[8] (LDS offset of
-  //             its book's code table plus its field width), gmask[4][4] (per
-  //             slot i, the fp16 halves of the 8 positions in group glo + i).
-  //             A pair K-step (all 32 positions nibble codes, each even
-  //             position in the book of the next) reads two codes per packed
-  //             byte from its book's pair table: tbo[k2], k2 < 4, is then the
-  //             offset of the pair table of positions 2 k2, 2 k2 + 1 among
-  //             the pair slots (kPairSlots of 2 KB).
+  //             records, [K-step s][lane group gq][kLaneRecordWords] uint32
+  //             for positions j = 32 s + 8 gq + k: koff (row byte of code 0),
+  //             hib (byte where the word of codes 4..7 starts), glo (group of
+  //             position 32 s), nsl (groups in the K-step), ext[8] (bit offset
+  //             of each code in its word), tbo[8] (LDS offset of its book's
+  //             code table plus its field width), gmask[4][4] (per slot i, the
+  //             fp16 halves of the 8 positions in group glo + i), then for a
+  //             pair K-step phi[4] and plo[4]: the LDS offsets, among the pair
+  //             slots (kPairSlots of 2 KB: hi pairs, then lo pairs), of the
+  //             pair table entries of positions 2 k2, 2 k2 + 1. A pair K-step
+  //             (all 32 positions nibble codes, each even position in the book
+  //             of the next; only leading K-steps, pair_lead of them) reads
+  //             two codes per packed byte.
 };
 constexpr int kMfmaTableBytes = 3072;
-constexpr int kPairSlots = 4;  // pair tables (2 KB each) the fused decode keeps in LDS
+constexpr int kPairSlots = 4;         // pair tables (2 KB each) the fused decode keeps in LDS
+constexpr int kLaneRecordWords = 44;  // words of one per-lane code-lookup record
 __host__ __device__ constexpr int rot_q_bytes(int dim) { return dim * dim * 4; }
 
 __host__ __device__ inline const uint8_t *tables_lut(const DevTables *t) {
@@ -269,6 +272,7 @@ struct FastLayout {
   int16_t grb[kMaxKvHeads], gns[kMaxKvHeads], gnb[kMaxKvHeads], gbstride[kMaxKvHeads];
   uint8_t gbnib[kMaxKvHeads], galign[kMaxKvHeads];
   uint32_t gpair[kMaxKvHeads];  // DevTables::pair_books
+  int32_t gpair_lead;           // leading pair K-steps of every head of the launch
 };
 
 // Sets the calling thread's bgtq_last_error() message; returns code.

@@ -142,7 +142,8 @@ __device__ __noinline__ void merge_one_round(float *part, float *out, float *sta
 // KF: 1 = packed codes of a structured layout, 2 = packed codes of any
 // layout, 0 = FP16 K rows. NN: leading nibble K-steps (KF 2: scale DMAs).
 // SG: K-steps in group 0 (== KS: one scale per token; unused by KF 2).
-template <int D, int KF, int NN, int SG>
+// PK (KF 2): leading pair K-steps of every head (two codes per packed byte).
+template <int D, int KF, int NN, int SG, int PK = 0>
 __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
   using Sl = Slot<D, KF, NN>;
@@ -346,15 +347,18 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         }
       }
     }
-    // The pair tables ([byte]: hi pair, lo pair) of the pair K-steps' books.
+    // The pair tables ([byte]: hi pair, lo pair) of the pair K-steps' books,
+    // split into a table of hi pairs and one of lo pairs (1 KB each).
     const uint32_t pair_books = fl.gpair[kv];
 #pragma unroll
-    for (int ps = 0; ps < kPairSlots; ++ps) {
+    for (int ps = 0; ps < (PK > 0 ? kPairSlots : 0); ++ps) {
       const uint32_t bk = (pair_books >> (8 * ps)) & 0xffu;
       if (bk != 0xffu) {
         const __amdgpu_buffer_rsrc_t rt = rsrc(fl.mfma[kv] + bk * kMfmaTableBytes, 2048);
-        dma16(rt, tabs + Sl::CTABLES + ps * 2048, lane * 16, 0);
-        dma16(rt, tabs + Sl::CTABLES + ps * 2048 + 1024, 1024 + lane * 16, 0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          dma4(rt, tabs + Sl::CTABLES + ps * 2048 + (q & 1) * 1024 + (q >> 1) * 256,
+               ((q >> 1) * 64 + lane) * 8 + (q & 1) * 4, 0);
       }
     }
   }
@@ -386,13 +390,15 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // tables, one per K-step and lane group gq): koff, hib, glo, nsl, ext[8],
   // tbo[8], gmask[4][4] (36 words, described where they are used).
   constexpr int KS2 = KF == 2 ? KS : 1;
-  u32x4 grec[KS2][9];
+  constexpr int RW = kLaneRecordWords / 4;
+  u32x4 grec[KS2][RW];
   if (KF == 2) {
     const u32x4 *gr = reinterpret_cast<const u32x4 *>(fl.glane[kv]);
 #pragma unroll
     for (int s = 0; s < KS2; ++s)
 #pragma unroll
-      for (int m = 0; m < 9; ++m) grec[s][m] = gr[(s * 4 + gq) * 9 + m];
+      for (int m = 0; m < RW; ++m)
+        if (m < 9 || s < PK) grec[s][m] = gr[(s * 4 + gq) * RW + m];
   }
   // Unconditional, so every wave has exactly AHEAD * L chunk loads in flight
   // behind its prologue loads (chunks past the end are zero-sized). The
@@ -499,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // lane c ends with head hc's logit, and the real heads (c < G <= HW) are
   // where the softmax expects them.
   constexpr int kSlots = 4;
-  int glo[KS2], nsl[KS2], koff[KS2], hib[KS2], nmf[KS2], pair[KS2];
+  int glo[KS2], nsl[KS2], koff[KS2], hib[KS2], nmf[KS2];
   uint32_t ext[KS2][8], tbo[KS2][8];
   half8 qbh[KS2][kSlots], qbl[KS2][kSlots];  // masked (packed) query operands of MFMA m
   const int GP = KF == 2 ? (G <= 4 ? 4 : G <= 8 ? 2 : 1) : 1;  // group slots per MFMA
@@ -513,12 +519,12 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       koff[s] = (int)grec[s][0][0];
       hib[s] = (int)grec[s][0][1];
       glo[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][2]);
-      nsl[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][3]) & 0xff;
-      pair[s] = ((int)__builtin_amdgcn_readfirstlane(grec[s][0][3]) >> 8) & 1;
+      nsl[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][3]);
+      // A pair K-step keeps its pair table offsets in tbo (hi) and ext (lo).
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        ext[s][k] = grec[s][1 + (k >> 2)][k & 3];
-        tbo[s][k] = grec[s][3 + (k >> 2)][k & 3];
+        ext[s][k] = s < PK ? (k < 4 ? grec[s][10][k] : 0u) : grec[s][1 + (k >> 2)][k & 3];
+        tbo[s][k] = s < PK ? (k < 4 ? grec[s][9][k] : 0u) : grec[s][3 + (k >> 2)][k & 3];
       }
       nmf[s] = (nsl[s] + GP - 1) / GP;
       // Head hc's operands come from lane (gq, hc); slot cg + m * GP's mask
@@ -679,64 +685,73 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int r = 0; r < 4; ++r) x2[u][r] = 0.0f;
+      // The lane's row words of every (K-step, tile) first, so the LDS reads
+      // of all four are in flight together, then every code lookup.
+      uint32_t w0[KS2][2], wh[KS2][2];
+      {
+        uint32_t dw[KS2][2][3];
+#pragma unroll
+        for (int s = 0; s < KS2; ++s)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int rofs = (16 * u + col) * rb + koff[s];
+            // kbuf is 16-byte aligned: the row offset's low bits are the address's
+            const uint32_t *wp = reinterpret_cast<const uint32_t *>(kbuf + (rows_aligned ? rofs : rofs & ~3));
+            dw[s][u][0] = wp[0];
+            if (!rows_aligned || s >= PK) dw[s][u][1] = wp[1];
+            if (!rows_aligned && s >= PK) dw[s][u][2] = wp[2];
+          }
+#pragma unroll
+        for (int s = 0; s < KS2; ++s)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const uint32_t sh = (uint32_t)(((16 * u + col) * rb + koff[s]) & 3);
+            uint32_t w1 = 0;
+            if (rows_aligned) {
+              w0[s][u] = dw[s][u][0];
+              if (s >= PK) w1 = dw[s][u][1];
+            } else {
+              w0[s][u] = __builtin_amdgcn_alignbyte(dw[s][u][1], dw[s][u][0], sh);
+              if (s >= PK) w1 = __builtin_amdgcn_alignbyte(dw[s][u][2], dw[s][u][1], sh);
+            }
+            wh[s][u] = s < PK || hib[s] == 4 ? w1 : __builtin_amdgcn_alignbyte(w1, w0[s][u], (uint32_t)hib[s]);
+          }
+      }
+      half8 ah[KS2][2], al[KS2][2];
+#pragma unroll
+      for (int s = 0; s < KS2; ++s)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          u32x4 hi, lo;
+          if (s < PK) {
+            // Pair K-step: the lane's 8 nibble codes are the 4 bytes of w0;
+            // each byte's pair table entries are an (hi, lo) operand pair.
+            const uint8_t *pt = tabs + Sl::CTABLES;
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) {
+              const uint32_t byte4 = 4 * __builtin_amdgcn_ubfe(w0[s][u], 8 * k2, 8);
+              hi[k2] = *reinterpret_cast<const uint32_t *>(pt + tbo[s][k2] + byte4);
+              lo[k2] = *reinterpret_cast<const uint32_t *>(pt + ext[s][k2] + byte4);
+            }
+          } else {
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) {
+              uint32_t e[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const int k = 2 * k2 + h;
+                const uint32_t code = __builtin_amdgcn_ubfe(k < 4 ? w0[s][u] : wh[s][u], ext[s][k], tbo[s][k]);
+                e[h] = *reinterpret_cast<const uint32_t *>(tabs + tbo[s][k] + 4 * code);
+              }
+              hi[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
+              lo[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
+            }
+          }
+          ah[s][u] = __builtin_bit_cast(half8, hi);
+          al[s][u] = __builtin_bit_cast(half8, lo);
+        }
 #pragma unroll
       for (int s = 0; s < KS2; ++s) {
-        half8 ah[2], al[2];
-#pragma unroll
-        for (int u = 0; u < 2 && pair[s]; ++u) {
-          // Pair K-step: the lane's 8 nibble codes are the 4 bytes from
-          // koff; each byte's pair table entry is an (hi, lo) operand pair.
-          const int rofs = (16 * u + col) * rb + koff[s];
-          uint32_t w0;
-          if (rows_aligned) {
-            w0 = *reinterpret_cast<const uint32_t *>(kbuf + rofs);
-          } else {
-            const int sh = rofs & 3;
-            const uint32_t *wp = reinterpret_cast<const uint32_t *>(kbuf + (rofs - sh));
-            w0 = __builtin_amdgcn_alignbyte(wp[1], wp[0], (uint32_t)sh);
-          }
-          u32x4 hi, lo;
-#pragma unroll
-          for (int k2 = 0; k2 < 4; ++k2) {
-            const uint32_t byte = __builtin_amdgcn_ubfe(w0, 8 * k2, 8);
-            const u32x2 e = *reinterpret_cast<const u32x2 *>(tabs + Sl::CTABLES + tbo[s][k2] + 8 * byte);
-            hi[k2] = e[0];
-            lo[k2] = e[1];
-          }
-          ah[u] = __builtin_bit_cast(half8, hi);
-          al[u] = __builtin_bit_cast(half8, lo);
-        }
-#pragma unroll
-        for (int u = 0; u < 2 && !pair[s]; ++u) {
-          const int rofs = (16 * u + col) * rb + koff[s];
-          uint32_t w0, w1;
-          if (rows_aligned) {
-            w0 = *reinterpret_cast<const uint32_t *>(kbuf + rofs);
-            w1 = *reinterpret_cast<const uint32_t *>(kbuf + rofs + 4);
-          } else {  // kbuf is 16-byte aligned: the row offset's low bits are the address's
-            const int sh = rofs & 3;
-            const uint32_t *wp = reinterpret_cast<const uint32_t *>(kbuf + (rofs - sh));
-            const uint32_t d0 = wp[0], d1 = wp[1], d2 = wp[2];
-            w0 = __builtin_amdgcn_alignbyte(d1, d0, (uint32_t)sh);
-            w1 = __builtin_amdgcn_alignbyte(d2, d1, (uint32_t)sh);
-          }
-          const uint32_t wh = hib[s] == 4 ? w1 : __builtin_amdgcn_alignbyte(w1, w0, (uint32_t)hib[s]);
-          u32x4 hi, lo;
-#pragma unroll
-          for (int k2 = 0; k2 < 4; ++k2) {
-            uint32_t e[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const int k = 2 * k2 + h;
-              const uint32_t code = __builtin_amdgcn_ubfe(k < 4 ? w0 : wh, ext[s][k], tbo[s][k]);
-              e[h] = *reinterpret_cast<const uint32_t *>(tabs + tbo[s][k] + 4 * code);
-            }
-            hi[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
-            lo[k2] = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
-          }
-          ah[u] = __builtin_bit_cast(half8, hi);
-          al[u] = __builtin_bit_cast(half8, lo);
-        }
 #pragma unroll
         for (int m = 0; m < kSlots; ++m) {
           if (m >= nmf[s]) continue;
@@ -746,9 +761,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             f32x4 a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            a = mfma(ah[u], qbh[s][m], a);
-            a = mfma(al[u], qbh[s][m], a);
-            a = mfma(ah[u], qbl[s][m], a);
+            a = mfma(ah[s][u], qbh[s][m], a);
+            a = mfma(al[s][u], qbh[s][m], a);
+            a = mfma(ah[s][u], qbl[s][m], a);
             const u32x2 w = *reinterpret_cast<const u32x2 *>(sb + Sl::NOFF + 2 * (g * 32 + 16 * u + 4 * gq));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -1039,18 +1054,18 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   if (tid == 0) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int KF, int NN, int SG>
+template <int D, int KF, int NN, int SG, int PK = 0>
 hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
-  static const hipError_t allowed = hipFuncSetAttribute(
-      (const void *)decode_fast_kernel<D, KF, NN, SG>, hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN>::DYN);
+  static const hipError_t allowed = hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN>::DYN);
   if (allowed != hipSuccess) {
     (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
     return allowed;
   }
   constexpr int lds = Slot<D, KF, NN>::DYN;
   dim3 grid((unsigned)p.splits, (unsigned)(p.batch * p.kv_heads));
-  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG>), grid, dim3(kThreads), lds, stream, p, fl);
+  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK>), grid, dim3(kThreads), lds, stream, p, fl);
   return hipGetLastError();
 }
 
@@ -1089,8 +1104,14 @@ hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int n
   if (nn < 0) {  // any packed layout: one or two scale DMAs per chunk
     int ns = 0;
     for (int h = 0; h < p.kv_heads; ++h) ns = fl.gns[h] > ns ? fl.gns[h] : ns;
-    if (D == 64) return ns <= 4 ? launch_one<64, 2, 1, 1>(p, fl, stream) : launch_one<64, 2, 2, 1>(p, fl, stream);
-    return ns <= 4 ? launch_one<128, 2, 1, 1>(p, fl, stream) : launch_one<128, 2, 2, 1>(p, fl, stream);
+    // Pair lookups for K-step 0 when every head's K-step 0 is a pair K-step.
+    const bool pk = fl.gpair_lead >= 1;
+    if (D == 64) {
+      if (ns <= 4) return pk ? launch_one<64, 2, 1, 1, 1>(p, fl, stream) : launch_one<64, 2, 1, 1>(p, fl, stream);
+      return pk ? launch_one<64, 2, 2, 1, 1>(p, fl, stream) : launch_one<64, 2, 2, 1>(p, fl, stream);
+    }
+    if (ns <= 4) return pk ? launch_one<128, 2, 1, 1, 1>(p, fl, stream) : launch_one<128, 2, 1, 1>(p, fl, stream);
+    return pk ? launch_one<128, 2, 2, 1, 1>(p, fl, stream) : launch_one<128, 2, 2, 1>(p, fl, stream);
   }
   if (p.key_format == 0) return D == 64 ? launch_one<64, 0, 0, 2>(p, fl, stream) : launch_one<128, 0, 0, 4>(p, fl, stream);
 #define BGTQ_FAST(DD, N, S) \
