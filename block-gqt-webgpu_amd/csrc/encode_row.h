@@ -33,7 +33,7 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // Per-wave LDS scratch of one row: leaf[D] f32, xn[D] f32, part[64] f32,
-// tot[8] f32, codes[D] u8.
+// tot[8] f32 (unused; kept so the scratch layout is unchanged), codes[D] u8.
 __host__ __device__ constexpr int scratch_bytes(int D) { return ((D * 4 * 2 + 64 * 4 + 8 * 4 + D) + 15) & ~15; }
 
 template <int D>
@@ -51,14 +51,16 @@ struct Scratch {
 
 // ATen's 8-lane inner sum over leaf[0..D) restricted to each group's positions,
 // for all ng groups; lane (l, g) = 8 g + l passes its group's range [gs, ge).
-// Every lane then reads tot[g].
+// Lane 8 g returns group g's total; pick() hands it to any lane. The eight
+// partials of a group lie in one 16-lane row, so lane 8 g adds them in order
+// through row shifts (no LDS round trip).
 template <int D>
-__device__ __forceinline__ void group_sums(const float *leaf, float *part, float *tot, int lane, int ng, int gs,
-                                           int ge) {
+__device__ __forceinline__ float group_tree(const float *leaf, int lane, int ng, int gs, int ge) {
   constexpr int NV = D / 8, SI = NV / 4;
+  float a0 = 0.0f;
   if (lane < 8 * ng) {
-    const int l = lane & 7, g = lane >> 3;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    const int l = lane & 7;
+    float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
     for (int i = 0; i < SI; ++i) {
       const int p0 = (4 * i + 0) * 8 + l, p1 = (4 * i + 1) * 8 + l, p2 = (4 * i + 2) * 8 + l, p3 = (4 * i + 3) * 8 + l;
@@ -75,16 +77,29 @@ __device__ __forceinline__ void group_sums(const float *leaf, float *part, float
     a0 += a1;
     a0 += a2;
     a0 += a3;
-    part[g * 8 + l] = a0;
   }
-  wave_sync();
-  if (lane < ng) {
-    float t = 0.0f;
+  // t = part 0 + part 1 + ... + part 7 (lane 8 g + k's part reaches lane 8 g by a row shift of k).
+  const int ai = __float_as_int(a0);
+  float t = a0;
+  t += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x101, 0xf, 0xf, false));
+  t += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x102, 0xf, 0xf, false));
+  t += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x103, 0xf, 0xf, false));
+  t += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x104, 0xf, 0xf, false));
+  t += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x105, 0xf, 0xf, false));
+  t += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x106, 0xf, 0xf, false));
+  t += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x107, 0xf, 0xf, false));
+  return t;
+}
+
+// Group g's total (g < ng) from group_tree's result, in any lane.
+__device__ __forceinline__ float pick(float t, int g) {
+  float r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0));
 #pragma unroll
-    for (int l = 0; l < 8; ++l) t += part[lane * 8 + l];
-    tot[lane] = t;
+  for (int k = 1; k < kMaxGroups; ++k) {
+    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 8 * k));
+    r = g == k ? v : r;
   }
-  wave_sync();
+  return r;
 }
 
 // Per-lane constants of the dimensions a lane owns, from the tables.
@@ -124,42 +139,35 @@ __device__ __forceinline__ uint16_t encode_row(const DevTables *T, const Lane<D>
                                                int lane) {
   constexpr int JL = Lane<D>::JL;
   const int ng = T->groups, mc = T->max_centroids;
-  // production_math.py:12  n_g = sqrt(sum((x*x)*mask) + 1e-30)
+  // production_math.py:12  n_g = sqrt(sum((x*x)*mask) + 1e-30): each lane
+  // forms the values of its own dimensions' groups and, below ng, of group
+  // `lane` (the final scale), so nothing is computed for groups it does not use.
+  const int gl = lane < ng ? lane : 0;
 #pragma unroll
   for (int jl = 0; jl < JL; ++jl)
     if (c.own[jl]) s.leaf[lane + 64 * jl] = x[jl] * x[jl];
   wave_sync();
-  group_sums<D>(s.leaf, s.part, s.tot, lane, ng, c.gs, c.ge);
-  float nrm[kMaxGroups];
+  const float t1 = group_tree<D>(s.leaf, lane, ng, c.gs, c.ge);
+  float nrm[JL];
 #pragma unroll
-  for (int g = 0; g < kMaxGroups; ++g) nrm[g] = g < ng ? __builtin_sqrtf(s.tot[g] + 1e-30f) : 1.0f;
+  for (int jl = 0; jl < JL; ++jl) nrm[jl] = __builtin_sqrtf(pick(t1, c.grp[jl]) + 1e-30f);
   // production_math.py:14  raw_g = sum(n_g*mask)/|g| (more than one group)
-  float raw[kMaxGroups];
+  float raw;
   if (ng > 1) {
     wave_sync();
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl) {
-      float n = nrm[0];
-#pragma unroll
-      for (int g = 1; g < kMaxGroups; ++g) n = c.grp[jl] == g ? nrm[g] : n;
-      if (c.own[jl]) s.leaf[lane + 64 * jl] = n;
-    }
+    for (int jl = 0; jl < JL; ++jl)
+      if (c.own[jl]) s.leaf[lane + 64 * jl] = nrm[jl];
     wave_sync();
-    group_sums<D>(s.leaf, s.part, s.tot, lane, ng, c.gs, c.ge);
-#pragma unroll
-    for (int g = 0; g < kMaxGroups; ++g) raw[g] = g < ng ? s.tot[g] / (float)T->gsize[g] : 0.0f;
+    const float t2 = group_tree<D>(s.leaf, lane, ng, c.gs, c.ge);
+    raw = pick(t2, gl) / (float)T->gsize[gl];
   } else {
-#pragma unroll
-    for (int g = 0; g < kMaxGroups; ++g) raw[g] = nrm[g];
+    raw = __builtin_sqrtf(pick(t1, 0) + 1e-30f);
   }
   // production_math.py:15  xn = x / where(n > 1e-10, n, 1)
 #pragma unroll
-  for (int jl = 0; jl < JL; ++jl) {
-    float n = nrm[0];
-#pragma unroll
-    for (int g = 1; g < kMaxGroups; ++g) n = c.grp[jl] == g ? nrm[g] : n;
-    if (c.own[jl]) s.xn[lane + 64 * jl] = x[jl] / (n > 1e-10f ? n : 1.0f);
-  }
+  for (int jl = 0; jl < JL; ++jl)
+    if (c.own[jl]) s.xn[lane + 64 * jl] = x[jl] / (nrm[jl] > 1e-10f ? nrm[jl] : 1.0f);
   wave_sync();
   // production_math.py:16-18  y_j (FMA chain, i ascending), bin, code
   float cent[JL];
@@ -180,15 +188,10 @@ __device__ __forceinline__ uint16_t encode_row(const DevTables *T, const Lane<D>
   for (int jl = 0; jl < JL; ++jl)
     if (c.own[jl]) s.leaf[lane + 64 * jl] = cent[jl] * cent[jl];
   wave_sync();
-  group_sums<D>(s.leaf, s.part, s.tot, lane, ng, c.gs, c.ge);
+  const float t3 = group_tree<D>(s.leaf, lane, ng, c.gs, c.ge);
+  const float cc = fmaxf(__builtin_sqrtf(pick(t3, gl)), 1e-10f);
   uint16_t h = 0;
-  if (lane < T->norm_stride && lane < ng) {
-    const float cc = fmaxf(__builtin_sqrtf(s.tot[lane]), 1e-10f);
-    float rg = raw[0];
-#pragma unroll
-    for (int g = 1; g < kMaxGroups; ++g) rg = lane == g ? raw[g] : rg;
-    h = f32_to_f16_bits(rg / cc);
-  }
+  if (lane < T->norm_stride && lane < ng) h = f32_to_f16_bits(raw / cc);
   return h;
 }
 
