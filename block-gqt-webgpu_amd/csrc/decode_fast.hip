@@ -99,42 +99,76 @@ struct Slot {
   static_assert(AHEAD >= 1 && AHEAD <= 3, "ring waits cover up to three chunks in flight");
 };
 
-// Split merge in one round trip: each output element of the KV head's G
-// query heads loads every split's (m, l, o) at once, S <= SMAX. Out of line,
-// and instantiated for a few SMAX, so the kernel's own code stays as small.
+// Split merge in one round trip, one wave per query head (heads wave,
+// wave + 4, ..., two at a time): lane s loads split s's (m, l), and every lane
+// loads each split's o at its DL dimensions, all loads in flight at once
+// (S <= SMAX).
+// The weights w_s = 2^(m_s - M) come from wave reductions and reach every
+// lane through lane reads. Out of line, and instantiated for a few SMAX, so
+// the kernel's own code stays as small.
 template <int D, int SMAX>
 __device__ __noinline__ void merge_one_round(float *part, float *out, float *stats, int64_t head0, int G, int S,
-                                             int tid) {
-  for (int e = tid; e < G * D; e += kThreads) {
-    const int g = e / D, dm = e - g * D;
-    const int64_t head = head0 + g;
-    float *pp = part + head * S * (D + 2);
-    float m[SMAX], l[SMAX], o[SMAX];
+                                             int wave, int lane) {
+  static_assert(SMAX <= 64, "one split per lane");
+  constexpr int DL = D / 64;  // dimensions per lane
+  constexpr int NH = 2;       // heads of one wave merged together (heads g and g + 4)
+  for (int g0 = wave; g0 < G; g0 += NH * kWaves) {
+    float ms[NH], ls[NH], o[NH][SMAX][DL];
 #pragma unroll
-    for (int s = 0; s < SMAX; ++s) {
-      if (s < S) {
-        m[s] = coherent_load(pp + s * (D + 2));
-        l[s] = coherent_load(pp + s * (D + 2) + 1);
-        o[s] = coherent_load(pp + s * (D + 2) + 2 + dm);
+    for (int h = 0; h < NH; ++h) {
+      const int g = g0 + h * kWaves;
+      ms[h] = -INFINITY;
+      ls[h] = 0.0f;
+      if (g >= G) continue;
+      float *pp = part + (head0 + g) * S * (D + 2);
+      if (lane < S) {
+        ms[h] = coherent_load(pp + lane * (D + 2));
+        ls[h] = coherent_load(pp + lane * (D + 2) + 1);
+      }
+#pragma unroll
+      for (int s = 0; s < SMAX; ++s) {
+        if (s < S) {
+          if (DL == 2) {
+            const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t *>(pp + s * (D + 2) + 2 + 2 * lane),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            o[h][s][0] = __uint_as_float((uint32_t)v);
+            o[h][s][DL - 1] = __uint_as_float((uint32_t)(v >> 32));
+          } else {
+            o[h][s][0] = coherent_load(pp + s * (D + 2) + 2 + lane);
+          }
+        }
       }
     }
-    float M = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < SMAX; ++s)
-      if (s < S) M = fmaxf(M, m[s]);
-    float Lsum = 0.0f, Ov = 0.0f;
+    for (int h = 0; h < NH; ++h) {
+      const int g = g0 + h * kWaves;
+      if (g >= G) continue;
+      const int64_t head = head0 + g;
+      const float M = col_max(row_max(ms[h]));
+      const float w = ms[h] == -INFINITY ? 0.0f : exp2f(ms[h] - M);
+      float lw = ls[h] * w;
+      lw += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(lw), 0x128, 0xf, 0xf, false));
+      lw += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(lw), 0x124, 0xf, 0xf, false));
+      lw += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(lw), 0x122, 0xf, 0xf, false));
+      lw += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(lw), 0x121, 0xf, 0xf, false));
+      const float Lsum = col_sum(lw);
+      float acc[DL];
 #pragma unroll
-    for (int s = 0; s < SMAX; ++s) {
-      if (s < S) {
-        const float w = m[s] == -INFINITY ? 0.0f : exp2f(m[s] - M);
-        Lsum = __builtin_fmaf(l[s], w, Lsum);
-        Ov = __builtin_fmaf(o[s], w, Ov);
+      for (int dl = 0; dl < DL; ++dl) acc[dl] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < SMAX; ++s) {
+        if (s < S) {
+          const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s));
+#pragma unroll
+          for (int dl = 0; dl < DL; ++dl) acc[dl] = __builtin_fmaf(o[h][s][dl], ws, acc[dl]);
+        }
       }
-    }
-    out[head * D + dm] = Ov / Lsum;
-    if (dm == 0 && stats) {
-      stats[head * 2] = M * kLn2;
-      stats[head * 2 + 1] = Lsum;
+#pragma unroll
+      for (int dl = 0; dl < DL; ++dl) out[head * D + DL * lane + dl] = acc[dl] / Lsum;
+      if (lane == 0 && stats) {
+        stats[head * 2] = M * kLn2;
+        stats[head * 2 + 1] = Lsum;
+      }
     }
   }
 }
@@ -240,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // Per-head causal limits (read before the ring's loads are in flight).
   const bool head_ok = col < G;
   const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)b * Hq + hq0 + col], T_b) : T_b) : 0;
-  const int lim = min(end_h, t_end);
+  int lim = min(end_h, t_end);
   // Wave-uniform: chunks reaching past lim_min need the per-head mask.
   int lim_min = head_ok ? lim : t_end;
 #pragma unroll
@@ -248,22 +282,32 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 
   // ---------------- decode-step append ----------------
   // With p.k_new the sequence's newest token (row T_b - 1) arrives in this
-  // launch. The wave whose chunk holds it loads the new K and V rows (and,
-  // at d=64, its column of the transposed rotation) with the prologue's
-  // loads; after the prologue it encodes the K (packed K; FP16 K rows are
-  // converted) and converts the V, stores both rows to the caches for the
-  // later steps and keeps them in registers: after that chunk's loads land it
-  // writes them over the chunk's LDS copy, whose loads may have read the rows
-  // before they were stored.
+  // launch. The wave whose chunk holds it (the owner) loads the new V row
+  // with the prologue's loads, converts it, stores it to the cache for the
+  // later steps and, after that chunk's loads land, writes it over the
+  // chunk's LDS copy (whose loads may have read the row before it was
+  // stored). FP16 K rows go the same way. Packed K takes longer to encode,
+  // so another wave of the workgroup (the encoder) does it while the owner
+  // works through its chunk without the new token: the encoder loads the
+  // new K (and, at d=64, its column of the transposed rotation) and V,
+  // encodes and stores the K row, and starts its own attention state with
+  // the new token (its logit from the row it encoded); the workgroup's merge
+  // of its waves' states then counts the token once.
   constexpr int JL = D > 64 ? 2 : 1;
   const int t_new = T_b - 1;
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
-  const bool app = p.k_new != nullptr && t_new >= 0 && c_new % (p.splits * kWaves) == split * kWaves + wave;
-  const int i_new = app ? c_new / (p.splits * kWaves) : -1;  // the wave's loop iteration of that chunk
-  // The q rotation stages through the last ring slot of a wave other than
-  // the new token's, whose slot receives the encoder's tables meanwhile.
   const int own_w = p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
+  const bool owner = own_w == wave;
+  const bool encoder = KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
+  const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
+  // The q rotation stages through the last ring slot of a wave other than
+  // the encoder, whose slot receives the encoder's tables meanwhile.
   const int stage_w = own_w >= 0 && own_w < kWaves ? (own_w + 1) % kWaves : 0;
+  if (owner && KF >= 1) {  // the owner's chunk pass leaves the new token to the encoder
+    lim = min(lim, t_new);
+    lim_min = min(lim_min, t_new);
+  }
+  const int t_logit = owner && KF >= 1 ? t_new : t_end;  // logits this wave materialises: tokens below
   uint32_t pk_new[JL] = {};                    // packed K bytes lane, lane + 64
   uint32_t h_new = 0;                          // FP16 scale bits (lanes below the norm stride)
   u32x4 v_new16{0u, 0u, 0u, 0u}, k_new16{0u, 0u, 0u, 0u};  // FP16 pieces of the V / K row (lanes below D / 8)
@@ -290,30 +334,28 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
                  : r[k];
     return h;
   };
-  if (app) {
-    if (KF >= 1) {
-      // The tables' header, code LUT and books (contiguous from the start of
-      // the table set, fl.enc_bytes[kv] bytes) into this wave's last ring
-      // slot, first of this wave's loads: the prologue's wait covers them.
-      const __amdgpu_buffer_rsrc_t rt =
-          rsrc(reinterpret_cast<const uint8_t *>(p.tables[kv]) + fl.enc_from[kv], fl.enc_bytes[kv]);
-      uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
+  if (encoder) {
+    // The tables' header, code LUT and books (contiguous from the start of
+    // the table set, fl.enc_bytes[kv] bytes) into this wave's last ring
+    // slot, first of this wave's loads: the prologue's wait covers them.
+    const __amdgpu_buffer_rsrc_t rt =
+        rsrc(reinterpret_cast<const uint8_t *>(p.tables[kv]) + fl.enc_from[kv], fl.enc_bytes[kv]);
+    uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
 #pragma unroll
-      for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
-    }
+    for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
     if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
-    if (KF >= 1) {
 #pragma unroll
-      for (int jl = 0; jl < JL; ++jl)
-        k_nat[jl] = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new)[k_off + lane + 64 * jl]
-                                : (uint32_t)static_cast<const uint16_t *>(p.k_new)[k_off + lane + 64 * jl];
-      if (D == 64) {
+    for (int jl = 0; jl < JL; ++jl)
+      k_nat[jl] = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new)[k_off + lane + 64 * jl]
+                              : (uint32_t)static_cast<const uint16_t *>(p.k_new)[k_off + lane + 64 * jl];
+    if (D == 64) {
 #pragma unroll
-        for (int i = 0; i < D; ++i) rt_col[i] = fl.rot_t[kv][i * D + lane];
-      }
-    } else if (lane < PR) {
-      load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
+      for (int i = 0; i < D; ++i) rt_col[i] = fl.rot_t[kv][i * D + lane];
     }
+  }
+  if (owner) {
+    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
+    if (KF == 0 && lane < PR) load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
   }
 
   // ---------------- prologue ----------------
@@ -559,12 +601,20 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
   }
 
-  if (app) {  // the new token's rows: convert / encode, store to the caches
+  float new_x = -INFINITY;  // encoder: the new token's logit for head col (log2 domain; -inf: not attended)
+  if (owner) {  // the new token's V (and FP16 K) row: convert, store to the caches
     if (lane < PR) {
       v_new16 = half_piece(p.v_new_f32, v_raw);
       *reinterpret_cast<u32x4 *>(const_cast<_Float16 *>(v_base) + (int64_t)t_new * D + 8 * lane) = v_new16;
     }
-    if (KF >= 1) {
+    if (KF == 0 && lane < PR) {
+      k_new16 = half_piece(p.k_new_f32, k_raw);
+      *reinterpret_cast<u32x4 *>(reinterpret_cast<_Float16 *>(const_cast<uint8_t *>(k_base)) + (int64_t)t_new * D +
+                                 8 * lane) = k_new16;
+    }
+  }
+  if (encoder) {  // encode the new K row, store it, start this wave's state with the new token
+    {
       // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
       // T, lut, books: the LDS copy of the tables (header, LUT, books) loaded in
       // the prologue; for KF 2 tables larger than the slot holds, the header in
@@ -602,6 +652,29 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
           }
         }
         if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
+        // The new row in the code domain, k_j = c_j s_g(j) (positions j in
+        // head-perm order), and the FP16-rounded new V row, for its logits and
+        // its share of the output.
+#pragma unroll
+        for (int jl = 0; jl < JL; ++jl) {
+          const float sc = row_enc::f16_bits_to_f32((uint16_t)__shfl((int)h_new, lc.grp[jl], 64));
+          if (lc.own[jl]) scr.xn[lane + 64 * jl] = books[lc.bk[jl] * T->max_centroids + scr.codes[lane + 64 * jl]] * sc;
+        }
+        if (lane < PR) reinterpret_cast<u32x4 *>(scr.leaf)[lane] = half_piece(p.v_new_f32, v_raw);
+        row_enc::wave_sync();
+        // Logit of head col: sum over this lane's positions 32 s + 8 gq + k of
+        // k_j (qhi + qlo)[s][k], then over the column's four lanes; the query
+        // operands carry 2^eq, kq * 2^ec takes it off (the centroids here are
+        // not scaled by 2^ec).
+        float part = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            part = __builtin_fmaf(scr.xn[32 * s2 + 8 * gq + k], (float)qhi[s2][k] + (float)qlo[s2][k], part);
+        const float xt = col_sum(part) * __builtin_ldexpf(kq, ec);
+        new_x = head_ok && t_new < lim ? xt : -INFINITY;
+        if (p.logits && head_ok) p.logits[((int64_t)b * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
       };
       const uint8_t *enc_lds = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
       const DevTables *T_dev = reinterpret_cast<const DevTables *>(p.tables[kv]);
@@ -618,11 +691,6 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         books_use = reinterpret_cast<const float *>(enc_lds + (T_dev->off_books - T_dev->off_lut));
       }
       encode_new(T_use, lut_use, books_use);
-      row_enc::wave_sync();  // scratch reads done before the slot's first load
-    } else if (lane < PR) {
-      k_new16 = half_piece(p.k_new_f32, k_raw);
-      *reinterpret_cast<u32x4 *>(reinterpret_cast<_Float16 *>(const_cast<uint8_t *>(k_base)) + (int64_t)t_new * D +
-                                 8 * lane) = k_new16;
     }
   }
 
@@ -631,6 +699,21 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   f32x4 O[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) O[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (encoder) {
+    // The state of the new token alone: m = its logit, l = p = 2^15 (the P
+    // scale; one lane of the column holds it), O rows (heads 4 gq + r) =
+    // 2^15 v, v from the scratch copy (read before the slot's first load).
+    const _Float16 *vh = reinterpret_cast<const _Float16 *>(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
+    m_run = new_x;
+    l_run = new_x != -INFINITY && gq == 0 ? kPScale : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool vr = __shfl(new_x, 4 * gq + r, 64) != -INFINITY;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) O[dt][r] = vr ? kPScale * (float)vh[16 * dt + col] : 0.0f;
+    }
+    row_enc::wave_sync();
+  }
   // Lane-constant parts of the transposed V reads.
   const int trow = 4 * gq + (col >> 2);
   const int tpiece = (col & 3) >> 1, thalf = (col & 1) * 8;
@@ -652,17 +735,13 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     const uint8_t *sb = slot_base(i % Sl::RING);
     const uint8_t *kbuf = sb + Sl::KOFF;
     if (i == i_new) {  // the appended row over the chunk's LDS copy (wave-uniform)
+      // Packed K: the new token's logit is masked here (the encoder counts
+      // it), so only its V row has to be finite.
       const int r = t_new % kChunk;
       uint8_t *wsb = const_cast<uint8_t *>(sb);
       if (lane < PR) *reinterpret_cast<u32x4 *>(wsb + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = v_new16;
-      if (KF >= 1) {
-#pragma unroll
-        for (int jl = 0; jl < JL; ++jl)
-          if (lane + 64 * jl < rb) wsb[Sl::KOFF + r * rb + lane + 64 * jl] = (uint8_t)pk_new[jl];
-        if (lane < ns) reinterpret_cast<uint16_t *>(wsb + Sl::NOFF)[ns * r + lane] = (uint16_t)h_new;
-      } else if (lane < PR) {
+      if (KF == 0 && lane < PR)
         *reinterpret_cast<u32x4 *>(wsb + Sl::KOFF + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = k_new16;
-      }
     }
 
     // KF 2: transpose the scale rows (every read of the wave's slot precedes
@@ -874,7 +953,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
-        if (head_ok && tok < t_end) p.logits[((int64_t)b * Hq + hq0 + col) * p.logit_stride + tok] = x[j] * kLn2;
+        if (head_ok && tok < t_logit) p.logits[((int64_t)b * Hq + hq0 + col) * p.logit_stride + tok] = x[j] * kLn2;
       }
     }
     // online softmax (log2 domain) for head col
@@ -1000,9 +1079,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   __syncthreads();
   if (!*last) return;
   if (S <= kMergeOneRound) {
-    if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
-    else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
-    else merge_one_round<D, kMergeOneRound>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, tid);
+    if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, wave, lane);
+    else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, wave, lane);
+    else merge_one_round<D, kMergeOneRound>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, wave, lane);
     if (tid == 0) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }

@@ -57,27 +57,28 @@ struct Scratch {
 template <int D>
 __device__ __forceinline__ float group_tree(const float *leaf, int lane, int ng, int gs, int ge) {
   constexpr int NV = D / 8, SI = NV / 4;
-  float a0 = 0.0f;
-  if (lane < 8 * ng) {
-    const int l = lane & 7;
-    float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  // Every leaf of the lane's column is read (one round of LDS reads) and the
+  // ones outside the group enter as +0: the leaves are never negative, so the
+  // accumulators are never -0 and adding +0 changes nothing.
+  const int l = lane & 7;
+  float lv[NV];
 #pragma unroll
-    for (int i = 0; i < SI; ++i) {
-      const int p0 = (4 * i + 0) * 8 + l, p1 = (4 * i + 1) * 8 + l, p2 = (4 * i + 2) * 8 + l, p3 = (4 * i + 3) * 8 + l;
-      if (p0 >= gs && p0 < ge) a0 += leaf[p0];
-      if (p1 >= gs && p1 < ge) a1 += leaf[p1];
-      if (p2 >= gs && p2 < ge) a2 += leaf[p2];
-      if (p3 >= gs && p3 < ge) a3 += leaf[p3];
-    }
+  for (int v = 0; v < NV; ++v) lv[v] = leaf[v * 8 + l];
+  const bool act = lane < 8 * ng;
+  auto in = [&](int v) { return act && v * 8 + l >= gs && v * 8 + l < ge ? lv[v] : 0.0f; };
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-    for (int v = SI * 4; v < NV; ++v) {
-      const int p = v * 8 + l;
-      if (p >= gs && p < ge) a0 += leaf[p];
-    }
-    a0 += a1;
-    a0 += a2;
-    a0 += a3;
+  for (int i = 0; i < SI; ++i) {
+    a0 += in(4 * i + 0);
+    a1 += in(4 * i + 1);
+    a2 += in(4 * i + 2);
+    a3 += in(4 * i + 3);
   }
+#pragma unroll
+  for (int v = SI * 4; v < NV; ++v) a0 += in(v);
+  a0 += a1;
+  a0 += a2;
+  a0 += a3;
   // t = part 0 + part 1 + ... + part 7 (lane 8 g + k's part reaches lane 8 g by a row shift of k).
   const int ai = __float_as_int(a0);
   float t = a0;

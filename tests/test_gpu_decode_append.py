@@ -1,9 +1,13 @@
 """The decode step with its new token in one launch (bgtq_decode_append) against
 the two-call path of the reference's model step (src/model/decoder.ts:46-56 at
 rows = 1): bgtq_encode_batched of the new K rows, the V rows written, then
-bgtq_decode. Packed K rows, FP16 scales, K and V rows must be bit-identical and
-the outputs equal, for new tokens at every position inside a 32-token chunk,
-ragged batches and forced splits."""
+bgtq_decode. Packed K rows, FP16 scales, K and V rows must be bit-identical,
+for new tokens at every position inside a 32-token chunk, ragged batches and
+forced splits. The outputs agree within the attention tolerance
+(1e-5 + 1e-4 |ref|): with packed K the launch takes the new token's logit and
+its share of the output on a separate wave (it is encoded there while the
+others attend to the history), an equally precise but differently rounded
+sum; FP16 K rows give bit-identical outputs."""
 import numpy as np
 import pytest
 
@@ -75,7 +79,12 @@ def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="
     for a, b in zip(caches[0], caches[1]):
         assert torch.equal(a, b), "caches differ"
     assert not torch.isnan(outs[1]).any()
-    assert torch.equal(outs[0], outs[1]), float((outs[0] - outs[1]).abs().max())
+    if key_format == "packed":
+        err = (outs[1] - outs[0]).abs()
+        lim = 1e-5 + 1e-4 * outs[0].abs()
+        assert bool((err <= lim).all()), float((err / lim).max())
+    else:
+        assert torch.equal(outs[0], outs[1]), float((outs[0] - outs[1]).abs().max())
     for t in tabs:
         t.destroy()
 
