@@ -1272,6 +1272,9 @@ struct PrefillPlan {
   int tiles, tile_queries, ranges, range_blocks;
   size_t records;    // bytes of the workgroups' partial records
   size_t workspace;  // records, then the tile table (16 bytes per tile)
+  bool rowwise;      // the fused decode kernel, one unit per (query row, KV head)
+  int splits;        // rowwise: token splits per unit
+  size_t counters, part;  // rowwise: workspace offsets (the split counters first)
 };
 
 // Query tiles: four waves of one 16-query block each for small chunks (more
@@ -1307,6 +1310,17 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   if (d->split_tokens < 0) return fail(BGTQ_ERR_RANGE, "negative split_tokens");
   if ((int64_t)d->batch * d->kv_heads > 65535) return fail(BGTQ_ERR_UNSUPPORTED, "prefill handles up to 65535 sequence x KV head units");
   const int64_t G = d->q_heads / d->kv_heads, nq = (int64_t)d->rows * G;
+  const int64_t row_units = (int64_t)d->batch * d->rows * d->kv_heads;
+  plan->rowwise = d->rows <= kPrefillRowwiseRows && row_units <= 65535;
+  if (plan->rowwise) {
+    const int64_t want = d->split_tokens > 0 ? ((int64_t)d->max_length + d->split_tokens - 1) / d->split_tokens : 0;
+    plan->splits = choose_splits(row_units, d->max_length, (int32_t)std::min<int64_t>(want, 256));
+    plan->counters = 0;
+    plan->part = kPrefillCounterBytes;
+    plan->workspace =
+        kPrefillCounterBytes + sizeof(float) * (size_t)d->batch * d->rows * d->q_heads * plan->splits * (d->dim + 2);
+    return BGTQ_OK;
+  }
   plan->tile_queries = nq >= 2048 ? 64 * prefill_column_blocks(d->dim) : 64;
   plan->tiles = (int)((nq + plan->tile_queries - 1) / plan->tile_queries);
   if ((int64_t)d->batch * plan->tiles > INT32_MAX / 2) return fail(BGTQ_ERR_UNSUPPORTED, "too many query tiles");
@@ -1333,7 +1347,7 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   plan->range_blocks = (int)range_blocks;
   plan->records = plan->ranges > 1 ? sizeof(float) * (size_t)plan->ranges * 2 * tq * (d->dim + 2) : 0;
   const size_t info = plan->ranges > 1 ? 16 * (size_t)d->batch * d->kv_heads * plan->tiles : 0;
-  plan->workspace = plan->records + info;
+  plan->workspace = kPrefillCounterBytes + plan->records + info;
   return BGTQ_OK;
 }
 
@@ -1391,6 +1405,22 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
                                       "fused kernels hold (books, groups per 32 dims and norm stride within their limits)");
   if (reinterpret_cast<uintptr_t>(d->q) & 15) return fail(BGTQ_ERR_RANGE, "q must be 16-byte aligned");
   if (bgtq_status s = ctx->use()) return s;
+  if (plan.rowwise) {  // every query row as a decode step over its causal history
+    uint8_t *ws = static_cast<uint8_t *>(d->workspace);
+    dp.q = d->q;
+    dp.q_rotated = d->q_rotated;
+    dp.rows = d->rows;
+    dp.starts = d->starts;
+    dp.max_length = (int32_t)d->max_length;
+    dp.splits = plan.splits;
+    dp.split_tokens = 0;
+    dp.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
+    dp.counters = reinterpret_cast<uint32_t *>(ws + plan.counters);
+    dp.part = reinterpret_cast<float *>(ws + plan.part);
+    dp.out = d->out;
+    HIP_TRY(launch_decode_fast(dp, fl, nn, sg, ctx->stream), "prefill launch");
+    return BGTQ_OK;
+  }
   PrefillParams p{};
   for (int h = 0; h < d->kv_heads; ++h) p.tables[h] = dp.tables[h];
   p.batch = d->batch;
@@ -1425,8 +1455,8 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   // most of its issue slots (measured: the second takes about 1.3 times as
   // long for the same work), so the first round gets the longer ranges.
   p.first_round = plan.range_blocks == 0 && plan.ranges == 2 * device_cus() ? device_cus() : 0;
-  p.part = static_cast<float *>(d->workspace);
-  p.tile_info = plan.workspace ? reinterpret_cast<int32_t *>(static_cast<uint8_t *>(d->workspace) + plan.records) : nullptr;
+  p.part = reinterpret_cast<float *>(static_cast<uint8_t *>(d->workspace) + kPrefillCounterBytes);
+  p.tile_info = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(d->workspace) + kPrefillCounterBytes + plan.records);
   p.out = d->out;
   HIP_TRY(launch_prefill(p, fl, nn, sg, ctx->stream), "prefill launch");
   return BGTQ_OK;

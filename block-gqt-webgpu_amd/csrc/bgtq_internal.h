@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "bgtq.h"
+
 namespace bgtq {
 
 constexpr int kMaxDim = 128;
@@ -154,6 +156,12 @@ struct DecodeParams {
   int32_t q_rotated;      // 1: q is already R q[perm] (code domain); the kernels do not rotate it
   const float *qr;        // [B*Hq*dim] rotated, permuted, scaled by 1/sqrt(dim)
   const uint32_t *lengths;  // [B]; kernels clamp them to max_length
+  // Chunked prefill through the fused decode kernel (small chunks): units are
+  // (query row, KV head) pairs, row r of sequence b attending to the first
+  // starts[b] + r + 1 tokens; q, out, part and stats are indexed by query row
+  // b * rows + r instead of b. Plain decode: rows = 1, starts = null.
+  int32_t rows;
+  const uint32_t *starts;
   int32_t max_length;       // tokens every K/V buffer holds per (sequence, KV head)
   const int32_t *ends;      // optional [B*Hq] exclusive causal ends
   int32_t splits, split_tokens;
@@ -209,6 +217,14 @@ __host__ __device__ constexpr int prefill_column_blocks(int dim) { return dim ==
 constexpr int kPrefillMinRange = 2;       // cost units per workgroup range the kernel picks at least
 constexpr int kPrefillSegmentCost = 4;    // cost units of a tile's set-up (a 32-token block is one)
 constexpr int kPrefillMaxRanges = 2048;   // workgroups of one launch at most (bounds the records)
+// Chunks of at most this many rows run row-wise through the fused decode
+// kernel (a unit per query row and KV head, its split merge); longer chunks
+// tile their queries in the prefill kernel.
+constexpr int kPrefillRowwiseRows = BGTQ_PREFILL_ROWWISE_ROWS;
+// The prefill workspace starts with the row-wise path's split counters (a
+// word per unit, up to 65535 units): zero before a workspace's first call,
+// left zero by every call, never written by the tiled path.
+constexpr size_t kPrefillCounterBytes = BGTQ_PREFILL_COUNTER_BYTES;
 
 // The model step's separate attention passes (model_ops.hip), in the
 // reference's buffer layouts: q [rows][q_heads][dim] FP32, K/V caches

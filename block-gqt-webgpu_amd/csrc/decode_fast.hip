@@ -193,11 +193,14 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int unit = blockIdx.y, split = blockIdx.x;
-  const int b = unit / p.kv_heads, kv = unit - b * p.kv_heads;
+  // qrow: the unit's query row (decode: its sequence); b: the sequence whose caches it reads.
+  const int qrow = unit / p.kv_heads, kv = unit - qrow * p.kv_heads;
+  const int b = p.starts ? qrow / p.rows : qrow;
   const int G = p.G, Hq = p.q_heads, hq0 = kv * G;
   const int tid = threadIdx.x, lane = tid & 63, gq = lane >> 4, col = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
-  const int T_b = (int)min(p.lengths[b], (uint32_t)p.max_length);
+  const int T_b = p.starts ? min((int)p.starts[b] + (qrow - b * p.rows) + 1, p.max_length)
+                           : (int)min(p.lengths[b], (uint32_t)p.max_length);
   // Splits of one (sequence, KV head) interleave at chunk granularity: wave w
   // of split s takes chunks (s * 4 + w) + 4 S i, so the waves working on a
   // sequence at any moment sweep adjacent memory.
@@ -273,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   };
   // Per-head causal limits (read before the ring's loads are in flight).
   const bool head_ok = col < G;
-  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)b * Hq + hq0 + col], T_b) : T_b) : 0;
+  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)qrow * Hq + hq0 + col], T_b) : T_b) : 0;
   int lim = min(end_h, t_end);
   // Wave-uniform: chunks reaching past lim_min need the per-head mask.
   int lim_min = head_ok ? lim : t_end;
@@ -406,7 +409,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   }
   f32x4 qload[KS][2];  // unconditional loads of a valid row; heads past G are zeroed after the chunk issue
   {
-    const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + ((int64_t)b * Hq + hq0 + (head_ok ? col : 0)) * D);
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + ((int64_t)qrow * Hq + hq0 + (head_ok ? col : 0)) * D);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -674,7 +677,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
             part = __builtin_fmaf(scr.xn[32 * s2 + 8 * gq + k], (float)qhi[s2][k] + (float)qlo[s2][k], part);
         const float xt = col_sum(part) * __builtin_ldexpf(kq, ec);
         new_x = head_ok && t_new < lim ? xt : -INFINITY;
-        if (p.logits && head_ok) p.logits[((int64_t)b * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
+        if (p.logits && head_ok) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
       };
       const uint8_t *enc_lds = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
       const DevTables *T_dev = reinterpret_cast<const DevTables *>(p.tables[kv]);
@@ -953,7 +956,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
-        if (head_ok && tok < t_logit) p.logits[((int64_t)b * Hq + hq0 + col) * p.logit_stride + tok] = x[j] * kLn2;
+        if (head_ok && tok < t_logit) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + tok] = x[j] * kLn2;
       }
     }
     // online softmax (log2 domain) for head col
@@ -1045,7 +1048,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
         Ov = __builtin_fmaf(c[2 + dm], wt, Ov);
       }
     }
-    const int64_t head = (int64_t)b * Hq + hq0 + g;
+    const int64_t head = (int64_t)qrow * Hq + hq0 + g;
     if (S == 1) {
       p.out[head * D + dm] = Ov / Lsum;
       if (dm == 0 && p.stats) {
@@ -1079,9 +1082,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   __syncthreads();
   if (!*last) return;
   if (S <= kMergeOneRound) {
-    if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, wave, lane);
-    else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, wave, lane);
-    else merge_one_round<D, kMergeOneRound>(p.part, p.out, p.stats, (int64_t)b * Hq + hq0, G, S, wave, lane);
+    if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
+    else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
+    else merge_one_round<D, kMergeOneRound>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     if (tid == 0) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -1092,7 +1095,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   float *mrow = wgt + 16 * S;                     // [16 heads][S] split maxima
   for (int e = tid; e < G * S; e += kThreads) {
     const int g = e / S, s = e - g * S;
-    float *pp = p.part + (((int64_t)b * Hq + hq0 + g) * S + s) * (D + 2);
+    float *pp = p.part + (((int64_t)qrow * Hq + hq0 + g) * S + s) * (D + 2);
     mrow[g * S + s] = coherent_load(pp);
     wgt[g * S + s] = coherent_load(pp + 1);
   }
@@ -1109,7 +1112,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
     for (int s = 0; s < S; ++s) wgt[tid * S + s] = mrow[tid * S + s] / Lsum;
     if (p.stats) {
-      const int64_t head = (int64_t)b * Hq + hq0 + tid;
+      const int64_t head = (int64_t)qrow * Hq + hq0 + tid;
       p.stats[head * 2] = M * kLn2;
       p.stats[head * 2 + 1] = Lsum;
     }
@@ -1117,7 +1120,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   __syncthreads();
   for (int e = tid; e < G * D; e += kThreads) {
     const int g = e / D, dm = e - g * D;
-    const int64_t head = (int64_t)b * Hq + hq0 + g;
+    const int64_t head = (int64_t)qrow * Hq + hq0 + g;
     float *pp = p.part + head * S * (D + 2) + 2 + dm;
     float Ov = 0.0f;
     for (int s0 = 0; s0 < S; s0 += 8) {
@@ -1143,7 +1146,7 @@ hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t s
     return allowed;
   }
   constexpr int lds = Slot<D, KF, NN>::DYN;
-  dim3 grid((unsigned)p.splits, (unsigned)(p.batch * p.kv_heads));
+  dim3 grid((unsigned)p.splits, (unsigned)(p.batch * (p.starts ? p.rows : 1) * p.kv_heads));  // (split, unit)
   hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK>), grid, dim3(kThreads), lds, stream, p, fl);
   return hipGetLastError();
 }

@@ -283,16 +283,25 @@ bgtq_status bgtq_decode_noalloc(bgtq_context *ctx, const bgtq_decode_desc *d);
  *   starts: device uint32 [B], starts[b] + rows <= max_length (kernels clamp).
  *   v: FP16. Key formats and strides are those of bgtq_decode.
  *   workspace: 16-byte aligned device memory of at least
- *   bgtq_prefill_workspace_size() bytes for the partial results of tiles
- *   whose history several workgroups share (no initial contents needed);
- *   calls sharing a workspace must be ordered on one stream.
- *   split_tokens: the work (every sequence, KV head and query tile's causal
- *   history) is divided into equal ranges of this many history tokens, one
- *   workgroup each (rounded up to 32); 0 = about two workgroups per compute
- *   unit, sized on the device for the actual starts.
+ *   bgtq_prefill_workspace_size() bytes for the partial results of query
+ *   rows or tiles whose history several workgroups share. Its first
+ *   BGTQ_PREFILL_COUNTER_BYTES bytes (split arrival counters) must be zero
+ *   before the first call on it, and every call leaves them zero, whatever
+ *   its geometry; the rest needs no initial contents. Calls sharing a
+ *   workspace must be ordered on one stream.
+ *   Chunks of at most BGTQ_PREFILL_ROWWISE_ROWS rows run every query row as
+ *   a decode step over its causal history (the fused decode kernel and its
+ *   split merge); longer chunks tile their queries.
+ *   split_tokens: the history is divided into ranges of this many tokens, one
+ *   workgroup each (tiled: every sequence, KV head and query tile's causal
+ *   history, rounded up to 32; row-wise: each row's, as max_length /
+ *   split_tokens splits); 0 = about two workgroups per compute unit (tiled:
+ *   sized on the device for the actual starts).
  * Layouts: FP16 K, or packed layouts the fused decode takes (see
  * bgtq_decode_append) whose centroid books (n_books * max_centroids floats)
  * fit 4 KB at d=64, 8 KB at d=128; others return BGTQ_ERR_UNSUPPORTED. */
+#define BGTQ_PREFILL_COUNTER_BYTES (4u * 65536u)
+#define BGTQ_PREFILL_ROWWISE_ROWS 32
 typedef struct {
   int32_t batch, rows, q_heads, kv_heads, dim;
   int32_t key_format;

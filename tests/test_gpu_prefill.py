@@ -302,3 +302,36 @@ def test_rejections(device):
             batched.prefill(device, batched.prefill_desc(workspace=ws, **kw))
     finally:
         t.destroy()
+
+
+def test_workspace_shared_across_paths(device, oracle):
+    """One workspace for a tiled chunk (64 rows), then row-wise chunks (32, 7 rows) of other geometry:
+    the split counters at the workspace's start stay zero after every call and each output matches
+    the oracle."""
+    import torch
+    from bgtq import batched, calibrate
+    p = calibrate.layout_b(64)
+    cache = Cache(device, params=[p, p], batch=2, hkv=2, dim=64, cap=700)
+    try:
+        ws = torch.zeros(32 << 20, dtype=torch.uint8, device="cuda")
+        counter_words = 65536  # BGTQ_PREFILL_COUNTER_BYTES / 4
+        for rows, hq, starts in ((64, 14, [300, 611]), (32, 14, [0, 668]), (7, 6, [693, 250])):
+            g = torch.Generator().manual_seed(rows)
+            q = torch.randn((2, rows, hq, 64), generator=g)
+            out = torch.full((2, rows, hq, 64), float("nan"), device="cuda")
+            kw = dict(batch=2, rows=rows, q_heads=hq, kv_heads=2, dim=64, q=q.cuda(), out=out,
+                      starts=torch.tensor(starts, dtype=torch.int32).cuda(), max_length=700, v=cache.vd,
+                      v_seq_stride=cache.vd.stride(0), v_head_stride=cache.vd.stride(1), **cache.kw)
+            assert batched.prefill_workspace_bytes(batched.prefill_desc(**kw)) <= ws.numel()
+            print("shared workspace", rows, hq, starts, flush=True)
+            batched.prefill(device, batched.prefill_desc(workspace=ws, **kw))
+            torch.cuda.synchronize()
+            assert not ws[:4 * counter_words].any(), "split counters left nonzero"
+            got = out.cpu().numpy()
+            G = hq // 2
+            for b in range(2):
+                for h in range(2):
+                    ref = _reference(oracle, cache, q, starts, b, h, G)
+                    _check(got[b, :, h * G:(h + 1) * G], ref.astype(np.float64), f"rows {rows} b{b} kv{h}")
+    finally:
+        cache.destroy()
