@@ -1002,6 +1002,7 @@ static bgtq_status validate_decode(const bgtq_decode_desc *d, int *splits) {
   if (d->batch < 1 || d->kv_heads < 1 || d->kv_heads > kMaxKvHeads || d->q_heads < d->kv_heads ||
       d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 16)
     return fail(BGTQ_ERR_RANGE, "invalid head geometry");
+  if (d->batch > 65535) return fail(BGTQ_ERR_UNSUPPORTED, "decode handles up to 65535 sequences per call");
   if (d->dim < 2 || d->dim > 128 || d->dim % 2) return fail(BGTQ_ERR_RANGE, "invalid head dim");
   if (d->max_length < 1 || d->max_length > (1u << 24)) return fail(BGTQ_ERR_RANGE, "max_length must be in 1..2^24");
   if (d->key_format == BGTQ_KEYS_PACKED) {

@@ -192,20 +192,41 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
   extern __shared__ __align__(16) uint8_t smem[];
 
-  const int unit = blockIdx.y, split = blockIdx.x;
-  // qrow: the unit's query row (decode: its sequence); b: the sequence whose caches it reads.
-  const int qrow = unit / p.kv_heads, kv = unit - qrow * p.kv_heads;
-  const int b = p.starts ? qrow / p.rows : qrow;
+  // Grid (split, KV head, query row): the head's layout words are loaded with
+  // the kernel arguments, with no division ahead of them.
+  // qrow: the query row (decode: its sequence); b: the sequence whose caches it reads.
+  const int split = blockIdx.x, kv = blockIdx.y, qrow = blockIdx.z;
+  // Every kernel argument the set-up reads, loaded at once: left to itself
+  // the compiler loads them a basic block at a time, a chain of dependent
+  // scalar round trips ahead of the first DMA.
+  // One asm statement: the wait for its operands is the only one.
+#define BGTQ_ARGS                                                                                              \
+  "s"(p.kv_heads), "s"(p.rows), "s"(p.starts), "s"(p.lengths), "s"(p.max_length), "s"(p.G), "s"(p.q_heads), \
+      "s"(p.splits), "s"(p.ends), "s"(p.k_new), "s"(p.q_rotated), "s"(p.q), "s"(p.v), "s"(p.packed),         \
+      "s"(p.norms), "s"(p.k), "s"(p.logits)
+  if constexpr (KF == 0) asm volatile("" ::BGTQ_ARGS);
+  if constexpr (KF == 1)
+    asm volatile("" ::BGTQ_ARGS, "s"(fl.mfma[kv]), "s"(fl.rot_q[kv]), "s"(fl.cent_exp[kv]), "s"(fl.book[0]),
+                 "s"(fl.book[1]), "s"(fl.book[Gm::KS - 2]), "s"(fl.book[Gm::KS - 1]));
+  if constexpr (KF == 2)
+    asm volatile("" ::BGTQ_ARGS, "s"(fl.mfma[kv]), "s"(fl.rot_q[kv]), "s"(fl.cent_exp[kv]), "s"(fl.glane[kv]),
+                 "s"((int)fl.gnb[kv]), "s"((int)fl.gbstride[kv]), "s"((int)fl.gbnib[kv]), "s"(fl.gpair[kv]),
+                 "s"((int)fl.grb[kv]), "s"((int)fl.gns[kv]));
+#undef BGTQ_ARGS
+  __builtin_amdgcn_sched_barrier(0);
+  const int unit = qrow * p.kv_heads + kv;
+  const bool rowwise = p.starts != nullptr;
+  const int rows = rowwise ? p.rows : 1;
+  const int b = qrow / rows;
+  // A scalar load (constant address space): its wait goes where the value is
+  // first used, after the loads below are issued.
+  typedef const __attribute__((address_space(4))) uint32_t const_u32;
+  const uint32_t len_b = reinterpret_cast<const_u32 *>(
+      reinterpret_cast<uintptr_t>(rowwise ? p.starts : p.lengths))[b];
   const int G = p.G, Hq = p.q_heads, hq0 = kv * G;
   const int tid = threadIdx.x, lane = tid & 63, gq = lane >> 4, col = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
-  const int T_b = p.starts ? min((int)p.starts[b] + (qrow - b * p.rows) + 1, p.max_length)
-                           : (int)min(p.lengths[b], (uint32_t)p.max_length);
-  // Splits of one (sequence, KV head) interleave at chunk granularity: wave w
-  // of split s takes chunks (s * 4 + w) + 4 S i, so the waves working on a
-  // sequence at any moment sweep adjacent memory.
-  const int t_end = kInterleaved ? T_b : min(T_b, split * p.split_tokens + p.split_tokens);
-  const int stride = kInterleaved ? p.splits * kWaves * kChunk : kWaves * kChunk;
+  const bool head_ok = col < G;
   // The K-steps' lookup tables are static LDS (an address fixed at compile
   // time, so a lookup's address is the code byte shifted: one instruction);
   // the ring is the dynamic LDS.
@@ -233,132 +254,6 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   for (int k = 0; k < VI; ++k) {
     const int P = 64 * k + lane, r = P / PR, c = P % PR;
     voff_rows[k] = r * (2 * D) + ((c ^ swz<D>(r)) * 16);
-  }
-  // This wave's chunks start at first + 128 i.
-  const int first = kInterleaved ? (split * kWaves + wave) * kChunk : split * p.split_tokens + wave * kChunk;
-  const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
-  auto issue = [&](int i) {
-    const int c0 = first + i * stride;
-    // Tokens of the chunk inside the sequence; none for a chunk past the end
-    // (a zero-sized descriptor: the DMA only writes zeros to LDS).
-    const int in_seq = min(T_b - c0, kChunk);
-    const uint32_t rest = __builtin_amdgcn_readfirstlane(in_seq > 0 ? in_seq : 0);  // wave-uniform: SGPR descriptor
-    uint8_t *sb = slot_base(i % Sl::RING);
-    const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
-#pragma unroll
-    for (int k = 0; k < VI; ++k) dma16<kStream>(rV, sb + k * 1024, voff_rows[k], 0);
-    uint8_t *kb = sb + Sl::KOFF;
-    if (KF == 1) {
-      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * RB, rest * RB);
-      const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * 2, rest * 4);
-#pragma unroll
-      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
-      dma4<kStream>(rN, sb + Sl::NOFF, lane * 4, 0);
-    } else if (KF == 2) {
-      // Rows of rb bytes and ns scales, packed back to back: the chunk's rows
-      // fill the K area's front, its scale rows the scale area's. The range
-      // check zeroes a whole access that reaches past the range, so the ranges
-      // end on the access size (16 and 4 bytes): the last row's bytes arrive,
-      // and the few bytes past it lie in the same aligned 16 bytes as the row's
-      // end (both bases are 16-byte aligned, c0 a multiple of 32).
-      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * rb, (rest * rb + 15u) & ~15u);
-      const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * ns, (rest * ns * 2 + 3u) & ~3u);
-#pragma unroll
-      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
-#pragma unroll
-      for (int k = 0; k < Sl::NSC; ++k)
-        if (k * 256 + lane * 4 < Sl::NBYTES) dma4<kStream>(rN, sb + Sl::NOFF + k * 256, k * 256 + lane * 4, 0);
-    } else {
-      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
-#pragma unroll
-      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, voff_rows[k], 0);
-    }
-  };
-  // Per-head causal limits (read before the ring's loads are in flight).
-  const bool head_ok = col < G;
-  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)qrow * Hq + hq0 + col], T_b) : T_b) : 0;
-  int lim = min(end_h, t_end);
-  // Wave-uniform: chunks reaching past lim_min need the per-head mask.
-  int lim_min = head_ok ? lim : t_end;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o, 64));
-
-  // ---------------- decode-step append ----------------
-  // With p.k_new the sequence's newest token (row T_b - 1) arrives in this
-  // launch. The wave whose chunk holds it (the owner) loads the new V row
-  // with the prologue's loads, converts it, stores it to the cache for the
-  // later steps and, after that chunk's loads land, writes it over the
-  // chunk's LDS copy (whose loads may have read the row before it was
-  // stored). FP16 K rows go the same way. Packed K takes longer to encode,
-  // so another wave of the workgroup (the encoder) does it while the owner
-  // works through its chunk without the new token: the encoder loads the
-  // new K (and, at d=64, its column of the transposed rotation) and V,
-  // encodes and stores the K row, and starts its own attention state with
-  // the new token (its logit from the row it encoded); the workgroup's merge
-  // of its waves' states then counts the token once.
-  constexpr int JL = D > 64 ? 2 : 1;
-  const int t_new = T_b - 1;
-  const int c_new = t_new >= 0 ? t_new / kChunk : 0;
-  const int own_w = p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
-  const bool owner = own_w == wave;
-  const bool encoder = KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
-  const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
-  // The q rotation stages through the last ring slot of a wave other than
-  // the encoder, whose slot receives the encoder's tables meanwhile.
-  const int stage_w = own_w >= 0 && own_w < kWaves ? (own_w + 1) % kWaves : 0;
-  if (owner && KF >= 1) {  // the owner's chunk pass leaves the new token to the encoder
-    lim = min(lim, t_new);
-    lim_min = min(lim_min, t_new);
-  }
-  const int t_logit = owner && KF >= 1 ? t_new : t_end;  // logits this wave materialises: tokens below
-  uint32_t pk_new[JL] = {};                    // packed K bytes lane, lane + 64
-  uint32_t h_new = 0;                          // FP16 scale bits (lanes below the norm stride)
-  u32x4 v_new16{0u, 0u, 0u, 0u}, k_new16{0u, 0u, 0u, 0u};  // FP16 pieces of the V / K row (lanes below D / 8)
-  uint32_t v_raw[8] = {}, k_raw[8] = {};       // lane's 8 values of the new V / K row: FP32 bits, or FP16 pairs
-  uint32_t k_nat[JL] = {};                     // packed K: new K element lane + 64 jl (FP32 or FP16 bits)
-  float rt_col[D == 64 ? D : 1];               // d=64: R[lane][i] for every i
-  row_enc::Lane<D> lc;
-  const int64_t v_off = (int64_t)b * p.v_new_seq_stride + kv * p.v_new_head_stride;
-  const int64_t k_off = (int64_t)b * p.k_new_seq_stride + kv * p.k_new_head_stride;
-  auto load_piece = [&](const void *src, int f32, int64_t off, uint32_t (&r)[8]) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (f32) r[k] = static_cast<const uint32_t *>(src)[off + 8 * lane + k];
-      else if (k < 4) r[k] = (uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k] |
-                             ((uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k + 1] << 16);
-    }
-  };
-  auto half_piece = [&](int f32, const uint32_t (&r)[8]) {
-    u32x4 h;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      h[k] = f32 ? (uint32_t)row_enc::f32_to_f16_bits(__uint_as_float(r[2 * k])) |
-                       ((uint32_t)row_enc::f32_to_f16_bits(__uint_as_float(r[2 * k + 1])) << 16)
-                 : r[k];
-    return h;
-  };
-  if (encoder) {
-    // The tables' header, code LUT and books (contiguous from the start of
-    // the table set, fl.enc_bytes[kv] bytes) into this wave's last ring
-    // slot, first of this wave's loads: the prologue's wait covers them.
-    const __amdgpu_buffer_rsrc_t rt =
-        rsrc(reinterpret_cast<const uint8_t *>(p.tables[kv]) + fl.enc_from[kv], fl.enc_bytes[kv]);
-    uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
-#pragma unroll
-    for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
-    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
-#pragma unroll
-    for (int jl = 0; jl < JL; ++jl)
-      k_nat[jl] = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new)[k_off + lane + 64 * jl]
-                              : (uint32_t)static_cast<const uint16_t *>(p.k_new)[k_off + lane + 64 * jl];
-    if (D == 64) {
-#pragma unroll
-      for (int i = 0; i < D; ++i) rt_col[i] = fl.rot_t[kv][i * D + lane];
-    }
-  }
-  if (owner) {
-    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
-    if (KF == 0 && lane < PR) load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
   }
 
   // ---------------- prologue ----------------
@@ -445,6 +340,140 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       for (int m = 0; m < RW; ++m)
         if (m < 9 || s < PK) grec[s][m] = gr[(s * 4 + gq) * RW + m];
   }
+  // The sequence's length arrives while the loads above are in flight: what
+  // depends on it comes after them.
+  const int T_b = rowwise ? min((int)len_b + (qrow - b * rows) + 1, p.max_length)
+                          : (int)min(len_b, (uint32_t)p.max_length);
+  // Splits of one (sequence, KV head) interleave at chunk granularity: wave w
+  // of split s takes chunks (s * 4 + w) + 4 S i, so the waves working on a
+  // sequence at any moment sweep adjacent memory.
+  const int t_end = kInterleaved ? T_b : min(T_b, split * p.split_tokens + p.split_tokens);
+  const int stride = kInterleaved ? p.splits * kWaves * kChunk : kWaves * kChunk;
+  // This wave's chunks start at first + 128 i.
+  const int first = kInterleaved ? (split * kWaves + wave) * kChunk : split * p.split_tokens + wave * kChunk;
+  const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
+  auto issue = [&](int i) {
+    const int c0 = first + i * stride;
+    // Tokens of the chunk inside the sequence; none for a chunk past the end
+    // (a zero-sized descriptor: the DMA only writes zeros to LDS).
+    const int in_seq = min(T_b - c0, kChunk);
+    const uint32_t rest = __builtin_amdgcn_readfirstlane(in_seq > 0 ? in_seq : 0);  // wave-uniform: SGPR descriptor
+    uint8_t *sb = slot_base(i % Sl::RING);
+    const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
+#pragma unroll
+    for (int k = 0; k < VI; ++k) dma16<kStream>(rV, sb + k * 1024, voff_rows[k], 0);
+    uint8_t *kb = sb + Sl::KOFF;
+    if (KF == 1) {
+      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * RB, rest * RB);
+      const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * 2, rest * 4);
+#pragma unroll
+      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+      dma4<kStream>(rN, sb + Sl::NOFF, lane * 4, 0);
+    } else if (KF == 2) {
+      // Rows of rb bytes and ns scales, packed back to back: the chunk's rows
+      // fill the K area's front, its scale rows the scale area's. The range
+      // check zeroes a whole access that reaches past the range, so the ranges
+      // end on the access size (16 and 4 bytes): the last row's bytes arrive,
+      // and the few bytes past it lie in the same aligned 16 bytes as the row's
+      // end (both bases are 16-byte aligned, c0 a multiple of 32).
+      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * rb, (rest * rb + 15u) & ~15u);
+      const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * ns, (rest * ns * 2 + 3u) & ~3u);
+#pragma unroll
+      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+#pragma unroll
+      for (int k = 0; k < Sl::NSC; ++k)
+        if (k * 256 + lane * 4 < Sl::NBYTES) dma4<kStream>(rN, sb + Sl::NOFF + k * 256, k * 256 + lane * 4, 0);
+    } else {
+      const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
+#pragma unroll
+      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, voff_rows[k], 0);
+    }
+  };
+  // Per-head causal limits.
+  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)qrow * Hq + hq0 + col], T_b) : T_b) : 0;
+  int lim = min(end_h, t_end);
+  // Wave-uniform: chunks reaching past lim_min need the per-head mask.
+  int lim_min = head_ok ? lim : t_end;
+  lim_min = wave_min(lim_min);
+
+  // ---------------- decode-step append ----------------
+  // With p.k_new the sequence's newest token (row T_b - 1) arrives in this
+  // launch. The wave whose chunk holds it (the owner) loads the new V row
+  // with the prologue's loads, converts it, stores it to the cache for the
+  // later steps and, after that chunk's loads land, writes it over the
+  // chunk's LDS copy (whose loads may have read the row before it was
+  // stored). FP16 K rows go the same way. Packed K takes longer to encode,
+  // so another wave of the workgroup (the encoder) does it while the owner
+  // works through its chunk without the new token: the encoder loads the
+  // new K (and, at d=64, its column of the transposed rotation) and V,
+  // encodes and stores the K row, and starts its own attention state with
+  // the new token (its logit from the row it encoded); the workgroup's merge
+  // of its waves' states then counts the token once.
+  constexpr int JL = D > 64 ? 2 : 1;
+  const int t_new = T_b - 1;
+  const int c_new = t_new >= 0 ? t_new / kChunk : 0;
+  const int own_w = p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
+  const bool owner = own_w == wave;
+  const bool encoder = KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
+  const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
+  // The q rotation stages through the last ring slot of a wave other than
+  // the encoder, whose slot receives the encoder's tables meanwhile.
+  const int stage_w = own_w >= 0 && own_w < kWaves ? (own_w + 1) % kWaves : 0;
+  if (owner && KF >= 1) {  // the owner's chunk pass leaves the new token to the encoder
+    lim = min(lim, t_new);
+    lim_min = min(lim_min, t_new);
+  }
+  const int t_logit = owner && KF >= 1 ? t_new : t_end;  // logits this wave materialises: tokens below
+  uint32_t pk_new[JL] = {};                    // packed K bytes lane, lane + 64
+  uint32_t h_new = 0;                          // FP16 scale bits (lanes below the norm stride)
+  u32x4 v_new16{0u, 0u, 0u, 0u}, k_new16{0u, 0u, 0u, 0u};  // FP16 pieces of the V / K row (lanes below D / 8)
+  uint32_t v_raw[8] = {}, k_raw[8] = {};       // lane's 8 values of the new V / K row: FP32 bits, or FP16 pairs
+  uint32_t k_nat[JL] = {};                     // packed K: new K element lane + 64 jl (FP32 or FP16 bits)
+  float rt_col[D == 64 ? D : 1];               // d=64: R[lane][i] for every i
+  row_enc::Lane<D> lc;
+  const int64_t v_off = (int64_t)b * p.v_new_seq_stride + kv * p.v_new_head_stride;
+  const int64_t k_off = (int64_t)b * p.k_new_seq_stride + kv * p.k_new_head_stride;
+  auto load_piece = [&](const void *src, int f32, int64_t off, uint32_t (&r)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (f32) r[k] = static_cast<const uint32_t *>(src)[off + 8 * lane + k];
+      else if (k < 4) r[k] = (uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k] |
+                             ((uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k + 1] << 16);
+    }
+  };
+  auto half_piece = [&](int f32, const uint32_t (&r)[8]) {
+    u32x4 h;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      h[k] = f32 ? (uint32_t)row_enc::f32_to_f16_bits(__uint_as_float(r[2 * k])) |
+                       ((uint32_t)row_enc::f32_to_f16_bits(__uint_as_float(r[2 * k + 1])) << 16)
+                 : r[k];
+    return h;
+  };
+  if (encoder) {
+    // The tables' header, code LUT and books (contiguous from the start of
+    // the table set, fl.enc_bytes[kv] bytes) into this wave's last ring
+    // slot, first of this wave's loads: the prologue's wait covers them.
+    const __amdgpu_buffer_rsrc_t rt =
+        rsrc(reinterpret_cast<const uint8_t *>(p.tables[kv]) + fl.enc_from[kv], fl.enc_bytes[kv]);
+    uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
+#pragma unroll
+    for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
+    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl)
+      k_nat[jl] = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new)[k_off + lane + 64 * jl]
+                              : (uint32_t)static_cast<const uint16_t *>(p.k_new)[k_off + lane + 64 * jl];
+    if (D == 64) {
+#pragma unroll
+      for (int i = 0; i < D; ++i) rt_col[i] = fl.rot_t[kv][i * D + lane];
+    }
+  }
+  if (owner) {
+    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
+    if (KF == 0 && lane < PR) load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
+  }
+
   // Unconditional, so every wave has exactly AHEAD * L chunk loads in flight
   // behind its prologue loads (chunks past the end are zero-sized). The
   // scheduling barriers keep the prologue's loads ahead of them, so waiting
@@ -1146,7 +1175,7 @@ hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t s
     return allowed;
   }
   constexpr int lds = Slot<D, KF, NN>::DYN;
-  dim3 grid((unsigned)p.splits, (unsigned)(p.batch * (p.starts ? p.rows : 1) * p.kv_heads));  // (split, unit)
+  dim3 grid((unsigned)p.splits, (unsigned)p.kv_heads, (unsigned)(p.batch * (p.starts ? p.rows : 1)));
   hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK>), grid, dim3(kThreads), lds, stream, p, fl);
   return hipGetLastError();
 }

@@ -509,8 +509,7 @@ prefill_kernel(PrefillParams p, FastLayout fl) {
         if (i < n_blocks) issue(i);
     }
     // Wave-uniform: blocks reaching past lim_min need the per-query mask.
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o, 64));
+    lim_min = wave_min(lim_min);
     // Block 0 (and the books before it) landed for every wave; the later
     // blocks stay in flight.
     wait_blocks<Sl::LW, AHEAD - 1>(min(n_blocks, AHEAD) - 1);
