@@ -25,9 +25,26 @@
 #include <type_traits>
 
 #include "bgtq_internal.h"
+#include "gfx950_common.h"
 
 namespace bgtq {
 namespace {
+
+using gfx::dma16;
+using gfx::dma4;
+using gfx::f32x4;
+using gfx::rsrc;
+using gfx::u32x4;
+using gfx::wait_vm;
+
+// The job table and the table sets are not written while the kernel runs:
+// read through the constant address space, their wave-uniform fields are
+// scalar loads whatever the kernel's other memory operations are.
+#define BGTQ_CONST __attribute__((address_space(4)))
+template <typename X>
+__device__ __forceinline__ const BGTQ_CONST X *to_const(const void *p) {
+  return (const BGTQ_CONST X *)reinterpret_cast<uintptr_t>(p);
+}
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
@@ -50,6 +67,9 @@ struct Bulk {
   // the columns are read through the scalar cache instead.
   static constexpr bool ROT_LDS = D <= 64;
   static constexpr int ROT = ROT_LDS ? 2 * (D / 2) * (D / 2) * 4 : 0;
+  // The LUT and book areas are whole 256-byte pieces (the LDS DMA's unit).
+  static constexpr int lut_area(int lut_bytes) { return (lut_bytes + 255) & ~255; }
+  static constexpr int book_area(int book_floats) { return ((book_floats + 63) & ~63) * 4; }
 };
 
 // ATen's 8-lane inner sum (vectorized_inner_sum: four interleaved
@@ -97,43 +117,96 @@ __global__ __launch_bounds__(WG) void encode_bulk_kernel(const EncodeJobDev *__r
   float *books = reinterpret_cast<float *>(lut + lut_area);
   // The groups' diagonal rotation blocks, rot[g][i][j] = R[P0 + j][P0 + i]
   // (column i of the block contiguous): read as wave-wide broadcasts.
-  float *rot = books + ((book_floats + 3) & ~3);
+  float *rot = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(books) + Bulk<D, WG>::book_area(book_floats));
 
-  const EncodeJobDev job = jobs[blockIdx.y];
+  struct JobWords {
+    u32x4 w[4];
+  };
+  static_assert(sizeof(JobWords) == sizeof(EncodeJobDev), "job words");
+  const BGTQ_CONST u32x4 *jw = to_const<u32x4>(jobs + blockIdx.y);
+  const EncodeJobDev job = __builtin_bit_cast(EncodeJobDev, (JobWords{{jw[0], jw[1], jw[2], jw[3]}}));
   const int64_t row0 = (int64_t)blockIdx.x * ROWS;
   if (row0 >= job.rows) return;  // uniform for the workgroup
   const int nr = (int)min((int64_t)ROWS, job.rows - row0);
-  const BGTQ_GLOBAL DevTables *__restrict__ T = to_global(job.t);
+  const BGTQ_CONST DevTables *T = to_const<DevTables>(job.t);
   const int tid = threadIdx.x;
   const int mc = T->max_centroids;
 
   // Stage the rows (FP16 bits; FP32 sources rounded to FP16 first,
-  // src/model/codec.wgsl:14), the code LUT and the centroid books.
-  for (int e = tid; e < nr * D; e += ROWS) {
-    const int r = e / D, c = e - r * D;
-    const int64_t at = (row0 + r) * job.src_stride + c;
-    stage[r * SSTR + c] = SRC_F32 ? f32_to_f16_bits(to_global(static_cast<const float *>(job.src))[at])
-                                  : to_global(static_cast<const uint16_t *>(job.src))[at];
-  }
-  {
-    const auto lut_g = tables_lut(T);
-    const int lut_bytes = T->n_codebooks * 256;
-    for (int e = tid; e < lut_bytes; e += ROWS) lut[e] = lut_g[e];
-    const auto books_g = tables_books(T);
-    const int nbf = T->n_books * mc;
-    for (int e = tid; e < nbf; e += ROWS) books[e] = books_g[e];
-    if constexpr (Bulk<D, WG>::ROT_LDS) {
-      const BGTQ_GLOBAL float *__restrict__ Rt_g = tables_rot_t(T);  // Rt[i * D + j] = R[j][i]
-      for (int e = tid; e < NG * GW * GW; e += ROWS) {
-        const int g = e / (GW * GW), r = e - g * (GW * GW), i = r / GW, j = r - i * GW;
-        rot[e] = Rt_g[(g * GW + i) * D + g * GW + j];
+  // src/model/codec.wgsl:14), the code LUT, the centroid books and the
+  // rotation blocks, every load of the workgroup in flight at once: the rows
+  // as 16-byte pieces into registers (lane-consecutive pieces, coalesced),
+  // the tables by LDS DMA; one wait, then the rows' LDS writes.
+  constexpr int PR = D / 8;  // 8-element pieces per row
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uintptr_t src_addr = reinterpret_cast<uintptr_t>(job.src);
+  const bool vec = src_addr % 16 == 0 && job.src_stride % 8 == 0;  // uniform
+  u32x4 piece[PR];
+  if (vec) {
+#pragma unroll
+    for (int k = 0; k < PR; ++k) {
+      const int e = tid + ROWS * k, r = e / PR, c = e - r * PR;
+      const int64_t at = (row0 + r) * job.src_stride + 8 * c;
+      if (r < nr) {
+        if constexpr (SRC_F32) {
+          const BGTQ_GLOBAL f32x4 *sp = reinterpret_cast<const BGTQ_GLOBAL f32x4 *>(
+              to_global(static_cast<const float *>(job.src)) + at);
+          const f32x4 a = sp[0], b = sp[1];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            piece[k][h] = (uint32_t)f32_to_f16_bits(a[2 * h]) | ((uint32_t)f32_to_f16_bits(a[2 * h + 1]) << 16);
+            piece[k][2 + h] = (uint32_t)f32_to_f16_bits(b[2 * h]) | ((uint32_t)f32_to_f16_bits(b[2 * h + 1]) << 16);
+          }
+        } else {
+          piece[k] = *reinterpret_cast<const BGTQ_GLOBAL u32x4 *>(to_global(static_cast<const uint16_t *>(job.src)) + at);
+        }
+      } else {
+        piece[k] = u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
+  {
+    const uint8_t *tb = reinterpret_cast<const uint8_t *>(job.t);
+    constexpr int NW = WG / 64;
+    const int lut_bytes = T->n_codebooks * 256;
+    const __amdgpu_buffer_rsrc_t rl = rsrc(tb + T->off_lut, lut_bytes);
+    for (int c = wave; c * 256 < lut_bytes; c += NW) dma4(rl, lut + c * 256, c * 256 + lane * 4, 0);
+    const int nbb = T->n_books * mc * 4;  // the LDS area is whole 256-byte pieces
+    const __amdgpu_buffer_rsrc_t rb = rsrc(tb + T->off_books, nbb);
+    for (int c = wave; c * 256 < nbb; c += NW)
+      dma4(rb, reinterpret_cast<uint8_t *>(books) + c * 256, c * 256 + lane * 4, 0);
+    if constexpr (Bulk<D, WG>::ROT_LDS) {
+      // Eight rows i of block g (GW = 32 floats each) per instruction:
+      // lane l brings Rt[(g GW + i0 + l / 8) D + g GW + 4 (l % 8) ...+3].
+      static_assert(GW == 32, "eight 128-byte block rows per 16-byte DMA");
+      const __amdgpu_buffer_rsrc_t rr = rsrc(tb + T->off_rot_t, D * D * 4);
+      for (int c = wave; c < NG * GW / 8; c += NW) {
+        const int g = c / (GW / 8), i = 8 * c - g * GW + lane / 8;
+        dma16(rr, reinterpret_cast<uint8_t *>(rot) + c * 1024, ((g * GW + i) * D + g * GW + 4 * (lane % 8)) * 4, 0);
+      }
+    }
+  }
+  if (vec) {
+#pragma unroll
+    for (int k = 0; k < PR; ++k) {
+      const int e = tid + ROWS * k, r = e / PR, c = e - r * PR;
+      uint32_t *dst = reinterpret_cast<uint32_t *>(stage + r * SSTR + 8 * c);  // 4-byte aligned: SSTR even
+#pragma unroll
+      for (int h = 0; h < 4; ++h) dst[h] = piece[k][h];
+    }
+  } else {
+    for (int e = tid; e < nr * D; e += ROWS) {
+      const int r = e / D, c = e - r * D;
+      const int64_t at = (row0 + r) * job.src_stride + c;
+      stage[r * SSTR + c] = SRC_F32 ? f32_to_f16_bits(to_global(static_cast<const float *>(job.src))[at])
+                                    : to_global(static_cast<const uint16_t *>(job.src))[at];
+    }
+  }
+  wait_vm<0>();  // the DMAs
   __syncthreads();
   if (tid >= nr) return;  // no barrier below
 
-  const BGTQ_GLOBAL float *__restrict__ Rt = tables_rot_t(T);  // Rt[i * D + j] = R[j][i]
+  const BGTQ_CONST float *Rt = to_const<float>(reinterpret_cast<const uint8_t *>(job.t) + T->off_rot_t);  // Rt[i * D + j] = R[j][i]
   uint32_t packed[LOGICAL / 4];
 #pragma unroll
   for (int w = 0; w < LOGICAL / 4; ++w) packed[w] = 0u;
@@ -181,7 +254,7 @@ __global__ __launch_bounds__(WG) void encode_bulk_kernel(const EncodeJobDev *__r
           y[4 * j4 + 3] = __builtin_fmaf(x[i], c.w, y[4 * j4 + 3]);
         }
       } else {
-        const BGTQ_GLOBAL float *__restrict__ Ci = Rt + (P0 + i) * D + P0;
+        const BGTQ_CONST float *Ci = Rt + (P0 + i) * D + P0;
 #pragma unroll
         for (int j = 0; j < GW; ++j) y[j] = __builtin_fmaf(x[i], Ci[j], y[j]);
       }
@@ -221,7 +294,7 @@ __global__ __launch_bounds__(WG) void encode_bulk_kernel(const EncodeJobDev *__r
 template <int D, int NG, int NS, int WG>
 hipError_t launch_kind(const EncodeJobDev *jobs, int n_jobs, int src_f32, int64_t max_rows, int lut_area,
                        int book_floats, hipStream_t stream) {
-  const int lds = Bulk<D, WG>::STAGE + lut_area + ((book_floats + 3) & ~3) * 4 + Bulk<D, WG>::ROT;
+  const int lds = Bulk<D, WG>::STAGE + lut_area + Bulk<D, WG>::book_area(book_floats) + Bulk<D, WG>::ROT;
   dim3 grid((unsigned)((max_rows + WG - 1) / WG), (unsigned)n_jobs);
   if (src_f32)
     hipLaunchKernelGGL((encode_bulk_kernel<D, NG, NS, true, WG>), grid, dim3(WG), lds, stream, jobs, lut_area,
@@ -244,13 +317,13 @@ int encode_bulk_kind(const DevTables *T) {
 
 int encode_bulk_lds_bytes(int kind, int wg, int lut_bytes, int book_floats) {
   const int d = kind == 1 ? 64 : 128;
-  return wg * (d + 2) * 2 + ((lut_bytes + 15) & ~15) + ((book_floats + 3) & ~3) * 4 +
+  return wg * (d + 2) * 2 + Bulk<64, 256>::lut_area(lut_bytes) + Bulk<64, 256>::book_area(book_floats) +
          (d <= 64 ? 2 * (d / 2) * (d / 2) * 4 : 0);
 }
 
 hipError_t launch_encode_bulk(const EncodeJobDev *jobs, int n_jobs, int kind, int wg, int src_f32, int64_t max_rows,
                               int lut_bytes, int book_floats, hipStream_t stream) {
-  const int lut_area = (lut_bytes + 15) & ~15;
+  const int lut_area = Bulk<64, 256>::lut_area(lut_bytes);
 #define BGTQ_BULK(K, DD, NS, W)                                                                           \
   if (kind == K && wg == W)                                                                               \
     return launch_kind<DD, 2, NS, W>(jobs, n_jobs, src_f32, max_rows, lut_area, book_floats, stream);

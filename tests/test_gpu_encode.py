@@ -247,6 +247,36 @@ def test_bulk_layout_b_encoder_bit_exact(device, oracle):
                 t_other.destroy()
 
 
+def test_bulk_encoder_unaligned_source(device, oracle):
+    """The bulk encoder stages rows as 16-byte pieces when the source and its row stride allow it; a
+    source starting one element past a 16-byte boundary with an odd row stride takes its element-wise
+    staging, FP16 and FP32, over a partial last workgroup of rows."""
+    import torch
+    import bgtq
+    from bgtq import batched, calibrate
+    rng = np.random.default_rng(321)
+    dim, rows = 64, 1000
+    stride = dim + 1
+    p = calibrate.layout_b(dim)
+    k = _random_half_rows(rng, rows, dim)
+    tables = bgtq.Tables(device, p)
+    try:
+        ref_p, ref_n = oracle.encode_pack(_olayout(oracle, p), np.ascontiguousarray(k))
+        for src_kind in ("f16", "f32"):
+            flat = np.zeros(1 + rows * stride, dtype=np.float16)
+            flat[1:].reshape(rows, stride)[:, :dim] = k.view(np.float16)
+            src = torch.from_numpy(flat.view(np.int16) if src_kind == "f16" else flat.astype(np.float32)).cuda()
+            packed = torch.zeros((rows, p.rowBytes), dtype=torch.uint8, device="cuda")
+            norms = torch.zeros((rows, p.normStride), dtype=torch.int16, device="cuda")
+            batched.encode(device, [dict(tables=tables, src=src[1:], src_row_stride=stride, rows=rows, packed=packed,
+                                         norms=norms, dst_row0=0)], src_kind)
+            device.synchronize()
+            assert np.array_equal(packed.cpu().numpy(), ref_p), src_kind
+            assert np.array_equal(norms.cpu().numpy().view(np.uint16), ref_n), src_kind
+    finally:
+        tables.destroy()
+
+
 def test_calibration_load_encodes_every_head(device, oracle):
     """Calibration.load (src/model/calibration.ts:7-21) puts the 90 SmolLM2 heads on the device;
     each head's tables then encode its KV head's post-RoPE rows bit for bit as the oracle does
