@@ -328,3 +328,16 @@ def test_graph_replays_match_eager(device, oracle):
         assert torch.equal(out, eager)
     for t in tabs:
         t.destroy()
+
+
+def test_batch_beyond_grid_refused(device):
+    """The fused kernel's grid carries the sequence in its third dimension (at most 65535): a larger batch
+    is refused before any launch."""
+    import torch
+    import bgtq
+    from bgtq import batched
+    z = torch.zeros(16, device="cuda")
+    args = dict(batch=65536, q_heads=2, kv_heads=1, dim=64, q=z, out=z, lengths=z, max_length=32, v=z, v_dtype="f16",
+                v_seq_stride=0, v_head_stride=0, k_f16=z, k_seq_stride=0, k_head_stride=0, splits=1)
+    with pytest.raises(bgtq.UnsupportedError, match="65535 sequences"):
+        batched.workspace_bytes(batched.decode_desc(**args))
