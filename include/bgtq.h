@@ -195,6 +195,7 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
  *   packed[b*packed_seq_stride + kv*packed_head_stride + t*row_bytes]
  *   norms [b*norms_seq_stride  + kv*norms_head_stride  + t*norm_stride]
  *   v/k   [b*seq_stride        + kv*head_stride        + t*dim]
+ *   batch: 1..65535 sequences.
  *   q, out: [B, Hq, dim] FP32 contiguous; lengths: device uint32 [B] (tokens
  *   attended per sequence, 1..max_length). workspace: device memory of at
  *   least bgtq_decode_workspace_size() bytes, zero-filled by the caller
