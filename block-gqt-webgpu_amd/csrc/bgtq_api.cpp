@@ -990,7 +990,7 @@ static DecodeWorkspace decode_ws(int64_t units, int64_t heads, int dim, int spli
   auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
   DecodeWorkspace w;
   w.counters = 0;
-  w.qr = al(sizeof(uint32_t) * units);
+  w.qr = al(sizeof(uint32_t) * kCounterStride * units);
   w.part = w.qr + al(sizeof(float) * heads * dim);
   w.stats = w.part + al(sizeof(float) * heads * splits * (dim + 2));
   w.total = w.stats + al(sizeof(float) * heads * 2);
@@ -1227,6 +1227,7 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
   p.v_head_stride = d->v_head_stride;
   uint8_t *ws = static_cast<uint8_t *>(d->workspace);
   p.counters = reinterpret_cast<uint32_t *>(ws + w.counters);
+  p.counter_stride = kCounterStride;
   p.qr = reinterpret_cast<float *>(ws + w.qr);
   p.part = reinterpret_cast<float *>(ws + w.part);
   p.stats = reinterpret_cast<float *>(ws + w.stats);
@@ -1417,6 +1418,8 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
     dp.split_tokens = 0;
     dp.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
     dp.counters = reinterpret_cast<uint32_t *>(ws + plan.counters);
+    // The counter prefix holds 65536 words: units on lines of their own while they fit.
+    dp.counter_stride = (int)std::max<int64_t>(1, std::min<int64_t>(kCounterStride, 65536 / ((int64_t)d->batch * d->rows * d->kv_heads)));
     dp.part = reinterpret_cast<float *>(ws + plan.part);
     dp.out = d->out;
     HIP_TRY(launch_decode_fast(dp, fl, nn, sg, ctx->stream), "prefill launch");
@@ -1590,6 +1593,7 @@ bgtq_status bgtq_attention_record(bgtq_attention *a) {
   p.part = static_cast<float *>(a->part.ptr);
   p.stats = static_cast<float *>(a->stats.ptr);
   p.counters = static_cast<uint32_t *>(a->counters.ptr);
+  p.counter_stride = 1;
   p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)k->dim));
   p.out = static_cast<float *>(a->out.ptr);
   if (a->materialize) {

@@ -67,7 +67,8 @@ struct DevTables {
 };
 constexpr int kMfmaTableBytes = 3072;
 constexpr int kPairSlots = 4;         // pair tables (2 KB each) the fused decode keeps in LDS
-constexpr int kLaneRecordWords = 44;  // words of one per-lane code-lookup record
+constexpr int kLaneRecordWords = 44;
+constexpr int kCounterStride = 16;   // words between the decode's split counters (one per 64-byte line)  // words of one per-lane code-lookup record
 __host__ __device__ constexpr int rot_q_bytes(int dim) { return dim * dim * 4; }
 
 __host__ __device__ inline const uint8_t *tables_lut(const DevTables *t) {
@@ -166,7 +167,11 @@ struct DecodeParams {
   const int32_t *ends;      // optional [B*Hq] exclusive causal ends
   int32_t splits, split_tokens;
   float inv_sqrt_d;
-  uint32_t *counters;  // [B*Hkv] split arrival counters: zero between launches
+  uint32_t *counters;  // split arrival counters, one per unit: zero between launches
+  // Words from one unit's counter to the next (0 counts as 1): counters on
+  // lines of their own keep the arrivals of different units from queueing
+  // behind each other at the memory's atomic unit.
+  int32_t counter_stride;
   float *part;    // [B*Hq*splits*(dim+2)] (m, l, o[dim])
   float *stats;   // [B*Hq*2] final (m, l)
   float *out;     // [B*Hq*dim]

@@ -215,6 +215,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #undef BGTQ_ARGS
   __builtin_amdgcn_sched_barrier(0);
   const int unit = qrow * p.kv_heads + kv;
+  uint32_t *const counter = p.counters + (int64_t)unit * (p.counter_stride > 0 ? p.counter_stride : 1);
   const bool rowwise = p.starts != nullptr;
   const int rows = rowwise ? p.rows : 1;
   const int b = qrow / rows;
@@ -1106,7 +1107,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0)
-    *last = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    *last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
             (unsigned)(S - 1);
   __syncthreads();
   if (!*last) return;
@@ -1114,7 +1115,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     else merge_one_round<D, kMergeOneRound>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
-    if (tid == 0) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   // More splits: every load of a stage in flight at once: (m, l) of all
@@ -1162,7 +1163,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
     p.out[head * D + dm] = Ov;
   }
-  if (tid == 0) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int KF, int NN, int SG, int PK = 0>

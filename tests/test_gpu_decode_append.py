@@ -73,7 +73,7 @@ def _run(device, *, dim, key_format, lengths, splits=0, k_dtype="f32", v_dtype="
         else:
             batched.decode_append(device, desc, batched.append_desc(k_new=k_new, v_new=v_new))
         torch.cuda.synchronize()
-        assert not ws[:4 * B * hkv].any(), "split counters left nonzero"
+        assert not ws[:64 * B * hkv].any(), "split counters (one per 64-byte line) left nonzero"
         outs.append(out.cpu())
         caches.append([c.cpu() for c in cache])
     for a, b in zip(caches[0], caches[1]):
