@@ -739,11 +739,16 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     const _Float16 *vh = reinterpret_cast<const _Float16 *>(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
     m_run = new_x;
     l_run = new_x != -INFINITY && gq == 0 ? kPScale : 0.0f;
+    // The V row's values first, unconditionally: a read under the select
+    // below is a branch and an LDS round trip per element.
+    float vcol[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vcol[dt] = (float)vh[16 * dt + col];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool vr = __shfl(new_x, 4 * gq + r, 64) != -INFINITY;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) O[dt][r] = vr ? kPScale * (float)vh[16 * dt + col] : 0.0f;
+      for (int dt = 0; dt < DT; ++dt) O[dt][r] = vr ? kPScale * vcol[dt] : 0.0f;
     }
     row_enc::wave_sync();
   }
