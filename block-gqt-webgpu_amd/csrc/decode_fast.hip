@@ -655,6 +655,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       // all three in device memory.
       auto encode_new = [&](const DevTables *T, const uint8_t *lut, const float *books) {
         lc.init(T, lane);
+        const int ndims = __builtin_amdgcn_readfirstlane(T->nibble_dims);  // read with the lane set-up
         float x[JL];
 #pragma unroll
         for (int jl = 0; jl < JL; ++jl) {
@@ -674,13 +675,13 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
             T, lc, x,
             [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
             lut, books, scr, lane);
-        const int logical = T->nibble_dims / 2 + D - T->nibble_dims;
+        const int logical = ndims / 2 + D - ndims;
         uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
 #pragma unroll
         for (int jl = 0; jl < JL; ++jl) {
           const int bb = lane + 64 * jl;
           if (bb < rb) {
-            pk_new[jl] = row_enc::packed_byte(scr.codes, bb, T->nibble_dims, logical);
+            pk_new[jl] = row_enc::packed_byte(scr.codes, bb, ndims, logical);
             prow[bb] = (uint8_t)pk_new[jl];
           }
         }
@@ -1159,12 +1160,17 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     float *pp = p.part + head * S * (D + 2) + 2 + dm;
     float Ov = 0.0f;
     for (int s0 = 0; s0 < S; s0 += 8) {
-      float o[8];
+      // Unconditional loads (past S: split S - 1, weighted zero), all eight in
+      // flight together; loads under a branch would go one after another.
+      float o[8], w8[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) o[k] = s0 + k < S ? coherent_load(pp + (s0 + k) * (D + 2)) : 0.0f;
+      for (int k = 0; k < 8; ++k) {
+        const int sk = min(s0 + k, S - 1);
+        o[k] = coherent_load(pp + sk * (D + 2));
+        w8[k] = wgt[g * S + sk];
+      }
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (s0 + k < S) Ov = __builtin_fmaf(o[k], wgt[g * S + s0 + k], Ov);
+      for (int k = 0; k < 8; ++k) Ov = __builtin_fmaf(o[k], s0 + k < S ? w8[k] : 0.0f, Ov);
     }
     p.out[head * D + dm] = Ov;
   }

@@ -199,9 +199,13 @@ __device__ __forceinline__ uint16_t encode_row(const DevTables *T, const Lane<D>
 // Byte b of the packed row (src/reference/mixed_layout.py:21-27): nibble
 // bytes, then byte codes, then zero padding.
 __device__ __forceinline__ uint8_t packed_byte(const uint8_t *codes, int b, int nibble_dims, int logical) {
-  if (b < nibble_dims / 2) return (uint8_t)((codes[2 * b] & 15) | ((codes[2 * b + 1] & 15) << 4));
-  if (b < logical) return codes[nibble_dims + b - nibble_dims / 2];
-  return 0;
+  // Both code reads unconditional (index 0 past the logical bytes): reads
+  // under branches would be one LDS round trip after another.
+  const int nb = nibble_dims / 2;
+  const bool nib = b < nb;
+  const int j = b >= logical ? 0 : nib ? 2 * b : nibble_dims + b - nb;
+  const uint32_t c0 = codes[j], c1 = codes[nib ? j + 1 : j];
+  return b >= logical ? 0 : nib ? (uint8_t)((c0 & 15) | ((c1 & 15) << 4)) : (uint8_t)c0;
 }
 
 }  // namespace row_enc

@@ -57,17 +57,19 @@ __global__ __launch_bounds__(64 * kWaves) void encode_wave_kernel(EncodeLaunch l
       gfx::dma16(rt, smem + L.tab + k * 1024, k * 1024 + lane * 16, 0);
   }
   // Natural-order row values: lane holds element lane + 64 jl (FP16-rounded).
+  // Unconditional loads (a row past the job's reads its row 0, an element
+  // past D its element 0; both are then zeroed), so the next row's load stays
+  // in flight while the current row is encoded instead of being waited for
+  // under a branch.
   auto load_row = [&](int64_t r, float (&v)[JL]) {
+    const bool row_ok = r < job.rows;
 #pragma unroll
     for (int jl = 0; jl < JL; ++jl) {
-      float x = 0.0f;
       const int e = lane + 64 * jl;
-      if (e < D && r < job.rows) {
-        const int64_t at = r * job.src_stride + e;
-        if (SRC_F32) x = f16_bits_to_f32(f32_to_f16_bits(static_cast<const float *>(job.src)[at]));
-        else x = f16_bits_to_f32(static_cast<const uint16_t *>(job.src)[at]);
-      }
-      v[jl] = x;
+      const int64_t at = (row_ok ? r : 0) * job.src_stride + (e < D ? e : 0);
+      const float x = SRC_F32 ? f16_bits_to_f32(f32_to_f16_bits(static_cast<const float *>(job.src)[at]))
+                              : f16_bits_to_f32(static_cast<const uint16_t *>(job.src)[at]);
+      v[jl] = row_ok && e < D ? x : 0.0f;
     }
   };
   int64_t row = (int64_t)blockIdx.x * kWaves + wave;
