@@ -1178,6 +1178,12 @@ bgtq_status bgtq_decode_append(bgtq_context *ctx, const bgtq_decode_desc *d, con
     if (t != BGTQ_DTYPE_F16 && t != BGTQ_DTYPE_F32) return fail(BGTQ_ERR_RANGE, "invalid new K/V dtype");
   if (d && (a->k_new_seq_stride < 0 || a->k_new_head_stride < 0 || a->v_new_seq_stride < 0 || a->v_new_head_stride < 0))
     return fail(BGTQ_ERR_RANGE, "negative new K/V stride");
+  // The kernel reads the new rows as 4-byte words.
+  if (reinterpret_cast<uintptr_t>(a->k_new) % 4 || reinterpret_cast<uintptr_t>(a->v_new) % 4)
+    return fail(BGTQ_ERR_RANGE, "new K and V must be 4-byte aligned");
+  if ((a->k_new_dtype == BGTQ_DTYPE_F16 && (a->k_new_seq_stride % 2 || a->k_new_head_stride % 2)) ||
+      (a->v_new_dtype == BGTQ_DTYPE_F16 && (a->v_new_seq_stride % 2 || a->v_new_head_stride % 2)))
+    return fail(BGTQ_ERR_RANGE, "FP16 new K/V strides must be even");
   return decode_impl(ctx, d, a);
 }
 

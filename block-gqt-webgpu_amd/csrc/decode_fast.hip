@@ -434,12 +434,20 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   row_enc::Lane<D> lc;
   const int64_t v_off = (int64_t)b * p.v_new_seq_stride + kv * p.v_new_head_stride;
   const int64_t k_off = (int64_t)b * p.k_new_seq_stride + kv * p.k_new_head_stride;
+  // The new rows' loads carry no branch (a load under a lane test or a
+  // format select compiles to a branch whose join waits for it, holding back
+  // every load after it). Lane i < D / 8 gets elements 8 i .. 8 i + 7: FP32
+  // as eight words, FP16 as four words of two halves; the other lanes re-read
+  // lane 0's piece. The rows are 4-byte aligned (checked on the host).
   auto load_piece = [&](const void *src, int f32, int64_t off, uint32_t (&r)[8]) {
+    const int pl = lane < PR ? lane : 0;
+    const uint8_t *base = static_cast<const uint8_t *>(src) + (off + 8 * pl) * (f32 ? 4 : 2);
+    const uint32_t *p0 = reinterpret_cast<const uint32_t *>(base);
+    const uint32_t *p1 = reinterpret_cast<const uint32_t *>(base + (f32 ? 16 : 0));
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (f32) r[k] = static_cast<const uint32_t *>(src)[off + 8 * lane + k];
-      else if (k < 4) r[k] = (uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k] |
-                             ((uint32_t)static_cast<const uint16_t *>(src)[off + 8 * lane + 2 * k + 1] << 16);
+    for (int k = 0; k < 4; ++k) {
+      r[k] = p0[k];
+      r[4 + k] = p1[k];
     }
   };
   auto half_piece = [&](int f32, const uint32_t (&r)[8]) {
@@ -460,19 +468,25 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
 #pragma unroll
     for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
-    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
+    load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl)
-      k_nat[jl] = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new)[k_off + lane + 64 * jl]
-                              : (uint32_t)static_cast<const uint16_t *>(p.k_new)[k_off + lane + 64 * jl];
+    for (int jl = 0; jl < JL; ++jl) {
+      // FP16: the word holding the element (k_off is even).
+      const int64_t idx = k_off + lane + 64 * jl;
+      const uint32_t *w = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new) + idx
+                                      : reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(p.k_new) +
+                                                                           (idx & ~(int64_t)1));
+      const uint32_t kw = *w;
+      k_nat[jl] = p.k_new_f32 ? kw : (kw >> (16 * (uint32_t)(idx & 1))) & 0xffffu;
+    }
     if (D == 64) {
 #pragma unroll
       for (int i = 0; i < D; ++i) rt_col[i] = fl.rot_t[kv][i * D + lane];
     }
   }
   if (owner) {
-    if (lane < PR) load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
-    if (KF == 0 && lane < PR) load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
+    load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
+    if (KF == 0) load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
   }
 
   // Unconditional, so every wave has exactly AHEAD * L chunk loads in flight

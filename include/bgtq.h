@@ -247,7 +247,8 @@ bgtq_status bgtq_decode(bgtq_context *ctx, const bgtq_decode_desc *d);
  * 32 head-perm positions, 8 books whose code tables fit its LDS, norm_stride
  * up to 8; the reference's layouts and SmolLM2 calibration heads qualify);
  * others return BGTQ_ERR_UNSUPPORTED and write nothing (use the two calls).
- * The workspace is the decode's. */
+ * k_new and v_new are 4-byte aligned, FP16 ones with even strides
+ * (BGTQ_ERR_RANGE otherwise). The workspace is the decode's. */
 typedef struct {
   const void *k_new;
   int32_t k_new_dtype; /* BGTQ_DTYPE_F32 or BGTQ_DTYPE_F16 */
