@@ -391,7 +391,10 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
   };
   // Per-head causal limits.
-  const int end_h = head_ok ? (p.ends ? min(p.ends[(int64_t)qrow * Hq + hq0 + col], T_b) : T_b) : 0;
+  // The causal end is read for every lane (heads past G read head 0's) and
+  // then selected: a load under the lane test would be waited for at once.
+  const int end_any = p.ends ? p.ends[(int64_t)qrow * Hq + hq0 + (head_ok ? col : 0)] : T_b;
+  const int end_h = head_ok ? min(end_any, T_b) : 0;
   int lim = min(end_h, t_end);
   // Wave-uniform: chunks reaching past lim_min need the per-head mask.
   int lim_min = head_ok ? lim : t_end;
