@@ -692,23 +692,33 @@ static bgtq_status append_count(const uint16_t *v, size_t n, uint32_t dim, uint3
   return BGTQ_OK;
 }
 
+// An append first claims the store (pending), so two threads appending at
+// once cannot both pass the capacity check on the same length: the loser is
+// refused as the reference refuses a second append while one is in flight.
+// The length is read once, after the claim, and used for both the capacity
+// check and the destination row; it grows before the claim is released.
 bgtq_status bgtq_keys_append(bgtq_keys *k, const uint16_t *v, size_t n) {
   if (!k) return fail(BGTQ_ERR_RANGE, "null keys");
-  if (k->pending) return fail(BGTQ_ERR_STATE, "Concurrent K appends unsupported");
+  bool idle = false;
+  if (!k->pending.compare_exchange_strong(idle, true, std::memory_order_acq_rel))
+    return fail(BGTQ_ERR_STATE, "Concurrent K appends unsupported");
+  struct Release {
+    std::atomic<bool> &flag;
+    ~Release() { flag.store(false, std::memory_order_release); }
+  } release{k->pending};
+  const uint32_t length = k->length.load(std::memory_order_acquire);
   uint32_t count = 0;
-  if (bgtq_status s = append_count(v, n, k->dim, k->length, k->capacity, &count)) return s;
+  if (bgtq_status s = append_count(v, n, k->dim, length, k->capacity, &count)) return s;
   bgtq_context *ctx = k->ctx;
   if (bgtq_status s = ctx->use()) return s;
   if (k->kind == BGTQ_KEYS_FP16) {
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    HIP_TRY(hipMemcpy(static_cast<uint16_t *>(k->fp16.ptr) + (size_t)k->length * k->dim, v, n * 2,
+    HIP_TRY(hipMemcpy(static_cast<uint16_t *>(k->fp16.ptr) + (size_t)length * k->dim, v, n * 2,
                       hipMemcpyHostToDevice),
             "FP16 K upload");
-    k->length += count;
+    k->length.store(length + count, std::memory_order_release);
     return BGTQ_OK;
   }
-  bool idle = false;
-  if (!k->pending.compare_exchange_strong(idle, true)) return fail(BGTQ_ERR_STATE, "Concurrent K appends unsupported");
   std::lock_guard<std::mutex> lock(ctx->staging_mutex);
   bgtq_status s = ctx->ensure_staging(n * 2);
   if (!s) {
@@ -718,15 +728,14 @@ bgtq_status bgtq_keys_append(bgtq_keys *k, const uint16_t *v, size_t n) {
   if (!s) {
     bgtq_encode_job job{k->tables, ctx->staging.ptr, (int64_t)k->dim, (int64_t)count,
                         static_cast<uint8_t *>(k->packed.ptr), static_cast<uint16_t *>(k->norms.ptr),
-                        (int64_t)k->length};
+                        (int64_t)length};
     s = bgtq_encode_batched(ctx, BGTQ_DTYPE_F16, &job, 1);
   }
   if (!s) {
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) s = hip_fail(e, "K encode");
   }
-  k->pending = false;
-  if (!s) k->length += count;  // only after the encode has completed
+  if (!s) k->length.store(length + count, std::memory_order_release);  // only after the encode has completed
   return s;
 }
 
@@ -1280,8 +1289,11 @@ struct PrefillPlan {
   int tiles, tile_queries, ranges, range_blocks;
   size_t records;    // bytes of the workgroups' partial records
   size_t workspace;  // records, then the tile table (16 bytes per tile)
-  bool rowwise;      // the fused decode kernel, one unit per (query row, KV head)
-  int splits;        // rowwise: token splits per unit
+  bool rowwise;      // the fused decode kernel, units of 16 (row, head) query columns
+  int qgroups;       // rowwise: units per (sequence, KV head)
+  int unit_cols;     // rowwise: query columns per unit
+  int splits;        // rowwise: token splits per unit (a unit uses those its history needs)
+  int split_floor;   // rowwise: tokens per split at least
   size_t counters, part;  // rowwise: workspace offsets (the split counters first)
 };
 
@@ -1318,15 +1330,25 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
   if (d->split_tokens < 0) return fail(BGTQ_ERR_RANGE, "negative split_tokens");
   if ((int64_t)d->batch * d->kv_heads > 65535) return fail(BGTQ_ERR_UNSUPPORTED, "prefill handles up to 65535 sequence x KV head units");
   const int64_t G = d->q_heads / d->kv_heads, nq = (int64_t)d->rows * G;
-  const int64_t row_units = (int64_t)d->batch * d->rows * d->kv_heads;
-  plan->rowwise = d->rows <= kPrefillRowwiseRows && row_units <= 65535;
+  const int64_t uc = kPrefillUnitCols, qgroups = (nq + uc - 1) / uc;
+  const int64_t row_units = (int64_t)d->batch * qgroups * d->kv_heads;
+  plan->rowwise = d->rows <= kPrefillRowwiseRows && (int64_t)d->batch * qgroups <= 65535;
   if (plan->rowwise) {
-    const int64_t want = d->split_tokens > 0 ? ((int64_t)d->max_length + d->split_tokens - 1) / d->split_tokens : 0;
-    plan->splits = choose_splits(row_units, d->max_length, (int32_t)std::min<int64_t>(want, 256));
+    // Splits of at least split_floor tokens (two 32-token chunks per wave
+    // by default: below that a split merge costs more than the chunks it
+    // saves), as many as the longest history allowed needs, at most enough
+    // for two workgroups per compute unit and kPrefillMaxSplits.
+    const int64_t floor_tok = d->split_tokens > 0 ? d->split_tokens : kPrefillSplitFloor;
+    int64_t splits = ((int64_t)d->max_length + floor_tok - 1) / floor_tok;
+    if (d->split_tokens <= 0) splits = std::min<int64_t>(splits, std::max<int64_t>(1, 2 * (int64_t)device_cus() / row_units));
+    plan->qgroups = (int)qgroups;
+    plan->unit_cols = (int)uc;
+    plan->splits = (int)std::max<int64_t>(1, std::min<int64_t>(splits, kPrefillMaxSplits));
+    plan->split_floor = (int)std::max<int64_t>(floor_tok, ((int64_t)d->max_length + plan->splits - 1) / plan->splits);
     plan->counters = 0;
     plan->part = kPrefillCounterBytes;
-    plan->workspace =
-        kPrefillCounterBytes + sizeof(float) * (size_t)d->batch * d->rows * d->q_heads * plan->splits * (d->dim + 2);
+    // Partial rows o[dim], m, l, pad.
+    plan->workspace = kPrefillCounterBytes + sizeof(float) * (size_t)row_units * uc * plan->splits * (d->dim + 4);
     return BGTQ_OK;
   }
   plan->tile_queries = nq >= 2048 ? 64 * prefill_column_blocks(d->dim) : 64;
@@ -1420,12 +1442,16 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
     dp.rows = d->rows;
     dp.starts = d->starts;
     dp.max_length = (int32_t)d->max_length;
+    dp.qgroups = plan.qgroups;
+    dp.unit_cols = plan.unit_cols;
     dp.splits = plan.splits;
+    dp.split_floor = plan.split_floor;
     dp.split_tokens = 0;
     dp.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
     dp.counters = reinterpret_cast<uint32_t *>(ws + plan.counters);
     // The counter prefix holds 65536 words: units on lines of their own while they fit.
-    dp.counter_stride = (int)std::max<int64_t>(1, std::min<int64_t>(kCounterStride, 65536 / ((int64_t)d->batch * d->rows * d->kv_heads)));
+    dp.counter_stride = (int)std::max<int64_t>(
+        1, std::min<int64_t>(kCounterStride, 65536 / ((int64_t)d->batch * plan.qgroups * d->kv_heads)));
     dp.part = reinterpret_cast<float *>(ws + plan.part);
     dp.out = d->out;
     HIP_TRY(launch_decode_fast(dp, fl, nn, sg, ctx->stream), "prefill launch");

@@ -157,12 +157,17 @@ struct DecodeParams {
   int32_t q_rotated;      // 1: q is already R q[perm] (code domain); the kernels do not rotate it
   const float *qr;        // [B*Hq*dim] rotated, permuted, scaled by 1/sqrt(dim)
   const uint32_t *lengths;  // [B]; kernels clamp them to max_length
-  // Chunked prefill through the fused decode kernel (small chunks): units are
-  // (query row, KV head) pairs, row r of sequence b attending to the first
-  // starts[b] + r + 1 tokens; q, out, part and stats are indexed by query row
-  // b * rows + r instead of b. Plain decode: rows = 1, starts = null.
+  // Chunked prefill through the fused decode kernel (small chunks): row r of
+  // sequence b attends to the first min(starts[b], max_length - rows) + r + 1
+  // tokens; q and out are indexed by query row b * rows + r instead of b. A
+  // unit is unit_cols (8 or 16) query columns of one (sequence, KV head): the
+  // chunk's rows x G heads flattened row-major, qgroups = ceil(rows * G /
+  // unit_cols) units per (sequence, KV head), partials at row unit *
+  // unit_cols + column. A unit runs min(splits, ceil(history / split_floor))
+  // of its splits. Plain decode: rows = 1, starts = null.
   int32_t rows;
   const uint32_t *starts;
+  int32_t qgroups, split_floor, unit_cols;
   int32_t max_length;       // tokens every K/V buffer holds per (sequence, KV head)
   const int32_t *ends;      // optional [B*Hq] exclusive causal ends
   int32_t splits, split_tokens;
@@ -226,6 +231,12 @@ constexpr int kPrefillMaxRanges = 2048;   // workgroups of one launch at most (b
 // kernel (a unit per query row and KV head, its split merge); longer chunks
 // tile their queries in the prefill kernel.
 constexpr int kPrefillRowwiseRows = BGTQ_PREFILL_ROWWISE_ROWS;
+// Row-wise prefill: tokens per split at least (two 32-token chunks per
+// wave), splits per unit at most.
+constexpr int kPrefillSplitFloor = 256;
+constexpr int kPrefillMaxSplits = 16;
+// Row-wise prefill: query columns per unit (8 or 16).
+constexpr int kPrefillUnitCols = 16;
 // The prefill workspace starts with the row-wise path's split counters (a
 // word per unit, up to 65535 units): zero before a workspace's first call,
 // left zero by every call, never written by the tiled path.

@@ -86,7 +86,7 @@ struct Slot {
   // code tables (CTABLES bytes), then kPairSlots pair tables of 2 KB.
   static constexpr int CTABLES = KF == 2 && D == 64 ? 3584 : KF >= 1 ? KS * 2048 : 0;
   static constexpr int TABLES = CTABLES + (KF == 2 ? kPairSlots * 2048 : 0);
-  static constexpr int RING = kRing * kWaves * BYTES + TABLES <= kLdsLimit ? kRing : 2;
+  static constexpr int RING = kRing;
   static constexpr int AHEAD = RING - 1;
   static constexpr int DYN = RING * kWaves * BYTES;  // dynamic LDS: the ring (the tables are static)
   // Decode-step append: the new token's wave encodes it with its last ring
@@ -106,6 +106,18 @@ struct Slot {
 // The weights w_s = 2^(m_s - M) come from wave reductions and reach every
 // lane through lane reads. Out of line, and instantiated for a few SMAX, so
 // the kernel's own code stays as small.
+// Rows of a row-wise unit's columns: column g's partials at row pbase + g of
+// the partial array; its output at row obase + (j / G) * Hq + j % G, with
+// j = jbase + g its query in the chunk's rows x G heads.
+struct MergeRows {
+  int64_t pbase, obase;
+  int jbase, G, Hq, ncol;
+  __device__ int64_t out_row(int g) const {
+    const int j = jbase + g, r = j / G;
+    return obase + (int64_t)r * Hq + (j - r * G);
+  }
+};
+
 template <int D, int SMAX>
 __device__ __noinline__ void merge_one_round(float *part, float *out, float *stats, int64_t head0, int G, int S,
                                              int wave, int lane) {
@@ -173,14 +185,122 @@ __device__ __noinline__ void merge_one_round(float *part, float *out, float *sta
   }
 }
 
+// Row-wise prefill split merge (PF). Wave w merges the unit's columns w,
+// w + 4, ... (NH of them), all their loads in flight at once. Partial rows are
+// o[D], m, l, pad (16-byte aligned). A lane is (split group sg, dimension
+// quad dq): it loads the o quads of splits sg, sg + SG, ... as 16-byte loads
+// and lane s the (m, l) of split s; the weights reach the lanes by lane
+// reads and the split groups' sums meet through lane swaps. Inlined, so the
+// buffer resource's base stays in scalar registers.
+template <int D, int SMAX, int NH>
+__device__ __forceinline__ void merge_rows(float *part, float *out, const MergeRows mr, int S, int wave, int lane) {
+  constexpr int DQ = D / 4;                // dimension quads
+  constexpr int SG = 64 / DQ;              // split groups (4 at d=64, 2 at d=128)
+  constexpr int J = (SMAX + SG - 1) / SG;  // splits per lane at most
+  constexpr uint32_t ROWB = (D + 4) * 4;   // bytes per partial row
+  S = __builtin_amdgcn_readfirstlane(S);
+  const int G = mr.ncol;
+  if (wave >= G) return;
+  const int sg = lane / DQ, dq = lane - sg * DQ;
+  const int sl = min(lane, S - 1);
+  // The unit's partials: 4 NH columns x S rows.
+  const __amdgpu_buffer_rsrc_t r = rsrc(part + mr.pbase * S * (D + 4), 4u * NH * (uint32_t)S * ROWB);
+  u32x2 ml[NH];
+  f32x4 o[NH][J];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const int g = wave + 4 * h;
+    const uint32_t col = (uint32_t)(g < G ? g : wave) * (uint32_t)S * ROWB;
+    ml[h] = coherent_load2(r, col + (uint32_t)sl * ROWB + D * 4);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int s = min(sg + SG * j, S - 1);
+      o[h][j] = coherent_load4(r, col + (uint32_t)s * ROWB + 16u * dq);
+    }
+  }
+  // The four columns step by step side by side (no branch between them), so
+  // their chains of lane reductions overlap; only the stores are predicated.
+  float m[NH], w[NH], Lsum[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) m[h] = lane < S ? __uint_as_float(ml[h][0]) : -INFINITY;
+  float M[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) M[h] = row_max(m[h]);
+#pragma unroll
+  for (int h = 0; h < NH; ++h) M[h] = col_max(M[h]);
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    w[h] = m[h] == -INFINITY ? 0.0f : exp2f(m[h] - M[h]);
+    Lsum[h] = (lane < S ? __uint_as_float(ml[h][1]) : 0.0f) * w[h];
+  }
+  // Row sums: rotations by 8, 4, 2, 1 lanes (DPP row_ror).
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    Lsum[h] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(Lsum[h]), 0x128, 0xf, 0xf, false));
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    Lsum[h] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(Lsum[h]), 0x124, 0xf, 0xf, false));
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    Lsum[h] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(Lsum[h]), 0x122, 0xf, 0xf, false));
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    Lsum[h] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(Lsum[h]), 0x121, 0xf, 0xf, false));
+#pragma unroll
+  for (int h = 0; h < NH; ++h) Lsum[h] = col_sum(Lsum[h]);
+  f32x4 acc[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    acc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int s = sg + SG * j;
+      const float ws = __shfl(w[h], s < 64 ? s : 0, 64);
+      acc[h] = s < S ? acc[h] + o[h][j] * ws : acc[h];
+    }
+  }
+  // Sum over the split groups: lanes dq + DQ k.
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float v = acc[h][k];
+      if (SG == 4) {
+        auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+      }
+      auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      acc[h][k] = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+    }
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const int g = wave + 4 * h;
+    // One reciprocal per column (within an ulp; the outputs' tolerance is 1e-4 relative).
+    const float inv = __builtin_amdgcn_rcpf(Lsum[h]);
+    if (g < G && sg == 0)
+      *reinterpret_cast<f32x4 *>(out + mr.out_row(g) * D + 4 * dq) = acc[h] * inv;
+  }
+}
+
 // KF: 1 = packed codes of a structured layout, 2 = packed codes of any
 // layout, 0 = FP16 K rows. NN: leading nibble K-steps (KF 2: scale DMAs).
 // SG: K-steps in group 0 (== KS: one scale per token; unused by KF 2).
 // PK (KF 2): leading pair K-steps of every head (two codes per packed byte).
-template <int D, int KF, int NN, int SG, int PK = 0>
+// PF (8 or 16): row-wise chunked prefill (p.starts set). A unit is PF query
+// columns of one (sequence, KV head): the chunk's rows x G heads flattened
+// row-major (query j = row * G + head), so a unit fills its MFMA columns
+// whatever G is and the chunk's history is streamed once per PF queries
+// (16: least streaming; 8: twice the units, each with half the epilogue and
+// merge, which is shorter on the latency-bound small launches). Column j sees
+// the first min(starts[b], max_length - rows) + row + 1 tokens. A unit uses
+// only as many of its splits as its history needs (p.split_floor tokens per
+// split at least); the others exit before their first chunk.
+template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0>
 __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
   using Sl = Slot<D, KF, NN>;
+  static_assert(PF == 0 || PF == 8 || PF == 16, "row-wise unit width");
+  constexpr int UC = PF ? PF : 16;  // columns of a row-wise unit
   static_assert(KF == 0 || row_enc::scratch_bytes(D) <= Sl::BYTES, "append scratch fits a ring slot");
   constexpr int KS = Gm::KS, DT = Gm::DT, PR = Gm::PR, VI = Gm::VI;
   constexpr int RB = Sl::RB, KI = Sl::KI, L = Sl::L, AHEAD = Sl::AHEAD;
@@ -192,10 +312,15 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
   extern __shared__ __align__(16) uint8_t smem[];
 
-  // Grid (split, KV head, query row): the head's layout words are loaded with
-  // the kernel arguments, with no division ahead of them.
-  // qrow: the query row (decode: its sequence); b: the sequence whose caches it reads.
-  const int split = blockIdx.x, kv = blockIdx.y, qrow = blockIdx.z;
+  // Grid (split, KV head, sequence); PF: (KV head, query group, split). The
+  // head's layout words are loaded with the kernel arguments, with no
+  // division ahead of them. Workgroups go to the XCDs round-robin by linear
+  // index, so PF puts the split slowest: the units' first splits, the ones
+  // every history has, spread over all XCDs (split fastest put every unit's
+  // split 0 on one XCD), and an XCD's units share one KV head's history.
+  // qrow: the sequence (PF: b * qgroups + query group).
+  const int split = PF ? blockIdx.z : blockIdx.x, kv = PF ? blockIdx.x : blockIdx.y,
+            qrow = PF ? blockIdx.y : blockIdx.z;
   // Every kernel argument the set-up reads, loaded at once: left to itself
   // the compiler loads them a basic block at a time, a chain of dependent
   // scalar round trips ahead of the first DMA.
@@ -203,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #define BGTQ_ARGS                                                                                              \
   "s"(p.kv_heads), "s"(p.rows), "s"(p.starts), "s"(p.lengths), "s"(p.max_length), "s"(p.G), "s"(p.q_heads), \
       "s"(p.splits), "s"(p.ends), "s"(p.k_new), "s"(p.q_rotated), "s"(p.q), "s"(p.v), "s"(p.packed),         \
-      "s"(p.norms), "s"(p.k), "s"(p.logits)
+      "s"(p.norms), "s"(p.k), "s"(p.logits), "s"(p.qgroups), "s"(p.split_floor)
   if constexpr (KF == 0) asm volatile("" ::BGTQ_ARGS);
   if constexpr (KF == 1)
     asm volatile("" ::BGTQ_ARGS, "s"(fl.mfma[kv]), "s"(fl.rot_q[kv]), "s"(fl.cent_exp[kv]), "s"(fl.book[0]),
@@ -216,9 +341,12 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   __builtin_amdgcn_sched_barrier(0);
   const int unit = qrow * p.kv_heads + kv;
   uint32_t *const counter = p.counters + (int64_t)unit * (p.counter_stride > 0 ? p.counter_stride : 1);
-  const bool rowwise = p.starts != nullptr;
+  constexpr bool rowwise = PF != 0;
   const int rows = rowwise ? p.rows : 1;
-  const int b = qrow / rows;
+  // PF: qrow = b * qgroups + qg (query group qg of sequence b).
+  const int ngroups = rowwise ? p.qgroups : 1;
+  const int b = rowwise ? qrow / ngroups : qrow;
+  const int qg = rowwise ? qrow - b * ngroups : 0;
   // A scalar load (constant address space): its wait goes where the value is
   // first used, after the loads below are issued.
   typedef const __attribute__((address_space(4))) uint32_t const_u32;
@@ -227,7 +355,23 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   const int G = p.G, Hq = p.q_heads, hq0 = kv * G;
   const int tid = threadIdx.x, lane = tid & 63, gq = lane >> 4, col = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
-  const bool head_ok = col < G;
+  // The unit's query columns: decode, its G heads; PF, flattened queries
+  // j = 16 qg + col of the chunk's rows x G heads.
+  const int ncol = rowwise ? min(UC, rows * G - UC * qg) : G;
+  const bool head_ok = col < ncol;
+  // This lane's column (columns past ncol read column 0's query): its query
+  // row of the chunk and head, and the row of q / out it indexes.
+  const int jq = rowwise ? UC * qg + (head_ok ? col : 0) : 0;
+  const int row_c = rowwise ? jq / G : 0;
+  const int head_c = rowwise ? jq - row_c * G : (head_ok ? col : 0);
+  const int64_t qidx = rowwise ? ((int64_t)b * rows + row_c) * Hq + hq0 + head_c : (int64_t)qrow * Hq + hq0 + head_c;
+  // Rows of out and of the split partials of column g.
+  auto out_row = [&](int g) -> int64_t {
+    if (!rowwise) return (int64_t)qrow * Hq + hq0 + g;
+    const int j = UC * qg + g, r = j / G;
+    return ((int64_t)b * rows + r) * Hq + hq0 + (j - r * G);
+  };
+  const int64_t pbase = rowwise ? (int64_t)unit * UC : (int64_t)qrow * Hq + hq0;
   // The K-steps' lookup tables are static LDS (an address fixed at compile
   // time, so a lookup's address is the code byte shifted: one instruction);
   // the ring is the dynamic LDS.
@@ -305,7 +449,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   }
   f32x4 qload[KS][2];  // unconditional loads of a valid row; heads past G are zeroed after the chunk issue
   {
-    const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + ((int64_t)qrow * Hq + hq0 + (head_ok ? col : 0)) * D);
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + qidx * D);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -343,13 +487,23 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   }
   // The sequence's length arrives while the loads above are in flight: what
   // depends on it comes after them.
-  const int T_b = rowwise ? min((int)len_b + (qrow - b * rows) + 1, p.max_length)
-                          : (int)min(len_b, (uint32_t)p.max_length);
+  // PF: the chunk starts at min(starts[b], max_length - rows) (rows <= max_length);
+  // the unit's history ends after its last column's row.
+  const int start_c = rowwise ? (int)min(len_b, (uint32_t)(p.max_length - rows)) : 0;
+  const int T_b = rowwise ? start_c + (UC * qg + ncol - 1) / G + 1 : (int)min(len_b, (uint32_t)p.max_length);
+  // PF: the splits this unit's history needs (every workgroup of the unit
+  // computes the same number); the others leave before their first chunk,
+  // once the prologue's DMAs into their LDS have landed.
+  const int S = rowwise ? min(p.splits, max(1, (T_b + p.split_floor - 1) / p.split_floor)) : p.splits;
+  if (rowwise && split >= S) {
+    wait_vm<0>();
+    return;
+  }
   // Splits of one (sequence, KV head) interleave at chunk granularity: wave w
   // of split s takes chunks (s * 4 + w) + 4 S i, so the waves working on a
   // sequence at any moment sweep adjacent memory.
   const int t_end = kInterleaved ? T_b : min(T_b, split * p.split_tokens + p.split_tokens);
-  const int stride = kInterleaved ? p.splits * kWaves * kChunk : kWaves * kChunk;
+  const int stride = kInterleaved ? S * kWaves * kChunk : kWaves * kChunk;
   // This wave's chunks start at first + 128 i.
   const int first = kInterleaved ? (split * kWaves + wave) * kChunk : split * p.split_tokens + wave * kChunk;
   const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
@@ -393,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // Per-head causal limits.
   // The causal end is read for every lane (heads past G read head 0's) and
   // then selected: a load under the lane test would be waited for at once.
-  const int end_any = p.ends ? p.ends[(int64_t)qrow * Hq + hq0 + (head_ok ? col : 0)] : T_b;
+  const int end_any = rowwise ? start_c + row_c + 1 : p.ends ? p.ends[qidx] : T_b;
   const int end_h = head_ok ? min(end_any, T_b) : 0;
   int lim = min(end_h, t_end);
   // Wave-uniform: chunks reaching past lim_min need the per-head mask.
@@ -416,7 +570,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   constexpr int JL = D > 64 ? 2 : 1;
   const int t_new = T_b - 1;
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
-  const int own_w = p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
+  const int own_w = !rowwise && p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
   const bool owner = own_w == wave;
   const bool encoder = KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
   const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
@@ -600,7 +754,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   int glo[KS2], nsl[KS2], koff[KS2], hib[KS2], nmf[KS2];
   uint32_t ext[KS2][8], tbo[KS2][8];
   half8 qbh[KS2][kSlots], qbl[KS2][kSlots];  // masked (packed) query operands of MFMA m
-  const int GP = KF == 2 ? (G <= 4 ? 4 : G <= 8 ? 2 : 1) : 1;  // group slots per MFMA
+  const int GP = KF == 2 ? (ncol <= 4 ? 4 : ncol <= 8 ? 2 : 1) : 1;  // group slots per MFMA
   const int HW = 16 / GP, cg = col / HW;
   constexpr int NSV = KF == 2 ? 2 * Sl::NSC : 1;  // scale entries a lane moves
   int sc_src[NSV], sc_dst[NSV];
@@ -1050,8 +1204,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     // faster than keeping a ring full across iterations: 6264 GB/s against
     // 5826 for these two slots waited for at the next iteration's top, 5780
     // for three slots (two chunks ahead), 6170 for three slots waited for
-    // here.
-    wait_vm<0>();
+    // here. PF: the history is in L2 and the ring deeper, so only the chunk
+    // computed is waited for (at the top of the iteration).
+    if (!PF) wait_vm<0>();
     u32x2 vt[DT][2];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -1084,38 +1239,103 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     for (int r = 0; r < 4; ++r)
       comb[(wave * 16 + 4 * gq + r) * (D + 2) + 2 + 16 * dt + col] = O[dt][r] * (1.0f / kPScale);
   __syncthreads();
-  const int S = p.splits;
-  for (int e = tid; e < G * D; e += kThreads) {
-    const int g = e / D, dm = e - g * D;
-    float M = -INFINITY;
+  if constexpr (!PF) {
+    // Decode: a loop over the G heads' elements (few heads: fewer than one
+    // element per thread).
+    for (int e = tid; e < G * D; e += kThreads) {
+      const int g = e / D, dm = e - g * D;
+      float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[(w * 16 + g) * (D + 2)]);
-    float Lsum = 0.0f, Ov = 0.0f;
-    if (M != -INFINITY) {
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[(w * 16 + g) * (D + 2)]);
+      float Lsum = 0.0f, Ov = 0.0f;
+      if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float *c = comb + (w * 16 + g) * (D + 2);
-        if (c[0] == -INFINITY) continue;
-        const float wt = exp2f(c[0] - M);
-        Lsum = __builtin_fmaf(c[1], wt, Lsum);
-        Ov = __builtin_fmaf(c[2 + dm], wt, Ov);
+        for (int w = 0; w < kWaves; ++w) {
+          const float *c = comb + (w * 16 + g) * (D + 2);
+          if (c[0] == -INFINITY) continue;
+          const float wt = exp2f(c[0] - M);
+          Lsum = __builtin_fmaf(c[1], wt, Lsum);
+          Ov = __builtin_fmaf(c[2 + dm], wt, Ov);
+        }
+      }
+      const int64_t head = (int64_t)qrow * Hq + hq0 + g;
+      if (S == 1) {
+        p.out[head * D + dm] = Ov / Lsum;
+        if (dm == 0 && p.stats) {
+          p.stats[head * 2] = M * kLn2;
+          p.stats[head * 2 + 1] = Lsum;
+        }
+      } else {
+        // Device-coherent (write-through) stores: the merging workgroup may run
+        // on another XCD, whose L2 does not see this one's.
+        float *pp = p.part + (head * S + split) * (D + 2);
+        coherent_store(pp + 2 + dm, Ov);
+        if (dm == 0) {
+          coherent_store(pp, M);
+          coherent_store(pp + 1, Lsum);
+        }
       }
     }
-    const int64_t head = (int64_t)qrow * Hq + hq0 + g;
-    if (S == 1) {
-      p.out[head * D + dm] = Ov / Lsum;
-      if (dm == 0 && p.stats) {
-        p.stats[head * 2] = M * kLn2;
-        p.stats[head * 2 + 1] = Lsum;
+  } else {
+    // Row-wise prefill: the four waves' states of each column merged by
+    // log-sum-exp. Every LDS
+    // read of a thread's elements (column g, dimension dm) is issued before
+    // any of them is used (columns past ncol read column 0's and store
+    // nothing), and the waves without tokens (m = -inf) drop out through
+    // selects: reads under a per-wave test would each be an LDS round trip of
+    // their own.
+    constexpr int EPT = UC * D / kThreads;  // elements per thread
+    float mw[EPT][kWaves], lw[EPT][kWaves], ow[EPT][kWaves];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * kThreads;
+      const int g = e / D, dm = e - g * D;
+      const int gr = g < ncol ? g : 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float *c = comb + (w * 16 + gr) * (D + 2);
+        mw[k][w] = c[0];
+        lw[k][w] = c[1];
+        ow[k][w] = c[2 + dm];
       }
-    } else {
-      // Device-coherent (write-through) stores: the merging workgroup may run
-      // on another XCD, whose L2 does not see this one's.
-      float *pp = p.part + (head * S + split) * (D + 2);
-      coherent_store(pp + 2 + dm, Ov);
-      if (dm == 0) {
-        coherent_store(pp, M);
-        coherent_store(pp + 1, Lsum);
+    }
+    // Partial rows: o[D], then m, l (16-byte aligned rows of D + 4 floats).
+    constexpr int PROW = D + 4;
+    float Mk[EPT], Lk[EPT], Ok[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mw[k][w]);
+      float Lsum = 0.0f, Ov = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const bool live = mw[k][w] != -INFINITY;
+        const float wt = exp2f(mw[k][w] - M);
+        Lsum = live ? __builtin_fmaf(lw[k][w], wt, Lsum) : Lsum;
+        Ov = live ? __builtin_fmaf(ow[k][w], wt, Ov) : Ov;
+      }
+      Mk[k] = M;
+      Lk[k] = Lsum;
+      Ok[k] = Ov;
+    }
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * kThreads;
+      const int g = e / D, dm = e - g * D;
+      const float M = Mk[k], Lsum = Lk[k], Ov = Ok[k];
+      if (g >= ncol) continue;
+      const int64_t head = out_row(g);
+      if (S == 1) {
+        p.out[head * D + dm] = Ov / Lsum;
+      } else {
+        // Device-coherent (write-through) stores, as above.
+        float *pp = p.part + ((pbase + g) * S + split) * PROW;
+        coherent_store(pp + dm, Ov);
+        if (dm == 0) {
+          coherent_store(pp + D, M);
+          coherent_store(pp + D + 1, Lsum);
+        }
       }
     }
   }
@@ -1134,6 +1354,14 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
             (unsigned)(S - 1);
   __syncthreads();
   if (!*last) return;
+  if (PF) {
+    const MergeRows mr{pbase, (int64_t)b * rows * Hq + hq0, UC * qg, G, Hq, ncol};
+    static_assert(kPrefillMaxSplits == 16, "merge_rows instances");
+    if (S <= 8) merge_rows<D, 8, UC / 4>(p.part, p.out, mr, S, wave, lane);
+    else merge_rows<D, 16, UC / 4>(p.part, p.out, mr, S, wave, lane);
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   if (S <= kMergeOneRound) {
     if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
@@ -1146,14 +1374,14 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // groups of eight splits.
   float *wgt = reinterpret_cast<float *>(smem);  // [16 heads][S] (reuses the ring)
   float *mrow = wgt + 16 * S;                     // [16 heads][S] split maxima
-  for (int e = tid; e < G * S; e += kThreads) {
+  for (int e = tid; e < ncol * S; e += kThreads) {
     const int g = e / S, s = e - g * S;
-    float *pp = p.part + (((int64_t)qrow * Hq + hq0 + g) * S + s) * (D + 2);
+    float *pp = p.part + ((pbase + g) * S + s) * (D + 2);
     mrow[g * S + s] = coherent_load(pp);
     wgt[g * S + s] = coherent_load(pp + 1);
   }
   __syncthreads();
-  if (tid < G) {
+  if (tid < ncol) {
     float M = -INFINITY;
     for (int s = 0; s < S; ++s) M = fmaxf(M, mrow[tid * S + s]);
     float Lsum = 0.0f;
@@ -1165,16 +1393,16 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     }
     for (int s = 0; s < S; ++s) wgt[tid * S + s] = mrow[tid * S + s] / Lsum;
     if (p.stats) {
-      const int64_t head = (int64_t)qrow * Hq + hq0 + tid;
+      const int64_t head = out_row(tid);
       p.stats[head * 2] = M * kLn2;
       p.stats[head * 2 + 1] = Lsum;
     }
   }
   __syncthreads();
-  for (int e = tid; e < G * D; e += kThreads) {
+  for (int e = tid; e < ncol * D; e += kThreads) {
     const int g = e / D, dm = e - g * D;
-    const int64_t head = (int64_t)qrow * Hq + hq0 + g;
-    float *pp = p.part + head * S * (D + 2) + 2 + dm;
+    const int64_t head = out_row(g);
+    float *pp = p.part + (pbase + g) * S * (D + 2) + 2 + dm;
     float Ov = 0.0f;
     for (int s0 = 0; s0 < S; s0 += 8) {
       // Unconditional loads (past S: split S - 1, weighted zero), all eight in
@@ -1194,19 +1422,29 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int KF, int NN, int SG, int PK = 0>
-hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
+template <int D, int KF, int NN, int SG, int PK, int PF>
+hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
-  static const hipError_t allowed = hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN>::DYN);
+  static const hipError_t allowed = hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                        Slot<D, KF, NN>::DYN);
   if (allowed != hipSuccess) {
     (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
     return allowed;
   }
   constexpr int lds = Slot<D, KF, NN>::DYN;
-  dim3 grid((unsigned)p.splits, (unsigned)p.kv_heads, (unsigned)(p.batch * (p.starts ? p.rows : 1)));
-  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK>), grid, dim3(kThreads), lds, stream, p, fl);
+  const dim3 grid = PF ? dim3((unsigned)p.kv_heads, (unsigned)(p.batch * p.qgroups), (unsigned)p.splits)
+                       : dim3((unsigned)p.splits, (unsigned)p.kv_heads, (unsigned)p.batch);
+  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF>), grid, dim3(kThreads), lds, stream, p, fl);
   return hipGetLastError();
+}
+
+// Row-wise prefill (p.starts set) runs the PF variant of its unit width.
+template <int D, int KF, int NN, int SG, int PK = 0>
+hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
+  if (!p.starts) return launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream);
+  return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8>(p, fl, stream)
+                          : launch_mode<D, KF, NN, SG, PK, 16>(p, fl, stream);
 }
 
 }  // namespace

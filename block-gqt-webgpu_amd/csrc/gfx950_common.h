@@ -151,6 +151,15 @@ __device__ __forceinline__ void coherent_store(float *ptr, float v) {
 __device__ __forceinline__ float coherent_load(float *ptr) {
   return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16- and 8-byte loads at the same level (cache policy sc1), through a
+// buffer resource: off is a byte offset inside its range.
+constexpr int kPolicySc1 = 16;
+__device__ __forceinline__ f32x4 coherent_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kPolicySc1));
+}
+__device__ __forceinline__ u32x2 coherent_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kPolicySc1));
+}
 
 // Waits for all but the newest N vector-memory operations of this wave. The
 // LDS writes of buffer_load ... lds are not tracked by the compiler, so ring

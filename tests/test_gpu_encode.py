@@ -358,3 +358,59 @@ def test_job_table_batches_and_stream_switch(device, oracle):
         device.set_stream(None)
         torch.cuda.synchronize()
         tables.destroy()
+
+
+def test_concurrent_appends_near_capacity(device, oracle):
+    """Two threads append at once near the end of a store's capacity (the Node addon runs appends off
+    the JS thread). The store is claimed before the capacity check, as the reference refuses a second
+    append while one is in flight (src/runtime/packed-keys.ts:40-49): each append either completes or
+    is refused ("Concurrent K appends unsupported" while the other runs, "K capacity exceeded" after
+    it committed), never both complete, the length counts the completed rows, and the committed rows
+    are the oracle's encode of the base rows and the winning append."""
+    import threading
+    import bgtq
+    from bgtq import calibrate
+    p = calibrate.layout_b(64)
+    ol = _olayout(oracle, p)
+    rng = np.random.default_rng(77)
+    cap, base_rows, add = 96, 80, 12
+    outcomes = set()
+    for trial in range(24):
+        keys = bgtq.PackedKeys.create(device, p, cap)
+        try:
+            base = _random_half_rows(rng, base_rows, 64)
+            keys.append(base)
+            batches = [_random_half_rows(rng, add, 64) for _ in range(2)]
+            results = [None, None]
+            gate = threading.Barrier(2)
+
+            def run(i):
+                gate.wait()
+                try:
+                    keys.append(batches[i])
+                    results[i] = "ok"
+                except (bgtq.StateError, bgtq.RangeError) as e:
+                    results[i] = str(e)
+
+            threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+            for t in threads:
+                t.start()
+            for t in threads:
+                t.join()
+            assert results.count("ok") == 1, results
+            for r in results:
+                assert r in ("ok", "Concurrent K appends unsupported", "K capacity exceeded"), r
+            outcomes.add(tuple(sorted(results)))
+            winner = results.index("ok")
+            assert keys.length == base_rows + add
+            rows = base_rows + add
+            ref_p, ref_n = oracle.encode_pack(ol, np.concatenate([base, batches[winner]]))
+            packed, norms = keys.read()
+            np.testing.assert_array_equal(packed[: rows * p.rowBytes].reshape(rows, -1), ref_p)
+            np.testing.assert_array_equal(norms[: rows * p.normStride].reshape(rows, -1), ref_n)
+            assert not packed[rows * p.rowBytes:].any(), "rows past the length were written"
+            with pytest.raises(bgtq.RangeError, match="K capacity exceeded"):
+                keys.append(batches[1 - winner])
+        finally:
+            keys.destroy()
+    print("outcomes", sorted(outcomes), flush=True)

@@ -307,7 +307,8 @@ def test_rejections(device):
 def test_workspace_shared_across_paths(device, oracle):
     """One workspace for a tiled chunk (64 rows), then row-wise chunks (32, 7 rows) of other geometry:
     the split counters at the workspace's start stay zero after every call and each output matches
-    the oracle."""
+    the oracle. Starts past max_length - rows clamp to it on both paths (the chunk then ends at
+    max_length)."""
     import torch
     from bgtq import batched, calibrate
     p = calibrate.layout_b(64)
@@ -315,7 +316,8 @@ def test_workspace_shared_across_paths(device, oracle):
     try:
         ws = torch.zeros(32 << 20, dtype=torch.uint8, device="cuda")
         counter_words = 65536  # BGTQ_PREFILL_COUNTER_BYTES / 4
-        for rows, hq, starts in ((64, 14, [300, 611]), (32, 14, [0, 668]), (7, 6, [693, 250])):
+        for rows, hq, starts in ((64, 14, [300, 611]), (32, 14, [0, 668]), (7, 6, [693, 250]),
+                                 (64, 14, [690, 5]), (32, 14, [699, 40]), (5, 6, [1000, 695])):
             g = torch.Generator().manual_seed(rows)
             q = torch.randn((2, rows, hq, 64), generator=g)
             out = torch.full((2, rows, hq, 64), float("nan"), device="cuda")
@@ -329,9 +331,10 @@ def test_workspace_shared_across_paths(device, oracle):
             assert not ws[:4 * counter_words].any(), "split counters left nonzero"
             got = out.cpu().numpy()
             G = hq // 2
+            eff = [min(s, 700 - rows) for s in starts]
             for b in range(2):
                 for h in range(2):
-                    ref = _reference(oracle, cache, q, starts, b, h, G)
+                    ref = _reference(oracle, cache, q, eff, b, h, G)
                     _check(got[b, :, h * G:(h + 1) * G], ref.astype(np.float64), f"rows {rows} b{b} kv{h}")
     finally:
         cache.destroy()
