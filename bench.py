@@ -48,6 +48,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def rope(torch, x, positions, base):
+    """Split-half RoPE as the reference's model applies it (pairs (i, i + d/2), angle
+    pos * base^(-2i/d); vendor/blockgtq-calibration/rope_utils.py:10-20): x [..., T, d] FP32,
+    positions [T]; angles in FP64, rotation in FP32."""
+    d = x.shape[-1]
+    half = d // 2
+    inv = 1.0 / (base ** (torch.arange(0, d, 2, device=x.device, dtype=torch.float64) / d))
+    ang = positions.to(device=x.device, dtype=torch.float64)[:, None] * inv[None, :]
+    c, sn = torch.cos(ang).float(), torch.sin(ang).float()
+    x1, x2 = x[..., :half], x[..., half:]
+    return torch.cat([x1 * c - x2 * sn, x2 * c + x1 * sn], dim=-1)
+
+
+def pair_energy(torch, dim, ratio=0.9, device="cuda"):
+    """Per-dimension scale sqrt(ratio^i) of frequency pair i (dims i and i + d/2): post-RoPE K
+    whose pair energies decay geometrically."""
+    i = torch.arange(dim, device=device) % (dim // 2)
+    return (ratio ** i.double()).sqrt().float()
+
+
 def layout_params(name, dim):
     from bgtq import calibrate
     if name == "S":
@@ -76,7 +96,7 @@ class DecodeWorkload:
     """All layers' caches for one decode shape, plus per-layer descriptors."""
 
     def __init__(self, dev, layout="B", layers=LAYERS, batch=BATCH, ctx=CTX, hq=HQ, hkv=HKV, dim=DIM, seed=0,
-                 key_format="packed", splits=0):
+                 key_format="packed", splits=0, rope_base=None):
         import torch
         import bgtq
         from bgtq import batched
@@ -92,10 +112,15 @@ class DecodeWorkload:
         self.lengths = torch.full((batch,), ctx, dtype=torch.int32, device="cuda")
         self.out = torch.empty((batch, hq, dim), dtype=torch.float32, device="cuda")
         ws = None
+        pos = torch.arange(ctx, device="cuda")
         for layer in range(layers):
             q = torch.randn((batch, hq, dim), generator=g, device="cuda", dtype=torch.float32)
             v = torch.randn((batch, hkv, ctx, dim), generator=g, device="cuda", dtype=torch.float32).half()
-            k = torch.randn((batch, hkv, ctx, dim), generator=g, device="cuda", dtype=torch.float32).half()
+            k = torch.randn((batch, hkv, ctx, dim), generator=g, device="cuda", dtype=torch.float32)
+            if rope_base:  # keys at positions 0..ctx-1, the query at the last one
+                k = rope(torch, k, pos, rope_base)
+                q = rope(torch, q.unsqueeze(-2), pos[-1:], rope_base).squeeze(-2).contiguous()
+            k = k.half()
             if key_format == "packed":
                 hp = smollm2_heads(layer, hkv) if layout == "S" else [p] * hkv
                 tabs = [bgtq.Tables(dev, x) for x in hp]  # one table set per (layer, KV head)
@@ -200,28 +225,54 @@ def time_eager(torch, fn, steps, warmup):
     return a.elapsed_time(b) / steps
 
 
+class EncodeWorkload:
+    """Prefill K encode at SmolLM2 geometry: 4096 tokens x 3 KV heads x 30 layers, d=64, one table set
+    per (layer, KV head), all 90 jobs in one bgtq_encode_batched call."""
+
+    def __init__(self, dev, layout="B", seed=3):
+        import torch
+        import bgtq
+        self.dev, self.p = dev, layout_params(layout, 64)
+        p = self.p
+        self.tabs = [bgtq.Tables(dev, p) for _ in range(90)]
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        # post-RoPE K whose per-pair energy decays geometrically (ratio 0.9)
+        self.k = (torch.randn((30, 4096, 3, 64), generator=g, device="cuda") * pair_energy(torch, 64)).half()
+        self.packed = torch.zeros((90, 4096 * p.rowBytes + 64), dtype=torch.uint8, device="cuda")
+        self.norms = torch.zeros((90, 4096 * p.normStride + 32), dtype=torch.int16, device="cuda")
+        self.jobs = [dict(tables=self.tabs[l * 3 + h], src=self.k[l, :, h], src_row_stride=3 * 64, rows=4096,
+                          packed=self.packed[l * 3 + h], norms=self.norms[l * 3 + h], dst_row0=0)
+                     for l in range(30) for h in range(3)]
+        self.rows = 30 * 3 * 4096
+
+    def call(self):
+        from bgtq import batched
+        batched.encode(self.dev, self.jobs, "f16")
+
+    def destroy(self):
+        for t in self.tabs:
+            t.destroy()
+
+
 def encode_throughput(dev, layout="B", reps=10):
-    """Prefill K encode at SmolLM2 geometry: 4096 tokens x 3 KV heads x 30 layers, d=64."""
+    """The SmolLM2 prefill K encode (EncodeWorkload) as one call replayed in a HIP graph."""
     import torch
-    import bgtq
-    from bgtq import batched
-    p = layout_params(layout, 64)
-    tabs = [bgtq.Tables(dev, p) for _ in range(90)]
-    k = torch.randn((30, 4096, 3, 64), device="cuda").half()
-    packed = torch.empty((90, 4096 * p.rowBytes + 64), dtype=torch.uint8, device="cuda")
-    norms = torch.empty((90, 4096 * p.normStride + 32), dtype=torch.int16, device="cuda")
-    jobs = [dict(tables=tabs[l * 3 + h], src=k[l, :, h], src_row_stride=3 * 64, rows=4096, packed=packed[l * 3 + h],
-                 norms=norms[l * 3 + h], dst_row0=0) for l in range(30) for h in range(3)]
-    call = lambda: batched.encode(dev, jobs, "f16")
-    ms = time_graph(torch, graph_of(torch, dev, call), reps, 5)
-    ms_eager = time_eager(torch, call, reps, 2)
-    rows = 30 * 3 * 4096
-    for t in tabs:
-        t.destroy()
+    w = EncodeWorkload(dev, layout)
+    p = w.p
+    ms = time_graph(torch, graph_of(torch, dev, w.call), reps, 5)
+    ms_eager = time_eager(torch, w.call, reps, 2)
+    rows = w.rows
+    w.destroy()
+    nbytes = rows * (128 + p.rowBytes + 2 * p.normStride)
     return {"rows_per_s": round(rows / (ms / 1e3)), "tokens_per_s": round(4096 / (ms / 1e3)), "ms": round(ms, 4),
-            "gbs_algorithmic": round(rows * (128 + p.rowBytes + 2 * p.normStride) / (ms / 1e3) / 1e9, 1),
+            "gbs_algorithmic": round(nbytes / (ms / 1e3) / 1e9, 1),
             "eager_ms": round(ms_eager, 4),
-            "timing": "one encode call (90 tables) replayed as a HIP graph; eager_ms: issued directly each time"}
+            "timing": "one encode call (90 tables) replayed as a HIP graph; eager_ms: issued directly each time",
+            "data": "FP16 N(0,1) K rows, frequency pair i scaled by sqrt(0.9^i)",
+            "working_set_bytes": nbytes,
+            "residency": "the working set fits the 256 MB Infinity Cache: replays read it from there, not HBM; "
+                         "the line is VALU-bound, not an HBM rate"}
 
 
 class SmolLM2Step:
@@ -318,6 +369,89 @@ def smollm2_decode_step(dev, steps, layout="B", splits=0):
                         f"tokens), d=64, batch 1, layout {layout}, FP16 V; one bgtq_decode_append launch per layer"}
 
 
+class SmolLM2DispatchStep:
+    """The same SmolLM2 decode step (30 layers, 3 KV heads, 9 query heads, 4096 cached tokens + 1,
+    layout B) through the reference decoder's per-layer dispatches (src/model/decoder.ts:46-56 with
+    rows = 1): encode_k per KV head, append of the V row, compressed_dot per KV head, softmax and
+    weighted, each its own pass with the scores and probabilities in device memory
+    (bgtq_model_submit). The dispatch arrays are built once; the timed call queues them."""
+
+    L, HKV, HQ, T, D = 30, 3, 9, 4096, 64
+
+    def __init__(self, dev, seed=0):
+        import torch
+        import bgtq
+        from bgtq import _lib, batched
+        from bgtq.model_ops import _binding
+        L, HKV2, HQ2, T, D = self.L, self.HKV, self.HQ, self.T, self.D
+        cap, gqa = T + 1, HQ2 // HKV2
+        self.dev, self._lib = dev, _lib
+        p = layout_params("B", D)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.tabs = [bgtq.Tables(dev, p) for _ in range(L * HKV2)]
+        self.keep, self.arrays = [], []
+        for l in range(L):
+            codes = [torch.zeros(cap * p.rowBytes, dtype=torch.uint8, device="cuda") for _ in range(HKV2)]
+            norms = [torch.zeros(cap * p.normStride, dtype=torch.int16, device="cuda") for _ in range(HKV2)]
+            hist = torch.randn((HKV2, T, D), generator=g, device="cuda").half()
+            batched.encode(dev, [dict(tables=self.tabs[l * HKV2 + h], src=hist[h], src_row_stride=D, rows=T,
+                                      packed=codes[h], norms=norms[h], dst_row0=0) for h in range(HKV2)], "f16")
+            vcache = torch.randn((HKV2 * cap * D,), generator=g, device="cuda").half().view(torch.int16)
+            kr = torch.randn((HKV2 * D,), generator=g, device="cuda")
+            vv = torch.randn((HKV2 * D,), generator=g, device="cuda")
+            qr = torch.randn((HQ2 * D,), generator=g, device="cuda")
+            scores = torch.empty((HQ2 * cap,), device="cuda")
+            probs = torch.empty((HQ2 * cap,), device="cuda")
+            attn = torch.empty((HQ2 * D,), device="cuda")
+            tabs = self.tabs[l * HKV2:(l + 1) * HKV2]
+            prm = [1, cap, cap, T, HQ2, HKV2, gqa, D]
+            bufs = [qr, None, vcache, scores, probs, attn]
+            disp = [("encode_k", [1, T, h, HKV2], [tabs[h], tabs[h], kr, codes[h], norms[h]], 1, 1) for h in range(HKV2)]
+            disp.append(("append", [1, T, cap, HKV2], [vv, vcache], -(-HKV2 * D // 2 // 128), 1))
+            disp += [("compressed_dot", [1, T, h, cap, HQ2, gqa, D],
+                      [tabs[h], tabs[h], qr, codes[h], norms[h], None, scores], cap, 1) for h in range(HKV2)]
+            disp.append(("softmax", prm, bufs, HQ2, 1))
+            disp.append(("weighted", prm, bufs, HQ2 * D, 1))
+            arr = (_lib.ModelDispatch * len(disp))()
+            for i, (name, params, buffers, x, y) in enumerate(disp):
+                binds = (_lib.Binding * len(buffers))(*[_binding(b) for b in buffers])
+                nm = name.encode()
+                self.keep += [binds, nm]
+                arr[i] = _lib.ModelDispatch(nm, (ctypes.c_uint32 * 8)(*(params + [0] * (8 - len(params)))),
+                                            ctypes.cast(binds, ctypes.POINTER(_lib.Binding)), len(buffers), x, y)
+            self.arrays.append((arr, len(disp)))
+            self.keep += [codes, norms, vcache, kr, vv, qr, scores, probs, attn]
+        self.bytes = L * HKV2 * cap * (p.rowBytes + 2 * p.normStride + 2 * D)
+        torch.cuda.synchronize()
+
+    def step(self):
+        for arr, n in self.arrays:
+            self._lib.check(self._lib.lib().bgtq_model_submit(self.dev.handle, arr, n))
+
+    def destroy(self):
+        for t in self.tabs:
+            t.destroy()
+
+
+def smollm2_dispatch_step(dev, steps):
+    import torch
+    w = SmolLM2DispatchStep(dev)
+    try:
+        ms = time_graph(torch, graph_of(torch, dev, w.step), steps, 3)
+        timing = "HIP graph of the 30 layers' dispatches"
+    except Exception as e:  # a pass the capture refuses: time it issued directly
+        ms = time_eager(torch, w.step, steps, 2)
+        timing = f"issued directly ({type(e).__name__} under graph capture)"
+    out = {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(w.bytes / (ms / 1e3) / 1e9, 1),
+           "timing": timing,
+           "workload": "the SmolLM2 decode step at batch 1 (layout B) through bgtq_model_submit: per layer "
+                       "3 x encode_k, append, 3 x compressed_dot, softmax, weighted (src/model/decoder.ts:46-56), "
+                       "scores and probabilities materialised [9 x 4097] as the reference's passes keep them"}
+    w.destroy()
+    return out
+
+
 def prefill_flops(prompt, hq, dim, layers):
     """Algorithmic causal attention FLOPs of a prompt: QK and PV, 2 * dim each per (query, visible token)."""
     return layers * hq * (prompt * (prompt + 1) // 2) * dim * 4
@@ -365,9 +499,13 @@ class PrefillWorkload:
         self.tabs = [bgtq.Tables(dev, p) for _ in range(layers * HKV)]
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
-        self.k = torch.randn((layers, HKV, prompt, DIM), generator=g, device="cuda").half()
+        # Q/K/V FP16 N(0,1), RoPE base 1e6 on Q and K (Qwen2.5)
+        pos = torch.arange(prompt, device="cuda")
+        self.k = rope(torch, torch.randn((layers, HKV, prompt, DIM), generator=g, device="cuda").half().float(),
+                      pos, 1e6).half()
         self.v = torch.randn((layers, 1, HKV, prompt, DIM), generator=g, device="cuda").half()
-        self.q = torch.randn((layers, prompt, HQ, DIM), generator=g, device="cuda")
+        q = torch.randn((layers, prompt, HQ, DIM), generator=g, device="cuda").half().float()
+        self.q = rope(torch, q.transpose(1, 2), pos, 1e6).transpose(1, 2).contiguous()
         self.out = torch.empty((layers, prompt, HQ, DIM), device="cuda")
         self.packed = torch.empty((layers, 1, HKV, prompt * p.rowBytes), dtype=torch.uint8, device="cuda")
         self.norms = torch.empty((layers, 1, HKV, prompt * p.normStride), dtype=torch.int16, device="cuda")
@@ -427,17 +565,87 @@ def qwen_prefill(dev, steps, layout="B", chunk=0, prompt=4096, layers=LAYERS):
                         + ("one chunk" if w.chunk == prompt else f"chunks of {w.chunk} rows")}
 
 
-def single_head(dev, steps, layout="B"):
-    """One query over T=4096, d=128, one head (the reference's CPU-runnable shape)."""
+def single_head(dev, steps, layout="B", calls=32):
+    """One query over T=4096, d=128, one head (the reference's CPU-runnable shape: Q/K/V N(0,1), RoPE
+    base 1e4 on Q and K), timed as a HIP graph of `calls` launches, each over caches, tables and a
+    query of its own, so the per-call figure is the GPU's and not the rate at which the host replays
+    a one-launch graph. kernel_us: the kernel's own duration from the committed rocprofv3 trace."""
     import torch
-    w = DecodeWorkload(dev, layout, layers=1, batch=1, ctx=4096, hq=1, hkv=1, dim=128)
-    g = graph_of(torch, dev, w.step)
-    ms = time_graph(torch, g, steps * 10, 5)
+    w = DecodeWorkload(dev, layout, layers=calls, batch=1, ctx=4096, hq=1, hkv=1, dim=128, rope_base=1e4)
+    ms = time_graph(torch, graph_of(torch, dev, w.step), steps * 2, 3) / calls
     w.set_q_rotated(True)
-    ms_rot = time_graph(torch, graph_of(torch, dev, w.step), steps * 10, 5)
-    return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(w.bytes_per_layer() / (ms / 1e3) / 1e9, 1),
-            "q_rotated_us_per_step": round(ms_rot * 1e3, 2),
-            "workload": "1 query, T=4096, d=128, one head, layout B, FP16 V"}
+    ms_rot = time_graph(torch, graph_of(torch, dev, w.step), steps * 2, 3) / calls
+    nbytes = w.bytes_per_layer()
+    return {"us_per_step": round(ms * 1e3, 2), "gbs_algorithmic": round(nbytes / (ms / 1e3) / 1e9, 1),
+            "q_rotated_us_per_step": round(ms_rot * 1e3, 2), "launches_per_graph": calls,
+            "kernel_us": read_profile_value("decode_fast_single_head_t4096_d128_trace.txt", "kernel_avg_us"),
+            "kernel_us_source": "profiles/decode_fast_single_head_t4096_d128_trace.txt (rocprofv3 --kernel-trace "
+                                "of bench.py --single-head-only; committed, not measured in this run)",
+            "working_set_bytes": calls * nbytes,
+            "residency": f"{calls} distinct caches of {nbytes} B: beyond the L2s, inside the 256 MB Infinity Cache",
+            "workload": "1 query, T=4096, d=128, one head, layout B, FP16 V, RoPE base 1e4 on Q and K"}
+
+
+# The reference's published phase-4 times (benchmarks/raw/2026-09-15T09-27-00-112Z-phase4-phase4-bench.json,
+# an Intel Gen12LP integrated GPU under WebGPU), microseconds, by (T, d).
+PHASE4_REFERENCE_US = {(512, 64): 196.6, (1024, 64): 262.1, (2048, 64): 524.3, (4096, 64): 917.5,
+                       (512, 128): 327.7, (1024, 128): 720.9, (2048, 128): 1048.6, (4096, 128): 2162.7}
+
+
+def phase4_attention(dev, samples=20, warmup=5):
+    """OptimizedAttention over FP32 Values at the reference's benchmark shapes (benchmarks/phase4.ts:19-47):
+    T in {512, 1024, 2048, 4096} x d in {64, 128}, the mixed_d{d} calibration, 3 queries at (0, T/2, T-1),
+    non-causal, its workload generator (tests/oracles/export_attention.py:20-26). Timed as
+    benchmarks/timing.ts:7-31 times it: GPU timestamps around the attention work of record() (after the
+    queries' upload), 5 warmups, the median of 20 samples."""
+    import numpy as np
+    import torch
+    import bgtq
+    out = {}
+    for d in (64, 128):
+        params = bgtq.BlockGTQParameters.load_mixed_fixture(
+            ROOT / "tests" / "golden" / "reference" / "mixed" / f"mixed_d{d}.json")
+        for T in (512, 1024, 2048, 4096):
+            g = torch.Generator().manual_seed(731 + d + T)
+            q = torch.randn(3, d, generator=g).numpy()
+            k = (torch.randn(T, d, generator=g) * 0.7).half().numpy()
+            v = (torch.randn(T, d, generator=g) * 0.5).numpy()
+            pos = np.array([0, T // 2, T - 1], np.uint32)
+            keys = bgtq.PackedKeys.create(dev, params, T)
+            values = bgtq.Values(dev, d, T)
+            sessions = {"us": bgtq.OptimizedAttention.create(dev, keys, values, 3),
+                        "us_no_intermediates": bgtq.OptimizedAttention.create(dev, keys, values, 3,
+                                                                              materialize=False)}
+            ts = bgtq.Timestamps(dev, 2 * (samples + warmup))
+            try:
+                keys.append(k.view(np.uint16))
+                values.append(v)
+                rec = {}
+                for key, s in sessions.items():
+                    s.setQueries(q, pos, False)
+                    for i in range(samples + warmup):
+                        s.record(ts, 2 * i, 2 * i + 1)
+                    ns = ts.resolve().astype(np.int64)
+                    rec[key] = round(float(np.median((ns[1::2] - ns[0::2])[warmup:])) / 1e3, 2)
+                nbytes = T * (params.rowBytes + 2 * params.normStride + 4 * d)
+                rec["bytes_k_scales_v"] = nbytes
+                rec["gbs_algorithmic"] = round(nbytes / (rec["us"] * 1e3), 2)
+                rec["kernel_us"] = read_profile_value("decode_fast_fp32v_phase4_trace.txt", f"t{T}_d{d}_kernel_us")
+                rec["reference_us_gen12lp"] = PHASE4_REFERENCE_US[(T, d)]
+                out[f"t{T}_d{d}"] = rec
+            finally:
+                ts.destroy()
+                for s in sessions.values():
+                    s.destroy()
+                values.destroy()
+                keys.destroy()
+    out["protocol"] = ("record() with timestamps at begin and end of the attention work (the fused kernel, plus "
+                       "the probabilities pass when intermediates are materialised), 5 warmups, median of 20; "
+                       "FP32 V read by the kernel's FP32-V variant; kernel_us: first kernel start to last kernel end "
+                       "per record() in profiles/decode_fast_fp32v_phase4_trace.txt (rocprofv3 --kernel-trace of "
+                       "bench.py --attention-only; committed, not measured in this run); reference_us_gen12lp: the reference's "
+                       "published phase-4 time on its own hardware, for context only")
+    return out
 
 
 def cpu_model():
@@ -513,6 +721,115 @@ def cpu_baseline(layout="B", budget_s=10.0, threads=None):
     nproc = os.cpu_count() or 1
     threads = threads or min(16, nproc)
     nn, dtn = timed(threads)
+
+    def rate(make, budget, nthreads):
+        """Calls of make(slot)() completed in about `budget` seconds on nthreads threads (each its own
+        inputs); returns (calls, seconds)."""
+        counts = [0] * nthreads
+        fns = [make(i) for i in range(nthreads)]
+        t0 = time.perf_counter()
+
+        def go(i):
+            n = 0
+            while time.perf_counter() < t0 + budget or n == 0:
+                fns[i]()
+                n += 1
+            counts[i] = n
+        ts = [threading.Thread(target=go, args=(i,)) for i in range(nthreads)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join()
+        return sum(counts), time.perf_counter() - t0
+
+    legs = {}
+    leg_s = budget_s / 3
+    # C3: bulk K encode (SmolLM2 rows: FP16 N(0,1), pair i scaled by sqrt(0.9^i)), 4096 rows per call
+    pe = np.sqrt(0.9 ** (np.arange(64) % 32))
+
+    def make_encode(slot):
+        L = olayout(layout_params(layout, 64))
+        k = (np.random.default_rng(500 + slot).standard_normal((4096, 64)) * pe).astype(np.float16).view(np.uint16)
+        return lambda: O.encode_pack(L, k)
+    c3 = {}
+    for nt in (1, threads):
+        calls, dt = rate(make_encode, leg_s, nt)
+        c3["rows_per_s" if nt > 1 else "one_thread_rows_per_s"] = round(calls * 4096 / dt)
+    c3.update({"threads": threads, "ms_per_call_extrapolated": round(368640 / c3["rows_per_s"] * 1e3, 1),
+               "sample": "calls of oracle encode + pack on 4096 rows (d=64, layout " + layout + "), each thread its "
+                         "own rows; ms_per_call: the 368,640-row call at the all-threads rate"})
+    legs["encode_smollm2_prefill"] = c3
+    # C2: one decode step at SmolLM2 geometry (per layer: encode the new token's K for 3 KV heads,
+    # reconstruct each head's 4097 rows, FP32 attention of its 3 query heads); layers spread over threads
+    p64 = layout_params(layout, 64)
+
+    def make_layer(slot):
+        L = olayout(p64)
+        rng = np.random.default_rng(700 + slot)
+        hist = [O.encode_pack(L, rng.standard_normal((4096, 64)).astype(np.float16).view(np.uint16)) for _ in range(3)]
+        knew = [rng.standard_normal((1, 64)).astype(np.float16).view(np.uint16) for _ in range(3)]
+        v = [rng.standard_normal((4097, 64)).astype(np.float16).astype(np.float32) for _ in range(3)]
+        q = [rng.standard_normal((3, 64)).astype(np.float32) for _ in range(3)]
+        pos = np.full(3, 4096, np.uint32)
+
+        def run():
+            for h in range(3):
+                pk, nm = O.encode_pack(L, knew[h])
+                packed = np.concatenate([hist[h][0], pk])
+                scales = np.concatenate([hist[h][1], nm]).view(np.float16).astype(np.float32)
+                keff = O.reconstruct(L, O.unpack(packed, 64, p64.nibbleDims), scales)
+                O.attention(q[h], keff, v[h], pos, False, fp32=True)
+        return run
+    c2 = {}
+    for nt in (1, threads):
+        calls, dt = rate(make_layer, leg_s, nt)
+        c2["us_per_step" if nt > 1 else "one_thread_us_per_step"] = round(30 * dt / calls * 1e6, 1)
+    c2.update({"threads": threads, "sample": "SmolLM2 decode-step layers (encode 1 token x 3 KV heads, reconstruct "
+                                              "4097 rows per head, FP32 attention of 3 query heads each); "
+                                              "us_per_step: 30 layers at the measured layer rate"})
+    legs["smollm2_decode_step_b1"] = c2
+    # C4: the Qwen prompt's causal attention on sampled query rows (7 heads of one KV head over the
+    # row's prefix of a reconstructed 4096-token history, RoPE base 1e6 keys), as FLOP/s
+    pq = layout_params(layout, DIM)
+
+    def make_rows(slot):
+        L = olayout(pq)
+        rng = np.random.default_rng(900 + slot)
+        ang = np.arange(4096)[:, None] * (1.0 / (1e6 ** (np.arange(0, DIM, 2) / DIM)))[None, :]
+        x = rng.standard_normal((4096, DIM)).astype(np.float16).astype(np.float32)
+        x1, x2 = x[:, :DIM // 2], x[:, DIM // 2:]
+        kr = np.concatenate([x1 * np.cos(ang) - x2 * np.sin(ang), x2 * np.cos(ang) + x1 * np.sin(ang)], 1)
+        packed, norms = O.encode_pack(L, kr.astype(np.float16).view(np.uint16))
+        keff = O.reconstruct(L, O.unpack(packed, DIM, pq.nibbleDims), norms.view(np.float16).astype(np.float32))
+        v = rng.standard_normal((4096, DIM)).astype(np.float16).astype(np.float32)
+        rows = rng.integers(0, 4096, size=64)
+        qs = [rng.standard_normal((HQ // HKV, DIM)).astype(np.float32) for _ in rows]
+        state = {"i": 0, "flops": 0}
+
+        def run():
+            r = int(rows[state["i"] % len(rows)])
+            O.attention(qs[state["i"] % len(rows)], keff[:r + 1], v[:r + 1], np.full(HQ // HKV, r, np.uint32),
+                        True, fp32=True)
+            state["i"] += 1
+            state["flops"] += (HQ // HKV) * (r + 1) * DIM * 4
+        run.state = state
+        return run
+    c4 = {}
+    for nt in (1, threads):
+        fns = []
+
+        def mk(slot):
+            f = make_rows(slot)
+            fns.append(f)
+            return f
+        calls, dt = rate(mk, leg_s, nt)
+        gflops = sum(f.state["flops"] for f in fns) / dt / 1e9
+        c4["gflop_per_s" if nt > 1 else "one_thread_gflop_per_s"] = round(gflops, 2)
+    c4.update({"threads": threads,
+               "ms_per_prompt_extrapolated": round(prefill_flops(4096, HQ, DIM, LAYERS) / (c4["gflop_per_s"] * 1e9) * 1e3, 1),
+               "sample": "causal FP32 attention rows (7 query heads of one KV head over a random row's prefix of a "
+                         "reconstructed 4096-token layout-B history); the prompt's 721.7 GFLOP at that rate"})
+    legs["qwen_prefill_4096"] = c4
     # the single-head shape, one thread
     ph = calibrate_layout_b(128) if layout != "S" else None
     c1 = None
@@ -531,7 +848,7 @@ def cpu_baseline(layout="B", budget_s=10.0, threads=None):
             "one_thread_value": round(n1 * unit_bytes / dt1 / 1e9, 4), "nproc": nproc, "cpu_model": cpu_model(),
             "build": "oracle/bgtq_oracle.c, gcc -O3 -march=native -ffp-contract=off -fno-fast-math, built on this host",
             "arithmetic": "fp32 (attention), fp32 FMA chains (reconstruct)",
-            "single_head_t4096_d128": c1,
+            "single_head_t4096_d128": c1, "legs": legs,
             "sample": f"(sequence, KV head) units of {CTX} tokens x {HQ // HKV} query heads, d={DIM}: oracle "
                       f"unpack + reconstruct + FP32 attention; {nn} units on {threads} threads in {dtn:.1f} s "
                       f"({n1} units on one thread in {dt1:.1f} s)"}
@@ -540,6 +857,16 @@ def cpu_baseline(layout="B", budget_s=10.0, threads=None):
 def calibrate_layout_b(dim):
     from bgtq import calibrate
     return calibrate.layout_b(dim)
+
+
+def read_profile_value(name, key):
+    """A number recorded in a committed profile summary under profiles/, if present."""
+    f = ROOT / "profiles" / name
+    if f.exists():
+        m = re.search(re.escape(key) + r":\s*([0-9.]+)", f.read_text())
+        if m:
+            return float(m.group(1))
+    return None
 
 
 def read_traffic():
@@ -569,7 +896,14 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="only the Qwen prompt-prefill measurements")
     ap.add_argument("--encode-only", action="store_true", help="only the SmolLM2 bulk K-encode measurement")
     ap.add_argument("--smollm2-step-only", action="store_true", help="only the SmolLM2 batch-1 decode step")
+    ap.add_argument("--single-head-only", action="store_true", help="only the single-head T=4096 d=128 line")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the FP32-V attention sessions at the reference's phase-4 benchmark shapes")
+    ap.add_argument("--dispatch-step-only", action="store_true",
+                    help="only the SmolLM2 decode step through the model dispatch protocol")
     ap.add_argument("--prefill-chunks", default="0,32", help="with --prefill-only: chunk sizes (0 = whole prompt)")
+    ap.add_argument("--prefill-layers", type=int, default=LAYERS,
+                    help="with --prefill-only: layers of the prompt (fewer for counter passes of a profiler)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (HBM counter calibration)")
     a = ap.parse_args()
@@ -598,11 +932,20 @@ def main():
             print(json.dumps({"splits": sp, "smollm2_decode_step_b1": smollm2_decode_step(dev, a.steps, a.layout, sp)}),
                   flush=True)
         return
+    if a.dispatch_step_only:
+        print(json.dumps({"smollm2_decode_step_b1_dispatch_path": smollm2_dispatch_step(dev, a.steps)}))
+        return
+    if a.attention_only:
+        print(json.dumps({"phase4_attention_fp32v": phase4_attention(dev)}))
+        return
+    if a.single_head_only:
+        print(json.dumps({"single_head_t4096_d128": single_head(dev, a.steps, a.layout)}))
+        return
     if a.prefill_only:
         out = {}
         for c in [int(x) for x in a.prefill_chunks.split(",")]:
-            out["qwen_prefill_4096" + (f"_chunk{c}" if c else "")] = qwen_prefill(dev, a.steps if not c else 2,
-                                                                                 a.layout, chunk=c)
+            out["qwen_prefill_4096" + (f"_chunk{c}" if c else "")] = qwen_prefill(
+                dev, a.steps if not c else 2, a.layout, chunk=c, layers=a.prefill_layers)
         print(json.dumps(out))
         return
     log("building workload ...")
@@ -646,9 +989,19 @@ def main():
         extra["encode_smollm2_prefill"] = encode_throughput(dev, a.layout)
         log("SmolLM2 decode step ...")
         extra["smollm2_decode_step_b1"] = smollm2_decode_step(dev, a.steps, a.layout)
+        extra["smollm2_decode_step_b1"]["working_set_bytes"] = SmolLM2Step.L * SmolLM2Step.HKV * (
+            SmolLM2Step.T + 1) * (layout_params(a.layout, 64).rowBytes + 2 * layout_params(a.layout, 64).normStride + 128)
+        extra["smollm2_decode_step_b1"]["residency"] = ("the step's caches fit the 256 MB Infinity Cache: replays read "
+                                                        "them from there; the step is a chain of 30 latency-bound "
+                                                        "launches, not an HBM rate")
+        if a.layout == "B":
+            log("SmolLM2 decode step through the model dispatch protocol ...")
+            extra["smollm2_decode_step_b1_dispatch_path"] = smollm2_dispatch_step(dev, a.steps)
         log("single head ...")
         # layout S exists at d=64 only (the SmolLM2 calibration)
         extra["single_head_t4096_d128"] = single_head(dev, a.steps, a.layout) if a.layout != "S" else None
+        log("FP32-V attention sessions at the phase-4 shapes ...")
+        extra["phase4_attention_fp32v"] = phase4_attention(dev)
         log("Qwen prefill, one chunk ...")
         extra["qwen_prefill_4096"] = qwen_prefill(dev, max(2, a.steps // 2), a.layout)
         log("Qwen prefill, chunks of 32 ...")

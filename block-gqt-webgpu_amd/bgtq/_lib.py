@@ -107,6 +107,10 @@ SIGNATURES = {
     "bgtq_context_synchronize": (_I32, [_VP]),
     "bgtq_context_stream": (_VP, [_VP]),
     "bgtq_context_set_stream": (_I32, [_VP, _VP]),
+    "bgtq_timestamps_create": (_I32, [_VP, _U32, _PP]),
+    "bgtq_timestamps_write": (_I32, [_VP, _U32]),
+    "bgtq_timestamps_resolve": (_I32, [_VP, _U32, _U32, ctypes.POINTER(ctypes.c_uint64)]),
+    "bgtq_timestamps_destroy": (None, [_VP]),
     "bgtq_tables_create": (_I32, [_VP, _VP, _SZ, _VP, _SZ, _PP]),
     "bgtq_tables_info_get": (_I32, [_VP, ctypes.POINTER(TablesInfo)]),
     "bgtq_tables_destroy": (None, [_VP]),
@@ -132,6 +136,7 @@ SIGNATURES = {
     "bgtq_attention_create": (_I32, [_VP, _VP, _U32, _I32, _PP]),
     "bgtq_attention_set_queries": (_I32, [_VP, _VP, _SZ, _VP, _SZ, _I32]),
     "bgtq_attention_record": (_I32, [_VP]),
+    "bgtq_attention_record_timed": (_I32, [_VP, _VP, _U32, _U32]),
     "bgtq_attention_attend": (_I32, [_VP, _VP, _SZ, _VP, _SZ, _I32]),
     "bgtq_attention_read": (_I32, [_VP, _I32, _VP, _SZ]),
     "bgtq_attention_queries": (_U32, [_VP]),

@@ -35,8 +35,15 @@ class _Session:
         pa = np.ascontiguousarray(np.asarray(positions, dtype=np.uint32).reshape(-1))
         check(lib().bgtq_attention_set_queries(self.handle, ptr(qa), qa.size, ptr(pa), pa.size, int(bool(causal))))
 
-    def record(self) -> None:
-        check(lib().bgtq_attention_record(self.handle))
+    def record(self, timestamps=None, begin_index: int = 0, end_index: int = 1) -> None:
+        """record(encoder, timestamps?) (src/attention/attention.ts:44-58): with
+        a Timestamps set, begin_index is written right before the attention
+        work and end_index right after it."""
+        if timestamps is None:
+            check(lib().bgtq_attention_record(self.handle))
+        else:
+            check(lib().bgtq_attention_record_timed(self.handle, timestamps.handle, int(begin_index),
+                                                    int(end_index)))
 
     def attend(self, q, positions, causal: bool = False) -> np.ndarray:
         """Run attention and return the output [queries, dim] (the GPUBuffer's contents)."""

@@ -43,6 +43,28 @@ class BlockGTQParameters:
                    centroids=a["centroids"], offsets=a["lut_offsets"], inverseScales=a["lut_inv_scales"])
 
     @classmethod
+    def load_mixed_fixture(cls, path):
+        """A calibration fixture file (JSON manifest plus its little-endian
+        payload, tests/webgpu/fixture.ts) read into parameters: loadFixture
+        and the mapping of tests/webgpu/attention-fixture.ts:6-13."""
+        import hashlib
+        import json
+        from pathlib import Path
+        path = Path(path)
+        meta = json.loads(path.read_text(encoding="utf-8"))
+        if meta.get("endianness") != "little":
+            raise RangeError("Unsupported fixture format")
+        payload = path.with_name(meta["binary"]).read_bytes()
+        if len(payload) != meta["byte_length"] or hashlib.sha256(payload).hexdigest() != meta["sha256"]:
+            raise RangeError("Fixture payload length/hash mismatch")
+        kinds = {"f32": "<f4", "u32": "<u4", "u8": "u1", "f16": "<f2", "u16": "<u2"}
+        arrays = {}
+        for name, d in meta["arrays"].items():
+            dt = np.dtype(kinds[d["dtype"]])
+            arrays[name] = np.frombuffer(payload, dt, d["nbytes"] // dt.itemsize, d["offset"]).reshape(d["shape"])
+        return cls.from_mixed_fixture(meta, arrays)
+
+    @classmethod
     def from_serialized(cls, integer, floating):
         """Inverse of tables(): read a model calibration blob (config, table)."""
         c = np.asarray(integer, dtype=np.int64)

@@ -38,6 +38,32 @@ class Device:
             self.handle = None
 
 
+class Timestamps:
+    """A timestamp query set (device.createQuerySet({type: "timestamp", count}),
+    benchmarks/timing.ts:13-20): write(i) marks the time the work queued
+    before it on the device's stream completed; resolve() gives nanoseconds."""
+
+    def __init__(self, device: Device, count: int):
+        h = ctypes.c_void_p()
+        check(lib().bgtq_timestamps_create(device.handle, int(count), ctypes.byref(h)))
+        self.handle, self.count = h, int(count)
+
+    def write(self, index: int) -> None:
+        check(lib().bgtq_timestamps_write(self.handle, int(index)))
+
+    def resolve(self, first: int = 0, count: int | None = None) -> np.ndarray:
+        n = self.count - first if count is None else int(count)
+        out = np.zeros(n, np.uint64)
+        check(lib().bgtq_timestamps_resolve(self.handle, int(first), n,
+                                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))))
+        return out
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().bgtq_timestamps_destroy(self.handle)
+            self.handle = None
+
+
 class Tables:
     """Validated calibration tables resident on the device (tables(p))."""
 

@@ -199,6 +199,10 @@ struct bgtq_values {
   uint32_t dim = 0, capacity = 0, length = 0;
   int32_t dtype = BGTQ_DTYPE_F32;
   DeviceBuffer buf;
+  // FP32 V: every appended |v| < 65504, so the fused kernel can split each
+  // value into FP16 parts; a larger value sends the store to the general
+  // kernels.
+  bool fp16_range = true;
   Ledger ledger;
 };
 
@@ -220,7 +224,7 @@ struct bgtq_attention {
 extern "C" {
 
 const char *bgtq_last_error(void) { return g_error.c_str(); }
-int32_t bgtq_abi_version(void) { return 4; }
+int32_t bgtq_abi_version(void) { return 5; }
 
 // ---------------------------------------------------------------- context
 bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
@@ -836,6 +840,8 @@ bgtq_status bgtq_values_append(bgtq_values *v, const float *values, size_t n) {
     HIP_TRY(hipMemcpy(static_cast<float *>(v->buf.ptr) + (size_t)v->length * v->dim, values, n * 4,
                       hipMemcpyHostToDevice),
             "V upload");
+    for (size_t i = 0; i < n; ++i)
+      if (std::fabs(values[i]) >= 65504.0f) v->fp16_range = false;
   } else {
     std::vector<uint16_t> h(n);
     for (size_t i = 0; i < n; ++i) h[i] = f32_to_f16(values[i]);
@@ -1041,12 +1047,22 @@ bgtq_status bgtq_decode_workspace_size(const bgtq_decode_desc *d, size_t *bytes)
   return BGTQ_OK;
 }
 
+// Whether the fused kernel reads p's V: FP16 rows, or FP32 rows known to
+// lie within FP16's range in a decode without an appended token; 16-byte
+// aligned base and strides.
+static bool fused_v(const DecodeParams &p) {
+  const bool f32 = p.v_dtype == BGTQ_DTYPE_F32;
+  if (f32 ? !p.v_f32_split || p.k_new || p.starts : p.v_dtype != BGTQ_DTYPE_F16) return false;
+  const int64_t vb = f32 ? 4 : 2;
+  return (reinterpret_cast<uintptr_t>(p.v) & 15) == 0 && (p.v_seq_stride * vb) % 16 == 0 &&
+         (p.v_head_stride * vb) % 16 == 0;
+}
+
 // Whether the fused matrix-core kernel handles this launch (FastLayout in
 // bgtq_internal.h); on success fills the K-step books, nn and sg.
 static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables, FastLayout *fl, int *nn, int *sg) {
   auto a16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-  if (p.v_dtype != BGTQ_DTYPE_F16 || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
-  if (!a16(p.v) || (p.v_seq_stride * 2) % 16 || (p.v_head_stride * 2) % 16) return false;
+  if (!fused_v(p) || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
   const int ks = p.dim / 32;
   if (p.key_format == 0) {
     *nn = 0;
@@ -1100,8 +1116,7 @@ static bool fast_layout(const DecodeParams &p, const bgtq_tables *const *tables,
 // fields of fl.
 static bool general_layout(const DecodeParams &p, const bgtq_tables *const *tables, FastLayout *fl) {
   auto a16 = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-  if (p.key_format != 1 || p.v_dtype != BGTQ_DTYPE_F16 || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
-  if (!a16(p.v) || (p.v_seq_stride * 2) % 16 || (p.v_head_stride * 2) % 16) return false;
+  if (p.key_format != 1 || !fused_v(p) || (p.dim != 64 && p.dim != 128) || p.G > 16) return false;
   if (!a16(p.packed) || p.packed_seq_stride % 16 || p.packed_head_stride % 16) return false;
   if (!a16(p.norms) || (p.norms_seq_stride * 2) % 16 || (p.norms_head_stride * 2) % 16) return false;
   for (int h = 0; h < p.kv_heads; ++h) {
@@ -1579,7 +1594,9 @@ bgtq_status bgtq_attention_set_queries(bgtq_attention *a, const float *q, size_t
   return BGTQ_OK;
 }
 
-bgtq_status bgtq_attention_record(bgtq_attention *a) {
+// record(), with timestamps ts[i0] and ts[i1] (ts may be null) written on the
+// stream right around the attention passes, after the queries' upload.
+static bgtq_status attention_record(bgtq_attention *a, bgtq_timestamps *ts, uint32_t i0, uint32_t i1) {
   if (!a) return fail(BGTQ_ERR_RANGE, "null attention");
   bgtq_keys *k = a->keys;
   bgtq_values *v = a->values;
@@ -1615,6 +1632,7 @@ bgtq_status bgtq_attention_record(bgtq_attention *a) {
   }
   p.v = v->buf.ptr;
   p.v_dtype = v->dtype;
+  p.v_f32_split = v->dtype == BGTQ_DTYPE_F32 && v->fp16_range;
   p.qr = static_cast<float *>(a->qr.ptr);
   p.lengths = static_cast<const uint32_t *>(a->small.ptr);
   p.max_length = (int32_t)T;
@@ -1634,7 +1652,22 @@ bgtq_status bgtq_attention_record(bgtq_attention *a) {
     p.logit_stride = T;  // inspect() buffers are [queries x tokens]
   }
   const bgtq_tables *tabs[1] = {k->tables};
-  return launch_decode_common(ctx, p, static_cast<const float *>(a->q.ptr), tabs);
+  const float *q = static_cast<const float *>(a->q.ptr);
+  if (ts)
+    if (bgtq_status s = bgtq_timestamps_write(ts, i0)) return s;
+  bgtq_status st = launch_decode_common(ctx, p, q, tabs);
+  if (!st && ts) st = bgtq_timestamps_write(ts, i1);
+  return st;
+}
+
+bgtq_status bgtq_attention_record(bgtq_attention *a) { return attention_record(a, nullptr, 0, 0); }
+
+bgtq_status bgtq_attention_record_timed(bgtq_attention *a, bgtq_timestamps *ts, uint32_t begin_index,
+                                        uint32_t end_index) {
+  if (!ts) return fail(BGTQ_ERR_RANGE, "null timestamps");
+  if (begin_index >= ts->events.size() || end_index >= ts->events.size())
+    return fail(BGTQ_ERR_RANGE, "Invalid timestamp write");
+  return attention_record(a, ts, begin_index, end_index);
 }
 
 bgtq_status bgtq_attention_attend(bgtq_attention *a, const float *q, size_t n_q, const uint32_t *positions,

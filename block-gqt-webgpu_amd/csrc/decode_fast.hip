@@ -55,8 +55,7 @@ struct Geo {
   static constexpr int KS = D / 32;  // K-steps of QK
   static constexpr int DT = D / 16;  // 16-dim tiles of PV
   static constexpr int PR = D / 8;   // 16-byte pieces per FP16 row
-  static constexpr int VBYTES = kChunk * D * 2;
-  static constexpr int VI = VBYTES / 1024;  // 16-byte DMA instructions per V chunk
+  static constexpr int KRI = kChunk * D * 2 / 1024;  // 16-byte DMA instructions per chunk of FP16 rows
 };
 
 // One ring buffer: V chunk, FP16 scales (32 x 4 bytes), K chunk. Every DMA
@@ -69,7 +68,14 @@ struct Geo {
 // scale DMAs (one for norm strides up to 4, two up to 8; at d=64 the second
 // covers 128 bytes, norm strides up to 6, and the book tables get 3.5 KB, so
 // that two workgroups still share a CU).
-template <int D, int KF, int NN>
+// 16-byte piece swizzle of an FP32 row of D >= 64 values in LDS: rows
+// 4 g + 0..3 (mod 16) XOR their piece index with 4 g, so the PV reads of the
+// four lane groups (rows 4 apart, the same 16 values) hit different banks.
+__host__ __device__ constexpr int swz32(int row) { return ((row >> 2) & 3) << 2; }
+
+// VF: the V rows' format, 0 = FP16 (2 bytes per value), 1 = FP32 (4 bytes;
+// a ring of one slot per wave where two do not fit).
+template <int D, int KF, int NN, int VF = 0>
 struct Slot {
   static constexpr int KS = D / 32;
   static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : KF == 2 ? D : 2 * D;  // K row bytes
@@ -78,15 +84,17 @@ struct Slot {
   static constexpr int NSC = KF == 1 ? 1 : KF == 2 ? NN : 0;  // scale DMAs per chunk
   static constexpr bool SMALL2 = KF == 2 && NN == 2 && D == 64;
   static constexpr int NBYTES = SMALL2 ? 384 : NSC * 64 * 4;
-  static constexpr int NOFF = Geo<D>::VBYTES;         // scales
-  static constexpr int KOFF = NOFF + NBYTES;          // K
+  static constexpr int VBYTES = kChunk * D * (VF ? 4 : 2);
+  static constexpr int VI = VBYTES / 1024;    // 16-byte DMA instructions per V chunk
+  static constexpr int NOFF = VBYTES;         // scales
+  static constexpr int KOFF = NOFF + NBYTES;  // K
   static constexpr int BYTES = KOFF + KI * 1024;
-  static constexpr int L = Geo<D>::VI + KI + NSC;  // DMA instructions per chunk
+  static constexpr int L = VI + KI + NSC;  // DMA instructions per chunk
   // Lookup tables (static LDS): KF 1, the K-steps' books; KF 2, the books'
   // code tables (CTABLES bytes), then kPairSlots pair tables of 2 KB.
   static constexpr int CTABLES = KF == 2 && D == 64 ? 3584 : KF >= 1 ? KS * 2048 : 0;
   static constexpr int TABLES = CTABLES + (KF == 2 ? kPairSlots * 2048 : 0);
-  static constexpr int RING = kRing;
+  static constexpr int RING = VF && kRing * kWaves * BYTES + TABLES > kLdsLimit ? 1 : kRing;
   static constexpr int AHEAD = RING - 1;
   static constexpr int DYN = RING * kWaves * BYTES;  // dynamic LDS: the ring (the tables are static)
   // Decode-step append: the new token's wave encodes it with its last ring
@@ -95,8 +103,8 @@ struct Slot {
   static constexpr int ENC_OFF = KF >= 1 ? (row_enc::scratch_bytes(D) + 1023) / 1024 * 1024 : 0;
   static constexpr int ENC_DMAS = KF >= 1 ? (BYTES - ENC_OFF) / 1024 : 0;
   static_assert(DYN + TABLES <= kLdsLimit, "LDS of one workgroup");
-  static_assert(!SMALL2 || 2 * (DYN + TABLES) <= kLdsLimit, "two workgroups per CU");
-  static_assert(AHEAD >= 1 && AHEAD <= 3, "ring waits cover up to three chunks in flight");
+  static_assert(VF || !SMALL2 || 2 * (DYN + TABLES) <= kLdsLimit, "two workgroups per CU");
+  static_assert(AHEAD >= (VF ? 0 : 1) && AHEAD <= 3, "ring waits cover up to three chunks in flight");
 };
 
 // Split merge in one round trip, one wave per query head (heads wave,
@@ -295,14 +303,18 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
 // the first min(starts[b], max_length - rows) + row + 1 tokens. A unit uses
 // only as many of its splits as its history needs (p.split_floor tokens per
 // split at least); the others exit before their first chunk.
-template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0>
+// VF: V rows of FP32 values (1; decode without an appended token) or FP16
+// (0). FP32 V enters the PV MFMAs as three FP16 parts per value.
+template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0>
 __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
-  using Sl = Slot<D, KF, NN>;
+  using Sl = Slot<D, KF, NN, VF>;
+  static_assert(VF == 0 || PF == 0, "FP32 V: decode only");
   static_assert(PF == 0 || PF == 8 || PF == 16, "row-wise unit width");
   constexpr int UC = PF ? PF : 16;  // columns of a row-wise unit
   static_assert(KF == 0 || row_enc::scratch_bytes(D) <= Sl::BYTES, "append scratch fits a ring slot");
-  constexpr int KS = Gm::KS, DT = Gm::DT, PR = Gm::PR, VI = Gm::VI;
+  constexpr int KS = Gm::KS, DT = Gm::DT, PR = Gm::PR, VI = Sl::VI, KRI = Gm::KRI;
+  constexpr int VB = VF ? 4 : 2;  // bytes per V value
   constexpr int RB = Sl::RB, KI = Sl::KI, L = Sl::L, AHEAD = Sl::AHEAD;
   static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
   static_assert(Sl::BYTES >= 16 * (D + 4) * 4, "q staging fits one ring slot");
@@ -384,7 +396,10 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // Each chunk's loads use buffer descriptors based at the chunk's first token
   // and sized to the chunk's tokens inside the sequence: the hardware range
   // check (which covers the per-lane offset) returns zeros past the length.
-  const _Float16 *v_base = static_cast<const _Float16 *>(p.v) + b * p.v_seq_stride + kv * p.v_head_stride;
+  // V strides count values.
+  const uint8_t *v_rows =
+      static_cast<const uint8_t *>(p.v) + ((int64_t)b * p.v_seq_stride + (int64_t)kv * p.v_head_stride) * VB;
+  const _Float16 *v_base = reinterpret_cast<const _Float16 *>(v_rows);  // FP16 V: the appended row's store
   const uint8_t *k_base = KF >= 1 ? p.packed + b * p.packed_seq_stride + kv * p.packed_head_stride
                                   : reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(p.k) +
                                                                       b * p.k_seq_stride + kv * p.k_head_stride);
@@ -394,11 +409,17 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   const int ns = KF == 2 ? fl.gns[kv] : 2;
   // Per-lane source offsets of the swizzled FP16 row pieces: DMA instruction k,
   // lane i fills LDS piece 64k + i = (row r, slot c) with global piece c ^ swz(r).
-  uint32_t voff_rows[VI];
+  // FP32 V rows (D / 4 pieces) swizzle with swz32.
+  uint32_t voff_rows[VI], koff_rows[KF == 0 ? KRI : 1];
 #pragma unroll
   for (int k = 0; k < VI; ++k) {
+    const int P = 64 * k + lane, r = P / (VF ? D / 4 : PR), c = P % (VF ? D / 4 : PR);
+    voff_rows[k] = VF ? r * (4 * D) + ((c ^ swz32(r)) * 16) : r * (2 * D) + ((c ^ swz<D>(r)) * 16);
+  }
+#pragma unroll
+  for (int k = 0; k < (KF == 0 ? KRI : 0); ++k) {
     const int P = 64 * k + lane, r = P / PR, c = P % PR;
-    voff_rows[k] = r * (2 * D) + ((c ^ swz<D>(r)) * 16);
+    koff_rows[k] = r * (2 * D) + ((c ^ swz<D>(r)) * 16);
   }
 
   // ---------------- prologue ----------------
@@ -507,6 +528,10 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   // This wave's chunks start at first + 128 i.
   const int first = kInterleaved ? (split * kWaves + wave) * kChunk : split * p.split_tokens + wave * kChunk;
   const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
+  // Decode reads every byte once (non-temporal, nothing cached is displaced);
+  // a row-wise prefill chunk's history is read by every unit of its KV head,
+  // so those loads keep the default policy and the units share it in L2.
+  constexpr int kPol = PF ? kCached : kStream;
   auto issue = [&](int i) {
     const int c0 = first + i * stride;
     // Tokens of the chunk inside the sequence; none for a chunk past the end
@@ -514,16 +539,16 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     const int in_seq = min(T_b - c0, kChunk);
     const uint32_t rest = __builtin_amdgcn_readfirstlane(in_seq > 0 ? in_seq : 0);  // wave-uniform: SGPR descriptor
     uint8_t *sb = slot_base(i % Sl::RING);
-    const __amdgpu_buffer_rsrc_t rV = rsrc(v_base + (int64_t)c0 * D, rest * (2 * D));
+    const __amdgpu_buffer_rsrc_t rV = rsrc(v_rows + (int64_t)c0 * D * VB, rest * (VB * D));
 #pragma unroll
-    for (int k = 0; k < VI; ++k) dma16<kStream>(rV, sb + k * 1024, voff_rows[k], 0);
+    for (int k = 0; k < VI; ++k) dma16<kPol>(rV, sb + k * 1024, voff_rows[k], 0);
     uint8_t *kb = sb + Sl::KOFF;
     if (KF == 1) {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * RB, rest * RB);
       const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * 2, rest * 4);
 #pragma unroll
-      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
-      dma4<kStream>(rN, sb + Sl::NOFF, lane * 4, 0);
+      for (int k = 0; k < KI; ++k) dma16<kPol>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+      dma4<kPol>(rN, sb + Sl::NOFF, lane * 4, 0);
     } else if (KF == 2) {
       // Rows of rb bytes and ns scales, packed back to back: the chunk's rows
       // fill the K area's front, its scale rows the scale area's. The range
@@ -534,14 +559,14 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * rb, (rest * rb + 15u) & ~15u);
       const __amdgpu_buffer_rsrc_t rN = rsrc(n_base + (int64_t)c0 * ns, (rest * ns * 2 + 3u) & ~3u);
 #pragma unroll
-      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
+      for (int k = 0; k < KI; ++k) dma16<kPol>(rK, kb + k * 1024, k * 1024 + lane * 16, 0);
 #pragma unroll
       for (int k = 0; k < Sl::NSC; ++k)
-        if (k * 256 + lane * 4 < Sl::NBYTES) dma4<kStream>(rN, sb + Sl::NOFF + k * 256, k * 256 + lane * 4, 0);
+        if (k * 256 + lane * 4 < Sl::NBYTES) dma4<kPol>(rN, sb + Sl::NOFF + k * 256, k * 256 + lane * 4, 0);
     } else {
       const __amdgpu_buffer_rsrc_t rK = rsrc(k_base + (int64_t)c0 * (2 * D), rest * (2 * D));
 #pragma unroll
-      for (int k = 0; k < KI; ++k) dma16<kStream>(rK, kb + k * 1024, voff_rows[k], 0);
+      for (int k = 0; k < KI; ++k) dma16<kPol>(rK, kb + k * 1024, koff_rows[k], 0);
     }
   };
   // Per-head causal limits.
@@ -570,7 +595,8 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   constexpr int JL = D > 64 ? 2 : 1;
   const int t_new = T_b - 1;
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
-  const int own_w = !rowwise && p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
+  const int own_w =
+      !VF && !rowwise && p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
   const bool owner = own_w == wave;
   const bool encoder = KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
   const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
@@ -1207,20 +1233,56 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     // here. PF: the history is in L2 and the ring deeper, so only the chunk
     // computed is waited for (at the top of the iteration).
     if (!PF) wait_vm<0>();
-    u32x2 vt[DT][2];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int piece = 2 * dt + tpiece;
-      ds_read_tr16_pair(sb + trow * (2 * D) + ((piece ^ swz<D>(trow)) * 16) + thalf,
-                        sb + (16 + trow) * (2 * D) + ((piece ^ swz<D>(16 + trow)) * 16) + thalf, vt[dt][0], vt[dt][1]);
-    }
     const half8 pha = __builtin_bit_cast(half8, ph), pla = __builtin_bit_cast(half8, pl);
+    if constexpr (VF) {
+      // FP32 V: lane (gq, col) reads V[16 (j >> 2) + 4 gq + (j & 3)][16 dt + col],
+      // the B operand of its P slots j = 0..7 (row reads; the four lane groups
+      // hit different banks through swz32), and splits each value into FP16
+      // parts v = h0 + 2^-11 h1 + 2^-22 h2: each part holds the next 11 bits
+      // of what the ones before left, so the parts are exact for
+      // 2^-23 <= |v| < 65504 (the host keeps larger V off this path). The
+      // MFMAs weight h1 and h2 with P's hi part scaled by 2^-11 and 2^-22
+      // (exact powers of two; P lo times those terms is below 2^-22 of the
+      // result and left out).
+      const half8 ph1 = pha * (_Float16)0x1p-11f, ph2 = pha * (_Float16)0x1p-22f;
+      // Row 4 gq + (j & 3) + 16 (j >> 2), its piece 4 (dt ^ gq) + col / 4.
+      const uint8_t *vl = sb + 16 * gq * D + 4 * col;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      wait_dt<DT>(dt, vt[dt][0], vt[dt][1]);
-      const half8 vb = __builtin_bit_cast(half8, u32x4{vt[dt][0][0], vt[dt][0][1], vt[dt][1][0], vt[dt][1][1]});
-      O[dt] = mfma(pha, vb, O[dt]);
-      O[dt] = mfma(pla, vb, O[dt]);
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint8_t *vd = vl + 64 * (dt ^ gq);
+        half8 h0, h1, h2;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = *reinterpret_cast<const float *>(vd + (16 * (j >> 2) + (j & 3)) * (4 * D));
+          const _Float16 a = (_Float16)v;
+          const float r1 = v - (float)a;
+          const _Float16 c = (_Float16)(r1 * 0x1p11f);
+          const float r2 = __builtin_fmaf(-(float)c, 0x1p-11f, r1);
+          h0[j] = a;
+          h1[j] = c;
+          h2[j] = (_Float16)(r2 * 0x1p22f);
+        }
+        O[dt] = mfma(pha, h0, O[dt]);
+        O[dt] = mfma(pla, h0, O[dt]);
+        O[dt] = mfma(ph1, h1, O[dt]);
+        O[dt] = mfma(ph2, h2, O[dt]);
+      }
+    } else {
+      u32x2 vt[DT][2];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int piece = 2 * dt + tpiece;
+        ds_read_tr16_pair(sb + trow * (2 * D) + ((piece ^ swz<D>(trow)) * 16) + thalf,
+                          sb + (16 + trow) * (2 * D) + ((piece ^ swz<D>(16 + trow)) * 16) + thalf, vt[dt][0],
+                          vt[dt][1]);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        wait_dt<DT>(dt, vt[dt][0], vt[dt][1]);
+        const half8 vb = __builtin_bit_cast(half8, u32x4{vt[dt][0][0], vt[dt][0][1], vt[dt][1][0], vt[dt][1][1]});
+        O[dt] = mfma(pha, vb, O[dt]);
+        O[dt] = mfma(pla, vb, O[dt]);
+      }
     }
   }
 
@@ -1422,26 +1484,31 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int KF, int NN, int SG, int PK, int PF>
+template <int D, int KF, int NN, int SG, int PK, int PF, int VF = 0>
 hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
-  static const hipError_t allowed = hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF>,
+  static const hipError_t allowed = hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF, VF>,
                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                        Slot<D, KF, NN>::DYN);
+                                                        Slot<D, KF, NN, VF>::DYN);
   if (allowed != hipSuccess) {
     (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
     return allowed;
   }
-  constexpr int lds = Slot<D, KF, NN>::DYN;
+  constexpr int lds = Slot<D, KF, NN, VF>::DYN;
   const dim3 grid = PF ? dim3((unsigned)p.kv_heads, (unsigned)(p.batch * p.qgroups), (unsigned)p.splits)
                        : dim3((unsigned)p.splits, (unsigned)p.kv_heads, (unsigned)p.batch);
-  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF>), grid, dim3(kThreads), lds, stream, p, fl);
+  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF, VF>), grid, dim3(kThreads), lds, stream, p, fl);
   return hipGetLastError();
 }
 
-// Row-wise prefill (p.starts set) runs the PF variant of its unit width.
+// Row-wise prefill (p.starts set) runs the PF variant of its unit width;
+// FP32 V (decode without an appended token) the VF variant.
 template <int D, int KF, int NN, int SG, int PK = 0>
 hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
+  if (p.v_dtype == BGTQ_DTYPE_F32) {
+    if (p.starts || p.k_new) return hipErrorInvalidValue;
+    return launch_mode<D, KF, NN, SG, PK, 0, 1>(p, fl, stream);
+  }
   if (!p.starts) return launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream);
   return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8>(p, fl, stream)
                           : launch_mode<D, KF, NN, SG, PK, 16>(p, fl, stream);

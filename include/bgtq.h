@@ -52,7 +52,9 @@ typedef struct {
 const char *bgtq_last_error(void);
 /* 2: bgtq_tables_info gained device_bytes. 3: bgtq_model_submit, bgtq_buffer_*, bgtq_allocate_bits,
  * bgtq_layout_groups, bgtq_layout_build. 4: bgtq_decode_noalloc; q_rotated closes the decode and
- * prefill descriptors; bgtq_bake_qproj; bgtq_timestamps_*. */
+ * prefill descriptors; bgtq_bake_qproj; bgtq_timestamps_*; the prefill workspace is always needed
+ * (at least BGTQ_PREFILL_COUNTER_BYTES, 16-byte aligned, its counter prefix zeroed before the first
+ * call). 5: bgtq_attention_record_timed; attention over FP32 V runs on the fused kernel. */
 int32_t bgtq_abi_version(void);
 
 /* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
@@ -137,7 +139,10 @@ void bgtq_keys_destroy(bgtq_keys *k);
 
 /* ---- Values (src/runtime/values.ts:3-16) --------------------------------- *
  * dtype BGTQ_DTYPE_F32 stores FP32 V exactly (the synthetic path); F16 stores
- * RNE-rounded FP16 V (src/model/append.wgsl:6-10). append() is synchronous. */
+ * RNE-rounded FP16 V (src/model/append.wgsl:6-10). append() is synchronous.
+ * Attention over F32 V runs on the fused kernel, which splits each value into
+ * three FP16 parts that add back to it exactly, while every appended
+ * |v| < 65504; a larger value sends the store to the general kernels. */
 typedef struct bgtq_values bgtq_values;
 bgtq_status bgtq_values_create(bgtq_context *ctx, uint32_t dim, uint32_t capacity, int32_t dtype,
                                bgtq_values **out);
@@ -160,6 +165,12 @@ bgtq_status bgtq_attention_create(bgtq_keys *k, bgtq_values *v, uint32_t max_que
 bgtq_status bgtq_attention_set_queries(bgtq_attention *a, const float *q, size_t n_q_values,
                                        const uint32_t *positions, size_t n_positions, int32_t causal);
 bgtq_status bgtq_attention_record(bgtq_attention *a);
+/* record() with timestamps: index begin_index written on the stream after the
+ * queries' upload, right before the attention passes, end_index right after
+ * them (record(encoder, {querySet, beginningOfPassWriteIndex,
+ * endOfPassWriteIndex}), src/attention/attention.ts:44-58). */
+bgtq_status bgtq_attention_record_timed(bgtq_attention *a, bgtq_timestamps *ts, uint32_t begin_index,
+                                        uint32_t end_index);
 bgtq_status bgtq_attention_attend(bgtq_attention *a, const float *q, size_t n_q_values,
                                   const uint32_t *positions, size_t n_positions, int32_t causal);
 bgtq_status bgtq_attention_read(const bgtq_attention *a, int32_t which, float *out, size_t count);
@@ -299,6 +310,9 @@ bgtq_status bgtq_decode_noalloc(bgtq_context *ctx, const bgtq_decode_desc *d);
  *   history, rounded up to 32; row-wise: each row's, as max_length /
  *   split_tokens splits); 0 = about two workgroups per compute unit (tiled:
  *   sized on the device for the actual starts).
+ * q, V and the K scales must be finite: the tiled kernels are built without
+ * NaN/Inf semantics, so a non-finite input inside a history gives an
+ * unspecified output (packed K codes are always finite).
  * Layouts: FP16 K, or packed layouts the fused decode takes (see
  * bgtq_decode_append) whose centroid books (n_books * max_centroids floats)
  * fit 4 KB at d=64, 8 KB at d=128; others return BGTQ_ERR_UNSUPPORTED. */

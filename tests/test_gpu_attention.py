@@ -177,3 +177,117 @@ def test_mismatched_lengths_rejected(device, attention_cases):
         s.destroy()
         values.destroy()
         keys.destroy()
+
+
+def _bench_workload(T, d):
+    """The phase-4 benchmark workload t{T}_d{d} (tests/oracles/export_attention.py:20-26):
+    q ~ N(0, 1) [3, d], K = FP16(0.7 N(0, 1)), V = 0.5 N(0, 1) FP32, positions
+    (0, T / 2, T - 1), from torch's CPU generator seeded 731 + d + T."""
+    import torch
+    g = torch.Generator().manual_seed(731 + d + T)
+    q = torch.randn(3, d, generator=g)
+    k = (torch.randn(T, d, generator=g) * 0.7).half()
+    v = torch.randn(T, d, generator=g) * 0.5
+    return q.numpy(), k.numpy(), v.numpy(), np.array([0, T // 2, T - 1], np.uint32)
+
+
+@pytest.mark.parametrize("T", (1024, 2048, 4096))
+def test_fp32_values_benchmark_shapes(device, attention_cases, oracle, T):
+    """OptimizedAttention over FP32 Values at the benchmark's context lengths
+    (benchmarks/phase4.ts:19-47) through the fused kernel's FP32-V variant,
+    against the oracle on the reconstructed K, both d, causal and not."""
+    import bgtq
+    layouts = {m["dim"]: (lm, la) for _, m, _, lm, la in attention_cases}
+    for d in (64, 128):
+        print("case", T, d, flush=True)
+        q, k, v, pos = _bench_workload(T, d)
+        lm, la = layouts[d]
+        keys = bgtq.PackedKeys.create(device, _params(lm, la), T)
+        values = bgtq.Values(device, d, T)
+        att = bgtq.OptimizedAttention.create(device, keys, values, 3)
+        lean = bgtq.OptimizedAttention.create(device, keys, values, 3, materialize=False)
+        try:
+            keys.append(k.view(np.uint16))
+            values.append(v)
+            ol = oracle.Layout.from_mixed_fixture(lm, la)
+            packed, norms = keys.read()
+            codes = oracle.unpack(packed.reshape(T, -1), d, lm["nopack_start"])
+            k_eff = oracle.reconstruct(ol, codes, norms.view(np.float16).reshape(T, -1).astype(np.float32))
+            for causal in (False, True):
+                ref_l, ref_p, ref_o = oracle.attention(q, k_eff, v, pos, causal)
+                out = att.attend(q, pos, causal)
+                ins = att.inspect()
+                _close(out, ref_o, ATOL, RTOL, f"T{T} d{d} {causal} output")
+                _close(ins["logits"], ref_l, LOGIT_ATOL, LOGIT_RTOL, f"T{T} d{d} {causal} logits")
+                _close(ins["probabilities"], ref_p, PROB_ATOL, PROB_RTOL, f"T{T} d{d} {causal} probabilities")
+                # without materialised intermediates: the same output
+                np.testing.assert_array_equal(lean.attend(q, pos, causal), out)
+            # The first causal query attends to V0 alone: the FP16 parts of an
+            # FP32 value add back to it exactly.
+            np.testing.assert_array_equal(att.attend(q, pos, True)[0], v[0])
+        finally:
+            lean.destroy()
+            att.destroy()
+            values.destroy()
+            keys.destroy()
+
+
+def test_fp32_values_beyond_fp16_range(device, attention_cases, oracle):
+    """FP32 V with a value past FP16's range (|v| >= 65504) cannot be split
+    into FP16 parts: the session computes it on the general kernels, with the
+    same result bar, and an FP16 K session likewise."""
+    import bgtq
+    name, m, a, lm, la = next(c for c in attention_cases if c[0] == "t256_d64")
+    T, d = m["context_length"], m["dim"]
+    v = a["v"].copy()
+    v[5, 3] = 1.0e6
+    v[17, 0] = -7.0e4
+    keys = bgtq.PackedKeys.create(device, _params(lm, la), T)
+    fp16 = bgtq.FP16Keys(device, d, T)
+    values = bgtq.Values(device, d, T)
+    att = bgtq.OptimizedAttention.create(device, keys, values, m["queries"])
+    s16 = bgtq.AttentionEngine.create(device).session(fp16, values, m["queries"])
+    try:
+        keys.append(a["k"].view(np.uint16))
+        fp16.append(a["k"].view(np.uint16))
+        values.append(v)
+        for causal in (False, True):
+            _, _, ref_o = oracle.attention(a["q"], a["reconstructed_k"], v, a["positions"], causal)
+            _close(att.attend(a["q"], a["positions"], causal), ref_o, ATOL, RTOL, f"large V {causal}")
+            _, _, ref16 = oracle.attention(a["q"], a["k"].astype(np.float32), v, a["positions"], causal)
+            _close(s16.attend(a["q"], a["positions"], causal), ref16, ATOL, RTOL, f"large V fp16 K {causal}")
+    finally:
+        s16.destroy()
+        att.destroy()
+        values.destroy()
+        fp16.destroy()
+        keys.destroy()
+
+
+def test_record_with_timestamps(device, attention_cases):
+    """record(encoder, timestamps) (src/attention/attention.ts:44-58): the
+    begin and end writes bracket the attention work; bad indices are rejected
+    before any work is queued."""
+    import bgtq
+    name, m, a, lm, la = next(c for c in attention_cases if c[0] == "t512_d128")
+    T, d = m["context_length"], m["dim"]
+    keys = bgtq.PackedKeys.create(device, _params(lm, la), T)
+    values = bgtq.Values(device, d, T)
+    att = bgtq.OptimizedAttention.create(device, keys, values, m["queries"])
+    ts = bgtq.Timestamps(device, 4)
+    try:
+        keys.append(a["k"].view(np.uint16))
+        values.append(a["v"])
+        att.setQueries(a["q"], a["positions"], False)
+        att.record(ts, 0, 1)
+        att.record(ts, 2, 3)
+        ns = ts.resolve()
+        assert 0 < ns[1] - ns[0] < 10_000_000 and ns[2] >= ns[1] and ns[3] > ns[2]
+        _close(att.read("output"), a["compressed_output"], ATOL, RTOL, "timed record output")
+        with pytest.raises(bgtq.RangeError, match="timestamp"):
+            att.record(ts, 0, 4)
+    finally:
+        ts.destroy()
+        att.destroy()
+        values.destroy()
+        keys.destroy()

@@ -167,3 +167,32 @@ def test_smollm2_decode_step_b1(device, oracle, layout):
                 _check(out[l, 0, h * G:(h + 1) * G], ref.astype(np.float64), f"layer {l} kv{h}")
     finally:
         w.destroy()
+
+
+def test_smollm2_prefill_encode_one_call(device, oracle):
+    """The bulk K encode bench.py times: 30 layers x 3 KV heads x 4096 rows (FP16, pair energies
+    decaying by 0.9), 90 table sets, one bgtq_encode_batched call; every packed row and scale
+    bit-exact against the oracle's encoder (src/reference/production_math.py:4-24 and the
+    packing of src/reference/mixed_layout.py:21-27)."""
+    import torch
+    import bench
+    w = bench.EncodeWorkload(device, "B")
+    try:
+        w.call()
+        torch.cuda.synchronize()
+        p = w.p
+        ol = _olayout(oracle, p)
+        k = w.k.cpu().numpy().view(np.uint16)  # [30, 4096, 3, 64]
+        packed = w.packed.cpu().numpy()
+        norms = w.norms.cpu().numpy().view(np.uint16)
+        for j in range(90):
+            l, h = divmod(j, 3)
+            ref_p, ref_n = oracle.encode_pack(ol, np.ascontiguousarray(k[l, :, h]))
+            got_p = packed[j, :4096 * p.rowBytes].reshape(4096, p.rowBytes)
+            got_n = norms[j, :4096 * p.normStride].reshape(4096, p.normStride)
+            bad = np.nonzero(np.any(got_p != ref_p, axis=1) | np.any(got_n != ref_n, axis=1))[0]
+            assert bad.size == 0, f"job {j}: {bad.size} rows differ, first {bad[:5]}"
+            assert not packed[j, 4096 * p.rowBytes:].any() and not norms[j, 4096 * p.normStride:].any(), \
+                f"job {j}: bytes past its rows written"
+    finally:
+        w.destroy()

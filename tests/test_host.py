@@ -18,7 +18,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(bgtq.LIB_PATH))
     missing = [name for name in sorted(declared) if not hasattr(lib, name)]
     assert not missing, missing
-    assert lib.bgtq_abi_version() == 4
+    assert lib.bgtq_abi_version() == 5
     lib.bgtq_model_submit.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
     assert lib.bgtq_model_submit(None, None, 0) == 1  # BGTQ_ERR_RANGE: null context, nothing touched
 
@@ -317,7 +317,7 @@ def test_node_addon_loads_without_a_device():
     assert r.returncode == 0, r.stderr
     import json
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert out == {"abi": 4, "miss": [], "missc": []}, out
+    assert out == {"abi": 5, "miss": [], "missc": []}, out
 
 
 def _tampered_calibration(tmp_path, edit_manifest=None, edit_payload=None):
