@@ -1001,11 +1001,16 @@ struct DecodeWorkspace {
   size_t counters, qr, part, stats, total;
 };
 
+// The split counters come first, in a prefix of at least
+// BGTQ_DECODE_COUNTER_UNITS counters: every call with at most that many
+// (sequence, KV head) units writes its rotated queries and partials past it,
+// so calls of any such geometries can share a workspace in any order and its
+// counters stay zero.
 static DecodeWorkspace decode_ws(int64_t units, int64_t heads, int dim, int splits) {
   auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
   DecodeWorkspace w;
   w.counters = 0;
-  w.qr = al(sizeof(uint32_t) * kCounterStride * units);
+  w.qr = al(sizeof(uint32_t) * kCounterStride * std::max<int64_t>(units, BGTQ_DECODE_COUNTER_UNITS));
   w.part = w.qr + al(sizeof(float) * heads * dim);
   w.stats = w.part + al(sizeof(float) * heads * splits * (dim + 2));
   w.total = w.stats + al(sizeof(float) * heads * 2);
@@ -1215,6 +1220,9 @@ bgtq_status bgtq_decode_noalloc(bgtq_context *ctx, const bgtq_decode_desc *d) {
   if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
   int splits = 1;
   if (bgtq_status s = validate_decode(d, &splits)) return s;
+  if ((int64_t)d->batch * d->kv_heads > BGTQ_DECODE_COUNTER_UNITS)
+    return fail(BGTQ_ERR_RANGE, "bgtq_decode_noalloc takes up to %d (sequence, KV head) pairs per call",
+                BGTQ_DECODE_COUNTER_UNITS);
   const size_t need = decode_ws((int64_t)d->batch * d->kv_heads, (int64_t)d->batch * d->q_heads, d->dim, splits).total;
   if (need > BGTQ_DECODE_SCRATCH_BYTES)
     return fail(BGTQ_ERR_RANGE, "decode needs %zu bytes of workspace, above the %u-byte scratch of bgtq_decode_noalloc",

@@ -212,7 +212,13 @@ bgtq_status bgtq_encode_batched(bgtq_context *ctx, int32_t src_dtype, const bgtq
  *   least bgtq_decode_workspace_size() bytes, zero-filled by the caller
  *   before its first use (it holds per-(sequence, KV head) split counters
  *   that every call leaves at zero again); calls sharing a workspace must be
- *   ordered on one stream. */
+ *   ordered on one stream. The counters occupy a prefix of 64 bytes per
+ *   (sequence, KV head) pair, at least BGTQ_DECODE_COUNTER_UNITS pairs long,
+ *   which calls of up to that many pairs never write otherwise: such calls
+ *   share a workspace whatever their geometries. A call with more pairs uses
+ *   a longer prefix, which calls of other geometries may have written: zero
+ *   it again before such a call when geometries mix. */
+#define BGTQ_DECODE_COUNTER_UNITS 1024
 typedef struct {
   int32_t batch, q_heads, kv_heads, dim;
   int32_t key_format;
@@ -277,8 +283,10 @@ bgtq_status bgtq_decode_append(bgtq_context *ctx, const bgtq_decode_desc *d, con
  * the decode's workspace is a library-owned device array of
  * BGTQ_DECODE_SCRATCH_BYTES per device, held until the process ends and
  * resolved and cleared by bgtq_context_create (once per device). A launch
- * whose bgtq_decode_workspace_size exceeds it fails with BGTQ_ERR_RANGE and
- * queues nothing. Same kernels and results as bgtq_decode. Every call on one
+ * whose bgtq_decode_workspace_size exceeds it, or with more than
+ * BGTQ_DECODE_COUNTER_UNITS (sequence, KV head) pairs, fails with
+ * BGTQ_ERR_RANGE and queues nothing. Same kernels and results as
+ * bgtq_decode. Every call on one
  * device shares that device's array: calls that may overlap on one device
  * (several streams or contexts) race and must be ordered by the caller. */
 #define BGTQ_DECODE_SCRATCH_BYTES (4u << 20)

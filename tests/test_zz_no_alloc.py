@@ -51,8 +51,10 @@ def _both(device, args):
         if mode == "workspace":
             ws = torch.zeros(batched.workspace_bytes(batched.decode_desc(out=out, **args)), dtype=torch.uint8,
                              device="cuda")
+            torch.cuda.synchronize()  # torch's fills land before the library's stream reads
             batched.decode(device, batched.decode_desc(out=out, workspace=ws, **args))
         else:
+            torch.cuda.synchronize()
             desc = batched.decode_desc(out=out, **args)  # no workspace in the descriptor
             assert desc.workspace is None and desc.workspace_bytes == 0
             _lib.check(_lib.lib().bgtq_decode_noalloc(device.handle, ctypes.byref(desc)))
@@ -90,3 +92,92 @@ def test_noalloc_refuses_beyond_its_scratch(device):
     assert batched.workspace_bytes(desc) > (4 << 20)
     with pytest.raises(bgtq.RangeError, match="scratch of bgtq_decode_noalloc"):
         _lib.check(_lib.lib().bgtq_decode_noalloc(device.handle, ctypes.byref(desc)))
+
+
+@pytest.mark.parametrize("key_format,dim", [("packed", 64), ("fp16", 128)])
+def test_noalloc_allocates_nothing_and_captures(device, key_format, dim):
+    """What the entry point is for: after a first call, further calls leave the device's free
+    memory and torch's allocations unchanged; captured into a HIP graph on a side stream (where an
+    allocation could not be captured) and replayed three times, with eager calls in between, every
+    replay matches the eager output."""
+    import torch
+    from bgtq import _lib, batched
+    args, keep, tabs = _case(device, batch=3, hkv=2, hq=14, dim=dim, T=3000, key_format=key_format, v_dtype="f16",
+                             seed=5)
+    try:
+        out = torch.full((3, 14, dim), float("nan"), device="cuda")
+        torch.cuda.synchronize()  # the library's stream is not torch's: the fill lands first
+        desc = batched.decode_desc(out=out, **args)
+
+        def call():
+            _lib.check(_lib.lib().bgtq_decode_noalloc(device.handle, ctypes.byref(desc)))
+
+        call()
+        torch.cuda.synchronize()
+        eager = out.cpu().numpy().copy()
+        assert np.isfinite(eager).all()
+        free0, alloc0 = torch.cuda.mem_get_info()[0], torch.cuda.memory_allocated()
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0 and torch.cuda.memory_allocated() == alloc0
+        np.testing.assert_array_equal(out.cpu().numpy(), eager)
+        print("noalloc capture", key_format, dim, flush=True)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(g, stream=s):
+                batched.bind_torch_stream(device)
+                call()
+        finally:
+            device.set_stream(None)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy(), eager)
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            call()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy(), eager)
+        del g
+    finally:
+        for t in tabs:
+            t.destroy()
+
+
+def test_decode_workspace_shared_across_geometries(device):
+    """One workspace, zeroed once, shared by bgtq_decode calls of changing geometries (a small
+    batch on the general kernels, larger ones on the fused kernel, twice round), and the library
+    scratch of bgtq_decode_noalloc likewise: every output equals that of a fresh workspace."""
+    import torch
+    from bgtq import batched
+    shapes = [dict(batch=2, hkv=1, hq=7, T=900, seed=2, splits=5, key_format="packed", v_dtype="f32", dim=64),
+              dict(batch=3, hkv=2, hq=14, T=3000, seed=5, key_format="packed", v_dtype="f16", dim=64),
+              dict(batch=1, hkv=1, hq=7, T=500, seed=7, key_format="fp16", v_dtype="f16", dim=128),
+              dict(batch=6, hkv=2, hq=14, T=2000, seed=9, key_format="packed", v_dtype="f16", dim=64)]
+    cases = [_case(device, **s) for s in shapes]
+    try:
+        size = 0
+        for args, _, _ in cases:
+            out = torch.empty((args["batch"], args["q_heads"], args["dim"]), device="cuda")
+            size = max(size, batched.workspace_bytes(batched.decode_desc(out=out, **args)))
+        shared = torch.zeros(size, dtype=torch.uint8, device="cuda")
+        for rnd in range(2):
+            for i, (args, _, _) in enumerate(cases):
+                print("shared workspace", rnd, shapes[i], flush=True)
+                ref, got = _both(device, args)
+                np.testing.assert_array_equal(got, ref)
+                out = torch.full((args["batch"], args["q_heads"], args["dim"]), float("nan"), device="cuda")
+                torch.cuda.synchronize()
+                batched.decode(device, batched.decode_desc(out=out, workspace=shared, **args))
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    finally:
+        for _, _, tabs in cases:
+            for t in tabs:
+                t.destroy()
