@@ -7,6 +7,14 @@ Lloyd-Max codebook per width for N(0, 1/d_group) and one Haar rotation per
 width >= rotation_threshold (vendor/blockgtq/block_gtq_pipeline.py:24-92,
 151-246), and the 256-bin code LUT (vendor/blockgtq/quant_kernels.py:276-364).
 Tables are inputs of the hot path; this module only builds them.
+
+Attribution: the codebook, rotation and LUT steps (_cond_mean,
+gaussian_codebook, haar_rotation, code_lut) follow Block-GTQ
+(https://github.com/JIA-Lab-research/blockgtq, commit 3fe14e7), licensed under
+the Apache License, Version 2.0; they are restated step for step because the
+regenerated tables must equal the committed ones bit for bit. tie_order
+restates the ordering of the Microsoft STL's std::sort (Apache License 2.0
+WITH LLVM-exception).
 """
 from __future__ import annotations
 
@@ -44,8 +52,9 @@ def tie_order(widths) -> np.ndarray:
     (median of three; Tukey's ninther above 40 elements) with a three-way
     partition whose swaps set the order of equal widths: at 33..64 pairs the
     order differs from a stable sort (fixtures mixed_d128, low_d128). Restated
-    from that published algorithm; libbgtq's grouping (csrc/calibrate.cpp,
-    TieOrderSort) is the same code.
+    from that published algorithm (Microsoft STL, Apache License 2.0 WITH
+    LLVM-exception); libbgtq's grouping (csrc/calibrate.cpp, TieOrderSort) is
+    the same code.
     """
     key = [int(x) for x in np.asarray(widths, dtype=np.int64)]
     idx = list(range(len(key)))

@@ -3,7 +3,10 @@
 // RoPE pairs by width (src/reference/mixed_layout.py:5-18; upstream
 // _post_allocation_setup, vendor/blockgtq/block_gtq_pipeline.py:151-246) and
 // the 256-bin code LUT with its per-position offsets and inverse bin widths
-// (vendor/blockgtq/quant_kernels.py:276-364), serialised as tables(p)
+// (vendor/blockgtq/quant_kernels.py:276-364; Block-GTQ,
+// https://github.com/JIA-Lab-research/blockgtq commit 3fe14e7, Apache License
+// 2.0, whose setup steps are restated so the tables match bit for bit),
+// serialised as tables(p)
 // (src/webgpu/layout.ts:24-31). The per-width codebooks and rotations are
 // inputs: they come from the committed calibration blobs or from the
 // caller's own generator. Same arithmetic as the reference's tables:
@@ -51,7 +54,8 @@ constexpr int kBins = 256;
 // range of at most 32 elements, which keeps equal widths in pair order, and
 // splits a larger one around a median guess (median of three, Tukey's
 // ninther above 40 elements) with a three-way partition whose swaps decide
-// the order of equal widths. Restated from that published algorithm; with
+// the order of equal widths. Restated from that published algorithm
+// (Microsoft STL, Apache License 2.0 WITH LLVM-exception); with
 // 33..64 pairs the result differs from a stable sort (fixtures mixed_d128,
 // low_d128). Widths take at most 8 distinct values and every partition
 // removes all elements equal to its pivot, so no range is split more than 8
