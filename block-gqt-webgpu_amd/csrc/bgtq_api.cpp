@@ -1360,10 +1360,13 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
     // Splits of at least split_floor tokens (two 32-token chunks per wave
     // by default: below that a split merge costs more than the chunks it
     // saves), as many as the longest history allowed needs, at most enough
-    // for two workgroups per compute unit and kPrefillMaxSplits.
-    const int64_t floor_tok = d->split_tokens > 0 ? d->split_tokens : kPrefillSplitFloor;
+    // for the workgroups a compute unit holds (two of four waves, one of
+    // eight) and kPrefillMaxSplits.
+    const int64_t floor_tok = d->split_tokens > 0 ? d->split_tokens : prefill_split_floor(d->dim);
+    const int64_t per_cu = decode_fast_prefill_waves(d->dim) == 8 ? 1 : 2;
     int64_t splits = ((int64_t)d->max_length + floor_tok - 1) / floor_tok;
-    if (d->split_tokens <= 0) splits = std::min<int64_t>(splits, std::max<int64_t>(1, 2 * (int64_t)device_cus() / row_units));
+    if (d->split_tokens <= 0)
+      splits = std::min<int64_t>(splits, std::max<int64_t>(1, per_cu * (int64_t)device_cus() / row_units));
     plan->qgroups = (int)qgroups;
     plan->unit_cols = (int)uc;
     plan->splits = (int)std::max<int64_t>(1, std::min<int64_t>(splits, kPrefillMaxSplits));

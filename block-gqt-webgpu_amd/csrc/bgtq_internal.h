@@ -232,9 +232,12 @@ constexpr int kPrefillMaxRanges = 2048;   // workgroups of one launch at most (b
 // kernel (a unit per query row and KV head, its split merge); longer chunks
 // tile their queries in the prefill kernel.
 constexpr int kPrefillRowwiseRows = BGTQ_PREFILL_ROWWISE_ROWS;
-// Row-wise prefill: tokens per split at least (two 32-token chunks per
+// Row-wise prefill: waves per workgroup (d=64: 8, so a split covers twice
+// the tokens and a unit merges half the partials; d=128 keeps 4, whose ring
+// would not fit twice), tokens per split at least (two 32-token chunks per
 // wave), splits per unit at most.
-constexpr int kPrefillSplitFloor = 256;
+constexpr int decode_fast_prefill_waves(int dim) { return dim == 64 ? 8 : 4; }
+constexpr int prefill_split_floor(int dim) { return 64 * decode_fast_prefill_waves(dim); }
 constexpr int kPrefillMaxSplits = 16;
 // Row-wise prefill: query columns per unit (8 or 16).
 constexpr int kPrefillUnitCols = 16;

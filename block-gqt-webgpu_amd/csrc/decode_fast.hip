@@ -74,8 +74,8 @@ struct Geo {
 __host__ __device__ constexpr int swz32(int row) { return ((row >> 2) & 3) << 2; }
 
 // VF: the V rows' format, 0 = FP16 (2 bytes per value), 1 = FP32 (4 bytes;
-// a ring of one slot per wave where two do not fit).
-template <int D, int KF, int NN, int VF = 0>
+// a ring of one slot per wave where two do not fit). NW: waves per workgroup.
+template <int D, int KF, int NN, int VF = 0, int NW = kWaves>
 struct Slot {
   static constexpr int KS = D / 32;
   static constexpr int RB = KF == 1 ? NN * 16 + (KS - NN) * 32 : KF == 2 ? D : 2 * D;  // K row bytes
@@ -94,16 +94,16 @@ struct Slot {
   // code tables (CTABLES bytes), then kPairSlots pair tables of 2 KB.
   static constexpr int CTABLES = KF == 2 && D == 64 ? 3584 : KF >= 1 ? KS * 2048 : 0;
   static constexpr int TABLES = CTABLES + (KF == 2 ? kPairSlots * 2048 : 0);
-  static constexpr int RING = VF && kRing * kWaves * BYTES + TABLES > kLdsLimit ? 1 : kRing;
+  static constexpr int RING = VF && kRing * NW * BYTES + TABLES > kLdsLimit ? 1 : kRing;
   static constexpr int AHEAD = RING - 1;
-  static constexpr int DYN = RING * kWaves * BYTES;  // dynamic LDS: the ring (the tables are static)
+  static constexpr int DYN = RING * NW * BYTES;  // dynamic LDS: the ring (the tables are static)
   // Decode-step append: the new token's wave encodes it with its last ring
   // slot as scratch (from offset 0) and a copy of its KV head's tables header,
   // code LUT and centroid books (from ENC_OFF, ENC_DMAS 1 KB pieces).
   static constexpr int ENC_OFF = KF >= 1 ? (row_enc::scratch_bytes(D) + 1023) / 1024 * 1024 : 0;
   static constexpr int ENC_DMAS = KF >= 1 ? (BYTES - ENC_OFF) / 1024 : 0;
   static_assert(DYN + TABLES <= kLdsLimit, "LDS of one workgroup");
-  static_assert(VF || !SMALL2 || 2 * (DYN + TABLES) <= kLdsLimit, "two workgroups per CU");
+  static_assert(VF || NW != kWaves || !SMALL2 || 2 * (DYN + TABLES) <= kLdsLimit, "two workgroups per CU");
   static_assert(AHEAD >= (VF ? 0 : 1) && AHEAD <= 3, "ring waits cover up to three chunks in flight");
 };
 
@@ -193,14 +193,14 @@ __device__ __noinline__ void merge_one_round(float *part, float *out, float *sta
   }
 }
 
-// Row-wise prefill split merge (PF). Wave w merges the unit's columns w,
-// w + 4, ... (NH of them), all their loads in flight at once. Partial rows are
+// Row-wise prefill split merge (PF). Wave w of NW merges the unit's columns
+// w, w + NW, ... (NH of them), all their loads in flight at once. Partial rows are
 // o[D], m, l, pad (16-byte aligned). A lane is (split group sg, dimension
 // quad dq): it loads the o quads of splits sg, sg + SG, ... as 16-byte loads
 // and lane s the (m, l) of split s; the weights reach the lanes by lane
 // reads and the split groups' sums meet through lane swaps. Inlined, so the
 // buffer resource's base stays in scalar registers.
-template <int D, int SMAX, int NH>
+template <int D, int SMAX, int NH, int NW>
 __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeRows mr, int S, int wave, int lane) {
   constexpr int DQ = D / 4;                // dimension quads
   constexpr int SG = 64 / DQ;              // split groups (4 at d=64, 2 at d=128)
@@ -211,13 +211,13 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
   if (wave >= G) return;
   const int sg = lane / DQ, dq = lane - sg * DQ;
   const int sl = min(lane, S - 1);
-  // The unit's partials: 4 NH columns x S rows.
-  const __amdgpu_buffer_rsrc_t r = rsrc(part + mr.pbase * S * (D + 4), 4u * NH * (uint32_t)S * ROWB);
+  // The unit's partials: NW NH columns x S rows.
+  const __amdgpu_buffer_rsrc_t r = rsrc(part + mr.pbase * S * (D + 4), (uint32_t)(NW * NH) * (uint32_t)S * ROWB);
   u32x2 ml[NH];
   f32x4 o[NH][J];
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
-    const int g = wave + 4 * h;
+    const int g = wave + NW * h;
     const uint32_t col = (uint32_t)(g < G ? g : wave) * (uint32_t)S * ROWB;
     ml[h] = coherent_load2(r, col + (uint32_t)sl * ROWB + D * 4);
 #pragma unroll
@@ -226,7 +226,7 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
       o[h][j] = coherent_load4(r, col + (uint32_t)s * ROWB + 16u * dq);
     }
   }
-  // The four columns step by step side by side (no branch between them), so
+  // The columns step by step side by side (no branch between them), so
   // their chains of lane reductions overlap; only the stores are predicated.
   float m[NH], w[NH], Lsum[NH];
 #pragma unroll
@@ -282,7 +282,7 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
     }
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
-    const int g = wave + 4 * h;
+    const int g = wave + NW * h;
     // One reciprocal per column (within an ulp; the outputs' tolerance is 1e-4 relative).
     const float inv = __builtin_amdgcn_rcpf(Lsum[h]);
     if (g < G && sg == 0)
@@ -305,11 +305,16 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
 // split at least); the others exit before their first chunk.
 // VF: V rows of FP32 values (1; decode without an appended token) or FP16
 // (0). FP32 V enters the PV MFMAs as three FP16 parts per value.
-template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0>
-__global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
+// NW: waves per workgroup (4; row-wise prefill at d=64, 8: a unit's splits
+// then cover twice the tokens each and half as many partials are merged).
+template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves>
+__global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
-  using Sl = Slot<D, KF, NN, VF>;
+  using Sl = Slot<D, KF, NN, VF, NW>;
   static_assert(VF == 0 || PF == 0, "FP32 V: decode only");
+  static_assert(NW == kWaves || PF != 0, "decode: four waves");
+  static_assert(NW == 4 || NW == 8, "waves per workgroup");
+  constexpr int kWaves = NW, kThreads = 64 * NW;
   static_assert(PF == 0 || PF == 8 || PF == 16, "row-wise unit width");
   constexpr int UC = PF ? PF : 16;  // columns of a row-wise unit
   static_assert(KF == 0 || row_enc::scratch_bytes(D) <= Sl::BYTES, "append scratch fits a ring slot");
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   constexpr int RB = Sl::RB, KI = Sl::KI, L = Sl::L, AHEAD = Sl::AHEAD;
   static_assert(NN >= 0 && NN <= KS && SG >= 1 && SG <= KS, "layout");
   static_assert(Sl::BYTES >= 16 * (D + 4) * 4, "q staging fits one ring slot");
-  static_assert(KF == 0 || Gm::DT % kWaves == 0, "rotation tiles split evenly over the waves");
+  static_assert(KF == 0 || Gm::DT % kWaves == 0 || kWaves % Gm::DT == 0, "rotation tiles split evenly over the waves");
   static_assert(KF != 2 || (NN >= 1 && NN <= 2), "one or two scale DMAs");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= kWaves * 16 * (D + 2) * 4, "wave merge fits the ring");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
@@ -476,7 +481,10 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) qload[s][hh] = src[8 * s + 2 * gq + hh];
   }
-  constexpr int NT = KF >= 1 ? DT / kWaves : 1;  // 16-row tiles of the rotation per wave
+  // 16-row tiles of the rotation per wave (more waves than tiles: the first DT
+  // waves take one each).
+  constexpr int NT = KF >= 1 && DT >= kWaves ? DT / kWaves : 1;
+  const bool rot_wave = KF >= 1 && wave * NT < DT;
   u32x4 rq[NT][KS][2];
   // A query already in the code domain (q_rotated) is the QK operand as loaded.
   const bool rotate = KF >= 1 && !p.q_rotated;
@@ -486,7 +494,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const int at = (((wave * NT + t) * KS + s) * 64 + lane) * 2;
+        const int at = ((((rot_wave ? wave * NT : 0) + t) * KS + s) * 64 + lane) * 2;
         rq[t][s][0] = op[at];
         rq[t][s][1] = op[at + 1];
       }
@@ -704,6 +712,7 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
     const float unscale = __builtin_ldexpf(1.0f, -e0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
+      if (!rot_wave) break;  // wave-uniform: waves past the tiles only read the result
       f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -1419,8 +1428,9 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   if (PF) {
     const MergeRows mr{pbase, (int64_t)b * rows * Hq + hq0, UC * qg, G, Hq, ncol};
     static_assert(kPrefillMaxSplits == 16, "merge_rows instances");
-    if (S <= 8) merge_rows<D, 8, UC / 4>(p.part, p.out, mr, S, wave, lane);
-    else merge_rows<D, 16, UC / 4>(p.part, p.out, mr, S, wave, lane);
+    static_assert(UC % NW == 0, "merge_rows: whole columns per wave");
+    if (S <= 8) merge_rows<D, 8, UC / NW, NW>(p.part, p.out, mr, S, wave, lane);
+    else merge_rows<D, 16, UC / NW, NW>(p.part, p.out, mr, S, wave, lane);
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -1484,20 +1494,20 @@ __global__ __launch_bounds__(kThreads) void decode_fast_kernel(DecodeParams p, F
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int KF, int NN, int SG, int PK, int PF, int VF = 0>
+template <int D, int KF, int NN, int SG, int PK, int PF, int VF = 0, int NW = kWaves>
 hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
-  static const hipError_t allowed = hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF, VF>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                        Slot<D, KF, NN, VF>::DYN);
+  static const hipError_t allowed =
+      hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN, VF, NW>::DYN);
   if (allowed != hipSuccess) {
     (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
     return allowed;
   }
-  constexpr int lds = Slot<D, KF, NN, VF>::DYN;
+  constexpr int lds = Slot<D, KF, NN, VF, NW>::DYN;
   const dim3 grid = PF ? dim3((unsigned)p.kv_heads, (unsigned)(p.batch * p.qgroups), (unsigned)p.splits)
                        : dim3((unsigned)p.splits, (unsigned)p.kv_heads, (unsigned)p.batch);
-  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF, VF>), grid, dim3(kThreads), lds, stream, p, fl);
+  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW>), grid, dim3(64 * NW), lds, stream, p, fl);
   return hipGetLastError();
 }
 
@@ -1510,8 +1520,9 @@ hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t s
     return launch_mode<D, KF, NN, SG, PK, 0, 1>(p, fl, stream);
   }
   if (!p.starts) return launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream);
-  return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8>(p, fl, stream)
-                          : launch_mode<D, KF, NN, SG, PK, 16>(p, fl, stream);
+  constexpr int NW = decode_fast_prefill_waves(D);
+  return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW>(p, fl, stream)
+                          : launch_mode<D, KF, NN, SG, PK, 16, 0, NW>(p, fl, stream);
 }
 
 }  // namespace
