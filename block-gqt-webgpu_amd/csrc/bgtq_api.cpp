@@ -997,6 +997,21 @@ static int choose_splits(int64_t units, uint32_t max_length, int32_t requested) 
   return (int)std::min<int64_t>(want, max_splits);
 }
 
+// Decodes of few (sequence, KV head) units at d=64 on a structured layout or
+// FP16 K (at most one four-wave workgroup per compute unit): eight-wave
+// workgroups, each split covering twice the tokens (256), so the last
+// workgroup of a unit merges half as many partials (C2 step 289 -> 276 us).
+// The per-position path (nn < 0) measured slower that way (339 -> 372 us)
+// and keeps four. The split count only shrinks, so the workspace sized for
+// four waves still holds the partials. Forced split counts keep four waves.
+static void choose_waves(DecodeParams &p, int nn) {
+  p.waves = 4;
+  if (p.dim != 64 || p.splits_forced || nn < 0 || p.v_dtype != BGTQ_DTYPE_F16) return;
+  if ((int64_t)p.batch * p.kv_heads * p.splits > device_cus()) return;
+  p.waves = 8;
+  p.splits = (int)std::min<int64_t>(p.splits, std::max<int64_t>(1, ((int64_t)p.max_length + 255) / 256));
+}
+
 struct DecodeWorkspace {
   size_t counters, qr, part, stats, total;
 };
@@ -1179,6 +1194,7 @@ static bgtq_status launch_decode_common(bgtq_context *ctx, DecodeParams &p, cons
     fused = true;
   }
   if (fused) {
+    if (!p.starts) choose_waves(p, nn);
     HIP_TRY(launch_decode_fast(p, fl, nn, sg, ctx->stream), "decode launch");
     if (p.probs) HIP_TRY(launch_decode_probs(p, ctx->stream), "probabilities launch");
     return BGTQ_OK;
@@ -1274,7 +1290,8 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
   p.max_length = (int32_t)d->max_length;
   p.ends = nullptr;
   p.splits = splits;
-  p.split_tokens = (int)((d->max_length + splits - 1) / splits);
+  p.splits_forced = d->splits > 0;
+  p.split_tokens = (int)((d->max_length + p.splits - 1) / p.splits);
   p.split_tokens = ((p.split_tokens + 127) / 128) * 128;
   p.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
   p.out = d->out;
@@ -1301,6 +1318,7 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
     if (!fused)
       return fail(BGTQ_ERR_UNSUPPORTED,
                   "decode_append needs the fused kernel's layouts; use bgtq_encode_batched and bgtq_decode");
+    choose_waves(p, nn);
     HIP_TRY(launch_decode_fast(p, fl, nn, sg, ctx->stream), "decode append launch");
     return BGTQ_OK;
   }

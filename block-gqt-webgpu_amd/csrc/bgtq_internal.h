@@ -152,6 +152,8 @@ struct DecodeParams {
   int64_t k_seq_stride, k_head_stride;  // elements
   const void *v;
   int32_t v_dtype;  // 0 = FP32, 1 = FP16
+  int32_t waves;          // decode workgroup waves of the fused kernel: 8 (d=64, few units), else 4
+  int32_t splits_forced;  // the caller fixed the split count
   int32_t v_f32_split;  // FP32 V with every |v| < 65504: the fused kernel may split it into FP16 parts
   int64_t v_seq_stride, v_head_stride;  // elements
   const float *q;         // [B*Hq*dim] queries

@@ -126,9 +126,10 @@ struct MergeRows {
   }
 };
 
-template <int D, int SMAX>
+template <int D, int SMAX, int NW>
 __device__ __noinline__ void merge_one_round(float *part, float *out, float *stats, int64_t head0, int G, int S,
                                              int wave, int lane) {
+  constexpr int kWaves = NW;
   static_assert(SMAX <= 64, "one split per lane");
   constexpr int DL = D / 64;  // dimensions per lane
   constexpr int NH = 2;       // heads of one wave merged together (heads g and g + 4)
@@ -312,7 +313,6 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   using Gm = Geo<D>;
   using Sl = Slot<D, KF, NN, VF, NW>;
   static_assert(VF == 0 || PF == 0, "FP32 V: decode only");
-  static_assert(NW == kWaves || PF != 0, "decode: four waves");
   static_assert(NW == 4 || NW == 8, "waves per workgroup");
   constexpr int kWaves = NW, kThreads = 64 * NW;
   static_assert(PF == 0 || PF == 8 || PF == 16, "row-wise unit width");
@@ -1435,9 +1435,9 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     return;
   }
   if (S <= kMergeOneRound) {
-    if (S <= 8) merge_one_round<D, 8>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
-    else if (S <= 16) merge_one_round<D, 16>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
-    else merge_one_round<D, kMergeOneRound>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
+    if (S <= 8) merge_one_round<D, 8, NW>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
+    else if (S <= 16) merge_one_round<D, 16, NW>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
+    else merge_one_round<D, kMergeOneRound, NW>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -1519,7 +1519,11 @@ hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t s
     if (p.starts || p.k_new) return hipErrorInvalidValue;
     return launch_mode<D, KF, NN, SG, PK, 0, 1>(p, fl, stream);
   }
-  if (!p.starts) return launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream);
+  if (!p.starts) {
+    if constexpr (D == 64)
+      if (p.waves == 8) return launch_mode<D, KF, NN, SG, PK, 0, 0, 8>(p, fl, stream);
+    return launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream);
+  }
   constexpr int NW = decode_fast_prefill_waves(D);
   return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW>(p, fl, stream)
                           : launch_mode<D, KF, NN, SG, PK, 16, 0, NW>(p, fl, stream);
