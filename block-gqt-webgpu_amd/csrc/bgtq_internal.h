@@ -59,8 +59,9 @@ struct DevTables {
   //             code table plus its field width), gmask[4][4] (per slot i, the
   //             fp16 halves of the 8 positions in group glo + i), then for a
   //             pair K-step phi[4] and plo[4]: the LDS offsets, among the pair
-  //             slots (kPairSlots of 2 KB: hi pairs, then lo pairs), of the
-  //             pair table entries of positions 2 k2, 2 k2 + 1. A pair K-step
+  //             slots (kPairSlots of 2 KB, 8-byte (hi pair, lo pair) entries),
+  //             of the pair tables of positions 2 k2, 2 k2 + 1 (plo = phi + 1024,
+  //             unused by the kernel, which reads both halves at phi). A pair K-step
   //             (all 32 positions nibble codes, each even position in the book
   //             of the next; only leading K-steps, pair_lead of them) reads
   //             two codes per packed byte.

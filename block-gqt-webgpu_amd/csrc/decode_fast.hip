@@ -458,8 +458,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         }
       }
     }
-    // The pair tables ([byte]: hi pair, lo pair) of the pair K-steps' books,
-    // split into a table of hi pairs and one of lo pairs (1 KB each).
+    // The pair tables ([byte]: hi pair, lo pair, 8 bytes) of the pair
+    // K-steps' books, 2 KB each: one 8-byte read per packed byte.
     const uint32_t pair_books = fl.gpair[kv];
 #pragma unroll
     for (int ps = 0; ps < (PK > 0 ? kPairSlots : 0); ++ps) {
@@ -467,9 +467,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       if (bk != 0xffu) {
         const __amdgpu_buffer_rsrc_t rt = rsrc(fl.mfma[kv] + bk * kMfmaTableBytes, 2048);
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-          dma4(rt, tabs + Sl::CTABLES + ps * 2048 + (q & 1) * 1024 + (q >> 1) * 256,
-               ((q >> 1) * 64 + lane) * 8 + (q & 1) * 4, 0);
+        for (int q = 0; q < 2; ++q) dma16(rt, tabs + Sl::CTABLES + ps * 2048 + q * 1024, q * 1024 + lane * 16, 0);
       }
     }
   }
@@ -801,7 +799,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       hib[s] = (int)grec[s][0][1];
       glo[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][2]);
       nsl[s] = (int)__builtin_amdgcn_readfirstlane(grec[s][0][3]);
-      // A pair K-step keeps its pair table offsets in tbo (hi) and ext (lo).
+      // A pair K-step keeps its pair table offsets in tbo (ext unused).
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         ext[s][k] = s < PK ? (k < 4 ? grec[s][10][k] : 0u) : grec[s][1 + (k >> 2)][k & 3];
@@ -1049,13 +1047,14 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
           u32x4 hi, lo;
           if (s < PK) {
             // Pair K-step: the lane's 8 nibble codes are the 4 bytes of w0;
-            // each byte's pair table entries are an (hi, lo) operand pair.
+            // each byte's pair table entry is an (hi, lo) operand pair.
             const uint8_t *pt = tabs + Sl::CTABLES;
 #pragma unroll
             for (int k2 = 0; k2 < 4; ++k2) {
-              const uint32_t byte4 = 4 * __builtin_amdgcn_ubfe(w0[s][u], 8 * k2, 8);
-              hi[k2] = *reinterpret_cast<const uint32_t *>(pt + tbo[s][k2] + byte4);
-              lo[k2] = *reinterpret_cast<const uint32_t *>(pt + ext[s][k2] + byte4);
+              const uint32_t byte8 = 8 * __builtin_amdgcn_ubfe(w0[s][u], 8 * k2, 8);
+              const u32x2 e2 = *reinterpret_cast<const u32x2 *>(pt + tbo[s][k2] + byte8);
+              hi[k2] = e2[0];
+              lo[k2] = e2[1];
             }
           } else {
 #pragma unroll
