@@ -763,6 +763,12 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     kq = __builtin_ldexpf(kLog2e, -(eq + ec));
   }
   if (rotate) lds_barrier();  // q staging (last ring slot) is dead
+  // Row-wise prefill computes its chunks in pairs: the second ring slot's
+  // chunk goes out once the query staging no longer needs that slot.
+  if constexpr (PF != 0) {
+    static_assert(Sl::RING == 2 && AHEAD == 1, "row-wise pairs fill both ring slots");
+    issue(1);
+  }
 
   // KF 2: a K-step spans up to kSlots adjacent groups glo[s] .. glo[s] +
   // nsl[s] - 1. Each group's part of the K-step runs MFMAs against the query
@@ -961,32 +967,11 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   const int trow = 4 * gq + (col >> 2);
   const int tpiece = (col & 3) >> 1, thalf = (col & 1) * 8;
 
-  for (int i = 0; i < n_chunks; ++i) {
-    const int c0 = first + i * stride;
-    // Refill the buffer computed on last iteration with chunk i + AHEAD, then
-    // wait for chunk i: its DMA is older than the (up to AHEAD) chunks issued
-    // after it. With materialised logits the loop also stores, so wait for all.
-    if (i + AHEAD < n_chunks) {
-      wait_lds();
-      issue(i + AHEAD);
-    }
-    const int newer = p.logits ? 0 : min(n_chunks - 1 - i, AHEAD);
-    if (newer == AHEAD) wait_vm<AHEAD * L>();
-    else if (AHEAD > 2 && newer == 2) wait_vm<2 * L>();
-    else if (newer >= 1) wait_vm<L>();
-    else wait_vm<0>();
-    const uint8_t *sb = slot_base(i % Sl::RING);
+  // This lane's logits of the chunk in ring slot sb (first token c0): head
+  // col, tokens c0 + 16 u + 4 gq + r in x[4 u + r], log2 domain, masked past
+  // the causal ends.
+  auto chunk_logits = [&](const uint8_t *sb, int c0, float (&x)[8]) {
     const uint8_t *kbuf = sb + Sl::KOFF;
-    if (i == i_new) {  // the appended row over the chunk's LDS copy (wave-uniform)
-      // Packed K: the new token's logit is masked here (the encoder counts
-      // it), so only its V row has to be finite.
-      const int r = t_new % kChunk;
-      uint8_t *wsb = const_cast<uint8_t *>(sb);
-      if (lane < PR) *reinterpret_cast<u32x4 *>(wsb + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = v_new16;
-      if (KF == 0 && lane < PR)
-        *reinterpret_cast<u32x4 *>(wsb + Sl::KOFF + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = k_new16;
-    }
-
     // KF 2: transpose the scale rows (every read of the wave's slot precedes
     // its writes: one wave's LDS operations complete in order).
     if (KF == 2) {
@@ -1158,7 +1143,6 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       }
     }
     // logits of this lane: head col, tokens c0 + 16u + 4gq + r
-    float x[8];
 #pragma unroll
     for (int u = 0; u < 2 && KF == 2; ++u) {
 #pragma unroll
@@ -1193,55 +1177,10 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         x[j] = tok < lim ? x[j] : -INFINITY;
       }
     }
-    if (p.logits) {  // materialised logits for inspect() (natural units)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
-        if (head_ok && tok < t_logit) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + tok] = x[j] * kLn2;
-      }
-    }
-    // online softmax (log2 domain) for head col
-    float mloc = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-    const float m_new = fmaxf(m_run, col_max(mloc));
-    const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    const float mb = (m_new == -INFINITY ? 0.0f : m_new) - 15.0f;
-    float pr[8], psum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      pr[j] = __builtin_amdgcn_exp2f(x[j] - mb);
-      psum += pr[j];
-    }
-    l_run = __builtin_fmaf(l_run, alpha, psum);
-    m_run = m_new;
-    u32x4 ph, pl;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t h, l;
-      split2(pr[2 * k], pr[2 * k + 1], h, l);
-      ph[k] = h;
-      pl[k] = l;
-    }
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float ar = __shfl(alpha, 4 * gq + r, 64);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) O[dt][r] *= ar;
-      }
-    }
-    // PV: B operand = V[tokens of this lane's P slots][16 dt + col], read
-    // transposed (inline asm with explicit LDS waits; the appended row's LDS
-    // stores above are ordered before the reads by the memory clobber).
-    // Before them the wave waits for the chunk issued at the top of this
-    // iteration, so each wave has loads in flight only during the first half
-    // of an iteration. Measured at 64 x 32768 tokens (layout B), this is
-    // faster than keeping a ring full across iterations: 6264 GB/s against
-    // 5826 for these two slots waited for at the next iteration's top, 5780
-    // for three slots (two chunks ahead), 6170 for three slots waited for
-    // here. PF: the history is in L2 and the ring deeper, so only the chunk
-    // computed is waited for (at the top of the iteration).
-    if (!PF) wait_vm<0>();
-    const half8 pha = __builtin_bit_cast(half8, ph), pla = __builtin_bit_cast(half8, pl);
+  };
+  // PV of the chunk in ring slot sb: O += P V, P split into fp16 hi (pha) and
+  // lo (pla) parts in A-operand order.
+  auto chunk_pv = [&](const uint8_t *sb, const half8 pha, const half8 pla) {
     if constexpr (VF) {
       // FP32 V: lane (gq, col) reads V[16 (j >> 2) + 4 gq + (j & 3)][16 dt + col],
       // the B operand of its P slots j = 0..7 (row reads; the four lane groups
@@ -1292,6 +1231,144 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         O[dt] = mfma(pla, vb, O[dt]);
       }
     }
+  };
+
+  if constexpr (PF != 0) {
+    // Row-wise prefill: a wave takes its chunks two at a time, one per ring
+    // slot, as one 64-token step. The two chunks' lookups and QK products are
+    // independent chains the scheduler interleaves, and one softmax update
+    // (maximum, rescale) covers both. A chunk past the history (the second of
+    // an odd count) arrived as zeros and is masked whole.
+    for (int i = 0; i < n_chunks; i += 2) {
+      if (i > 0) {  // the previous pair's reads of both slots have completed
+        wait_lds();
+        issue(i);
+        issue(i + 1);
+      }
+      float x[2][8];
+      wait_vm<L>();  // chunk i has landed; chunk i + 1 may still be in flight
+      chunk_logits(slot_base(0), first + i * stride, x[0]);
+      wait_vm<0>();
+      chunk_logits(slot_base(1), first + (i + 1) * stride, x[1]);
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        mloc = fmaxf(mloc, fmaxf(fmaxf(fmaxf(x[c][0], x[c][1]), fmaxf(x[c][2], x[c][3])),
+                                 fmaxf(fmaxf(x[c][4], x[c][5]), fmaxf(x[c][6], x[c][7]))));
+      const float m_new = fmaxf(m_run, col_max(mloc));
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float mb = (m_new == -INFINITY ? 0.0f : m_new) - 15.0f;
+      float pr[2][8], psum = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          pr[c][j] = __builtin_amdgcn_exp2f(x[c][j] - mb);
+          psum += pr[c][j];
+        }
+      l_run = __builtin_fmaf(l_run, alpha, psum);
+      m_run = m_new;
+      u32x4 ph[2], pl[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t h, l;
+          split2(pr[c][2 * k], pr[c][2 * k + 1], h, l);
+          ph[c][k] = h;
+          pl[c][k] = l;
+        }
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, 4 * gq + r, 64);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) O[dt][r] *= ar;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        chunk_pv(slot_base(c), __builtin_bit_cast(half8, ph[c]), __builtin_bit_cast(half8, pl[c]));
+    }
+  } else {
+    for (int i = 0; i < n_chunks; ++i) {
+      const int c0 = first + i * stride;
+      // Refill the buffer computed on last iteration with chunk i + AHEAD, then
+      // wait for chunk i: its DMA is older than the (up to AHEAD) chunks issued
+      // after it. With materialised logits the loop also stores, so wait for all.
+      if (i + AHEAD < n_chunks) {
+        wait_lds();
+        issue(i + AHEAD);
+      }
+      const int newer = p.logits ? 0 : min(n_chunks - 1 - i, AHEAD);
+      if (newer == AHEAD) wait_vm<AHEAD * L>();
+      else if (AHEAD > 2 && newer == 2) wait_vm<2 * L>();
+      else if (newer >= 1) wait_vm<L>();
+      else wait_vm<0>();
+      const uint8_t *sb = slot_base(i % Sl::RING);
+      if (i == i_new) {  // the appended row over the chunk's LDS copy (wave-uniform)
+        // Packed K: the new token's logit is masked here (the encoder counts
+        // it), so only its V row has to be finite.
+        const int r = t_new % kChunk;
+        uint8_t *wsb = const_cast<uint8_t *>(sb);
+        if (lane < PR) *reinterpret_cast<u32x4 *>(wsb + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = v_new16;
+        if (KF == 0 && lane < PR)
+          *reinterpret_cast<u32x4 *>(wsb + Sl::KOFF + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = k_new16;
+      }
+
+      float x[8];
+      chunk_logits(sb, c0, x);
+      if (p.logits) {  // materialised logits for inspect() (natural units)
+  #pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
+          if (head_ok && tok < t_logit) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + tok] = x[j] * kLn2;
+        }
+      }
+      // online softmax (log2 domain) for head col
+      float mloc = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      const float m_new = fmaxf(m_run, col_max(mloc));
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float mb = (m_new == -INFINITY ? 0.0f : m_new) - 15.0f;
+      float pr[8], psum = 0.0f;
+  #pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pr[j] = __builtin_amdgcn_exp2f(x[j] - mb);
+        psum += pr[j];
+      }
+      l_run = __builtin_fmaf(l_run, alpha, psum);
+      m_run = m_new;
+      u32x4 ph, pl;
+  #pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t h, l;
+        split2(pr[2 * k], pr[2 * k + 1], h, l);
+        ph[k] = h;
+        pl[k] = l;
+      }
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, 4 * gq + r, 64);
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) O[dt][r] *= ar;
+        }
+      }
+      // PV: B operand = V[tokens of this lane's P slots][16 dt + col], read
+      // transposed (inline asm with explicit LDS waits; the appended row's LDS
+      // stores above are ordered before the reads by the memory clobber).
+      // Before them the wave waits for the chunk issued at the top of this
+      // iteration, so each wave has loads in flight only during the first half
+      // of an iteration. Measured at 64 x 32768 tokens (layout B), this is
+      // faster than keeping a ring full across iterations: 6264 GB/s against
+      // 5826 for these two slots waited for at the next iteration's top, 5780
+      // for three slots (two chunks ahead), 6170 for three slots waited for
+      // here. PF: the history is in L2 and the ring deeper, so only the chunk
+      // computed is waited for (at the top of the iteration).
+      if (!PF) wait_vm<0>();
+      const half8 pha = __builtin_bit_cast(half8, ph), pla = __builtin_bit_cast(half8, pl);
+      chunk_pv(sb, pha, pla);
+    }
   }
 
   // ---------------- epilogue ----------------
@@ -1310,24 +1387,39 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       comb[(wave * 16 + 4 * gq + r) * (D + 2) + 2 + 16 * dt + col] = O[dt][r] * (1.0f / kPScale);
   __syncthreads();
   if constexpr (!PF) {
-    // Decode: a loop over the G heads' elements (few heads: fewer than one
-    // element per thread).
-    for (int e = tid; e < G * D; e += kThreads) {
+    // Decode: the waves' states of each of the G heads merged by log-sum-exp,
+    // a thread per element (head g, dimension dm) in rounds of kThreads. A
+    // round's LDS reads of every wave's (m, l, o) are issued before any is
+    // used (threads past G D read head G - 1's and store nothing), and the
+    // waves without tokens (m = -inf) drop out through selects: a read under
+    // a per-wave test would be an LDS round trip of its own.
+    constexpr int EPR = (16 * D + kThreads - 1) / kThreads;  // rounds for up to 16 heads
+#pragma unroll
+    for (int k = 0; k < EPR; ++k) {
+      if (k * kThreads >= G * D) break;  // wave-uniform
+      const int e = tid + k * kThreads;
       const int g = e / D, dm = e - g * D;
+      const int gr = g < G ? g : G - 1;
+      float mw[kWaves], lw[kWaves], ow[kWaves];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float *c = comb + (w * 16 + gr) * (D + 2);
+        mw[w] = c[0];
+        lw[w] = c[1];
+        ow[w] = c[2 + dm];
+      }
       float M = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[(w * 16 + g) * (D + 2)]);
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mw[w]);
       float Lsum = 0.0f, Ov = 0.0f;
-      if (M != -INFINITY) {
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          const float *c = comb + (w * 16 + g) * (D + 2);
-          if (c[0] == -INFINITY) continue;
-          const float wt = exp2f(c[0] - M);
-          Lsum = __builtin_fmaf(c[1], wt, Lsum);
-          Ov = __builtin_fmaf(c[2 + dm], wt, Ov);
-        }
+      for (int w = 0; w < kWaves; ++w) {
+        const bool live = mw[w] != -INFINITY;
+        const float wt = exp2f(mw[w] - M);
+        Lsum = live ? __builtin_fmaf(lw[w], wt, Lsum) : Lsum;
+        Ov = live ? __builtin_fmaf(ow[w], wt, Ov) : Ov;
       }
+      if (g >= G) continue;
       const int64_t head = (int64_t)qrow * Hq + hq0 + g;
       if (S == 1) {
         p.out[head * D + dm] = Ov / Lsum;
