@@ -1027,7 +1027,8 @@ static DecodeWorkspace decode_ws(int64_t units, int64_t heads, int dim, int spli
   w.counters = 0;
   w.qr = al(sizeof(uint32_t) * kCounterStride * std::max<int64_t>(units, BGTQ_DECODE_COUNTER_UNITS));
   w.part = w.qr + al(sizeof(float) * heads * dim);
-  w.stats = w.part + al(sizeof(float) * heads * splits * (dim + 2));
+  // Partials of the splits and of a decode-step append's token (one more per head).
+  w.stats = w.part + al(sizeof(float) * heads * (splits + 1) * (dim + 2));
   w.total = w.stats + al(sizeof(float) * heads * 2);
   return w;
 }

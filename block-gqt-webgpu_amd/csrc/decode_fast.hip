@@ -326,7 +326,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   static_assert(KF == 0 || Gm::DT % kWaves == 0 || kWaves % Gm::DT == 0, "rotation tiles split evenly over the waves");
   static_assert(KF != 2 || (NN >= 1 && NN <= 2), "one or two scale DMAs");
   static_assert(Sl::RING * kWaves * Sl::BYTES >= kWaves * 16 * (D + 2) * 4, "wave merge fits the ring");
-  static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 256 * 4, "split merge (<= 256 splits) fits the ring");
+  static_assert(Sl::RING * kWaves * Sl::BYTES >= 2 * 16 * 257 * 4, "split merge (<= 256 splits + append) fits the ring");
   extern __shared__ __align__(16) uint8_t smem[];
 
   // Grid (split, KV head, sequence); PF: (KV head, query group, split). The
@@ -521,19 +521,30 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // PF: the splits this unit's history needs (every workgroup of the unit
   // computes the same number); the others leave before their first chunk,
   // once the prologue's DMAs into their LDS have landed.
-  const int S = rowwise ? min(p.splits, max(1, (T_b + p.split_floor - 1) / p.split_floor)) : p.splits;
-  if (rowwise && split >= S) {
+  const int S_hist = rowwise ? min(p.splits, max(1, (T_b + p.split_floor - 1) / p.split_floor)) : p.splits;
+  if (rowwise && split >= S_hist) {
     wait_vm<0>();
     return;
   }
+  // Decode-step append with packed K: the sequence's new token (row T_b - 1)
+  // belongs to one more workgroup of its (sequence, KV head), split index
+  // p.splits (the append workgroup), which encodes and stores it, stores its
+  // V row and leaves the token's partial (m, l, o) like a split; the history
+  // splits attend to the tokens before it and never wait for the encode.
+  const bool app = !rowwise && KF >= 1 && p.k_new != nullptr;
+  const bool app_wg = app && split == p.splits;
+  const int S = S_hist + (app ? 1 : 0);  // partials merged per (sequence, KV head)
+  // Tokens the history splits attend to (the append workgroup: all of them,
+  // so its new token lies inside the causal limits).
+  const int T_att = app && !app_wg ? T_b - 1 : T_b;
   // Splits of one (sequence, KV head) interleave at chunk granularity: wave w
   // of split s takes chunks (s * 4 + w) + 4 S i, so the waves working on a
   // sequence at any moment sweep adjacent memory.
-  const int t_end = kInterleaved ? T_b : min(T_b, split * p.split_tokens + p.split_tokens);
-  const int stride = kInterleaved ? S * kWaves * kChunk : kWaves * kChunk;
+  const int t_end = kInterleaved ? T_att : min(T_att, split * p.split_tokens + p.split_tokens);
+  const int stride = kInterleaved ? S_hist * kWaves * kChunk : kWaves * kChunk;
   // This wave's chunks start at first + 128 i.
   const int first = kInterleaved ? (split * kWaves + wave) * kChunk : split * p.split_tokens + wave * kChunk;
-  const int n_chunks = first < t_end ? (t_end - first + stride - 1) / stride : 0;
+  const int n_chunks = !app_wg && first < t_end ? (t_end - first + stride - 1) / stride : 0;
   // Decode reads every byte once (non-temporal, nothing cached is displaced);
   // a row-wise prefill chunk's history is read by every unit of its KV head,
   // so those loads keep the default policy and the units share it in L2.
@@ -541,8 +552,10 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   auto issue = [&](int i) {
     const int c0 = first + i * stride;
     // Tokens of the chunk inside the sequence; none for a chunk past the end
-    // (a zero-sized descriptor: the DMA only writes zeros to LDS).
-    const int in_seq = min(T_b - c0, kChunk);
+    // (a zero-sized descriptor: the DMA only writes zeros to LDS). A history
+    // split's range ends before the appended token, so its row arrives as
+    // zeros; the append workgroup streams nothing.
+    const int in_seq = app_wg ? 0 : min(T_att - c0, kChunk);
     const uint32_t rest = __builtin_amdgcn_readfirstlane(in_seq > 0 ? in_seq : 0);  // wave-uniform: SGPR descriptor
     uint8_t *sb = slot_base(i % Sl::RING);
     const __amdgpu_buffer_rsrc_t rV = rsrc(v_rows + (int64_t)c0 * D * VB, rest * (VB * D));
@@ -587,22 +600,24 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
 
   // ---------------- decode-step append ----------------
   // With p.k_new the sequence's newest token (row T_b - 1) arrives in this
-  // launch. The wave whose chunk holds it (the owner) loads the new V row
-  // with the prologue's loads, converts it, stores it to the cache for the
-  // later steps and, after that chunk's loads land, writes it over the
-  // chunk's LDS copy (whose loads may have read the row before it was
-  // stored). FP16 K rows go the same way. Packed K takes longer to encode,
-  // so another wave of the workgroup (the encoder) does it while the owner
-  // works through its chunk without the new token: the encoder loads the
-  // new K (and, at d=64, its column of the transposed rotation) and V,
-  // encodes and stores the K row, and starts its own attention state with
-  // the new token (its logit from the row it encoded); the workgroup's merge
-  // of its waves' states then counts the token once.
+  // launch. FP16 K: the wave whose chunk holds it (the owner) loads the new
+  // K and V rows with the prologue's loads, converts them, stores them to
+  // the caches for the later steps and, after that chunk's loads land,
+  // writes them over the chunk's LDS copy (whose loads may have read the
+  // rows before they were stored). Packed K takes longer to encode, so the
+  // token goes to the append workgroup: its wave 0 (the owner) stores the
+  // new V row, and its wave 2 (the encoder) loads the new K (and, at d=64,
+  // its column of the transposed rotation) and V, encodes and stores the K
+  // row before the query rotation (the workgroup's other waves have no
+  // chunks to wait for), then starts its attention state with the new token
+  // (its logit from the row it encoded); the workgroup's merge of its waves'
+  // states gives the token's partial.
   constexpr int JL = D > 64 ? 2 : 1;
   const int t_new = T_b - 1;
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
-  const int own_w =
-      !VF && !rowwise && p.k_new != nullptr && t_new >= 0 ? c_new % (p.splits * kWaves) - split * kWaves : -1;
+  const int own_w = VF || rowwise || p.k_new == nullptr || t_new < 0 ? -1
+                    : app                                             ? (app_wg ? 0 : -1)
+                                                                      : c_new % (p.splits * kWaves) - split * kWaves;
   const bool owner = own_w == wave;
   const bool encoder = KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
   const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
@@ -691,6 +706,72 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   for (int s = 0; s < KS; ++s)
 #pragma unroll
     for (int k = 0; k < 8; ++k) qv[s][k] = head_ok ? qload[s][k >> 2][k & 3] : 0.0f;
+  if (encoder) {
+    // The append workgroup's encoder encodes and stores the new K row as
+    // soon as its own loads have landed (the tables' header, LUT and books
+    // in its last ring slot, the new K and V rows, the rotation column),
+    // ahead of the query rotation: its workgroup's other waves have no
+    // chunks, so the rotation's barriers cost them nothing.
+    // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
+    // T, lut, books: the LDS copy of the tables (header, LUT, books) loaded in
+    // the prologue; for KF 2 tables larger than the slot holds, the header in
+    // device memory with an LDS copy of the LUT and books, or (larger still)
+    // all three in device memory.
+    wait_vm<AHEAD * L>();
+    const uint8_t *enc_lds = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
+    const DevTables *T_dev = reinterpret_cast<const DevTables *>(p.tables[kv]);
+    const DevTables *T_use = reinterpret_cast<const DevTables *>(enc_lds);
+    const uint8_t *lut_use = tables_lut(T_use);
+    const float *books_use = tables_books(T_use);
+    if (KF == 2 && fl.enc_bytes[kv] == 0) {
+      T_use = T_dev;
+      lut_use = tables_lut(T_dev);
+      books_use = tables_books(T_dev);
+    } else if (KF == 2 && fl.enc_from[kv] != 0) {
+      T_use = T_dev;
+      lut_use = enc_lds;
+      books_use = reinterpret_cast<const float *>(enc_lds + (T_dev->off_books - T_dev->off_lut));
+    }
+    const DevTables *T = T_use;
+    const uint8_t *lut = lut_use;
+    const float *books = books_use;
+    lc.init(T, lane);
+    const int ndims = __builtin_amdgcn_readfirstlane(T->nibble_dims);  // read with the lane set-up
+    float x[JL];
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl) {
+      const int src = lc.perm[jl];
+      uint32_t raw = __shfl(k_nat[0], src & 63, 64);
+      if (JL > 1) {
+        const uint32_t hi = __shfl(k_nat[JL - 1], src & 63, 64);
+        raw = src >= 64 ? hi : raw;
+      }
+      const uint16_t h16 = p.k_new_f32 ? row_enc::f32_to_f16_bits(__uint_as_float(raw)) : (uint16_t)raw;
+      x[jl] = lc.own[jl] ? row_enc::f16_bits_to_f32(h16) : 0.0f;
+    }
+    // Scratch: this wave's last ring slot, loaded into only from the loop on.
+    const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
+    const float *rt = fl.rot_t[kv];
+    h_new = row_enc::encode_row<D>(
+        T, lc, x,
+        [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
+        lut, books, scr, lane);
+    // The packed row's bytes; they are stored after the rotation, so the
+    // rotation's wait for this wave's loads does not wait for the stores.
+    const int logical = ndims / 2 + D - ndims;
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl) pk_new[jl] = row_enc::packed_byte(scr.codes, lane + 64 * jl, ndims, logical);
+    // The new row in the code domain, k_j = c_j s_g(j) (positions j in
+    // head-perm order), and the FP16-rounded new V row, for its logits and
+    // its share of the output.
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl) {
+      const float sc = row_enc::f16_bits_to_f32((uint16_t)__shfl((int)h_new, lc.grp[jl], 64));
+      if (lc.own[jl]) scr.xn[lane + 64 * jl] = books[lc.bk[jl] * T->max_centroids + scr.codes[lane + 64 * jl]] * sc;
+    }
+    if (lane < PR) reinterpret_cast<u32x4 *>(scr.leaf)[lane] = half_piece(p.v_new_f32, v_raw);
+    row_enc::wave_sync();
+  }
   if (rotate) {
     // qr^T = Rq q^T, Rq = R with the head permutation folded into its
     // columns, on the matrix cores (q and Rq split hi/lo, three MFMAs per
@@ -856,86 +937,26 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
                                  8 * lane) = k_new16;
     }
   }
-  if (encoder) {  // encode the new K row, store it, start this wave's state with the new token
-    {
-      // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
-      // T, lut, books: the LDS copy of the tables (header, LUT, books) loaded in
-      // the prologue; for KF 2 tables larger than the slot holds, the header in
-      // device memory with an LDS copy of the LUT and books, or (larger still)
-      // all three in device memory.
-      auto encode_new = [&](const DevTables *T, const uint8_t *lut, const float *books) {
-        lc.init(T, lane);
-        const int ndims = __builtin_amdgcn_readfirstlane(T->nibble_dims);  // read with the lane set-up
-        float x[JL];
+  if (encoder) {  // the encoded row to the caches; the new token's logit from it
+    uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
 #pragma unroll
-        for (int jl = 0; jl < JL; ++jl) {
-          const int src = lc.perm[jl];
-          uint32_t raw = __shfl(k_nat[0], src & 63, 64);
-          if (JL > 1) {
-            const uint32_t hi = __shfl(k_nat[JL - 1], src & 63, 64);
-            raw = src >= 64 ? hi : raw;
-          }
-          const uint16_t h16 = p.k_new_f32 ? row_enc::f32_to_f16_bits(__uint_as_float(raw)) : (uint16_t)raw;
-          x[jl] = lc.own[jl] ? row_enc::f16_bits_to_f32(h16) : 0.0f;
-        }
-        // Scratch: this wave's last ring slot, loaded into only from the loop on.
-        const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
-        const float *rt = fl.rot_t[kv];
-        h_new = row_enc::encode_row<D>(
-            T, lc, x,
-            [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
-            lut, books, scr, lane);
-        const int logical = ndims / 2 + D - ndims;
-        uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
+    for (int jl = 0; jl < JL; ++jl)
+      if (lane + 64 * jl < rb) prow[lane + 64 * jl] = (uint8_t)pk_new[jl];
+    if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
+    const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
+    // Logit of head col: sum over this lane's positions 32 s + 8 gq + k of
+    // k_j (qhi + qlo)[s][k], then over the column's four lanes; the query
+    // operands carry 2^eq, kq * 2^ec takes it off (the centroids here are
+    // not scaled by 2^ec).
+    float part = 0.0f;
 #pragma unroll
-        for (int jl = 0; jl < JL; ++jl) {
-          const int bb = lane + 64 * jl;
-          if (bb < rb) {
-            pk_new[jl] = row_enc::packed_byte(scr.codes, bb, ndims, logical);
-            prow[bb] = (uint8_t)pk_new[jl];
-          }
-        }
-        if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
-        // The new row in the code domain, k_j = c_j s_g(j) (positions j in
-        // head-perm order), and the FP16-rounded new V row, for its logits and
-        // its share of the output.
+    for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
-        for (int jl = 0; jl < JL; ++jl) {
-          const float sc = row_enc::f16_bits_to_f32((uint16_t)__shfl((int)h_new, lc.grp[jl], 64));
-          if (lc.own[jl]) scr.xn[lane + 64 * jl] = books[lc.bk[jl] * T->max_centroids + scr.codes[lane + 64 * jl]] * sc;
-        }
-        if (lane < PR) reinterpret_cast<u32x4 *>(scr.leaf)[lane] = half_piece(p.v_new_f32, v_raw);
-        row_enc::wave_sync();
-        // Logit of head col: sum over this lane's positions 32 s + 8 gq + k of
-        // k_j (qhi + qlo)[s][k], then over the column's four lanes; the query
-        // operands carry 2^eq, kq * 2^ec takes it off (the centroids here are
-        // not scaled by 2^ec).
-        float part = 0.0f;
-#pragma unroll
-        for (int s2 = 0; s2 < KS; ++s2)
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            part = __builtin_fmaf(scr.xn[32 * s2 + 8 * gq + k], (float)qhi[s2][k] + (float)qlo[s2][k], part);
-        const float xt = col_sum(part) * __builtin_ldexpf(kq, ec);
-        new_x = head_ok && t_new < lim ? xt : -INFINITY;
-        if (p.logits && head_ok) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
-      };
-      const uint8_t *enc_lds = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
-      const DevTables *T_dev = reinterpret_cast<const DevTables *>(p.tables[kv]);
-      const DevTables *T_use = reinterpret_cast<const DevTables *>(enc_lds);
-      const uint8_t *lut_use = tables_lut(T_use);
-      const float *books_use = tables_books(T_use);
-      if (KF == 2 && fl.enc_bytes[kv] == 0) {
-        T_use = T_dev;
-        lut_use = tables_lut(T_dev);
-        books_use = tables_books(T_dev);
-      } else if (KF == 2 && fl.enc_from[kv] != 0) {
-        T_use = T_dev;
-        lut_use = enc_lds;
-        books_use = reinterpret_cast<const float *>(enc_lds + (T_dev->off_books - T_dev->off_lut));
-      }
-      encode_new(T_use, lut_use, books_use);
-    }
+      for (int k = 0; k < 8; ++k)
+        part = __builtin_fmaf(scr.xn[32 * s2 + 8 * gq + k], (float)qhi[s2][k] + (float)qlo[s2][k], part);
+    const float xt = col_sum(part) * __builtin_ldexpf(kq, ec);
+    new_x = head_ok && t_new < lim ? xt : -INFINITY;
+    if (p.logits && head_ok) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
   }
 
   const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
@@ -1528,6 +1549,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   if (S <= kMergeOneRound) {
     if (S <= 8) merge_one_round<D, 8, NW>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     else if (S <= 16) merge_one_round<D, 16, NW>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
+    else if (S <= 24) merge_one_round<D, 24, NW>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     else merge_one_round<D, kMergeOneRound, NW>(p.part, p.out, p.stats, (int64_t)qrow * Hq + hq0, G, S, wave, lane);
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
@@ -1596,8 +1618,11 @@ hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t 
     return allowed;
   }
   constexpr int lds = Slot<D, KF, NN, VF, NW>::DYN;
+  // Decode-step append with packed K: one more workgroup per (sequence, KV
+  // head) for the new token.
+  const unsigned app = !PF && KF >= 1 && p.k_new ? 1u : 0u;
   const dim3 grid = PF ? dim3((unsigned)p.kv_heads, (unsigned)(p.batch * p.qgroups), (unsigned)p.splits)
-                       : dim3((unsigned)p.splits, (unsigned)p.kv_heads, (unsigned)p.batch);
+                       : dim3((unsigned)p.splits + app, (unsigned)p.kv_heads, (unsigned)p.batch);
   hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW>), grid, dim3(64 * NW), lds, stream, p, fl);
   return hipGetLastError();
 }
