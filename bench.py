@@ -528,6 +528,14 @@ class PrefillWorkload:
         need = max(batched.prefill_workspace_bytes(batched.prefill_desc(**a)) for a in args_list)
         self.ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
         self.descs = [batched.prefill_desc(workspace=self.ws, **a) for a in args_list]
+        # the chunk's own K and V rows, [B=1, rows, Hkv, dim], for the one-launch form (bgtq_prefill_append)
+        self.apps = []
+        if chunk <= 32:
+            for c, s in enumerate(starts):
+                rows = min(chunk, prompt - s)
+                for l in range(layers):
+                    self.apps.append(batched.prefill_append_desc(k_new=self.k[l, :, s:s + rows].transpose(0, 1)[None],
+                                                                 v_new=self.v[l, 0, :, s:s + rows].transpose(0, 1)[None]))
 
     def attend_only(self):
         from bgtq import batched
@@ -539,6 +547,12 @@ class PrefillWorkload:
         for e, d in zip(self.enc, self.descs):
             batched.encode(self.dev, e, "f16")
             batched.prefill(self.dev, d)
+
+    def step_fused(self):
+        """The same prompt with each chunk's K encode and V append inside its attention launch."""
+        from bgtq import batched
+        for d, a in zip(self.descs, self.apps):
+            batched.prefill_append(self.dev, d, a)
 
     def flops(self):
         return prefill_flops(self.prompt, HQ, DIM, self.layers)
@@ -554,8 +568,14 @@ def qwen_prefill(dev, steps, layout="B", chunk=0, prompt=4096, layers=LAYERS):
     flops = w.flops()
     ms = time_graph(torch, graph_of(torch, dev, w.step), steps, 2)
     ms_att = time_graph(torch, graph_of(torch, dev, w.attend_only), steps, 2)
+    fused = {}
+    if w.apps:
+        ms_f = time_graph(torch, graph_of(torch, dev, w.step_fused), steps, 2)
+        fused = {"one_launch_ms_per_prompt": round(ms_f, 4), "one_launch_tokens_per_s": round(prompt / (ms_f / 1e3)),
+                 "one_launch": "each chunk's K encode, V append and attention in one bgtq_prefill_append launch "
+                               "per layer (the K rows' bytes equal the two-launch form's)"}
     w.destroy()
-    return {"ms_per_prompt": round(ms, 4), "tokens_per_s": round(prompt / (ms / 1e3)),
+    return {"ms_per_prompt": round(ms, 4), "tokens_per_s": round(prompt / (ms / 1e3)), **fused,
             "attention_only_ms": round(ms_att, 4),
             "attention_tflops_algorithmic": round(flops / (ms_att / 1e3) / 1e12, 1),
             "mfma_frac_of_fp16_dense_peak": round(flops / (ms_att / 1e3) / 2.5e15, 4),

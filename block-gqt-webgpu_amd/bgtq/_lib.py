@@ -70,6 +70,13 @@ class AppendDesc(ctypes.Structure):
                 ("v_new_seq_stride", ctypes.c_int64), ("v_new_head_stride", ctypes.c_int64)]
 
 
+class PrefillAppendDesc(ctypes.Structure):
+    _fields_ = [("k_new", ctypes.c_void_p), ("k_new_dtype", ctypes.c_int32), ("k_new_seq_stride", ctypes.c_int64),
+                ("k_new_row_stride", ctypes.c_int64), ("k_new_head_stride", ctypes.c_int64),
+                ("v_new", ctypes.c_void_p), ("v_new_dtype", ctypes.c_int32), ("v_new_seq_stride", ctypes.c_int64),
+                ("v_new_row_stride", ctypes.c_int64), ("v_new_head_stride", ctypes.c_int64)]
+
+
 class PrefillDesc(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("rows", ctypes.c_int32), ("q_heads", ctypes.c_int32),
                 ("kv_heads", ctypes.c_int32), ("dim", ctypes.c_int32), ("key_format", ctypes.c_int32),
@@ -151,6 +158,7 @@ SIGNATURES = {
                                _VP, _VP]),
     "bgtq_prefill_workspace_size": (_I32, [ctypes.POINTER(PrefillDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "bgtq_prefill": (_I32, [_VP, ctypes.POINTER(PrefillDesc)]),
+    "bgtq_prefill_append": (_I32, [_VP, ctypes.POINTER(PrefillDesc), ctypes.POINTER(PrefillAppendDesc)]),
     "bgtq_model_submit": (_I32, [_VP, ctypes.POINTER(ModelDispatch), _SZ]),
     "bgtq_allocate_bits": (_I32, [_VP, _SZ, ctypes.c_int64, _I32, _I32, _VP]),
     "bgtq_layout_groups": (_I32, [_VP, _SZ, _VP, _VP, _VP]),

@@ -120,5 +120,22 @@ def prefill_workspace_bytes(desc) -> int:
     return n.value
 
 
+def prefill_append_desc(*, k_new, v_new):
+    """bgtq_prefill_append_desc over device tensors [B, rows, Hkv, dim] (FP32 or FP16, any strides in
+    elements)."""
+    a = _lib.PrefillAppendDesc()
+    dt = {"torch.float32": _lib.DTYPE_F32, "torch.float16": _lib.DTYPE_F16}
+    a.k_new, a.k_new_dtype = _addr(k_new), dt[str(k_new.dtype)]
+    a.k_new_seq_stride, a.k_new_row_stride, a.k_new_head_stride = k_new.stride(0), k_new.stride(1), k_new.stride(2)
+    a.v_new, a.v_new_dtype = _addr(v_new), dt[str(v_new.dtype)]
+    a.v_new_seq_stride, a.v_new_row_stride, a.v_new_head_stride = v_new.stride(0), v_new.stride(1), v_new.stride(2)
+    return a
+
+
+def prefill_append(device, desc, append) -> None:
+    """A prefill chunk with its own rows encoded and appended in the same launch (bgtq_prefill_append)."""
+    check(lib().bgtq_prefill_append(device.handle, ctypes.byref(desc), ctypes.byref(append)))
+
+
 def prefill(device, desc) -> None:
     check(lib().bgtq_prefill(device.handle, ctypes.byref(desc)))

@@ -224,7 +224,7 @@ struct bgtq_attention {
 extern "C" {
 
 const char *bgtq_last_error(void) { return g_error.c_str(); }
-int32_t bgtq_abi_version(void) { return 5; }
+int32_t bgtq_abi_version(void) { return 6; }
 
 // ---------------------------------------------------------------- context
 bgtq_status bgtq_context_create(int32_t device, bgtq_context **out) {
@@ -1308,6 +1308,7 @@ static bgtq_status decode_impl(bgtq_context *ctx, const bgtq_decode_desc *d, con
     p.v_new_f32 = a->v_new_dtype == BGTQ_DTYPE_F32;
     p.v_new_seq_stride = a->v_new_seq_stride;
     p.v_new_head_stride = a->v_new_head_stride;
+    p.app_parts = 1;  // packed K: one append workgroup per (sequence, KV head)
     FastLayout fl{};
     int nn = 0, sg = 0;
     p.q = d->q;
@@ -1336,6 +1337,7 @@ struct PrefillPlan {
   int unit_cols;     // rowwise: query columns per unit
   int splits;        // rowwise: token splits per unit (a unit uses those its history needs)
   int split_floor;   // rowwise: tokens per split at least
+  int app_parts;     // rowwise with appended rows: their workgroups per unit (one row per wave)
   size_t counters, part;  // rowwise: workspace offsets (the split counters first)
 };
 
@@ -1347,7 +1349,8 @@ struct PrefillPlan {
 // compute unit, sized here for the most work (every chunk at the end of the
 // cache: the starts are device values) and by the kernel for the actual one;
 // split_tokens > 0 fixes the range length instead.
-static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
+// append: the chunk's rows are appended in the same launch (bgtq_prefill_append).
+static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan, bool append = false) {
   if (!d) return fail(BGTQ_ERR_RANGE, "null descriptor");
   if (d->batch < 1 || d->rows < 1 || d->kv_heads < 1 || d->kv_heads > kMaxKvHeads || d->q_heads < d->kv_heads ||
       d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 16)
@@ -1386,14 +1389,22 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan) {
     int64_t splits = ((int64_t)d->max_length + floor_tok - 1) / floor_tok;
     if (d->split_tokens <= 0)
       splits = std::min<int64_t>(splits, std::max<int64_t>(1, per_cu * (int64_t)device_cus() / row_units));
+    // Appended rows: one more workgroup per unit for each wave's worth of
+    // rows, each leaving a partial; the merge takes up to kPrefillMaxSplits.
+    const int waves = decode_fast_prefill_waves(d->dim);
+    const int app_max = (d->rows + waves - 1) / waves;
+    plan->app_parts = append ? app_max : 0;
     plan->qgroups = (int)qgroups;
     plan->unit_cols = (int)uc;
-    plan->splits = (int)std::max<int64_t>(1, std::min<int64_t>(splits, kPrefillMaxSplits));
+    plan->splits = (int)std::max<int64_t>(1, std::min<int64_t>(splits, kPrefillMaxSplits - plan->app_parts));
     plan->split_floor = (int)std::max<int64_t>(floor_tok, ((int64_t)d->max_length + plan->splits - 1) / plan->splits);
     plan->counters = 0;
     plan->part = kPrefillCounterBytes;
-    // Partial rows o[dim], m, l, pad.
-    plan->workspace = kPrefillCounterBytes + sizeof(float) * (size_t)row_units * uc * plan->splits * (d->dim + 4);
+    // Partial rows o[dim], m, l, pad: the splits' and, whichever entry point
+    // takes the workspace, the appended rows' workgroups'.
+    const int64_t splits_plain = std::max<int64_t>(1, std::min<int64_t>(splits, kPrefillMaxSplits));
+    plan->workspace =
+        kPrefillCounterBytes + sizeof(float) * (size_t)row_units * uc * (splits_plain + app_max) * (d->dim + 4);
     return BGTQ_OK;
   }
   plan->tile_queries = nq >= 2048 ? 64 * prefill_column_blocks(d->dim) : 64;
@@ -1434,10 +1445,35 @@ bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *byte
   return BGTQ_OK;
 }
 
-bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
+static bgtq_status prefill_impl(bgtq_context *ctx, const bgtq_prefill_desc *d, const bgtq_prefill_append_desc *a);
+
+bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) { return prefill_impl(ctx, d, nullptr); }
+
+bgtq_status bgtq_prefill_append(bgtq_context *ctx, const bgtq_prefill_desc *d, const bgtq_prefill_append_desc *a) {
+  if (!a) return fail(BGTQ_ERR_RANGE, "null append descriptor");
+  if (!a->k_new || !a->v_new) return fail(BGTQ_ERR_RANGE, "null new K or V");
+  for (int32_t t : {a->k_new_dtype, a->v_new_dtype})
+    if (t != BGTQ_DTYPE_F16 && t != BGTQ_DTYPE_F32) return fail(BGTQ_ERR_RANGE, "invalid new K/V dtype");
+  if (a->k_new_seq_stride < 0 || a->k_new_row_stride < 0 || a->k_new_head_stride < 0 || a->v_new_seq_stride < 0 ||
+      a->v_new_row_stride < 0 || a->v_new_head_stride < 0)
+    return fail(BGTQ_ERR_RANGE, "negative new K/V stride");
+  // The kernel reads the new rows as 4-byte words.
+  if (reinterpret_cast<uintptr_t>(a->k_new) % 4 || reinterpret_cast<uintptr_t>(a->v_new) % 4)
+    return fail(BGTQ_ERR_RANGE, "new K and V must be 4-byte aligned");
+  if ((a->k_new_dtype == BGTQ_DTYPE_F16 && (a->k_new_seq_stride % 2 || a->k_new_row_stride % 2 || a->k_new_head_stride % 2)) ||
+      (a->v_new_dtype == BGTQ_DTYPE_F16 && (a->v_new_seq_stride % 2 || a->v_new_row_stride % 2 || a->v_new_head_stride % 2)))
+    return fail(BGTQ_ERR_RANGE, "FP16 new K/V strides must be even");
+  if (d && d->key_format != BGTQ_KEYS_PACKED) return fail(BGTQ_ERR_UNSUPPORTED, "prefill_append needs packed K");
+  if (d && d->rows > kPrefillRowwiseRows)
+    return fail(BGTQ_ERR_UNSUPPORTED, "prefill_append takes chunks of up to %d rows", kPrefillRowwiseRows);
+  return prefill_impl(ctx, d, a);
+}
+
+static bgtq_status prefill_impl(bgtq_context *ctx, const bgtq_prefill_desc *d, const bgtq_prefill_append_desc *a) {
   if (!ctx) return fail(BGTQ_ERR_RANGE, "null context");
   PrefillPlan plan{};
-  if (bgtq_status s = plan_prefill(d, &plan)) return s;
+  if (bgtq_status s = plan_prefill(d, &plan, a != nullptr)) return s;
+  if (a && !plan.rowwise) return fail(BGTQ_ERR_UNSUPPORTED, "prefill_append needs the row-wise path (batch x query groups up to 65535)");
   if (plan.workspace && (!d->workspace || d->workspace_bytes < plan.workspace))
     return fail(BGTQ_ERR_RANGE, "workspace of %zu bytes required", plan.workspace);
   if (plan.workspace && (reinterpret_cast<uintptr_t>(d->workspace) & 15))
@@ -1464,6 +1500,7 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
   dp.v_dtype = BGTQ_DTYPE_F16;
   dp.v_seq_stride = d->v_seq_stride;
   dp.v_head_stride = d->v_head_stride;
+  dp.k_new = a ? a->k_new : nullptr;  // the layout checks include the encoders' table copies
   FastLayout fl{};
   int nn = 0, sg = 0;
   bool fused = fast_layout(dp, d->tables, &fl, &nn, &sg);
@@ -1493,6 +1530,19 @@ bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d) {
     dp.split_floor = plan.split_floor;
     dp.split_tokens = 0;
     dp.inv_sqrt_d = (float)(1.0 / std::sqrt((double)d->dim));
+    if (a) {
+      dp.k_new = a->k_new;
+      dp.k_new_f32 = a->k_new_dtype == BGTQ_DTYPE_F32;
+      dp.k_new_seq_stride = a->k_new_seq_stride;
+      dp.k_new_row_stride = a->k_new_row_stride;
+      dp.k_new_head_stride = a->k_new_head_stride;
+      dp.v_new = a->v_new;
+      dp.v_new_f32 = a->v_new_dtype == BGTQ_DTYPE_F32;
+      dp.v_new_seq_stride = a->v_new_seq_stride;
+      dp.v_new_row_stride = a->v_new_row_stride;
+      dp.v_new_head_stride = a->v_new_head_stride;
+      dp.app_parts = plan.app_parts;
+    }
     dp.counters = reinterpret_cast<uint32_t *>(ws + plan.counters);
     // The counter prefix holds 65536 words: units on lines of their own while they fit.
     dp.counter_stride = (int)std::max<int64_t>(

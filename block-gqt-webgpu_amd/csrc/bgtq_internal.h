@@ -192,9 +192,17 @@ struct DecodeParams {
   // of sequence b sits at row lengths[b] - 1 of the caches; its post-RoPE K
   // [b][kv][dim] is encoded into packed/norms (or converted into the FP16 K
   // rows) and its V converted into the FP16 V rows within the launch.
+  // Row-wise prefill with the chunk's rows appended (packed K): row r of
+  // sequence b at k_new + b seq_stride + r row_stride + kv head_stride goes to
+  // cache row min(starts[b], max_length - rows) + r.
   const void *k_new, *v_new;
   int32_t k_new_f32, v_new_f32;
   int64_t k_new_seq_stride, k_new_head_stride, v_new_seq_stride, v_new_head_stride;  // elements
+  int64_t k_new_row_stride, v_new_row_stride;                                        // elements
+  // Workgroups per (sequence, KV head) or row-wise unit that take the
+  // appended rows (packed K: decode 1; row-wise prefill one row per wave),
+  // after the splits in the split dimension; each leaves one partial.
+  int32_t app_parts;
 };
 
 // Chunked-prefill attention of one layer (prefill.hip). Units are (sequence,

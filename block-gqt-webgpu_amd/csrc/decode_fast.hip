@@ -120,6 +120,7 @@ struct Slot {
 struct MergeRows {
   int64_t pbase, obase;
   int jbase, G, Hq, ncol;
+  int sp;  // partial rows per column (the launch's most partials per unit)
   __device__ int64_t out_row(int g) const {
     const int j = jbase + g, r = j / G;
     return obase + (int64_t)r * Hq + (j - r * G);
@@ -213,13 +214,14 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
   const int sg = lane / DQ, dq = lane - sg * DQ;
   const int sl = min(lane, S - 1);
   // The unit's partials: NW NH columns x S rows.
-  const __amdgpu_buffer_rsrc_t r = rsrc(part + mr.pbase * S * (D + 4), (uint32_t)(NW * NH) * (uint32_t)S * ROWB);
+  // The unit's partials: NW NH columns x mr.sp rows (its first S used).
+  const __amdgpu_buffer_rsrc_t r = rsrc(part + mr.pbase * mr.sp * (D + 4), (uint32_t)(NW * NH) * (uint32_t)mr.sp * ROWB);
   u32x2 ml[NH];
   f32x4 o[NH][J];
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
     const int g = wave + NW * h;
-    const uint32_t col = (uint32_t)(g < G ? g : wave) * (uint32_t)S * ROWB;
+    const uint32_t col = (uint32_t)(g < G ? g : wave) * (uint32_t)mr.sp * ROWB;
     ml[h] = coherent_load2(r, col + (uint32_t)sl * ROWB + D * 4);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -521,30 +523,51 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // PF: the splits this unit's history needs (every workgroup of the unit
   // computes the same number); the others leave before their first chunk,
   // once the prologue's DMAs into their LDS have landed.
-  const int S_hist = rowwise ? min(p.splits, max(1, (T_b + p.split_floor - 1) / p.split_floor)) : p.splits;
-  if (rowwise && split >= S_hist) {
+  // Appended rows with packed K (p.k_new): decode, the sequence's new token
+  // (row T_b - 1); row-wise prefill, the chunk's rows (start_c .. T_b - 1 of
+  // the unit's last column). They belong to p.app_parts more workgroups of
+  // the (sequence, KV head) or unit, after its splits (the append
+  // workgroups): decode, one, which encodes and stores the token and its V
+  // row and leaves the token's partial (m, l, o) like a split; prefill, one
+  // per kWaves rows, each wave encoding one row, and the part's rows then
+  // attended to as one chunk. The history splits attend to the tokens
+  // before them and never wait for an encode.
+  const bool app = KF >= 1 && p.k_new != nullptr;
+  const int part = split - p.splits;
+  const bool app_wg = app && part >= 0;
+  const int sf = p.split_floor;
+  const int S_hist = !rowwise ? p.splits
+                     : app    ? min(p.splits, (start_c + sf - 1) / sf)
+                              : min(p.splits, max(1, (T_b + sf - 1) / sf));
+  if (rowwise && !app_wg && split >= S_hist) {
     wait_vm<0>();
     return;
   }
-  // Decode-step append with packed K: the sequence's new token (row T_b - 1)
-  // belongs to one more workgroup of its (sequence, KV head), split index
-  // p.splits (the append workgroup), which encodes and stores it, stores its
-  // V row and leaves the token's partial (m, l, o) like a split; the history
-  // splits attend to the tokens before it and never wait for the encode.
-  const bool app = !rowwise && KF >= 1 && p.k_new != nullptr;
-  const bool app_wg = app && split == p.splits;
-  const int S = S_hist + (app ? 1 : 0);  // partials merged per (sequence, KV head)
-  // Tokens the history splits attend to (the append workgroup: all of them,
-  // so its new token lies inside the causal limits).
-  const int T_att = app && !app_wg ? T_b - 1 : T_b;
+  const int S = S_hist + (app ? p.app_parts : 0);  // partials merged per (sequence, KV head) or unit
+  // Partial rows per query column: the launch's most (row-wise units of one
+  // launch use different split counts; each column's rows start at the same
+  // stride, so units never share rows).
+  const int SP = p.splits + (app ? p.app_parts : 0);
+  const int pslot = app_wg ? S_hist + part : split;  // this workgroup's partial
+  // Prefill append workgroup: its rows r_a .. r_a + n_a - 1 of the chunk.
+  const int r_a = rowwise ? part * kWaves : 0;
+  const int n_a = rowwise ? min(kWaves, rows - r_a) : 0;
+  // Tokens the history splits attend to; the append workgroup's range ends
+  // after its rows (decode: all tokens, so the new one lies inside the causal
+  // limits).
+  const int T_att = !app ? T_b : app_wg ? (rowwise ? start_c + r_a + n_a : T_b) : rowwise ? start_c : T_b - 1;
   // Splits of one (sequence, KV head) interleave at chunk granularity: wave w
   // of split s takes chunks (s * 4 + w) + 4 S i, so the waves working on a
   // sequence at any moment sweep adjacent memory.
   const int t_end = kInterleaved ? T_att : min(T_att, split * p.split_tokens + p.split_tokens);
-  const int stride = kInterleaved ? S_hist * kWaves * kChunk : kWaves * kChunk;
-  // This wave's chunks start at first + 128 i.
-  const int first = kInterleaved ? (split * kWaves + wave) * kChunk : split * p.split_tokens + wave * kChunk;
-  const int n_chunks = !app_wg && first < t_end ? (t_end - first + stride - 1) / stride : 0;
+  const int stride = kInterleaved ? max(S_hist, 1) * kWaves * kChunk : kWaves * kChunk;
+  // This wave's chunks start at first + 128 i (a prefill append workgroup's
+  // wave 0: its rows, assembled in its ring slot 0).
+  const int first = app_wg && rowwise ? start_c + r_a
+                    : kInterleaved    ? (split * kWaves + wave) * kChunk
+                                      : split * p.split_tokens + wave * kChunk;
+  const int n_chunks = app_wg ? (rowwise && wave == 0 ? 1 : 0)
+                       : first < t_end ? (t_end - first + stride - 1) / stride : 0;
   // Decode reads every byte once (non-temporal, nothing cached is displaced);
   // a row-wise prefill chunk's history is read by every unit of its KV head,
   // so those loads keep the default policy and the units share it in L2.
@@ -613,13 +636,16 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // (its logit from the row it encoded); the workgroup's merge of its waves'
   // states gives the token's partial.
   constexpr int JL = D > 64 ? 2 : 1;
-  const int t_new = T_b - 1;
+  // Prefill append workgroup: wave w encodes chunk row r_a + w (cache row
+  // start_c + r_a + w) if the chunk has it.
+  const int t_new = rowwise ? start_c + r_a + wave : T_b - 1;
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
   const int own_w = VF || rowwise || p.k_new == nullptr || t_new < 0 ? -1
                     : app                                             ? (app_wg ? 0 : -1)
                                                                       : c_new % (p.splits * kWaves) - split * kWaves;
   const bool owner = own_w == wave;
-  const bool encoder = KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
+  const bool encoder = rowwise ? app_wg && wave < n_a
+                               : KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
   const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
   // The q rotation stages through the last ring slot of a wave other than
   // the encoder, whose slot receives the encoder's tables meanwhile.
@@ -636,8 +662,9 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   uint32_t k_nat[JL] = {};                     // packed K: new K element lane + 64 jl (FP32 or FP16 bits)
   float rt_col[D == 64 ? D : 1];               // d=64: R[lane][i] for every i
   row_enc::Lane<D> lc;
-  const int64_t v_off = (int64_t)b * p.v_new_seq_stride + kv * p.v_new_head_stride;
-  const int64_t k_off = (int64_t)b * p.k_new_seq_stride + kv * p.k_new_head_stride;
+  const int r_new = rowwise ? r_a + wave : 0;  // prefill: the encoder's row of the chunk
+  const int64_t v_off = (int64_t)b * p.v_new_seq_stride + (int64_t)r_new * p.v_new_row_stride + kv * p.v_new_head_stride;
+  const int64_t k_off = (int64_t)b * p.k_new_seq_stride + (int64_t)r_new * p.k_new_row_stride + kv * p.k_new_head_stride;
   // The new rows' loads carry no branch (a load under a lane test or a
   // format select compiles to a branch whose join waits for it, holding back
   // every load after it). Lane i < D / 8 gets elements 8 i .. 8 i + 7: FP32
@@ -699,7 +726,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // for those loads never waits for the chunks.
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < AHEAD; ++i) issue(i);
+  for (int i = 0; i < AHEAD; ++i)
+    if (!app_wg) issue(i);
   __builtin_amdgcn_sched_barrier(0);
   float qv[KS][8];
 #pragma unroll
@@ -717,7 +745,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     // the prologue; for KF 2 tables larger than the slot holds, the header in
     // device memory with an LDS copy of the LUT and books, or (larger still)
     // all three in device memory.
-    wait_vm<AHEAD * L>();
+    if (app_wg) wait_vm<0>();  // no chunk DMAs behind the prologue's loads
+    else wait_vm<AHEAD * L>();
     const uint8_t *enc_lds = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
     const DevTables *T_dev = reinterpret_cast<const DevTables *>(p.tables[kv]);
     const DevTables *T_use = reinterpret_cast<const DevTables *>(enc_lds);
@@ -787,7 +816,10 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     half8 bh[KS], bl[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) split_scaled(qv[s], __builtin_ldexpf(1.0f, e0), bh[s], bl[s]);
-    float *qs = reinterpret_cast<float *>(ring + ((Sl::RING - 1) * kWaves + stage_w) * Sl::BYTES);  // [16][D + 4]
+    // (a prefill append workgroup, whose last slots hold its encoders' tables
+    // and scratch: wave 0's slot 0, where its rows are assembled afterwards)
+    const int stage_s = rowwise && app_wg ? 0 : Sl::RING - 1;
+    float *qs = reinterpret_cast<float *>(ring + (stage_s * kWaves + stage_w) * Sl::BYTES);  // [16][D + 4]
     const float unscale = __builtin_ldexpf(1.0f, -e0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -802,7 +834,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       }
       *reinterpret_cast<f32x4 *>(qs + col * (D + 4) + 16 * (wave * NT + t) + 4 * gq) = acc * unscale;
     }
-    wait_vm<AHEAD * L>();  // the table DMAs, which precede the chunks
+    if (app_wg) wait_vm<0>();  // the table DMAs (append workgroups issue no chunks)
+    else wait_vm<AHEAD * L>();  // the table DMAs, which precede the chunks
     lds_barrier();
 #pragma unroll
     for (int s = 0; s < KS; ++s)
@@ -813,7 +846,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         for (int k = 0; k < 4; ++k) qv[s][4 * hh + k] = v[k];
       }
   } else if (KF >= 1) {
-    wait_vm<AHEAD * L>();  // the table DMAs, which precede the chunks
+    if (app_wg) wait_vm<0>();  // the table DMAs (append workgroups issue no chunks)
+    else wait_vm<AHEAD * L>();  // the table DMAs, which precede the chunks
     lds_barrier();
   }
   // B operand of QK: lane holds qr[head = col][32 s + 8 gq + 0..7], split hi/lo
@@ -848,7 +882,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // chunk goes out once the query staging no longer needs that slot.
   if constexpr (PF != 0) {
     static_assert(Sl::RING == 2 && AHEAD == 1, "row-wise pairs fill both ring slots");
-    issue(1);
+    if (!app_wg) issue(1);
   }
 
   // KF 2: a K-step spans up to kSlots adjacent groups glo[s] .. glo[s] +
@@ -937,7 +971,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
                                  8 * lane) = k_new16;
     }
   }
-  if (encoder) {  // the encoded row to the caches; the new token's logit from it
+  if (!rowwise && encoder) {  // the encoded row to the caches; the new token's logit from it
     uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
 #pragma unroll
     for (int jl = 0; jl < JL; ++jl)
@@ -958,13 +992,47 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     new_x = head_ok && t_new < lim ? xt : -INFINITY;
     if (p.logits && head_ok) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
   }
+  if (rowwise && app_wg) {
+    // The part's rows as one chunk in wave 0's ring slot 0, laid out as a
+    // chunk's DMA leaves them (V rows with swizzled pieces, K rows of rb
+    // bytes, scale rows of ns): wave 0 clears the slot (rows past the part's
+    // are attended to as zeros) and its second slot's V rows (the paired
+    // loop's second chunk lies past the part), then each encoder writes its
+    // row.
+    if (wave == 0) {
+      for (int o = lane * 16; o < Sl::BYTES; o += 1024) *reinterpret_cast<u32x4 *>(ring + o) = u32x4{0u, 0u, 0u, 0u};
+      for (int o = lane * 16; o < Sl::VBYTES; o += 1024)
+        *reinterpret_cast<u32x4 *>(ring + kWaves * Sl::BYTES + o) = u32x4{0u, 0u, 0u, 0u};
+    }
+    lds_barrier();
+    if (encoder) {
+      uint8_t *krow = ring + Sl::KOFF + wave * rb;
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl)
+        if (lane + 64 * jl < rb) krow[lane + 64 * jl] = (uint8_t)pk_new[jl];
+      if (lane < ns) *reinterpret_cast<uint16_t *>(ring + Sl::NOFF + 2 * (wave * ns + lane)) = (uint16_t)h_new;
+      v_new16 = half_piece(p.v_new_f32, v_raw);
+      if (lane < PR) *reinterpret_cast<u32x4 *>(ring + wave * (2 * D) + ((lane ^ swz<D>(wave)) * 16)) = v_new16;
+    }
+    lds_barrier();
+    // The rows to the caches: every unit of the (sequence, KV head) encodes
+    // the same bytes, its first unit stores them.
+    if (encoder && qg == 0) {
+      uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl)
+        if (lane + 64 * jl < rb) prow[lane + 64 * jl] = (uint8_t)pk_new[jl];
+      if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
+      if (lane < PR) *reinterpret_cast<u32x4 *>(const_cast<_Float16 *>(v_base) + (int64_t)t_new * D + 8 * lane) = v_new16;
+    }
+  }
 
   const uint32_t *tn = reinterpret_cast<const uint32_t *>(tabs);
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 O[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) O[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (encoder) {
+  if (!rowwise && encoder) {
     // The state of the new token alone: m = its logit, l = p = 2^15 (the P
     // scale; one lane of the column holds it), O rows (heads 4 gq + r) =
     // 2^15 v, v from the scratch copy (read before the slot's first load).
@@ -1267,9 +1335,10 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         issue(i + 1);
       }
       float x[2][8];
-      wait_vm<L>();  // chunk i has landed; chunk i + 1 may still be in flight
+      // (an append workgroup's chunk comes from its own LDS writes)
+      if (!app_wg) wait_vm<L>();  // chunk i has landed; chunk i + 1 may still be in flight
       chunk_logits(slot_base(0), first + i * stride, x[0]);
-      wait_vm<0>();
+      if (!app_wg) wait_vm<0>();
       chunk_logits(slot_base(1), first + (i + 1) * stride, x[1]);
       float mloc = -INFINITY;
 #pragma unroll
@@ -1451,7 +1520,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       } else {
         // Device-coherent (write-through) stores: the merging workgroup may run
         // on another XCD, whose L2 does not see this one's.
-        float *pp = p.part + (head * S + split) * (D + 2);
+        float *pp = p.part + (head * S + pslot) * (D + 2);
         coherent_store(pp + 2 + dm, Ov);
         if (dm == 0) {
           coherent_store(pp, M);
@@ -1513,7 +1582,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         p.out[head * D + dm] = Ov / Lsum;
       } else {
         // Device-coherent (write-through) stores, as above.
-        float *pp = p.part + ((pbase + g) * S + split) * PROW;
+        float *pp = p.part + ((pbase + g) * SP + pslot) * PROW;
         coherent_store(pp + dm, Ov);
         if (dm == 0) {
           coherent_store(pp + D, M);
@@ -1538,7 +1607,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   __syncthreads();
   if (!*last) return;
   if (PF) {
-    const MergeRows mr{pbase, (int64_t)b * rows * Hq + hq0, UC * qg, G, Hq, ncol};
+    const MergeRows mr{pbase, (int64_t)b * rows * Hq + hq0, UC * qg, G, Hq, ncol, SP};
     static_assert(kPrefillMaxSplits == 16, "merge_rows instances");
     static_assert(UC % NW == 0, "merge_rows: whole columns per wave");
     if (S <= 8) merge_rows<D, 8, UC / NW, NW>(p.part, p.out, mr, S, wave, lane);
@@ -1618,10 +1687,10 @@ hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t 
     return allowed;
   }
   constexpr int lds = Slot<D, KF, NN, VF, NW>::DYN;
-  // Decode-step append with packed K: one more workgroup per (sequence, KV
-  // head) for the new token.
-  const unsigned app = !PF && KF >= 1 && p.k_new ? 1u : 0u;
-  const dim3 grid = PF ? dim3((unsigned)p.kv_heads, (unsigned)(p.batch * p.qgroups), (unsigned)p.splits)
+  // Appended rows with packed K: app_parts more workgroups per (sequence, KV
+  // head) or unit for them.
+  const unsigned app = KF >= 1 && p.k_new ? (unsigned)p.app_parts : 0u;
+  const dim3 grid = PF ? dim3((unsigned)p.kv_heads, (unsigned)(p.batch * p.qgroups), (unsigned)p.splits + app)
                        : dim3((unsigned)p.splits + app, (unsigned)p.kv_heads, (unsigned)p.batch);
   hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW>), grid, dim3(64 * NW), lds, stream, p, fl);
   return hipGetLastError();

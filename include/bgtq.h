@@ -54,7 +54,9 @@ const char *bgtq_last_error(void);
  * bgtq_layout_groups, bgtq_layout_build. 4: bgtq_decode_noalloc; q_rotated closes the decode and
  * prefill descriptors; bgtq_bake_qproj; bgtq_timestamps_*; the prefill workspace is always needed
  * (at least BGTQ_PREFILL_COUNTER_BYTES, 16-byte aligned, its counter prefix zeroed before the first
- * call). 5: bgtq_attention_record_timed; attention over FP32 V runs on the fused kernel. */
+ * call). 5: bgtq_attention_record_timed; attention over FP32 V runs on the fused kernel. 6:
+ * bgtq_prefill_append; the decode workspace holds one more partial per query head and the prefill
+ * workspace the appended rows' partials (allocate what the *_workspace_size calls return). */
 int32_t bgtq_abi_version(void);
 
 /* ---- context: replaces GPUDevice + GPUQueue ------------------------------ */
@@ -349,6 +351,31 @@ typedef struct {
 } bgtq_prefill_desc;
 bgtq_status bgtq_prefill_workspace_size(const bgtq_prefill_desc *d, size_t *bytes);
 bgtq_status bgtq_prefill(bgtq_context *ctx, const bgtq_prefill_desc *d);
+
+/* One chunk of a layer's prefill with the chunk's own rows, in one launch:
+ * the model step's encode_k, V append and attention passes of
+ * src/model/decoder.ts:46-56 for rows > 1 (called per chunk by
+ * src/model/decoder.ts:82, chunks of up to 32 rows: src/model/decoder.ts:15).
+ * Row r of sequence b (post-RoPE K at k_new + b k_new_seq_stride + r
+ * k_new_row_stride + kv k_new_head_stride, FP32 rounded to FP16 first; V
+ * likewise) is encoded with tables[kv] into packed/norms and its V converted
+ * into the FP16 V rows at cache row min(starts[b], max_length - rows) + r,
+ * and the chunk's queries attend causally to the history and to the chunk's
+ * rows. Same caches as bgtq_encode_batched of those rows plus the V rows
+ * written, same outputs (within the attention tolerance) as bgtq_prefill
+ * after them. Packed K, rows up to BGTQ_PREFILL_ROWWISE_ROWS, the layouts
+ * bgtq_decode_append takes (others: BGTQ_ERR_UNSUPPORTED, nothing written);
+ * the workspace is bgtq_prefill_workspace_size()'s. New rows 4-byte aligned,
+ * FP16 ones with even strides. */
+typedef struct {
+  const void *k_new;
+  int32_t k_new_dtype; /* BGTQ_DTYPE_F32 or BGTQ_DTYPE_F16 */
+  int64_t k_new_seq_stride, k_new_row_stride, k_new_head_stride; /* elements */
+  const void *v_new;
+  int32_t v_new_dtype;
+  int64_t v_new_seq_stride, v_new_row_stride, v_new_head_stride;
+} bgtq_prefill_append_desc;
+bgtq_status bgtq_prefill_append(bgtq_context *ctx, const bgtq_prefill_desc *d, const bgtq_prefill_append_desc *a);
 
 /* ---- calibration-table pipeline (host only, no device needed) ------------
  * The setup that produces the tables(p) blobs bgtq_tables_create takes:

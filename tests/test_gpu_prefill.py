@@ -219,6 +219,17 @@ def test_forced_splits_merge(device, oracle, split_tokens):
          split_tokens=split_tokens)
 
 
+@pytest.mark.parametrize("starts,split_tokens", [([1000, 300], 96), ([1900, 0], 0), ([1900, 0, 700], 256)])
+def test_rowwise_units_of_different_split_counts(device, oracle, starts, split_tokens):
+    """A row-wise chunk (32 rows) of a batch whose later sequences have shorter histories: the units
+    of one launch use different split counts, and each keeps its partials apart from the others'."""
+    from bgtq import calibrate
+    p = calibrate.layout_b(64)
+    print("prefill row-wise split counts", starts, split_tokens, flush=True)
+    _run(device, oracle, params=[p], batch=len(starts), rows=32, hq=7, hkv=1, dim=64, starts=starts, cap=2000,
+         split_tokens=split_tokens)
+
+
 def test_single_chunk_prompt(device, oracle):
     """A 1024-row prompt in one chunk: 28 query tiles per KV head, causal from token 0."""
     from bgtq import calibrate

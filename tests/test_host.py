@@ -18,7 +18,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(bgtq.LIB_PATH))
     missing = [name for name in sorted(declared) if not hasattr(lib, name)]
     assert not missing, missing
-    assert lib.bgtq_abi_version() == 5
+    assert lib.bgtq_abi_version() == 6
     lib.bgtq_model_submit.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
     assert lib.bgtq_model_submit(None, None, 0) == 1  # BGTQ_ERR_RANGE: null context, nothing touched
 
