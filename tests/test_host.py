@@ -317,7 +317,7 @@ def test_node_addon_loads_without_a_device():
     assert r.returncode == 0, r.stderr
     import json
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert out == {"abi": 5, "miss": [], "missc": []}, out
+    assert out == {"abi": 6, "miss": [], "missc": []}, out
 
 
 def _tampered_calibration(tmp_path, edit_manifest=None, edit_payload=None):
