@@ -1389,11 +1389,16 @@ static bgtq_status plan_prefill(const bgtq_prefill_desc *d, PrefillPlan *plan, b
     int64_t splits = ((int64_t)d->max_length + floor_tok - 1) / floor_tok;
     if (d->split_tokens <= 0)
       splits = std::min<int64_t>(splits, std::max<int64_t>(1, per_cu * (int64_t)device_cus() / row_units));
-    // Appended rows: one more workgroup per unit for each wave's worth of
-    // rows, each leaving a partial; the merge takes up to kPrefillMaxSplits.
-    const int waves = decode_fast_prefill_waves(d->dim);
-    const int app_max = (d->rows + waves - 1) / waves;
+    // Appended rows: one more workgroup per unit for every
+    // kPrefillAppendRowsPerWave rows per wave, each leaving a partial; the
+    // merge takes up to kPrefillMaxSplits.
+    const int per_wg = decode_fast_prefill_waves(d->dim) * kPrefillAppendRowsPerWave;
+    const int app_max = (d->rows + per_wg - 1) / per_wg;
     plan->app_parts = append ? app_max : 0;
+    // With appended rows the history splits leave room for their workgroups
+    // in the same round of compute units.
+    if (append && d->split_tokens <= 0)
+      splits = std::min<int64_t>(splits, std::max<int64_t>(1, per_cu * (int64_t)device_cus() / row_units - app_max));
     plan->qgroups = (int)qgroups;
     plan->unit_cols = (int)uc;
     plan->splits = (int)std::max<int64_t>(1, std::min<int64_t>(splits, kPrefillMaxSplits - plan->app_parts));

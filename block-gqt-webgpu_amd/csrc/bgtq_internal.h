@@ -250,6 +250,12 @@ constexpr int kPrefillRowwiseRows = BGTQ_PREFILL_ROWWISE_ROWS;
 constexpr int decode_fast_prefill_waves(int dim) { return dim == 64 ? 8 : 4; }
 constexpr int prefill_split_floor(int dim) { return 64 * decode_fast_prefill_waves(dim); }
 constexpr int kPrefillMaxSplits = 16;
+// Rows each wave of a row-wise prefill append workgroup encodes (side by
+// side). One: two or four rows per wave took as long per row as one (their
+// encode chains did not overlap), so fewer, longer append workgroups ended
+// later (4096-token prompt in 32-row chunks, one launch per chunk and layer:
+// 42.7 ms with one row per wave, 48.3 ms with two, 57.4 ms with four).
+constexpr int kPrefillAppendRowsPerWave = 1;
 // Row-wise prefill: query columns per unit (8 or 16).
 constexpr int kPrefillUnitCols = 16;
 // The prefill workspace starts with the row-wise path's split counters (a

@@ -550,8 +550,10 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   const int SP = p.splits + (app ? p.app_parts : 0);
   const int pslot = app_wg ? S_hist + part : split;  // this workgroup's partial
   // Prefill append workgroup: its rows r_a .. r_a + n_a - 1 of the chunk.
-  const int r_a = rowwise ? part * kWaves : 0;
-  const int n_a = rowwise ? min(kWaves, rows - r_a) : 0;
+  // (ER rows per wave: a wave encodes them side by side)
+  constexpr int ER = PF ? kPrefillAppendRowsPerWave : 1;
+  const int r_a = rowwise ? part * kWaves * ER : 0;
+  const int n_a = rowwise ? min(kWaves * ER, rows - r_a) : 0;
   // Tokens the history splits attend to; the append workgroup's range ends
   // after its rows (decode: all tokens, so the new one lies inside the causal
   // limits).
@@ -636,15 +638,15 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // (its logit from the row it encoded); the workgroup's merge of its waves'
   // states gives the token's partial.
   constexpr int JL = D > 64 ? 2 : 1;
-  // Prefill append workgroup: wave w encodes chunk row r_a + w (cache row
-  // start_c + r_a + w) if the chunk has it.
-  const int t_new = rowwise ? start_c + r_a + wave : T_b - 1;
+  // Prefill append workgroup: wave w encodes chunk rows r_a + ER w + e
+  // (cache rows start_c + r_a + ER w + e), e < ER, those the chunk has.
+  const int t_new = rowwise ? start_c + r_a + ER * wave : T_b - 1;
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
   const int own_w = VF || rowwise || p.k_new == nullptr || t_new < 0 ? -1
                     : app                                             ? (app_wg ? 0 : -1)
                                                                       : c_new % (p.splits * kWaves) - split * kWaves;
   const bool owner = own_w == wave;
-  const bool encoder = rowwise ? app_wg && wave < n_a
+  const bool encoder = rowwise ? app_wg && ER * wave < n_a
                                : KF >= 1 && own_w >= 0 && own_w < kWaves && wave == (own_w + 2) % kWaves;
   const int i_new = owner ? c_new / (p.splits * kWaves) : -1;  // the owner's loop iteration of that chunk
   // The q rotation stages through the last ring slot of a wave other than
@@ -655,16 +657,22 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     lim_min = min(lim_min, t_new);
   }
   const int t_logit = owner && KF >= 1 ? t_new : t_end;  // logits this wave materialises: tokens below
-  uint32_t pk_new[JL] = {};                    // packed K bytes lane, lane + 64
-  uint32_t h_new = 0;                          // FP16 scale bits (lanes below the norm stride)
+  // Row e of this wave's encoded rows (ER of them, decode: the one new token):
+  uint32_t pk_new[ER][JL] = {};                // packed K bytes lane, lane + 64
+  uint16_t h_new[ER] = {};                     // FP16 scale bits (lanes below the norm stride)
   u32x4 v_new16{0u, 0u, 0u, 0u}, k_new16{0u, 0u, 0u, 0u};  // FP16 pieces of the V / K row (lanes below D / 8)
-  uint32_t v_raw[8] = {}, k_raw[8] = {};       // lane's 8 values of the new V / K row: FP32 bits, or FP16 pairs
-  uint32_t k_nat[JL] = {};                     // packed K: new K element lane + 64 jl (FP32 or FP16 bits)
+  uint32_t v_raw[ER][8] = {}, k_raw[8] = {};   // lane's 8 values of the new V / K row: FP32 bits, or FP16 pairs
+  uint32_t k_nat[ER][JL] = {};                 // packed K: new K element lane + 64 jl (FP32 or FP16 bits)
   float rt_col[D == 64 ? D : 1];               // d=64: R[lane][i] for every i
   row_enc::Lane<D> lc;
-  const int r_new = rowwise ? r_a + wave : 0;  // prefill: the encoder's row of the chunk
-  const int64_t v_off = (int64_t)b * p.v_new_seq_stride + (int64_t)r_new * p.v_new_row_stride + kv * p.v_new_head_stride;
-  const int64_t k_off = (int64_t)b * p.k_new_seq_stride + (int64_t)r_new * p.k_new_row_stride + kv * p.k_new_head_stride;
+  // Source offsets of row e (prefill: chunk row r_a + ER wave + e, clamped to
+  // the part's rows; the rows past it are loaded but not used).
+  auto new_off = [&](int e, int64_t seq_stride, int64_t row_stride, int64_t head_stride) {
+    const int r_new = rowwise ? r_a + min(ER * wave + e, n_a - 1) : 0;
+    return (int64_t)b * seq_stride + (int64_t)r_new * row_stride + kv * head_stride;
+  };
+  const int64_t v_off = new_off(0, p.v_new_seq_stride, p.v_new_row_stride, p.v_new_head_stride);
+  const int64_t k_off = new_off(0, p.k_new_seq_stride, p.k_new_row_stride, p.k_new_head_stride);
   // The new rows' loads carry no branch (a load under a lane test or a
   // format select compiles to a branch whose join waits for it, holding back
   // every load after it). Lane i < D / 8 gets elements 8 i .. 8 i + 7: FP32
@@ -699,16 +707,21 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     uint8_t *dst = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
 #pragma unroll
     for (int k = 0; k < Sl::ENC_DMAS; ++k) dma16(rt, dst + k * 1024, k * 1024 + lane * 16, 0);
-    load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl) {
-      // FP16: the word holding the element (k_off is even).
-      const int64_t idx = k_off + lane + 64 * jl;
-      const uint32_t *w = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new) + idx
-                                      : reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(p.k_new) +
-                                                                           (idx & ~(int64_t)1));
-      const uint32_t kw = *w;
-      k_nat[jl] = p.k_new_f32 ? kw : (kw >> (16 * (uint32_t)(idx & 1))) & 0xffffu;
+    for (int e = 0; e < ER; ++e) {
+      load_piece(p.v_new, p.v_new_f32, new_off(e, p.v_new_seq_stride, p.v_new_row_stride, p.v_new_head_stride),
+                 v_raw[e]);
+      const int64_t ko = new_off(e, p.k_new_seq_stride, p.k_new_row_stride, p.k_new_head_stride);
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl) {
+        // FP16: the word holding the element (the row offset is even).
+        const int64_t idx = ko + lane + 64 * jl;
+        const uint32_t *w = p.k_new_f32 ? static_cast<const uint32_t *>(p.k_new) + idx
+                                        : reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(p.k_new) +
+                                                                             (idx & ~(int64_t)1));
+        const uint32_t kw = *w;
+        k_nat[e][jl] = p.k_new_f32 ? kw : (kw >> (16 * (uint32_t)(idx & 1))) & 0xffffu;
+      }
     }
     if (D == 64) {
 #pragma unroll
@@ -716,7 +729,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     }
   }
   if (owner) {
-    load_piece(p.v_new, p.v_new_f32, v_off, v_raw);
+    load_piece(p.v_new, p.v_new_f32, v_off, v_raw[0]);
     if (KF == 0) load_piece(p.k_new, p.k_new_f32, k_off, k_raw);
   }
 
@@ -734,19 +747,24 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   for (int s = 0; s < KS; ++s)
 #pragma unroll
     for (int k = 0; k < 8; ++k) qv[s][k] = head_ok ? qload[s][k >> 2][k & 3] : 0.0f;
-  if (encoder) {
-    // The append workgroup's encoder encodes and stores the new K row as
-    // soon as its own loads have landed (the tables' header, LUT and books
-    // in its last ring slot, the new K and V rows, the rotation column),
-    // ahead of the query rotation: its workgroup's other waves have no
-    // chunks, so the rotation's barriers cost them nothing.
-    // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
-    // T, lut, books: the LDS copy of the tables (header, LUT, books) loaded in
-    // the prologue; for KF 2 tables larger than the slot holds, the header in
-    // device memory with an LDS copy of the LUT and books, or (larger still)
-    // all three in device memory.
-    if (app_wg) wait_vm<0>();  // no chunk DMAs behind the prologue's loads
-    else wait_vm<AHEAD * L>();
+  // Encodes this wave's ER rows: codes and scales (pk_new, h_new) to
+  // registers; decode, also the new row in the code domain (k_j = c_j
+  // s_g(j), positions j in head-perm order) and its FP16-rounded V row into
+  // the scratch for the token's logits and output. Scratch of row e: row 0,
+  // the start of this wave's last ring slot (its tables from Sl::ENC_OFF);
+  // rows 1 .. ER - 1 (prefill), its slot 0 from the start (the query
+  // rotation stages through the end of wave 0's).
+  // src/model/codec.wgsl:14: the FP32 K is rounded to FP16 first; x in head-perm order.
+  // T, lut, books: the LDS copy of the tables (header, LUT, books) loaded in
+  // the prologue; for KF 2 tables larger than the slot holds, the header in
+  // device memory with an LDS copy of the LUT and books, or (larger still)
+  // all three in device memory.
+  static_assert(KF == 0 || (ER - 1) * row_enc::scratch_bytes(D) <= Sl::BYTES, "encoder scratch fits a ring slot");
+  auto enc_scratch = [&](int e) {
+    return row_enc::Scratch<D>(e == 0 ? ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES
+                                      : ring + wave * Sl::BYTES + (e - 1) * row_enc::scratch_bytes(D));
+  };
+  auto encode_block = [&]() {
     const uint8_t *enc_lds = ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES + Sl::ENC_OFF;
     const DevTables *T_dev = reinterpret_cast<const DevTables *>(p.tables[kv]);
     const DevTables *T_use = reinterpret_cast<const DevTables *>(enc_lds);
@@ -766,40 +784,54 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     const float *books = books_use;
     lc.init(T, lane);
     const int ndims = __builtin_amdgcn_readfirstlane(T->nibble_dims);  // read with the lane set-up
-    float x[JL];
+    float x[ER][JL];
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl) {
-      const int src = lc.perm[jl];
-      uint32_t raw = __shfl(k_nat[0], src & 63, 64);
-      if (JL > 1) {
-        const uint32_t hi = __shfl(k_nat[JL - 1], src & 63, 64);
-        raw = src >= 64 ? hi : raw;
+    for (int e = 0; e < ER; ++e)
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl) {
+        const int src = lc.perm[jl];
+        uint32_t raw = __shfl(k_nat[e][0], src & 63, 64);
+        if (JL > 1) {
+          const uint32_t hi = __shfl(k_nat[e][JL - 1], src & 63, 64);
+          raw = src >= 64 ? hi : raw;
+        }
+        const uint16_t h16 = p.k_new_f32 ? row_enc::f32_to_f16_bits(__uint_as_float(raw)) : (uint16_t)raw;
+        x[e][jl] = lc.own[jl] ? row_enc::f16_bits_to_f32(h16) : 0.0f;
       }
-      const uint16_t h16 = p.k_new_f32 ? row_enc::f32_to_f16_bits(__uint_as_float(raw)) : (uint16_t)raw;
-      x[jl] = lc.own[jl] ? row_enc::f16_bits_to_f32(h16) : 0.0f;
-    }
-    // Scratch: this wave's last ring slot, loaded into only from the loop on.
-    const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
+    row_enc::Scratch<D> scr[ER];
+#pragma unroll
+    for (int e = 0; e < ER; ++e) scr[e] = enc_scratch(e);
     const float *rt = fl.rot_t[kv];
-    h_new = row_enc::encode_row<D>(
+    row_enc::encode_rows<D, ER>(
         T, lc, x,
         [&](int i, int jl) { return D == 64 ? rt_col[D == 64 ? i : 0] : rt[i * D + (lc.own[jl] ? lane + 64 * jl : 0)]; },
-        lut, books, scr, lane);
-    // The packed row's bytes; they are stored after the rotation, so the
+        lut, books, scr, lane, h_new);
+    // The packed rows' bytes; they are stored after the rotation, so the
     // rotation's wait for this wave's loads does not wait for the stores.
     const int logical = ndims / 2 + D - ndims;
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl) pk_new[jl] = row_enc::packed_byte(scr.codes, lane + 64 * jl, ndims, logical);
-    // The new row in the code domain, k_j = c_j s_g(j) (positions j in
-    // head-perm order), and the FP16-rounded new V row, for its logits and
-    // its share of the output.
+    for (int e = 0; e < ER; ++e)
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl) {
-      const float sc = row_enc::f16_bits_to_f32((uint16_t)__shfl((int)h_new, lc.grp[jl], 64));
-      if (lc.own[jl]) scr.xn[lane + 64 * jl] = books[lc.bk[jl] * T->max_centroids + scr.codes[lane + 64 * jl]] * sc;
+      for (int jl = 0; jl < JL; ++jl) pk_new[e][jl] = row_enc::packed_byte(scr[e].codes, lane + 64 * jl, ndims, logical);
+    if constexpr (!PF) {
+      const row_enc::Scratch<D> &s0 = scr[0];
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl) {
+        const float sc = row_enc::f16_bits_to_f32((uint16_t)__shfl((int)h_new[0], lc.grp[jl], 64));
+        if (lc.own[jl]) s0.xn[lane + 64 * jl] = books[lc.bk[jl] * T->max_centroids + s0.codes[lane + 64 * jl]] * sc;
+      }
+      if (lane < PR) reinterpret_cast<u32x4 *>(s0.leaf)[lane] = half_piece(p.v_new_f32, v_raw[0]);
     }
-    if (lane < PR) reinterpret_cast<u32x4 *>(scr.leaf)[lane] = half_piece(p.v_new_f32, v_raw);
     row_enc::wave_sync();
+  };
+  if (encoder) {
+    // An append workgroup's encoders encode their rows as soon as their own
+    // loads have landed (the tables' header, LUT and books in the last ring
+    // slot, the new K and V rows, the rotation column), ahead of the query
+    // rotation: the workgroup's other waves have no chunks, so the rotation's
+    // barriers cost them nothing.
+    wait_vm<0>();  // no chunk DMAs behind the prologue's loads
+    encode_block();
   }
   if (rotate) {
     // qr^T = Rq q^T, Rq = R with the head permutation folded into its
@@ -817,9 +849,11 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
 #pragma unroll
     for (int s = 0; s < KS; ++s) split_scaled(qv[s], __builtin_ldexpf(1.0f, e0), bh[s], bl[s]);
     // (a prefill append workgroup, whose last slots hold its encoders' tables
-    // and scratch: wave 0's slot 0, where its rows are assembled afterwards)
-    const int stage_s = rowwise && app_wg ? 0 : Sl::RING - 1;
-    float *qs = reinterpret_cast<float *>(ring + (stage_s * kWaves + stage_w) * Sl::BYTES);  // [16][D + 4]
+    // and each slot 0 its scratch: the end of wave 0's slot 0)
+    constexpr int kStage = 16 * (D + 4) * 4;
+    static_assert(!PF || KF == 0 || (ER - 1) * row_enc::scratch_bytes(D) + kStage <= Sl::BYTES, "scratch and staging");
+    float *qs = reinterpret_cast<float *>(rowwise && app_wg ? ring + (Sl::BYTES - kStage) / 16 * 16
+                                                           : ring + ((Sl::RING - 1) * kWaves + stage_w) * Sl::BYTES);
     const float unscale = __builtin_ldexpf(1.0f, -e0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -962,7 +996,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   float new_x = -INFINITY;  // encoder: the new token's logit for head col (log2 domain; -inf: not attended)
   if (owner) {  // the new token's V (and FP16 K) row: convert, store to the caches
     if (lane < PR) {
-      v_new16 = half_piece(p.v_new_f32, v_raw);
+      v_new16 = half_piece(p.v_new_f32, v_raw[0]);
       *reinterpret_cast<u32x4 *>(const_cast<_Float16 *>(v_base) + (int64_t)t_new * D + 8 * lane) = v_new16;
     }
     if (KF == 0 && lane < PR) {
@@ -975,9 +1009,9 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
 #pragma unroll
     for (int jl = 0; jl < JL; ++jl)
-      if (lane + 64 * jl < rb) prow[lane + 64 * jl] = (uint8_t)pk_new[jl];
-    if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
-    const row_enc::Scratch<D> scr(ring + ((Sl::RING - 1) * kWaves + wave) * Sl::BYTES);
+      if (lane + 64 * jl < rb) prow[lane + 64 * jl] = (uint8_t)pk_new[0][jl];
+    if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = h_new[0];
+    const row_enc::Scratch<D> scr = enc_scratch(0);
     // Logit of head col: sum over this lane's positions 32 s + 8 gq + k of
     // k_j (qhi + qlo)[s][k], then over the column's four lanes; the query
     // operands carry 2^eq, kq * 2^ec takes it off (the centroids here are
@@ -993,37 +1027,51 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     if (p.logits && head_ok) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
   }
   if (rowwise && app_wg) {
-    // The part's rows as one chunk in wave 0's ring slot 0, laid out as a
-    // chunk's DMA leaves them (V rows with swizzled pieces, K rows of rb
-    // bytes, scale rows of ns): wave 0 clears the slot (rows past the part's
-    // are attended to as zeros) and its second slot's V rows (the paired
-    // loop's second chunk lies past the part), then each encoder writes its
-    // row.
+    // The part's rows (encoded before the rotation) laid out as one chunk in
+    // wave 0's ring slot 0 the way a chunk's DMA leaves it (V rows with
+    // swizzled pieces, K rows of rb bytes, scale rows of ns): wave 0 clears
+    // the slot (rows past the part's are attended to as zeros) and its second
+    // slot's V rows (the paired loop's second chunk lies past the part), then
+    // each encoder writes its rows.
+    lds_barrier();  // every encoder is done with its scratch
     if (wave == 0) {
       for (int o = lane * 16; o < Sl::BYTES; o += 1024) *reinterpret_cast<u32x4 *>(ring + o) = u32x4{0u, 0u, 0u, 0u};
       for (int o = lane * 16; o < Sl::VBYTES; o += 1024)
         *reinterpret_cast<u32x4 *>(ring + kWaves * Sl::BYTES + o) = u32x4{0u, 0u, 0u, 0u};
     }
     lds_barrier();
+    const int ne = min(ER, n_a - ER * wave);  // this wave's rows (encoders: 1 .. ER)
+    u32x4 vrow[ER];
     if (encoder) {
-      uint8_t *krow = ring + Sl::KOFF + wave * rb;
 #pragma unroll
-      for (int jl = 0; jl < JL; ++jl)
-        if (lane + 64 * jl < rb) krow[lane + 64 * jl] = (uint8_t)pk_new[jl];
-      if (lane < ns) *reinterpret_cast<uint16_t *>(ring + Sl::NOFF + 2 * (wave * ns + lane)) = (uint16_t)h_new;
-      v_new16 = half_piece(p.v_new_f32, v_raw);
-      if (lane < PR) *reinterpret_cast<u32x4 *>(ring + wave * (2 * D) + ((lane ^ swz<D>(wave)) * 16)) = v_new16;
+      for (int e = 0; e < ER; ++e) {
+        const int r = ER * wave + e;  // row in the chunk
+        vrow[e] = half_piece(p.v_new_f32, v_raw[e]);
+        if (e < ne) {
+          uint8_t *krow = ring + Sl::KOFF + r * rb;
+#pragma unroll
+          for (int jl = 0; jl < JL; ++jl)
+            if (lane + 64 * jl < rb) krow[lane + 64 * jl] = (uint8_t)pk_new[e][jl];
+          if (lane < ns) *reinterpret_cast<uint16_t *>(ring + Sl::NOFF + 2 * (r * ns + lane)) = h_new[e];
+          if (lane < PR) *reinterpret_cast<u32x4 *>(ring + r * (2 * D) + ((lane ^ swz<D>(r)) * 16)) = vrow[e];
+        }
+      }
     }
     lds_barrier();
     // The rows to the caches: every unit of the (sequence, KV head) encodes
     // the same bytes, its first unit stores them.
     if (encoder && qg == 0) {
-      uint8_t *prow = const_cast<uint8_t *>(k_base) + (int64_t)t_new * rb;
 #pragma unroll
-      for (int jl = 0; jl < JL; ++jl)
-        if (lane + 64 * jl < rb) prow[lane + 64 * jl] = (uint8_t)pk_new[jl];
-      if (lane < ns) const_cast<uint16_t *>(n_base)[(int64_t)t_new * ns + lane] = (uint16_t)h_new;
-      if (lane < PR) *reinterpret_cast<u32x4 *>(const_cast<_Float16 *>(v_base) + (int64_t)t_new * D + 8 * lane) = v_new16;
+      for (int e = 0; e < ER; ++e) {
+        if (e >= ne) break;
+        const int64_t t = t_new + e;
+        uint8_t *prow = const_cast<uint8_t *>(k_base) + t * rb;
+#pragma unroll
+        for (int jl = 0; jl < JL; ++jl)
+          if (lane + 64 * jl < rb) prow[lane + 64 * jl] = (uint8_t)pk_new[e][jl];
+        if (lane < ns) const_cast<uint16_t *>(n_base)[t * ns + lane] = h_new[e];
+        if (lane < PR) *reinterpret_cast<u32x4 *>(const_cast<_Float16 *>(v_base) + t * D + 8 * lane) = vrow[e];
+      }
     }
   }
 

@@ -40,6 +40,7 @@ template <int D>
 struct Scratch {
   float *leaf, *xn, *part, *tot;
   uint8_t *codes;
+  __device__ Scratch() {}
   __device__ explicit Scratch(uint8_t *base) {
     leaf = reinterpret_cast<float *>(base);
     xn = leaf + D;
@@ -129,15 +130,17 @@ struct Lane {
   }
 };
 
-// Encodes the row whose FP16-valued inputs x (head-perm order, lane's
-// dimensions) are given: codes land in s.codes[0..D); lanes below the norm
-// stride return their FP16 scale bits (zero past the groups), the others 0.
-// rot(i, jl) is R[j][i] for the lane's dimension j = lane + 64 jl (from LDS,
-// global memory or registers); lut and books may be in LDS or global memory.
-template <int D, typename Rot>
-__device__ __forceinline__ uint16_t encode_row(const DevTables *T, const Lane<D> &c, const float (&x)[Lane<D>::JL],
-                                               Rot rot, const uint8_t *lut, const float *books, const Scratch<D> &s,
-                                               int lane) {
+// Encodes ER rows at once (their chains interleaved, each row's arithmetic
+// exactly that of a single row): row r's FP16-valued inputs x[r] (head-perm
+// order, lane's dimensions), its scratch s[r]; codes land in s[r].codes[0..D),
+// and lanes below the norm stride get row r's FP16 scale bits in h[r] (zero
+// past the groups, 0 in the other lanes). rot(i, jl) is R[j][i] for the lane's
+// dimension j = lane + 64 jl (from LDS, global memory or registers), read once
+// for all rows; lut and books may be in LDS or global memory.
+template <int D, int ER, typename Rot>
+__device__ __forceinline__ void encode_rows(const DevTables *T, const Lane<D> &c, const float (&x)[ER][Lane<D>::JL],
+                                            Rot rot, const uint8_t *lut, const float *books,
+                                            const Scratch<D> (&s)[ER], int lane, uint16_t (&h)[ER]) {
   constexpr int JL = Lane<D>::JL;
   const int ng = T->groups, mc = T->max_centroids;
   // production_math.py:12  n_g = sqrt(sum((x*x)*mask) + 1e-30): each lane
@@ -145,55 +148,97 @@ __device__ __forceinline__ uint16_t encode_row(const DevTables *T, const Lane<D>
   // `lane` (the final scale), so nothing is computed for groups it does not use.
   const int gl = lane < ng ? lane : 0;
 #pragma unroll
-  for (int jl = 0; jl < JL; ++jl)
-    if (c.own[jl]) s.leaf[lane + 64 * jl] = x[jl] * x[jl];
-  wave_sync();
-  const float t1 = group_tree<D>(s.leaf, lane, ng, c.gs, c.ge);
-  float nrm[JL];
+  for (int r = 0; r < ER; ++r)
 #pragma unroll
-  for (int jl = 0; jl < JL; ++jl) nrm[jl] = __builtin_sqrtf(pick(t1, c.grp[jl]) + 1e-30f);
+    for (int jl = 0; jl < JL; ++jl)
+      if (c.own[jl]) s[r].leaf[lane + 64 * jl] = x[r][jl] * x[r][jl];
+  wave_sync();
+  float t1[ER];
+#pragma unroll
+  for (int r = 0; r < ER; ++r) t1[r] = group_tree<D>(s[r].leaf, lane, ng, c.gs, c.ge);
+  float nrm[ER][JL];
+#pragma unroll
+  for (int r = 0; r < ER; ++r)
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl) nrm[r][jl] = __builtin_sqrtf(pick(t1[r], c.grp[jl]) + 1e-30f);
   // production_math.py:14  raw_g = sum(n_g*mask)/|g| (more than one group)
-  float raw;
+  float raw[ER];
   if (ng > 1) {
     wave_sync();
 #pragma unroll
-    for (int jl = 0; jl < JL; ++jl)
-      if (c.own[jl]) s.leaf[lane + 64 * jl] = nrm[jl];
+    for (int r = 0; r < ER; ++r)
+#pragma unroll
+      for (int jl = 0; jl < JL; ++jl)
+        if (c.own[jl]) s[r].leaf[lane + 64 * jl] = nrm[r][jl];
     wave_sync();
-    const float t2 = group_tree<D>(s.leaf, lane, ng, c.gs, c.ge);
-    raw = pick(t2, gl) / (float)T->gsize[gl];
+#pragma unroll
+    for (int r = 0; r < ER; ++r) {
+      const float t2 = group_tree<D>(s[r].leaf, lane, ng, c.gs, c.ge);
+      raw[r] = pick(t2, gl) / (float)T->gsize[gl];
+    }
   } else {
-    raw = __builtin_sqrtf(pick(t1, 0) + 1e-30f);
+#pragma unroll
+    for (int r = 0; r < ER; ++r) raw[r] = __builtin_sqrtf(pick(t1[r], 0) + 1e-30f);
   }
   // production_math.py:15  xn = x / where(n > 1e-10, n, 1)
 #pragma unroll
-  for (int jl = 0; jl < JL; ++jl)
-    if (c.own[jl]) s.xn[lane + 64 * jl] = x[jl] / (nrm[jl] > 1e-10f ? nrm[jl] : 1.0f);
+  for (int r = 0; r < ER; ++r)
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl)
+      if (c.own[jl]) s[r].xn[lane + 64 * jl] = x[r][jl] / (nrm[r][jl] > 1e-10f ? nrm[r][jl] : 1.0f);
   wave_sync();
   // production_math.py:16-18  y_j (FMA chain, i ascending), bin, code
-  float cent[JL];
+  float cent[ER][JL];
 #pragma unroll
   for (int jl = 0; jl < JL; ++jl) {
-    float acc = 0.0f;
+    float acc[ER];
 #pragma unroll
-    for (int i = 0; i < D; ++i) acc = __builtin_fmaf(s.xn[i], rot(i, jl), acc);
-    float t = (acc - c.off[jl]) * c.inv[jl];
-    t = fminf(fmaxf(t, 0.0f), 255.0f);
-    const uint8_t code = lut[c.cb[jl] * 256 + (int)t];
-    if (c.own[jl]) s.codes[lane + 64 * jl] = code;
-    cent[jl] = books[c.bk[jl] * mc + code];
+    for (int r = 0; r < ER; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      const float rv = rot(i, jl);
+#pragma unroll
+      for (int r = 0; r < ER; ++r) acc[r] = __builtin_fmaf(s[r].xn[i], rv, acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < ER; ++r) {
+      float t = (acc[r] - c.off[jl]) * c.inv[jl];
+      t = fminf(fmaxf(t, 0.0f), 255.0f);
+      const uint8_t code = lut[c.cb[jl] * 256 + (int)t];
+      if (c.own[jl]) s[r].codes[lane + 64 * jl] = code;
+      cent[r][jl] = books[c.bk[jl] * mc + code];
+    }
   }
   // production_math.py:20-23  corrected_g = raw_g / max(sqrt(sum((c*c)*mask)), 1e-10)
   wave_sync();
 #pragma unroll
-  for (int jl = 0; jl < JL; ++jl)
-    if (c.own[jl]) s.leaf[lane + 64 * jl] = cent[jl] * cent[jl];
+  for (int r = 0; r < ER; ++r)
+#pragma unroll
+    for (int jl = 0; jl < JL; ++jl)
+      if (c.own[jl]) s[r].leaf[lane + 64 * jl] = cent[r][jl] * cent[r][jl];
   wave_sync();
-  const float t3 = group_tree<D>(s.leaf, lane, ng, c.gs, c.ge);
-  const float cc = fmaxf(__builtin_sqrtf(pick(t3, gl)), 1e-10f);
-  uint16_t h = 0;
-  if (lane < T->norm_stride && lane < ng) h = f32_to_f16_bits(raw / cc);
-  return h;
+#pragma unroll
+  for (int r = 0; r < ER; ++r) {
+    const float t3 = group_tree<D>(s[r].leaf, lane, ng, c.gs, c.ge);
+    const float cc = fmaxf(__builtin_sqrtf(pick(t3, gl)), 1e-10f);
+    h[r] = lane < T->norm_stride && lane < ng ? f32_to_f16_bits(raw[r] / cc) : (uint16_t)0;
+  }
+}
+
+// One row (encode_rows of a single row): the row's FP16 scale bits in lanes
+// below the norm stride, 0 elsewhere.
+template <int D, typename Rot>
+__device__ __forceinline__ uint16_t encode_row(const DevTables *T, const Lane<D> &c, const float (&x)[Lane<D>::JL],
+                                               Rot rot, const uint8_t *lut, const float *books, const Scratch<D> &s,
+                                               int lane) {
+  constexpr int JL = Lane<D>::JL;
+  float xr[1][JL];
+#pragma unroll
+  for (int jl = 0; jl < JL; ++jl) xr[0][jl] = x[jl];
+  const Scratch<D> sr[1] = {s};
+  uint16_t h[1];
+  encode_rows<D, 1>(T, c, xr, rot, lut, books, sr, lane, h);
+  return h[0];
 }
 
 // Byte b of the packed row (src/reference/mixed_layout.py:21-27): nibble
