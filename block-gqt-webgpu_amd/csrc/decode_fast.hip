@@ -1030,14 +1030,11 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     // The part's rows (encoded before the rotation) laid out as one chunk in
     // wave 0's ring slot 0 the way a chunk's DMA leaves it (V rows with
     // swizzled pieces, K rows of rb bytes, scale rows of ns): wave 0 clears
-    // the slot (rows past the part's are attended to as zeros) and its second
-    // slot's V rows (the paired loop's second chunk lies past the part), then
-    // each encoder writes its rows.
+    // the slot (rows past the part's are attended to as zeros), then each
+    // encoder writes its rows.
     lds_barrier();  // every encoder is done with its scratch
     if (wave == 0) {
       for (int o = lane * 16; o < Sl::BYTES; o += 1024) *reinterpret_cast<u32x4 *>(ring + o) = u32x4{0u, 0u, 0u, 0u};
-      for (int o = lane * 16; o < Sl::VBYTES; o += 1024)
-        *reinterpret_cast<u32x4 *>(ring + kWaves * Sl::BYTES + o) = u32x4{0u, 0u, 0u, 0u};
     }
     lds_barrier();
     const int ne = min(ER, n_a - ER * wave);  // this wave's rows (encoders: 1 .. ER)
@@ -1386,8 +1383,13 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       // (an append workgroup's chunk comes from its own LDS writes)
       if (!app_wg) wait_vm<L>();  // chunk i has landed; chunk i + 1 may still be in flight
       chunk_logits(slot_base(0), first + i * stride, x[0]);
-      if (!app_wg) wait_vm<0>();
-      chunk_logits(slot_base(1), first + (i + 1) * stride, x[1]);
+      if (app_wg) {  // an append workgroup's rows fill one chunk: no second one
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[1][j] = -INFINITY;
+      } else {
+        wait_vm<0>();
+        chunk_logits(slot_base(1), first + (i + 1) * stride, x[1]);
+      }
       float mloc = -INFINITY;
 #pragma unroll
       for (int c = 0; c < 2; ++c)
@@ -1424,9 +1426,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
           for (int dt = 0; dt < DT; ++dt) O[dt][r] *= ar;
         }
       }
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-        chunk_pv(slot_base(c), __builtin_bit_cast(half8, ph[c]), __builtin_bit_cast(half8, pl[c]));
+      chunk_pv(slot_base(0), __builtin_bit_cast(half8, ph[0]), __builtin_bit_cast(half8, pl[0]));
+      if (!app_wg) chunk_pv(slot_base(1), __builtin_bit_cast(half8, ph[1]), __builtin_bit_cast(half8, pl[1]));
     }
   } else {
     for (int i = 0; i < n_chunks; ++i) {
