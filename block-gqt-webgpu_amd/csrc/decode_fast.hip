@@ -112,8 +112,10 @@ struct Slot {
 // loads each split's o at its DL dimensions, all loads in flight at once
 // (S <= SMAX).
 // The weights w_s = 2^(m_s - M) come from wave reductions and reach every
-// lane through lane reads. Out of line, and instantiated for a few SMAX, so
-// the kernel's own code stays as small.
+// lane through lane reads. Instantiated for a few SMAX and inlined: as a
+// called function it saved the caller's registers it reuses to scratch
+// memory and reloaded them on return, a memory round trip at the end of
+// every merge.
 // Rows of a row-wise unit's columns: column g's partials at row pbase + g of
 // the partial array; its output at row obase + (j / G) * Hq + j % G, with
 // j = jbase + g its query in the chunk's rows x G heads.
@@ -128,7 +130,7 @@ struct MergeRows {
 };
 
 template <int D, int SMAX, int NW>
-__device__ __noinline__ void merge_one_round(float *part, float *out, float *stats, int64_t head0, int G, int S,
+__device__ __forceinline__ void merge_one_round(float *part, float *out, float *stats, int64_t head0, int G, int S,
                                              int wave, int lane) {
   constexpr int kWaves = NW;
   static_assert(SMAX <= 64, "one split per lane");
