@@ -1237,45 +1237,66 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     // QK: acc[u][g] = sum over the K-steps of group g.
     f32x4 acc[2][2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      acc[u][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      const int t = 16 * u + col;  // A-operand row (token) of this lane
+    for (int u = 0; u < 2; ++u) acc[u][0] = acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (KF == 1) {
+      // The lane's row words of both tiles and every K-step first, then every
+      // code lookup, then the MFMAs (in K-step order, as the sums were): the
+      // LDS reads go out in two rounds instead of a round trip per K-step.
+      uint32_t wn[2][KS];
+      u32x2 wb[2][KS];
 #pragma unroll
-      for (int s = 0; s < (KF == 2 ? 0 : KS); ++s) {
-        const int g = s < SG ? 0 : 1;
-        if (KF == 1) {
-          u32x4 hi, lo;
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const uint8_t *row = kbuf + (16 * u + col) * RB;  // A-operand row (token) of this lane
+          if (s < NN) wn[u][s] = *reinterpret_cast<const uint32_t *>(row + 16 * s + 4 * gq);
+          else wb[u][s] = *reinterpret_cast<const u32x2 *>(row + 16 * NN + 32 * (s - NN) + 8 * gq);
+        }
+      u32x4 hi[2][KS], lo[2][KS];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
           if (s < NN) {
-            const uint32_t w = *reinterpret_cast<const uint32_t *>(kbuf + t * RB + 16 * s + 4 * gq);
             const u32x2 *t64 = reinterpret_cast<const u32x2 *>(tn + s * 512);  // [byte]: hi pair, lo pair
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              const u32x2 v = t64[(w >> (8 * k)) & 255u];
-              hi[k] = v[0];
-              lo[k] = v[1];
+              const u32x2 v = t64[(wn[u][s] >> (8 * k)) & 255u];
+              hi[u][s][k] = v[0];
+              lo[u][s][k] = v[1];
             }
           } else {
-            const u32x2 w = *reinterpret_cast<const u32x2 *>(kbuf + t * RB + 16 * NN + 32 * (s - NN) + 8 * gq);
             const uint32_t *t32 = tn + s * 512;  // [code]: hi | lo << 16
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              const uint32_t c0 = t32[(w[k >> 1] >> (16 * (k & 1))) & 255u];
-              const uint32_t c1 = t32[(w[k >> 1] >> (16 * (k & 1) + 8)) & 255u];
-              hi[k] = __builtin_amdgcn_perm(c1, c0, 0x05040100u);  // c0.hi, c1.hi
-              lo[k] = __builtin_amdgcn_perm(c1, c0, 0x07060302u);  // c0.lo, c1.lo
+              const uint32_t c0 = t32[(wb[u][s][k >> 1] >> (16 * (k & 1))) & 255u];
+              const uint32_t c1 = t32[(wb[u][s][k >> 1] >> (16 * (k & 1) + 8)) & 255u];
+              hi[u][s][k] = __builtin_amdgcn_perm(c1, c0, 0x05040100u);  // c0.hi, c1.hi
+              lo[u][s][k] = __builtin_amdgcn_perm(c1, c0, 0x07060302u);  // c0.lo, c1.lo
             }
           }
-          const half8 ah = __builtin_bit_cast(half8, hi), al = __builtin_bit_cast(half8, lo);
+        }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int g = s < SG ? 0 : 1;
+          const half8 ah = __builtin_bit_cast(half8, hi[u][s]), al = __builtin_bit_cast(half8, lo[u][s]);
           acc[u][g] = mfma(ah, qhi[s], acc[u][g]);
           acc[u][g] = mfma(al, qhi[s], acc[u][g]);
           acc[u][g] = mfma(ah, qlo[s], acc[u][g]);
-        } else {
-          const int piece = 4 * s + gq;
-          const half8 a = *reinterpret_cast<const half8 *>(kbuf + t * (2 * D) + ((piece ^ swz<D>(t)) * 16));
-          acc[u][0] = mfma(a, qhi[s], acc[u][0]);
-          acc[u][0] = mfma(a, qlo[s], acc[u][0]);
         }
+    }
+    // FP16 K rows: swizzled 16-byte pieces.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = 16 * u + col;  // A-operand row (token) of this lane
+#pragma unroll
+      for (int s = 0; s < (KF == 0 ? KS : 0); ++s) {
+        const int piece = 4 * s + gq;
+        const half8 a = *reinterpret_cast<const half8 *>(kbuf + t * (2 * D) + ((piece ^ swz<D>(t)) * 16));
+        acc[u][0] = mfma(a, qhi[s], acc[u][0]);
+        acc[u][0] = mfma(a, qlo[s], acc[u][0]);
       }
     }
     // logits of this lane: head col, tokens c0 + 16u + 4gq + r
