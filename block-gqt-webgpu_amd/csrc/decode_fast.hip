@@ -73,6 +73,11 @@ struct Geo {
 // four lane groups (rows 4 apart, the same 16 values) hit different banks.
 __host__ __device__ constexpr int swz32(int row) { return ((row >> 2) & 3) << 2; }
 
+// Row-wise prefill stages its rotated queries (16 heads, rows padded to D + 4
+// floats) in dynamic LDS after the ring: no ring slot waits for the staging
+// to be read, and an append workgroup's slots keep its encoders' data.
+__host__ __device__ constexpr int prefill_stage_bytes(int D) { return 16 * (D + 4) * 4; }
+
 // VF: the V rows' format, 0 = FP16 (2 bytes per value), 1 = FP32 (4 bytes;
 // a ring of one slot per wave where two do not fit). NW: waves per workgroup.
 template <int D, int KF, int NN, int VF = 0, int NW = kWaves>
@@ -850,12 +855,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     half8 bh[KS], bl[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) split_scaled(qv[s], __builtin_ldexpf(1.0f, e0), bh[s], bl[s]);
-    // (a prefill append workgroup, whose last slots hold its encoders' tables
-    // and each slot 0 its scratch: the end of wave 0's slot 0)
-    constexpr int kStage = 16 * (D + 4) * 4;
-    static_assert(!PF || KF == 0 || (ER - 1) * row_enc::scratch_bytes(D) + kStage <= Sl::BYTES, "scratch and staging");
-    float *qs = reinterpret_cast<float *>(rowwise && app_wg ? ring + (Sl::BYTES - kStage) / 16 * 16
-                                                           : ring + ((Sl::RING - 1) * kWaves + stage_w) * Sl::BYTES);
+    // (row-wise prefill: its staging area after the ring)
+    float *qs = reinterpret_cast<float *>(PF ? ring + Sl::DYN : ring + ((Sl::RING - 1) * kWaves + stage_w) * Sl::BYTES);
     const float unscale = __builtin_ldexpf(1.0f, -e0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -913,11 +914,14 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       }
     kq = __builtin_ldexpf(kLog2e, -(eq + ec));
   }
-  if (rotate) lds_barrier();  // q staging (last ring slot) is dead
-  // Row-wise prefill computes its chunks in pairs: the second ring slot's
-  // chunk goes out once the query staging no longer needs that slot.
+  // The q staging (a ring slot's, whose chunk comes later) is dead; row-wise
+  // prefill's own staging area is never written again, so it needs no
+  // barrier, and its second ring slot's chunk goes out now (issued with the
+  // first, in the prologue, it measured slower: more loads in flight while
+  // the queries and tables are awaited).
+  if (rotate && !PF) lds_barrier();
+  static_assert(!PF || (Sl::RING == 2 && AHEAD == 1), "row-wise pairs fill both ring slots");
   if constexpr (PF != 0) {
-    static_assert(Sl::RING == 2 && AHEAD == 1, "row-wise pairs fill both ring slots");
     if (!app_wg) issue(1);
   }
 
@@ -1753,12 +1757,14 @@ hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t 
   // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
   static const hipError_t allowed =
       hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, Slot<D, KF, NN, VF, NW>::DYN);
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          Slot<D, KF, NN, VF, NW>::DYN + (PF ? prefill_stage_bytes(D) : 0));
   if (allowed != hipSuccess) {
     (void)hipGetLastError();  // do not leave the failure behind for the caller's next HIP call
     return allowed;
   }
-  constexpr int lds = Slot<D, KF, NN, VF, NW>::DYN;
+  constexpr int lds = Slot<D, KF, NN, VF, NW>::DYN + (PF ? prefill_stage_bytes(D) : 0);
+  static_assert(lds + Slot<D, KF, NN, VF, NW>::TABLES <= kLdsLimit, "LDS of one workgroup");
   // Appended rows with packed K: app_parts more workgroups per (sequence, KV
   // head) or unit for them.
   const unsigned app = KF >= 1 && p.k_new ? (unsigned)p.app_parts : 0u;
