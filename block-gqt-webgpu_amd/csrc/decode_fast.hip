@@ -495,13 +495,14 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   u32x4 rq[NT][KS][2];
   // A query already in the code domain (q_rotated) is the QK operand as loaded.
   const bool rotate = KF >= 1 && !p.q_rotated;
-  if (rotate) {
+  // (wave-uniform: waves past the tiles load none)
+  if (rotate && rot_wave) {
     const u32x4 *op = reinterpret_cast<const u32x4 *>(fl.rot_q[kv]);  // [tile][K-step][lane][hi, lo]
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const int at = ((((rot_wave ? wave * NT : 0) + t) * KS + s) * 64 + lane) * 2;
+        const int at = (((wave * NT + t) * KS + s) * 64 + lane) * 2;
         rq[t][s][0] = op[at];
         rq[t][s][1] = op[at + 1];
       }
