@@ -480,21 +480,27 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
       }
     }
   }
-  f32x4 qload[KS][2];  // unconditional loads of a valid row; heads past G are zeroed after the chunk issue
-  {
+  // 16-row tiles of the rotation per wave (more waves than tiles: the first DT
+  // waves take one each).
+  constexpr int NT = KF >= 1 && DT >= kWaves ? DT / kWaves : 1;
+  const bool rot_wave = KF >= 1 && wave * NT < DT;
+  // A query already in the code domain (q_rotated) is the QK operand as loaded.
+  const bool rotate = KF >= 1 && !p.q_rotated;
+  // Loads of a valid row (heads past G are zeroed after the chunk issue).
+  // Row-wise prefill: waves that neither rotate nor use the query as loaded
+  // (they read the rotated one from LDS) load none (a wave-uniform test;
+  // 32-row chunks 33.42 -> 32.70 ms of attention per prompt). Decode loads
+  // unconditionally: there the wait a branch puts where it joins (before the
+  // prologue's later loads go out) cost more than the loads (C2 step +8 us).
+  f32x4 qload[KS][2] = {};
+  if (PF == 0 || !rotate || rot_wave) {
     const f32x4 *src = reinterpret_cast<const f32x4 *>(p.q + qidx * D);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) qload[s][hh] = src[8 * s + 2 * gq + hh];
   }
-  // 16-row tiles of the rotation per wave (more waves than tiles: the first DT
-  // waves take one each).
-  constexpr int NT = KF >= 1 && DT >= kWaves ? DT / kWaves : 1;
-  const bool rot_wave = KF >= 1 && wave * NT < DT;
   u32x4 rq[NT][KS][2];
-  // A query already in the code domain (q_rotated) is the QK operand as loaded.
-  const bool rotate = KF >= 1 && !p.q_rotated;
   // (wave-uniform: waves past the tiles load none)
   if (rotate && rot_wave) {
     const u32x4 *op = reinterpret_cast<const u32x4 *>(fl.rot_q[kv]);  // [tile][K-step][lane][hi, lo]
