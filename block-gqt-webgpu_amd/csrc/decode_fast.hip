@@ -481,8 +481,9 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     }
   }
   // 16-row tiles of the rotation per wave (more waves than tiles: the first DT
-  // waves take one each).
-  constexpr int NT = KF >= 1 && DT >= kWaves ? DT / kWaves : 1;
+  // waves take one each; row-wise prefill, the first DT / 2 two each, so
+  // fewer waves load the queries).
+  constexpr int NT = KF >= 1 && DT >= kWaves ? DT / kWaves : PF && DT >= 2 ? 2 : 1;
   const bool rot_wave = KF >= 1 && wave * NT < DT;
   // A query already in the code domain (q_rotated) is the QK operand as loaded.
   const bool rotate = KF >= 1 && !p.q_rotated;
