@@ -317,7 +317,9 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
 // (0). FP32 V enters the PV MFMAs as three FP16 parts per value.
 // NW: waves per workgroup (4; row-wise prefill at d=64, 8: a unit's splits
 // then cover twice the tokens each and half as many partials are merged).
-template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves>
+// AP: 0 compiles the appended-row paths out (row-wise prefill launches
+// without them).
+template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves, int AP = 1>
 __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
   using Sl = Slot<D, KF, NN, VF, NW>;
@@ -547,7 +549,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // per kWaves rows, each wave encoding one row, and the part's rows then
   // attended to as one chunk. The history splits attend to the tokens
   // before them and never wait for an encode.
-  const bool app = KF >= 1 && p.k_new != nullptr;
+  const bool app = KF >= 1 && AP && p.k_new != nullptr;
   const int part = split - p.splits;
   const bool app_wg = app && part >= 0;
   const int sf = p.split_floor;
@@ -1760,11 +1762,11 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int KF, int NN, int SG, int PK, int PF, int VF = 0, int NW = kWaves>
+template <int D, int KF, int NN, int SG, int PK, int PF, int VF = 0, int NW = kWaves, int AP = 1>
 hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   // More than 64 KB of dynamic LDS has to be allowed per kernel (gfx950: up to 160 KB).
   static const hipError_t allowed =
-      hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW>,
+      hipFuncSetAttribute((const void *)decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW, AP>,
                           hipFuncAttributeMaxDynamicSharedMemorySize,
                           Slot<D, KF, NN, VF, NW>::DYN + (PF ? prefill_stage_bytes(D) : 0));
   if (allowed != hipSuccess) {
@@ -1778,7 +1780,7 @@ hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t 
   const unsigned app = KF >= 1 && p.k_new ? (unsigned)p.app_parts : 0u;
   const dim3 grid = PF ? dim3((unsigned)p.kv_heads, (unsigned)(p.batch * p.qgroups), (unsigned)p.splits + app)
                        : dim3((unsigned)p.splits + app, (unsigned)p.kv_heads, (unsigned)p.batch);
-  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW>), grid, dim3(64 * NW), lds, stream, p, fl);
+  hipLaunchKernelGGL((decode_fast_kernel<D, KF, NN, SG, PK, PF, VF, NW, AP>), grid, dim3(64 * NW), lds, stream, p, fl);
   return hipGetLastError();
 }
 
@@ -1795,7 +1797,12 @@ hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t s
       if (p.waves == 8) return launch_mode<D, KF, NN, SG, PK, 0, 0, 8>(p, fl, stream);
     return launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream);
   }
+  // Row-wise prefill without appended rows runs an instance without the
+  // append code (AP 0).
   constexpr int NW = decode_fast_prefill_waves(D);
+  if (!p.k_new)
+    return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW, 0>(p, fl, stream)
+                            : launch_mode<D, KF, NN, SG, PK, 16, 0, NW, 0>(p, fl, stream);
   return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW>(p, fl, stream)
                           : launch_mode<D, KF, NN, SG, PK, 16, 0, NW>(p, fl, stream);
 }
