@@ -317,8 +317,7 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
 // (0). FP32 V enters the PV MFMAs as three FP16 parts per value.
 // NW: waves per workgroup (4; row-wise prefill at d=64, 8: a unit's splits
 // then cover twice the tokens each and half as many partials are merged).
-// AP: 0 compiles the appended-row paths out (row-wise prefill launches
-// without them).
+// AP: 0 compiles the appended-row paths out (launches without them).
 template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves, int AP = 1>
 __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
@@ -1790,12 +1789,16 @@ template <int D, int KF, int NN, int SG, int PK = 0>
 hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   if (p.v_dtype == BGTQ_DTYPE_F32) {
     if (p.starts || p.k_new) return hipErrorInvalidValue;
-    return launch_mode<D, KF, NN, SG, PK, 0, 1>(p, fl, stream);
+    return launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 0>(p, fl, stream);
   }
   if (!p.starts) {
+    // Decodes without a new token run an instance without the append paths.
     if constexpr (D == 64)
-      if (p.waves == 8) return launch_mode<D, KF, NN, SG, PK, 0, 0, 8>(p, fl, stream);
-    return launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream);
+      if (p.waves == 8)
+        return p.k_new ? launch_mode<D, KF, NN, SG, PK, 0, 0, 8>(p, fl, stream)
+                       : launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 0>(p, fl, stream);
+    return p.k_new ? launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream)
+                   : launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 0>(p, fl, stream);
   }
   // Row-wise prefill without appended rows runs an instance without the
   // append code (AP 0).
