@@ -317,7 +317,8 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
 // (0). FP32 V enters the PV MFMAs as three FP16 parts per value.
 // NW: waves per workgroup (4; row-wise prefill at d=64, 8: a unit's splits
 // then cover twice the tokens each and half as many partials are merged).
-// AP: 0 compiles the appended-row paths out (launches without them).
+// AP: the launch's extra outputs, compiled in only where used: 0 none, 1 the
+// appended rows (decode or prefill append), 2 materialised logits (inspect()).
 template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves, int AP = 1>
 __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
   using Gm = Geo<D>;
@@ -548,7 +549,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // per kWaves rows, each wave encoding one row, and the part's rows then
   // attended to as one chunk. The history splits attend to the tokens
   // before them and never wait for an encode.
-  const bool app = KF >= 1 && AP && p.k_new != nullptr;
+  const bool app = KF >= 1 && AP == 1 && p.k_new != nullptr;
+  const bool lg = AP == 2 && p.logits != nullptr;  // materialised logits (inspect())
   const int part = split - p.splits;
   const bool app_wg = app && part >= 0;
   const int sf = p.split_floor;
@@ -1039,7 +1041,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         part = __builtin_fmaf(scr.xn[32 * s2 + 8 * gq + k], (float)qhi[s2][k] + (float)qlo[s2][k], part);
     const float xt = col_sum(part) * __builtin_ldexpf(kq, ec);
     new_x = head_ok && t_new < lim ? xt : -INFINITY;
-    if (p.logits && head_ok) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
+    if (lg && head_ok) p.logits[((int64_t)qrow * Hq + hq0 + col) * p.logit_stride + t_new] = new_x * kLn2;
   }
   if (rowwise && app_wg) {
     // The part's rows (encoded before the rotation) laid out as one chunk in
@@ -1475,7 +1477,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
         wait_lds();
         issue(i + AHEAD);
       }
-      const int newer = p.logits ? 0 : min(n_chunks - 1 - i, AHEAD);
+      const int newer = lg ? 0 : min(n_chunks - 1 - i, AHEAD);
       if (newer == AHEAD) wait_vm<AHEAD * L>();
       else if (AHEAD > 2 && newer == 2) wait_vm<2 * L>();
       else if (newer >= 1) wait_vm<L>();
@@ -1493,7 +1495,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
 
       float x[8];
       chunk_logits(sb, c0, x);
-      if (p.logits) {  // materialised logits for inspect() (natural units)
+      if (lg) {  // materialised logits for inspect() (natural units)
   #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int tok = c0 + 16 * (j >> 2) + 4 * gq + (j & 3);
@@ -1789,16 +1791,21 @@ template <int D, int KF, int NN, int SG, int PK = 0>
 hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
   if (p.v_dtype == BGTQ_DTYPE_F32) {
     if (p.starts || p.k_new) return hipErrorInvalidValue;
-    return launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 0>(p, fl, stream);
+    return p.logits ? launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 2>(p, fl, stream)
+                    : launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 0>(p, fl, stream);
   }
   if (!p.starts) {
-    // Decodes without a new token run an instance without the append paths.
+    // The instance with the extra outputs the launch has: appended rows (1),
+    // materialised logits (2) or neither (0).
+    const int ap = p.k_new ? 1 : p.logits ? 2 : 0;
     if constexpr (D == 64)
       if (p.waves == 8)
-        return p.k_new ? launch_mode<D, KF, NN, SG, PK, 0, 0, 8>(p, fl, stream)
-                       : launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 0>(p, fl, stream);
-    return p.k_new ? launch_mode<D, KF, NN, SG, PK, 0>(p, fl, stream)
-                   : launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 0>(p, fl, stream);
+        return ap == 1 ? launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 1>(p, fl, stream)
+               : ap == 2 ? launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 2>(p, fl, stream)
+                         : launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 0>(p, fl, stream);
+    return ap == 1 ? launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 1>(p, fl, stream)
+           : ap == 2 ? launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 2>(p, fl, stream)
+                     : launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 0>(p, fl, stream);
   }
   // Row-wise prefill without appended rows runs an instance without the
   // append code (AP 0).
