@@ -26,7 +26,8 @@ OBJ_DIR = PKG / "_build"
 INCLUDE = PKG.parent / "include"
 ARCH = os.environ.get("BGTQ_OFFLOAD_ARCH", "gfx950")
 
-DEVICE_SOURCES = ["encode.hip", "encode_bulk.hip", "encode_wave.hip", "decode.hip", "decode_fast.hip", "prefill.hip", "reconstruct.hip", "model_ops.hip",
+DEVICE_SOURCES = ["encode.hip", "encode_bulk.hip", "encode_wave.hip", "decode.hip", "decode_fast.hip", "decode_fast_any64.hip", "decode_fast_any128.hip",
+                  "decode_fast_d64.hip", "decode_fast_d128.hip", "prefill.hip", "reconstruct.hip", "model_ops.hip",
                   "decode_scratch.hip"]
 HOST_SOURCES = ["bgtq_api.cpp", "calibrate.cpp"]
 

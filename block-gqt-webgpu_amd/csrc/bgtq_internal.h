@@ -331,7 +331,7 @@ struct FastLayout {
 // Sets the calling thread's bgtq_last_error() message; returns code.
 int32_t set_error(int32_t code, const char *msg);
 
-// Launchers (kernels live in encode.hip / decode.hip / decode_fast.hip / reconstruct.hip).
+// Launchers (kernels live in encode.hip / decode.hip / decode_fast_kernel.h / reconstruct.hip).
 // The thread-per-row encoders read their jobs from a device job table
 // (jobs[0 .. n_jobs), one grid row per job); launch_encode_upload writes up to
 // kEncodeJobsPerLaunch jobs of a chunk (kernel arguments) to table[base ..]
@@ -365,7 +365,7 @@ hipError_t launch_decode(const DecodeParams &p, int lds_bytes, hipStream_t strea
 hipError_t launch_decode_tail(const DecodeParams &p, hipStream_t stream);
 // Materialised probabilities exp(logit - m)/l from the final statistics.
 hipError_t launch_decode_probs(const DecodeParams &p, hipStream_t stream);
-// Fused decode (decode_fast.hip): nn leading nibble K-steps, sg K-steps in group 0;
+// Fused decode (decode_fast_kernel.h): nn leading nibble K-steps, sg K-steps in group 0;
 // nn = -1: a packed layout of any structure (per-position code lookup).
 bool decode_fast_supported(int dim, int key_format, int nn, int sg);
 // LDS bytes the per-position path holds for the books' code tables

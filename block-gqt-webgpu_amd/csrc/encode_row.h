@@ -2,7 +2,7 @@
 // d=128): the arithmetic of src/reference/production_math.py:4-24 as its
 // torch code evaluates on the CPU, bit for bit. Shared by the wave encoder
 // (encode_wave.hip) and the decode-step append inside the fused decode
-// kernel (decode_fast.hip).
+// kernel (decode_fast_kernel.h).
 //  * the FP32 sums of production_math.py:12, :14 and :23 follow ATen's 8-lane
 //    inner-sum tree: lane (l, g) forms partial l of group g from the four
 //    interleaved accumulators in the tree's order, lane g then adds the eight
