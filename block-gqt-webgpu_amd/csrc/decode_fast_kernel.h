@@ -666,7 +666,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // (cache rows start_c + r_a + ER w + e), e < ER, those the chunk has.
   const int t_new = rowwise ? start_c + r_a + ER * wave : T_b - 1;
   const int c_new = t_new >= 0 ? t_new / kChunk : 0;
-  const int own_w = VF || rowwise || p.k_new == nullptr || t_new < 0 ? -1
+  const int own_w = VF || rowwise || AP != 1 || p.k_new == nullptr || t_new < 0 ? -1
                     : app                                             ? (app_wg ? 0 : -1)
                                                                       : c_new % (p.splits * kWaves) - split * kWaves;
   const bool owner = own_w == wave;
