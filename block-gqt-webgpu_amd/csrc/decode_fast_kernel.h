@@ -325,8 +325,11 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
 // then cover twice the tokens each and half as many partials are merged).
 // AP: the launch's extra outputs, compiled in only where used: 0 none, 1 the
 // appended rows (decode or prefill append), 2 materialised logits (inspect()).
-template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves, int AP = 1>
-__global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
+// RL: the workgroup's role in a launch with appended rows and packed K, known
+// from its split index before anything else: 1 a history split, 2 an append
+// workgroup; 0 either (decided at run time). The kernel below picks it.
+template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves, int AP = 1, int RL = 0>
+__device__ __forceinline__ void decode_fast_body(const DecodeParams &p, const FastLayout &fl, uint8_t *tabs) {
   using Gm = Geo<D>;
   using Sl = Slot<D, KF, NN, VF, NW>;
   static_assert(VF == 0 || PF == 0, "FP32 V: decode only");
@@ -409,8 +412,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // The K-steps' lookup tables are static LDS (an address fixed at compile
   // time, so a lookup's address is the code byte shifted: one instruction);
   // the ring is the dynamic LDS.
-  // KF 2: the code tables of the KV head's books, 1 KB each.
-  __shared__ __align__(16) uint8_t tabs[KF >= 1 ? Sl::TABLES : 16];
+  // KF 2: the code tables of the KV head's books, 1 KB each (tabs, declared
+  // by the kernel).
   uint8_t *ring = smem;
   auto slot_base = [&](int s) { return ring + (s * kWaves + wave) * Sl::BYTES; };
 
@@ -555,10 +558,10 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
   // per kWaves rows, each wave encoding one row, and the part's rows then
   // attended to as one chunk. The history splits attend to the tokens
   // before them and never wait for an encode.
-  const bool app = KF >= 1 && AP == 1 && p.k_new != nullptr;
+  const bool app = RL != 0 || (KF >= 1 && AP == 1 && p.k_new != nullptr);
   const bool lg = AP == 2 && p.logits != nullptr;  // materialised logits (inspect())
   const int part = split - p.splits;
-  const bool app_wg = app && part >= 0;
+  const bool app_wg = RL == 2 || (RL == 0 && app && part >= 0);
   const int sf = p.split_floor;
   const int S_hist = !rowwise ? p.splits
                      : app    ? min(p.splits, (start_c + sf - 1) / sf)
@@ -1767,6 +1770,22 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     p.out[head * D + dm] = Ov;
   }
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int KF, int NN, int SG, int PK = 0, int PF = 0, int VF = 0, int NW = kWaves, int AP = 1>
+__global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, FastLayout fl) {
+  using Sl = Slot<D, KF, NN, VF, NW>;
+  __shared__ __align__(16) uint8_t tabs[KF >= 1 ? Sl::TABLES : 16];
+  if constexpr (AP == 1 && KF >= 1) {
+    // With appended rows (every launch of this instance has them) the
+    // append workgroups come after the splits; each role gets code of its
+    // own, so a history split carries none of the encoder's.
+    const int split = PF ? blockIdx.z : blockIdx.x;
+    if (split >= p.splits) decode_fast_body<D, KF, NN, SG, PK, PF, VF, NW, AP, 2>(p, fl, tabs);
+    else decode_fast_body<D, KF, NN, SG, PK, PF, VF, NW, AP, 1>(p, fl, tabs);
+  } else {
+    decode_fast_body<D, KF, NN, SG, PK, PF, VF, NW, AP, 0>(p, fl, tabs);
+  }
 }
 
 template <int D, int KF, int NN, int SG, int PK, int PF, int VF = 0, int NW = kWaves, int AP = 1>
