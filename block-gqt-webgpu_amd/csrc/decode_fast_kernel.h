@@ -323,6 +323,24 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
 // (0). FP32 V enters the PV MFMAs as three FP16 parts per value.
 // NW: waves per workgroup (4; row-wise prefill at d=64, 8: a unit's splits
 // then cover twice the tokens each and half as many partials are merged).
+// Every kernel argument the set-up reads, loaded at once (one asm statement,
+// whose operands' wait is the only one): left to itself the compiler loads
+// them a basic block at a time, a chain of dependent scalar round trips ahead
+// of the first DMA. Needs p, fl and kv.
+#define BGTQ_ARGS                                                                                              \
+  "s"(p.kv_heads), "s"(p.rows), "s"(p.starts), "s"(p.lengths), "s"(p.max_length), "s"(p.G), "s"(p.q_heads), \
+      "s"(p.splits), "s"(p.ends), "s"(p.k_new), "s"(p.q_rotated), "s"(p.q), "s"(p.v), "s"(p.packed),         \
+      "s"(p.norms), "s"(p.k), "s"(p.logits), "s"(p.qgroups), "s"(p.split_floor)
+#define BGTQ_LOAD_ARGS                                                                                         \
+  if constexpr (KF == 0) asm volatile("" ::BGTQ_ARGS);                                                         \
+  if constexpr (KF == 1)                                                                                       \
+  asm volatile("" ::BGTQ_ARGS, "s"(fl.mfma[kv]), "s"(fl.rot_q[kv]), "s"(fl.cent_exp[kv]), "s"(fl.book[0]),     \
+  "s"(fl.book[1]), "s"(fl.book[Gm::KS - 2]), "s"(fl.book[Gm::KS - 1]));                                        \
+  if constexpr (KF == 2)                                                                                       \
+  asm volatile("" ::BGTQ_ARGS, "s"(fl.mfma[kv]), "s"(fl.rot_q[kv]), "s"(fl.cent_exp[kv]), "s"(fl.glane[kv]),   \
+  "s"((int)fl.gnb[kv]), "s"((int)fl.gbstride[kv]), "s"((int)fl.gbnib[kv]), "s"(fl.gpair[kv]),                  \
+  "s"((int)fl.grb[kv]), "s"((int)fl.gns[kv]));
+
 // AP: the launch's extra outputs, compiled in only where used: 0 none, 1 the
 // appended rows (decode or prefill append), 2 materialised logits (inspect()).
 // RL: the workgroup's role in a launch with appended rows and packed K, known
@@ -358,23 +376,9 @@ __device__ __forceinline__ void decode_fast_body(const DecodeParams &p, const Fa
   // qrow: the sequence (PF: b * qgroups + query group).
   const int split = PF ? blockIdx.z : blockIdx.x, kv = PF ? blockIdx.x : blockIdx.y,
             qrow = PF ? blockIdx.y : blockIdx.z;
-  // Every kernel argument the set-up reads, loaded at once: left to itself
-  // the compiler loads them a basic block at a time, a chain of dependent
-  // scalar round trips ahead of the first DMA.
-  // One asm statement: the wait for its operands is the only one.
-#define BGTQ_ARGS                                                                                              \
-  "s"(p.kv_heads), "s"(p.rows), "s"(p.starts), "s"(p.lengths), "s"(p.max_length), "s"(p.G), "s"(p.q_heads), \
-      "s"(p.splits), "s"(p.ends), "s"(p.k_new), "s"(p.q_rotated), "s"(p.q), "s"(p.v), "s"(p.packed),         \
-      "s"(p.norms), "s"(p.k), "s"(p.logits), "s"(p.qgroups), "s"(p.split_floor)
-  if constexpr (KF == 0) asm volatile("" ::BGTQ_ARGS);
-  if constexpr (KF == 1)
-    asm volatile("" ::BGTQ_ARGS, "s"(fl.mfma[kv]), "s"(fl.rot_q[kv]), "s"(fl.cent_exp[kv]), "s"(fl.book[0]),
-                 "s"(fl.book[1]), "s"(fl.book[Gm::KS - 2]), "s"(fl.book[Gm::KS - 1]));
-  if constexpr (KF == 2)
-    asm volatile("" ::BGTQ_ARGS, "s"(fl.mfma[kv]), "s"(fl.rot_q[kv]), "s"(fl.cent_exp[kv]), "s"(fl.glane[kv]),
-                 "s"((int)fl.gnb[kv]), "s"((int)fl.gbstride[kv]), "s"((int)fl.gbnib[kv]), "s"(fl.gpair[kv]),
-                 "s"((int)fl.grb[kv]), "s"((int)fl.gns[kv]));
-#undef BGTQ_ARGS
+  // Every kernel argument the set-up reads, in one round trip (with the
+  // role chosen by the kernel, already loaded there).
+  BGTQ_LOAD_ARGS
   __builtin_amdgcn_sched_barrier(0);
   const int unit = qrow * p.kv_heads + kv;
   uint32_t *const counter = p.counters + (int64_t)unit * (p.counter_stride > 0 ? p.counter_stride : 1);
@@ -1780,13 +1784,17 @@ __global__ __launch_bounds__(64 * NW) void decode_fast_kernel(DecodeParams p, Fa
     // With appended rows (every launch of this instance has them) the
     // append workgroups come after the splits; each role gets code of its
     // own, so a history split carries none of the encoder's.
-    const int split = PF ? blockIdx.z : blockIdx.x;
+    using Gm = Geo<D>;
+    const int split = PF ? blockIdx.z : blockIdx.x, kv = PF ? blockIdx.x : blockIdx.y;
+    BGTQ_LOAD_ARGS  // here, so the branch on p.splits waits for no load of its own
     if (split >= p.splits) decode_fast_body<D, KF, NN, SG, PK, PF, VF, NW, AP, 2>(p, fl, tabs);
     else decode_fast_body<D, KF, NN, SG, PK, PF, VF, NW, AP, 1>(p, fl, tabs);
   } else {
     decode_fast_body<D, KF, NN, SG, PK, PF, VF, NW, AP, 0>(p, fl, tabs);
   }
 }
+#undef BGTQ_LOAD_ARGS
+#undef BGTQ_ARGS
 
 template <int D, int KF, int NN, int SG, int PK, int PF, int VF = 0, int NW = kWaves, int AP = 1>
 hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
