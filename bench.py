@@ -661,8 +661,8 @@ def phase4_attention(dev, samples=20, warmup=5):
                 keys.destroy()
     out["protocol"] = ("record() with timestamps at begin and end of the attention work (the fused kernel, plus "
                        "the probabilities pass when intermediates are materialised), 5 warmups, median of 20; "
-                       "FP32 V read by the kernel's FP32-V variant; kernel_us: first kernel start to last kernel end "
-                       "per record() in profiles/decode_fast_fp32v_phase4_trace.txt (rocprofv3 --kernel-trace of "
+                       "FP32 V read by the kernel's FP32-V variant; kernel_us: the fused kernel plus the probabilities "
+                       "kernel per record() in profiles/decode_fast_fp32v_phase4_trace.txt (rocprofv3 --kernel-trace of "
                        "bench.py --attention-only; committed, not measured in this run); reference_us_gen12lp: the reference's "
                        "published phase-4 time on its own hardware, for context only")
     return out
@@ -1047,7 +1047,8 @@ def main():
                                        "FETCH_SIZE / WRITE_SIZE of this launch, calibrated on a copy; committed, "
                                        "not measured in this run)",
                      "frac_of_measured_read_ceiling": round(achieved / ceil["hbm_read_gbs"], 4),
-                     "kernel": "decode_fast_kernel<64,1,1,1> (one launch per layer)", "bytes_per_launch": bytes_layer},
+                     "kernel": "decode_fast_kernel<64,1,1,1,0,0,0,4,0> (one launch per layer)",
+                     "bytes_per_launch": bytes_layer},
         "cpu_baseline": cpu,
         **extra,
     }
