@@ -32,16 +32,27 @@ int decode_general_max_norm_stride(int dim) {
   return dim == 64 ? Slot<64, 2, 2>::NBYTES / 64 : Slot<128, 2, 2>::NBYTES / 64;
 }
 
-// Instances by family, each in a translation unit of its own.
+// Instances by family and kind of launch, each in a translation unit of its own.
 hipError_t launch_decode_fast_any64(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
+hipError_t launch_decode_fast_any64_append(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
 hipError_t launch_decode_fast_any128(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
 hipError_t launch_decode_fast_d64(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
+hipError_t launch_decode_fast_d64_append(const DecodeParams &p, const FastLayout &fl, int nn, int sg,
+                                         hipStream_t stream);
+hipError_t launch_decode_fast_d64_prefill(const DecodeParams &p, const FastLayout &fl, int nn, int sg,
+                                          hipStream_t stream);
 hipError_t launch_decode_fast_d128(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
 
 hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
-  if (nn < 0)  // any packed layout
-    return p.dim == 64 ? launch_decode_fast_any64(p, fl, stream) : launch_decode_fast_any128(p, fl, stream);
-  return p.dim == 64 ? launch_decode_fast_d64(p, fl, nn, sg, stream) : launch_decode_fast_d128(p, fl, nn, sg, stream);
+  const int kind = decode_fast_launch_kind(p);
+  if (nn < 0) {  // any packed layout
+    if (p.dim != 64) return launch_decode_fast_any128(p, fl, stream);
+    return kind == kKindAppend ? launch_decode_fast_any64_append(p, fl, stream) : launch_decode_fast_any64(p, fl, stream);
+  }
+  if (p.dim != 64) return launch_decode_fast_d128(p, fl, nn, sg, stream);
+  return kind == kKindAppend    ? launch_decode_fast_d64_append(p, fl, nn, sg, stream)
+         : kind == kKindPrefill ? launch_decode_fast_d64_prefill(p, fl, nn, sg, stream)
+                                : launch_decode_fast_d64(p, fl, nn, sg, stream);
 }
 
 }  // namespace bgtq

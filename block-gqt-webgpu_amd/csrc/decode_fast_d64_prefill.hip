@@ -1,0 +1,12 @@
+// Fused decode instances: structured layouts and FP16 K at d=64, row-wise
+// prefill.
+#include "decode_fast_kernel.h"
+
+namespace bgtq {
+
+hipError_t launch_decode_fast_d64_prefill(const DecodeParams &p, const FastLayout &fl, int nn, int sg,
+                                          hipStream_t stream) {
+  return launch_family_d64<kKindPrefill>(p, fl, nn, sg, stream);
+}
+
+}  // namespace bgtq

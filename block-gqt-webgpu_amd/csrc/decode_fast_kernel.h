@@ -1,8 +1,10 @@
 // Fused single-launch decode attention for gfx950 on the matrix cores: the
 // kernel template and its launch helpers. The instances are compiled in
-// decode_fast_any.hip (any packed layout), decode_fast_d64.hip and
-// decode_fast_d128.hip (structured layouts and FP16 K), so they build in
-// parallel; decode_fast.hip dispatches to them.
+// decode_fast_any64.hip, decode_fast_any64_append.hip, decode_fast_any128.hip
+// (any packed layout), decode_fast_d64.hip, decode_fast_d64_append.hip,
+// decode_fast_d64_prefill.hip and decode_fast_d128.hip (structured layouts
+// and FP16 K), so they build in parallel and each kind of launch can take its
+// own scheduling options; decode_fast.hip dispatches to them.
 //
 // One workgroup (4 waves) per (sequence, KV head, token split). Everything a
 // decode step of one layer needs happens in this one launch:
@@ -55,6 +57,18 @@ constexpr int kChunk = 32;  // tokens per wave iteration: two 16-token MFMA tile
 constexpr int kRing = 2;    // LDS chunk buffers per wave: compute one, the next in flight
 constexpr bool kInterleaved = true;
 constexpr int kMergeOneRound = 40;  // split counts merged with a single round of loads
+
+// Kinds of launch of the fused kernel. Each kind's instances can sit in a
+// translation unit of their own, compiled with the scheduling options that
+// measured best for that kind.
+constexpr int kKindDecode = 1;   // decode, no appended rows (FP32 V included)
+constexpr int kKindAppend = 2;   // decode with an appended token (bgtq_decode_append)
+constexpr int kKindPrefill = 4;  // row-wise prefill (p.starts), with or without appended rows
+constexpr int kKindAll = 7;
+
+inline int decode_fast_launch_kind(const DecodeParams &p) {
+  return p.starts ? kKindPrefill : p.k_new ? kKindAppend : kKindDecode;
+}
 
 template <int D>
 struct Geo {
@@ -1819,35 +1833,84 @@ hipError_t launch_mode(const DecodeParams &p, const FastLayout &fl, hipStream_t 
 }
 
 // Row-wise prefill (p.starts set) runs the PF variant of its unit width;
-// FP32 V (decode without an appended token) the VF variant.
-template <int D, int KF, int NN, int SG, int PK = 0>
+// FP32 V (decode without an appended token) the VF variant. KINDS: the kinds
+// of launch whose instances this translation unit holds (the others return
+// hipErrorInvalidValue; the dispatch routes each kind to its unit).
+template <int KINDS, int D, int KF, int NN, int SG, int PK = 0>
 hipError_t launch_one(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
+  const int kind = decode_fast_launch_kind(p);
+  if (!(kind & KINDS)) return hipErrorInvalidValue;
   if (p.v_dtype == BGTQ_DTYPE_F32) {
-    if (p.starts || p.k_new) return hipErrorInvalidValue;
-    return p.logits ? launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 2>(p, fl, stream)
-                    : launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 0>(p, fl, stream);
+    if constexpr ((KINDS & kKindDecode) != 0)
+      if (kind == kKindDecode)
+        return p.logits ? launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 2>(p, fl, stream)
+                        : launch_mode<D, KF, NN, SG, PK, 0, 1, kWaves, 0>(p, fl, stream);
+    return hipErrorInvalidValue;
   }
-  if (!p.starts) {
-    // The instance with the extra outputs the launch has: appended rows (1),
-    // materialised logits (2) or neither (0).
-    const int ap = p.k_new ? 1 : p.logits ? 2 : 0;
-    if constexpr (D == 64)
-      if (p.waves == 8)
-        return ap == 1 ? launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 1>(p, fl, stream)
-               : ap == 2 ? launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 2>(p, fl, stream)
-                         : launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 0>(p, fl, stream);
-    return ap == 1 ? launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 1>(p, fl, stream)
-           : ap == 2 ? launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 2>(p, fl, stream)
-                     : launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 0>(p, fl, stream);
+  if constexpr ((KINDS & kKindDecode) != 0)
+    if (kind == kKindDecode) {
+      // The instance with the extra outputs the launch has: materialised
+      // logits (2) or none (0).
+      if constexpr (D == 64)
+        if (p.waves == 8)
+          return p.logits ? launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 2>(p, fl, stream)
+                          : launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 0>(p, fl, stream);
+      return p.logits ? launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 2>(p, fl, stream)
+                      : launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 0>(p, fl, stream);
+    }
+  if constexpr ((KINDS & kKindAppend) != 0)
+    if (kind == kKindAppend) {
+      if constexpr (D == 64)
+        if (p.waves == 8) return launch_mode<D, KF, NN, SG, PK, 0, 0, 8, 1>(p, fl, stream);
+      return launch_mode<D, KF, NN, SG, PK, 0, 0, kWaves, 1>(p, fl, stream);
+    }
+  if constexpr ((KINDS & kKindPrefill) != 0) {
+    // Row-wise prefill without appended rows runs an instance without the
+    // append code (AP 0).
+    constexpr int NW = decode_fast_prefill_waves(D);
+    if (!p.k_new)
+      return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW, 0>(p, fl, stream)
+                              : launch_mode<D, KF, NN, SG, PK, 16, 0, NW, 0>(p, fl, stream);
+    return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW>(p, fl, stream)
+                            : launch_mode<D, KF, NN, SG, PK, 16, 0, NW>(p, fl, stream);
   }
-  // Row-wise prefill without appended rows runs an instance without the
-  // append code (AP 0).
-  constexpr int NW = decode_fast_prefill_waves(D);
-  if (!p.k_new)
-    return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW, 0>(p, fl, stream)
-                            : launch_mode<D, KF, NN, SG, PK, 16, 0, NW, 0>(p, fl, stream);
-  return p.unit_cols == 8 ? launch_mode<D, KF, NN, SG, PK, 8, 0, NW>(p, fl, stream)
-                          : launch_mode<D, KF, NN, SG, PK, 16, 0, NW>(p, fl, stream);
+  return hipErrorInvalidValue;
+}
+
+// The instance families, each over the kinds of launch in KINDS.
+// Structured layouts (NN nibble K-steps, SG K-steps in group 0) and FP16 K.
+template <int KINDS>
+hipError_t launch_family_d64(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
+  if (p.key_format == 0) return launch_one<KINDS, 64, 0, 0, 2>(p, fl, stream);
+  if (nn == 1 && sg == 1) return launch_one<KINDS, 64, 1, 1, 1>(p, fl, stream);
+  if (nn == 2 && sg == 2) return launch_one<KINDS, 64, 1, 2, 2>(p, fl, stream);
+  if (nn == 0 && sg == 2) return launch_one<KINDS, 64, 1, 0, 2>(p, fl, stream);
+  if (nn == 2 && sg == 1) return launch_one<KINDS, 64, 1, 2, 1>(p, fl, stream);
+  if (nn == 0 && sg == 1) return launch_one<KINDS, 64, 1, 0, 1>(p, fl, stream);
+  return hipErrorInvalidValue;
+}
+
+template <int KINDS>
+hipError_t launch_family_d128(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream) {
+  if (p.key_format == 0) return launch_one<KINDS, 128, 0, 0, 4>(p, fl, stream);
+  if (nn == 2 && sg == 2) return launch_one<KINDS, 128, 1, 2, 2>(p, fl, stream);
+  if (nn == 4 && sg == 4) return launch_one<KINDS, 128, 1, 4, 4>(p, fl, stream);
+  if (nn == 0 && sg == 4) return launch_one<KINDS, 128, 1, 0, 4>(p, fl, stream);
+  if (nn == 4 && sg == 2) return launch_one<KINDS, 128, 1, 4, 2>(p, fl, stream);
+  if (nn == 0 && sg == 2) return launch_one<KINDS, 128, 1, 0, 2>(p, fl, stream);
+  return hipErrorInvalidValue;
+}
+
+// Any packed layout: one or two scale DMAs per chunk (the largest norm stride
+// of the launch's heads), pair lookups for K-step 0 when every head's K-step
+// 0 is a pair K-step.
+template <int KINDS, int D>
+hipError_t launch_family_any(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
+  int ns = 0;
+  for (int h = 0; h < p.kv_heads; ++h) ns = fl.gns[h] > ns ? fl.gns[h] : ns;
+  const bool pk = fl.gpair_lead >= 1;
+  if (ns <= 4) return pk ? launch_one<KINDS, D, 2, 1, 1, 1>(p, fl, stream) : launch_one<KINDS, D, 2, 1, 1>(p, fl, stream);
+  return pk ? launch_one<KINDS, D, 2, 2, 1, 1>(p, fl, stream) : launch_one<KINDS, D, 2, 2, 1>(p, fl, stream);
 }
 
 }  // namespace
