@@ -27,7 +27,8 @@ INCLUDE = PKG.parent / "include"
 ARCH = os.environ.get("BGTQ_OFFLOAD_ARCH", "gfx950")
 
 DEVICE_SOURCES = ["encode.hip", "encode_bulk.hip", "encode_wave.hip", "decode.hip", "decode_fast.hip",
-                  "decode_fast_any64.hip", "decode_fast_any64_append.hip", "decode_fast_any128.hip",
+                  "decode_fast_any64.hip", "decode_fast_any64_append.hip", "decode_fast_any64_prefill.hip",
+                  "decode_fast_any128.hip",
                   "decode_fast_d64.hip", "decode_fast_d64_append.hip", "decode_fast_d64_prefill.hip",
                   "decode_fast_d128.hip", "prefill.hip", "reconstruct.hip", "model_ops.hip", "decode_scratch.hip"]
 HOST_SOURCES = ["bgtq_api.cpp", "calibrate.cpp"]
@@ -47,15 +48,19 @@ DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-ffp-contract=off", "-fno-gpu-flush-d
 # the other units keep the default):
 #   decode_fast_d64.hip (decode, structured layouts): max-ilp, C5 layout B
 #     6350 -> 6380 GB/s;
+#   decode_fast_any64.hip (decode, any packed layout): max-ilp, C5 on the
+#     SmolLM2 calibration heads 5379 -> 5445 GB/s;
 #   decode_fast_d64_append.hip (decode with an appended token): max-ilp and
 #     wave priorities raised around the memory-issue phase, the SmolLM2 step
 #     (layout B) 248.6 -> 243.4 us;
 #   decode_fast_any64_append.hip (the same on any packed layout): max-memory-
 #     clause, the SmolLM2 step on its calibration heads 301.6 -> 296.2 us.
-# (Row-wise prefill measured 1% slower under either and keeps the default.)
+# (Row-wise prefill measured up to 1% slower under these and the tiled
+# prefill no different: both keep the default.)
 _MAX_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 SOURCE_FLAGS = {"prefill.hip": ["-fno-honor-nans"],
                 "decode_fast_d64.hip": _MAX_ILP,
+                "decode_fast_any64.hip": _MAX_ILP,
                 "decode_fast_d64_append.hip": _MAX_ILP + ["-mllvm", "-amdgpu-set-wave-priority"],
                 "decode_fast_any64_append.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
 

@@ -35,6 +35,7 @@ int decode_general_max_norm_stride(int dim) {
 // Instances by family and kind of launch, each in a translation unit of its own.
 hipError_t launch_decode_fast_any64(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
 hipError_t launch_decode_fast_any64_append(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
+hipError_t launch_decode_fast_any64_prefill(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
 hipError_t launch_decode_fast_any128(const DecodeParams &p, const FastLayout &fl, hipStream_t stream);
 hipError_t launch_decode_fast_d64(const DecodeParams &p, const FastLayout &fl, int nn, int sg, hipStream_t stream);
 hipError_t launch_decode_fast_d64_append(const DecodeParams &p, const FastLayout &fl, int nn, int sg,
@@ -47,7 +48,9 @@ hipError_t launch_decode_fast(const DecodeParams &p, const FastLayout &fl, int n
   const int kind = decode_fast_launch_kind(p);
   if (nn < 0) {  // any packed layout
     if (p.dim != 64) return launch_decode_fast_any128(p, fl, stream);
-    return kind == kKindAppend ? launch_decode_fast_any64_append(p, fl, stream) : launch_decode_fast_any64(p, fl, stream);
+    return kind == kKindAppend    ? launch_decode_fast_any64_append(p, fl, stream)
+           : kind == kKindPrefill ? launch_decode_fast_any64_prefill(p, fl, stream)
+                                  : launch_decode_fast_any64(p, fl, stream);
   }
   if (p.dim != 64) return launch_decode_fast_d128(p, fl, nn, sg, stream);
   return kind == kKindAppend    ? launch_decode_fast_d64_append(p, fl, nn, sg, stream)

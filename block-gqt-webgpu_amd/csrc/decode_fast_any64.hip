@@ -1,11 +1,11 @@
 // Fused decode instances: any packed layout at d=64, decode without appended
-// rows and row-wise prefill.
+// rows.
 #include "decode_fast_kernel.h"
 
 namespace bgtq {
 
 hipError_t launch_decode_fast_any64(const DecodeParams &p, const FastLayout &fl, hipStream_t stream) {
-  return launch_family_any<kKindDecode | kKindPrefill, 64>(p, fl, stream);
+  return launch_family_any<kKindDecode, 64>(p, fl, stream);
 }
 
 }  // namespace bgtq

@@ -1,7 +1,7 @@
 // Fused single-launch decode attention for gfx950 on the matrix cores: the
 // kernel template and its launch helpers. The instances are compiled in
-// decode_fast_any64.hip, decode_fast_any64_append.hip, decode_fast_any128.hip
-// (any packed layout), decode_fast_d64.hip, decode_fast_d64_append.hip,
+// decode_fast_any64.hip, decode_fast_any64_append.hip,
+// decode_fast_any64_prefill.hip, decode_fast_any128.hip (any packed layout), decode_fast_d64.hip, decode_fast_d64_append.hip,
 // decode_fast_d64_prefill.hip and decode_fast_d128.hip (structured layouts
 // and FP16 K), so they build in parallel and each kind of launch can take its
 // own scheduling options; decode_fast.hip dispatches to them.
