@@ -194,7 +194,7 @@ __device__ __forceinline__ void merge_one_round(float *part, float *out, float *
       if (g >= G) continue;
       const int64_t head = head0 + g;
       const float M = col_max(row_max(ms[h]));
-      const float w = ms[h] == -INFINITY ? 0.0f : exp2f(ms[h] - M);
+      const float w = ms[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[h] - M);
       float lw = ls[h] * w;
       lw += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(lw), 0x128, 0xf, 0xf, false));
       lw += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(lw), 0x124, 0xf, 0xf, false));
@@ -268,7 +268,7 @@ __device__ __forceinline__ void merge_rows(float *part, float *out, const MergeR
   for (int h = 0; h < NH; ++h) M[h] = col_max(M[h]);
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
-    w[h] = m[h] == -INFINITY ? 0.0f : exp2f(m[h] - M[h]);
+    w[h] = m[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[h] - M[h]);
     Lsum[h] = (lane < S ? __uint_as_float(ml[h][1]) : 0.0f) * w[h];
   }
   // Row sums: rotations by 8, 4, 2, 1 lanes (DPP row_ror).
@@ -1619,7 +1619,7 @@ __device__ __forceinline__ void decode_fast_body(const DecodeParams &p, const Fa
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const bool live = mw[w] != -INFINITY;
-        const float wt = exp2f(mw[w] - M);
+        const float wt = __builtin_amdgcn_exp2f(mw[w] - M);
         Lsum = live ? __builtin_fmaf(lw[w], wt, Lsum) : Lsum;
         Ov = live ? __builtin_fmaf(ow[w], wt, Ov) : Ov;
       }
@@ -1677,7 +1677,7 @@ __device__ __forceinline__ void decode_fast_body(const DecodeParams &p, const Fa
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const bool live = mw[k][w] != -INFINITY;
-        const float wt = exp2f(mw[k][w] - M);
+        const float wt = __builtin_amdgcn_exp2f(mw[k][w] - M);
         Lsum = live ? __builtin_fmaf(lw[k][w], wt, Lsum) : Lsum;
         Ov = live ? __builtin_fmaf(ow[k][w], wt, Ov) : Ov;
       }
@@ -1755,7 +1755,7 @@ __device__ __forceinline__ void decode_fast_body(const DecodeParams &p, const Fa
     float Lsum = 0.0f;
     for (int s = 0; s < S; ++s) {
       const float m = mrow[tid * S + s];
-      const float w = m == -INFINITY ? 0.0f : exp2f(m - M);
+      const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
       Lsum = __builtin_fmaf(wgt[tid * S + s], w, Lsum);
       mrow[tid * S + s] = w;
     }
