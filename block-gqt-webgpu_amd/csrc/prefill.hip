@@ -905,13 +905,13 @@ __global__ __launch_bounds__(kThreads) void prefill_merge_kernel(PrefillParams p
     float Mn = M;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) Mn = fmaxf(Mn, m[kk]);
-    const float sc = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+    const float sc = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
     L *= sc;
 #pragma unroll
     for (int e = 0; e < DL; ++e) acc[e] *= sc;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const float w = m[kk] == -INFINITY ? 0.0f : exp2f(m[kk] - Mn);
+      const float w = m[kk] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[kk] - Mn);
       L = __builtin_fmaf(w, l[kk], L);
 #pragma unroll
       for (int e = 0; e < DL; ++e) acc[e] += o[kk][e] * w;
@@ -963,13 +963,13 @@ __global__ __launch_bounds__(kThreads) void prefill_merge_one_round_kernel(Prefi
       float Mn = M;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) Mn = fmaxf(Mn, m[kk]);
-      const float sc = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+      const float sc = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
       L *= sc;
 #pragma unroll
       for (int e = 0; e < DL; ++e) acc[e] *= sc;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
-        const float w = m[kk] == -INFINITY ? 0.0f : exp2f(m[kk] - Mn);
+        const float w = m[kk] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[kk] - Mn);
         L = __builtin_fmaf(w, l[kk], L);
 #pragma unroll
         for (int e = 0; e < DL; ++e) acc[e] = __builtin_fmaf(o[kk][e], w, acc[e]);
@@ -990,7 +990,7 @@ __global__ __launch_bounds__(kThreads) void prefill_merge_one_round_kernel(Prefi
   float M = ml;
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) M = fmaxf(M, __shfl_xor(M, s, 64));
-  float w = ml == -INFINITY ? 0.0f : exp2f(ml - M);
+  float w = ml == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml - M);
   float L = w * ll;
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) L += __shfl_xor(L, s, 64);
